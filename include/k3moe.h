@@ -1,0 +1,262 @@
+/* k3moe.h - C ABI of the MI355X routed-expert MoE layer.
+ *
+ * Three groups of entry points live here.
+ *
+ *  1. DROP-IN. The engine's own MoE entry points, with the engine's names, signatures,
+ *     struct layouts and error behaviour, so a decoder layer that calls k3_moe() links
+ *     against this library unchanged. Host pointers, synchronous. Each one cites the
+ *     reference declaration it replaces.
+ *
+ *  2. DEVICE API (k3g_*). The same layer with device pointers, an explicit HIP stream and
+ *     a preallocated workspace: no allocation and no host synchronisation on the hot
+ *     path. The drop-in functions are built on it.
+ *
+ *  3. HBM EXPERT CACHE (k3gc_*). The engine's expert cache re-planned for HBM: slots in
+ *     device memory, misses copied from a pinned host bank on a side stream. It is a
+ *     K3ExpertSrc whose get() hands back DEVICE pointers.
+ *
+ * Types shared with the engine (K3Cfg, K3ExpertQ, K3ExpertSrc, K3MoeW) are declared
+ * only when the engine's k3.h has not already been included; the layouts are the
+ * engine's, field for field, because callers build these structs and pass them in.
+ */
+#ifndef K3MOE_H
+#define K3MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===================================================================== engine types == */
+#ifndef K3_H
+/* Layout of include/k3/k3.h:73-120. Only the MoE fields (n_experts .. latent_norm,
+ * hidden, rms_eps, situ_b1/b2) are read by this library; the rest are carried so that a
+ * K3Cfg built by the engine's config loader can be passed straight in. */
+typedef struct {
+    int hidden;
+    int n_layers;
+    int vocab;
+    float rms_eps;
+
+    int kda_heads;
+    int kda_head_dim;
+    int conv_k;
+    float gate_lb;
+
+    int n_heads;
+    int q_lora;
+    int kv_lora;
+    int qk_nope;
+    int qk_rope;
+    int v_head;
+    int mla_out_gate;
+
+    int n_experts;
+    int topk;
+    int n_shared;
+    int latent;
+    int moe_inter;
+    float routed_scale;
+    int moe_renorm;
+    int latent_norm;
+
+    int first_dense;
+    int dense_inter;
+
+    int attn_res_block;
+
+    float situ_b1;
+    float situ_b2;
+
+    int  n_full_attn;
+    int *full_attn;
+} K3Cfg;
+
+/* Weight tags, include/k3/k3.h:270. */
+enum { K3_WF32 = 0, K3_WBF16 = 1, K3_WI8 = 2 };
+
+/* One MXFP4 expert, include/k3/k3.h:323-327. Row-major packed nibbles (low nibble is
+ * the even element) plus one E8M0 byte per 32 elements of a row. */
+typedef struct {
+    const unsigned char *p1, *s1;        /* w1 gate  [inter][latent/2], [inter][latent/32] */
+    const unsigned char *p3, *s3;        /* w3 up                                          */
+    const unsigned char *p2, *s2;        /* w2 down  [latent][inter/2], [latent][inter/32] */
+} K3ExpertQ;
+
+/* Expert source plugin, include/k3/k3.h:332-355. */
+typedef struct K3ExpertSrc {
+    int (*get)(struct K3ExpertSrc *self, int layer, int expert, K3ExpertQ *out);
+    int (*getmany)(struct K3ExpertSrc *self, int layer, const int *experts, int n);
+    int (*resident)(struct K3ExpertSrc *self, int layer, int expert, K3ExpertQ *out);
+    void *ctx;
+} K3ExpertSrc;
+
+/* One MoE layer's weights, include/k3/k3.h:357-380. Zero it before filling it.
+ *
+ * Extension, backward compatible because the engine would dereference NULL here:
+ *   down == NULL  no latent down-projection (z = x; requires latent == hidden)
+ *   up   == NULL  no latent up-projection   (out = routed aggregate)
+ * That is the Kimi-K2 layer shape, which the engine otherwise expresses with bf16
+ * identity matrices (exactly, at twice the traffic). */
+typedef struct {
+    const float *gate, *bias;
+    const float *w1, *w3, *w2;
+    const float *latent_norm;
+    const void  *down, *up;
+    const void  *sh1, *sh3, *sh2;
+    int          wdt;
+    struct K3ExpertSrc *src;
+    int          layer;
+    int          cache_only;
+} K3MoeW;
+
+#define K3_MXFP4_GROUP 32
+#define K3_MAX_TOPK 64
+#endif /* K3_H */
+
+/* ================================================================ 1. drop-in ABI == */
+
+/* Routed experts that could not be fetched and were left out of a sum.
+ * Replaces include/k3/k3.h:388 (defined at src/core/k3_ops.c:108). Callers must check
+ * it and fail the run when it changes. */
+extern long k3_expert_drops;
+
+/* Replaces include/k3/k3.h:241-243 (src/core/k3_ops.c:419-478). One token: logits =
+ * W x (fp32 weights, double accumulation), sigmoid scores, top-k on score + bias,
+ * weights gathered from the UNBIASED scores, renormalised with +1e-20, times
+ * routed_scale. idx/w are written in descending biased-score order, ties to the lower
+ * expert index. Runs on the GPU; the selection is bit-exact with the engine's. */
+void k3_router(int *idx, float *w, const float *x, const float *W,
+               const float *bias, int hidden, int n_experts, int topk,
+               int renorm, float routed_scale);
+
+/* Replaces include/k3/k3.h:382 (src/core/k3_ops.c:658-666). Same value. */
+size_t k3_moe_scratch(const K3Cfg *c);
+
+/* Replaces include/k3/k3.h:418-419 (src/core/k3_ops.c:556-656). x, out are host
+ * [T][hidden] fp32. idx/wt receive the LAST token's routing, as in the engine. scratch
+ * is accepted for ABI compatibility and not used: the GPU workspace is preallocated
+ * per device. Weights are uploaded to HBM on first use and keyed by host address, so
+ * they must not change afterwards (call k3moe_forget_weights() if they do). Experts
+ * come from w->src (MXFP4) or from the fp32 resident bank w->w1/w3/w2. A source that
+ * fails to deliver an expert bumps k3_expert_drops, as the engine does. */
+void k3_moe(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
+            int T, int *idx, float *wt, float *scratch);
+
+/* Replaces include/k3/k3.h:425-426 (src/core/k3_ops.c:689-808). Bit-identical routing
+ * to k3_moe and the same per-token arithmetic; all T tokens go to the GPU as one batch. */
+void k3_moe_prefill(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
+                    int T, int *idx, float *wt, float *scratch);
+
+/* Replaces include/k3/k3.h:559-560 (src/core/k3_ops.c:1770-1800). Exact. */
+void k3_mxfp4_dequant(float *out, const unsigned char *packed,
+                      const unsigned char *scales, int rows, int pcols, int group);
+
+/* Replaces include/k3/k3.h:565-566 (src/core/k3_ops.c:1363-1768). Aborts on odd `in`
+ * or group > 64, as the engine does. group must be 32 on the GPU path (the format
+ * K3_MXFP4_GROUP fixes); another group aborts with a message. */
+void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
+                     const unsigned char *scales, int in, int rows, int group);
+
+/* Drop every HBM copy of host weights made by k3_moe/k3_router. No reference
+ * counterpart: the engine reads host weights in place. */
+void k3moe_forget_weights(void);
+
+/* ============================================================== 2. device API == */
+
+typedef struct K3gCtx K3gCtx;        /* device, streams, workspace; opaque */
+
+/* Byte geometry of one expert run in the order the checkpoint stores it
+ * (src/io/k3_load.h:3-9): w1.packed w1.scale w2.packed w2.scale w3.packed w3.scale.
+ * Offsets are relative to the run start. */
+typedef struct {
+    int64_t p1_off, s1_off, p2_off, s2_off, p3_off, s3_off;
+    int64_t nbytes;
+} K3gExpertLayout;
+
+K3gExpertLayout k3g_expert_layout(int hidden, int inter);
+
+/* A layer whose weights are already in HBM. All pointers are device pointers.
+ *
+ *   gate [n_experts][hidden] fp32, bias [n_experts] fp32 or NULL
+ *   routed experts, running at width `latent`:
+ *     expert_fmt 0: `experts`, a device array of n_experts K3ExpertQ holding device
+ *                   pointers to MXFP4 matrices (entries of unrouted experts unused)
+ *     expert_fmt 1: the fp32 resident bank w1/w3 [n_experts][inter][latent] and
+ *                   w2 [n_experts][latent][inter] (the engine's fixture path)
+ *   shared expert, tagged by wdt (K3_WF32 or K3_WBF16): sh1/sh3 [shared_inter][hidden],
+ *     sh2 [hidden][shared_inter]; shared_inter == 0 means none
+ *   latent projections, tagged by wdt: down [latent][hidden], up [hidden][latent];
+ *     NULL for the Kimi-K2 shape (latent == hidden). latent_norm [latent] or NULL.
+ *   act_b1/act_b2: SiTU caps; a value >= 2^64 means uncapped (SwiGLU). */
+typedef struct {
+    int hidden, n_experts, topk, inter, shared_inter, latent;
+    int renorm;
+    float routed_scale;
+    float act_b1, act_b2;
+    float rms_eps;
+    const float *gate, *bias;
+    int expert_fmt;
+    const K3ExpertQ *experts;
+    const float *w1, *w3, *w2;
+    int wdt;
+    const void *sh1, *sh3, *sh2;
+    const void *down, *up;
+    const float *latent_norm;
+} K3gLayer;
+
+/* Create a context on `device` for layers of this shape (only the size fields of
+ * `shape` are read) and up to max_tokens tokens per call. Allocates the whole workspace
+ * once. Returns 0, or -1 with a message on stderr. */
+int  k3g_ctx_create(K3gCtx **ctx, int device, const K3gLayer *shape, int max_tokens);
+void k3g_ctx_destroy(K3gCtx *ctx);
+void *k3g_ctx_stream(K3gCtx *ctx);   /* the context's compute stream (hipStream_t) */
+
+/* Routing statistics since the context was created: [0] tokens whose certificate
+ * failed and were re-routed in the engine's serial order. */
+void k3g_ctx_stats(K3gCtx *ctx, int64_t *out, int n);
+
+/* Force the router's exact re-routing path: 0 normal, 1 every token re-routes its
+ * candidate set, 2 every token recomputes every expert serially (testing only). */
+void k3g_ctx_force_exact(K3gCtx *ctx, int mode);
+
+/* Router on the GPU for T tokens: x [T][hidden] fp32 -> idx [T][topk] int32,
+ * wt [T][topk] fp32, device pointers. Bit-exact selection (see k3_router). */
+int  k3g_router(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
+                int32_t *idx, float *wt, void *stream);
+
+/* The whole layer for T tokens: out [T][hidden] fp32 = routed combine + shared expert.
+ * idx/wt (device, [T][topk]) receive the routing. Asynchronous on `stream`
+ * (NULL = the context's stream). Returns 0, or -1 on a launch error. */
+int  k3g_moe(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
+             float *out, int32_t *idx, float *wt, void *stream);
+
+/* Synchronise the stream and report any error a kernel raised on the device
+ * (an exhausted bounded wait, a bad expert index). Returns 0 when clean. */
+int  k3g_sync(K3gCtx *ctx, void *stream);
+
+/* Seeded synthetic data, generated identically on host and device from a counter
+ * hash, so a CPU check can regenerate any slice of what the GPU holds.
+ * byte i of stream `stream` under `seed` is k3s_byte(seed, stream, i). */
+uint8_t k3s_byte(uint64_t seed, uint64_t stream, uint64_t i);
+void k3s_fill_bytes(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream, uint64_t first);
+/* MXFP4 E8M0 scale bytes: 127 + uniform{lo..hi}. */
+void k3s_fill_scales(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream, uint64_t first,
+                     int lo, int hi);
+/* N(mean, std) fp32 values (Box-Muller over the same counter hash). bf16_round != 0
+ * rounds each value to bf16 (nearest-even) and returns it widened. */
+void k3s_fill_normal(float *dst, size_t n, uint64_t seed, uint64_t stream, uint64_t first,
+                     float mean, float std, int bf16_round);
+/* Device fills, same values as the host fills. */
+int  k3g_fill_bytes(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream, uint64_t first,
+                    void *hstream);
+int  k3g_fill_scales(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream, uint64_t first,
+                     int lo, int hi, void *hstream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* K3MOE_H */

@@ -1,0 +1,274 @@
+/* k3g_ctx.c - device context and the k3g_* layer API (C99 host code).
+ *
+ * The layer runs as a fixed sequence of kernels on one stream:
+ *   router (fp64 logits, certified top-k)  ->  dispatch (stable counting sort)
+ *   -> [latent down] -> routed gate/up + activation -> routed down
+ *   -> shared gate/up + activation -> shared down -> combine (slot order, + shared)
+ *   -> [aggregate RMSNorm, latent up, + shared]
+ * All buffers come from one workspace allocated at context creation; a call allocates
+ * nothing. */
+#include "k3g_ctx.h"
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+void k3g_fatal_hip(const char *what, hipError_t e, const char *file, int line)
+{
+    fprintf(stderr,
+            "k3moe: FATAL, %s failed: %s (%s:%d).\n"
+            "    Aborting rather than returning an output the GPU did not finish.\n",
+            what, hipGetErrorString(e), file, line);
+    abort();
+}
+
+void k3g_fatal(const char *what)
+{
+    fprintf(stderr, "k3moe: FATAL, %s\n", what);
+    abort();
+}
+
+K3gExpertLayout k3g_expert_layout(int hidden, int inter)
+{
+    /* src/io/k3_load.h:3-9: w1.packed w1.scale w2.packed w2.scale w3.packed w3.scale */
+    K3gExpertLayout l;
+    const int64_t p13 = (int64_t)inter * (hidden / 2), s13 = (int64_t)inter * ((hidden + 31) / 32);
+    const int64_t p2 = (int64_t)hidden * (inter / 2), s2 = (int64_t)hidden * ((inter + 31) / 32);
+    l.p1_off = 0;
+    l.s1_off = l.p1_off + p13;
+    l.p2_off = l.s1_off + s13;
+    l.s2_off = l.p2_off + p2;
+    l.p3_off = l.s2_off + s2;
+    l.s3_off = l.p3_off + p13;
+    l.nbytes = l.s3_off + s13;
+    return l;
+}
+
+static size_t carve(size_t *at, size_t bytes)
+{
+    const size_t o = *at;
+    *at += (bytes + 255) & ~(size_t)255;
+    return o;
+}
+
+int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
+{
+    *out = NULL;
+    if (!s || max_tokens < 1 || s->topk < 1 || s->topk > K3G_MAX_TOPK || s->n_experts < 1 ||
+        s->n_experts > 1024 || s->hidden < 1) {
+        fprintf(stderr, "k3moe: k3g_ctx_create: unsupported shape\n");
+        return -1;
+    }
+    K3gCtx *c = (K3gCtx *)calloc(1, sizeof *c);
+    if (!c) return -1;
+    c->device = device;
+    c->hidden = s->hidden;
+    c->n_experts = s->n_experts;
+    c->topk = s->topk;
+    c->inter = s->inter;
+    c->shared_inter = s->shared_inter;
+    c->latent = s->latent > 0 ? s->latent : s->hidden;
+    c->max_tokens = max_tokens;
+
+    if (hipSetDevice(device) != hipSuccess) { free(c); return -1; }
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        free(c);
+        return -1;
+    }
+    const size_t T = (size_t)max_tokens, E = (size_t)c->n_experts, k = (size_t)c->topk;
+    const size_t P = T * k, nch = (P + 255) / 256;
+    const size_t L = (size_t)c->latent, I = (size_t)c->inter, SI = (size_t)c->shared_inter;
+    const size_t d = (size_t)c->hidden;
+    size_t at = 0;
+    const size_t o_logit = carve(&at, T * E * 8), o_asum = carve(&at, T * E * 8);
+    const size_t o_idx = carve(&at, P * 4), o_wt = carve(&at, P * 4);
+    const size_t o_cnt = carve(&at, nch * E * 4), o_base = carve(&at, nch * E * 4);
+    const size_t o_off = carve(&at, (E + 1) * 4), o_act = carve(&at, E * 4);
+    const size_t o_nact = carve(&at, 4), o_perm = carve(&at, P * 4);
+    const size_t o_z = carve(&at, T * L * 4), o_h = carve(&at, P * I * 4);
+    const size_t o_contrib = carve(&at, P * L * 4), o_accl = carve(&at, T * L * 4);
+    const size_t o_shh = carve(&at, T * (SI ? SI : 1) * 4), o_sho = carve(&at, T * d * 4);
+    const size_t o_err = carve(&at, 4), o_stats = carve(&at, 16 * 4);
+    c->ws_bytes = at;
+    if (hipMalloc(&c->ws, at) != hipSuccess) {
+        fprintf(stderr, "k3moe: cannot allocate %.2f GB of device workspace\n", at / 1e9);
+        hipStreamDestroy(c->stream);
+        free(c);
+        return -1;
+    }
+    char *b = (char *)c->ws;
+    c->logit = (double *)(b + o_logit);
+    c->asum = (double *)(b + o_asum);
+    c->idx = (int32_t *)(b + o_idx);
+    c->wt = (float *)(b + o_wt);
+    c->cnt = (int32_t *)(b + o_cnt);
+    c->base = (int32_t *)(b + o_base);
+    c->off = (int32_t *)(b + o_off);
+    c->act = (int32_t *)(b + o_act);
+    c->nact = (int32_t *)(b + o_nact);
+    c->perm = (int32_t *)(b + o_perm);
+    c->z = (float *)(b + o_z);
+    c->h = (float *)(b + o_h);
+    c->contrib = (float *)(b + o_contrib);
+    c->accl = (float *)(b + o_accl);
+    c->sh_h = (float *)(b + o_shh);
+    c->sh_out = (float *)(b + o_sho);
+    c->err = (int *)(b + o_err);
+    c->stats = (int *)(b + o_stats);
+    if (hipMemset(c->ws, 0, at) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        hipFree(c->ws);
+        hipStreamDestroy(c->stream);
+        free(c);
+        return -1;
+    }
+    *out = c;
+    return 0;
+}
+
+void k3g_ctx_destroy(K3gCtx *c)
+{
+    if (!c) return;
+    hipSetDevice(c->device);
+    hipStreamSynchronize(c->stream);
+    hipFree(c->ws);
+    hipStreamDestroy(c->stream);
+    free(c);
+}
+
+void *k3g_ctx_stream(K3gCtx *c) { return c ? (void *)c->stream : NULL; }
+
+void k3g_ctx_force_exact(K3gCtx *c, int mode) { if (c) c->force_exact = mode; }
+
+void k3g_ctx_stats(K3gCtx *c, int64_t *out, int n)
+{
+    int s[16] = {0};
+    if (!c || n <= 0) return;
+    hipSetDevice(c->device);
+    K3G_CHECK(hipStreamSynchronize(c->stream));
+    K3G_CHECK(hipMemcpy(s, c->stats, sizeof s, hipMemcpyDeviceToHost));
+    for (int i = 0; i < n && i < 16; i++) out[i] = s[i];
+}
+
+static int fits(const K3gCtx *c, const K3gLayer *L, int T)
+{
+    const int lat = L->latent > 0 ? L->latent : L->hidden;
+    if (T < 1 || T > c->max_tokens || L->hidden != c->hidden || L->n_experts > c->n_experts ||
+        L->topk > c->topk || L->inter > c->inter || L->shared_inter > c->shared_inter ||
+        lat > c->latent) {
+        fprintf(stderr, "k3moe: layer or token count exceeds the context's workspace\n");
+        return 0;
+    }
+    if (lat != L->hidden && (!L->down || !L->up)) {
+        fprintf(stderr, "k3moe: latent %d != hidden %d needs both down and up\n", lat,
+                L->hidden);
+        return 0;
+    }
+    return 1;
+}
+
+int k3g_route(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx, float *wt,
+              hipStream_t st)
+{
+    if (!fits(c, L, T)) return -1;
+    return k3k_router(x, T, L->gate, L->bias, L->hidden, L->n_experts, L->topk, L->renorm,
+                      L->routed_scale, c->logit, c->asum, idx, wt, c->force_exact,
+                      c->stats, st);
+}
+
+int k3g_router(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx, float *wt,
+               void *stream)
+{
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    return k3g_route(c, L, x, T, idx, wt, st);
+}
+
+static int wfmt(int wdt) { return wdt == K3_WBF16 ? K3K_BF16 : K3K_F32; }
+
+int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
+                const float *wt, float *out, hipStream_t st)
+{
+    if (!fits(c, L, T)) return -1;
+    const int d = L->hidden, E = L->n_experts, k = L->topk, I = L->inter;
+    const int SI = L->shared_inter, lat = L->latent > 0 ? L->latent : d;
+    const int P = T * k;
+    const int projected = L->down != NULL;
+    int rc = 0;
+
+    rc |= k3k_dispatch(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm, c->err,
+                       st);
+    const float *z = x;
+    if (projected) {
+        rc |= k3k_dense(wfmt(L->wdt), L->down, NULL, lat, d, x, d, T, c->z, lat, 0.f, 0.f, st);
+        z = c->z;
+    }
+    K3kRouted a;
+    memset(&a, 0, sizeof a);
+    a.fmt = L->expert_fmt == 1 ? K3K_F32 : K3K_MXFP4;
+    a.eq = L->experts;
+    a.w1 = L->w1;
+    a.w3 = L->w3;
+    a.w2 = L->w2;
+    a.act = c->act;
+    a.nact = c->nact;
+    a.off = c->off;
+    a.perm = c->perm;
+    a.topk = k;
+    a.inter = I;
+    a.latent = lat;
+    a.z = z;
+    a.h = c->h;
+    a.contrib = c->contrib;
+    a.b1 = L->act_b1;
+    a.b2 = L->act_b2;
+    a.err = c->err;
+    const int maxU = P < E ? P : E;
+    rc |= k3k_routed_gateup(&a, maxU, T, st);
+    rc |= k3k_routed_down(&a, maxU, T, st);
+    if (SI > 0) {
+        rc |= k3k_dense(wfmt(L->wdt), L->sh1, L->sh3, SI, d, x, d, T, c->sh_h, SI,
+                        L->act_b1, L->act_b2, st);
+        rc |= k3k_dense(wfmt(L->wdt), L->sh2, NULL, d, SI, c->sh_h, SI, T, c->sh_out, d,
+                        0.f, 0.f, st);
+    }
+    if (!projected && !L->up && !L->latent_norm) {
+        rc |= k3k_combine(c->contrib, idx, wt, T, k, d, SI > 0 ? c->sh_out : NULL, out, st);
+    } else {
+        rc |= k3k_combine(c->contrib, idx, wt, T, k, lat, NULL, c->accl, st);
+        if (L->latent_norm) rc |= k3k_rmsnorm(c->accl, c->accl, L->latent_norm, lat, T,
+                                              L->rms_eps, st);
+        if (L->up)
+            rc |= k3k_dense(wfmt(L->wdt), L->up, NULL, d, lat, c->accl, lat, T, out, d, 0.f,
+                            0.f, st);
+        else if (hipMemcpyAsync(out, c->accl, (size_t)T * d * 4, hipMemcpyDeviceToDevice, st) !=
+                 hipSuccess)
+            rc = -1;
+        if (SI > 0) rc |= k3k_add(out, c->sh_out, (size_t)T * d, st);
+    }
+    return rc ? -1 : 0;
+}
+
+int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int32_t *idx,
+            float *wt, void *stream)
+{
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    if (!idx) idx = c->idx;
+    if (!wt) wt = c->wt;
+    if (k3g_route(c, L, x, T, idx, wt, st) != 0) return -1;
+    return k3g_experts(c, L, x, T, idx, wt, out, st);
+}
+
+int k3g_sync(K3gCtx *c, void *stream)
+{
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    if (hipStreamSynchronize(st) != hipSuccess) return -1;
+    int e = 0;
+    if (hipMemcpy(&e, c->err, sizeof e, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    if (e) {
+        fprintf(stderr, "k3moe: device reported error %d (%s)\n", e,
+                e == 1 ? "routed expert index out of range" : "bounded wait ran out");
+        int z = 0;
+        hipMemcpy(c->err, &z, sizeof z, hipMemcpyHostToDevice);
+        return e;
+    }
+    return 0;
+}

@@ -1,0 +1,50 @@
+/* k3g_ctx.h - the device context behind the k3g_* API (private to the library). */
+#ifndef K3G_CTX_H
+#define K3G_CTX_H
+
+#include "k3g_kernels.h"
+
+/* Abort with a message when a HIP call fails on the hot path: the engine's rule is that
+ * a kernel never returns a partial or stale output (src/core/k3_ops.c:37-78). */
+#define K3G_CHECK(call)                                                                   \
+    do {                                                                                  \
+        hipError_t e_ = (call);                                                           \
+        if (e_ != hipSuccess) k3g_fatal_hip(#call, e_, __FILE__, __LINE__);               \
+    } while (0)
+
+void k3g_fatal_hip(const char *what, hipError_t e, const char *file, int line);
+void k3g_fatal(const char *what);
+
+struct K3gCtx {
+    int device;
+    hipStream_t stream;
+    /* shape the workspace was sized for */
+    int hidden, n_experts, topk, inter, shared_inter, latent, max_tokens;
+    int force_exact;
+    /* one device allocation, carved below */
+    void *ws;
+    size_t ws_bytes;
+    double *logit, *asum;        /* [T][E] */
+    int32_t *idx;                /* [T][k] when the caller passes none */
+    float *wt;
+    int32_t *cnt, *base;         /* [nch][E] */
+    int32_t *off, *act, *nact;   /* [E+1], [E], [1] */
+    int32_t *perm;               /* [T*k] */
+    float *z;                    /* [T][latent] when projected */
+    float *h;                    /* [T*k][inter] */
+    float *contrib;              /* [T*k][latent] */
+    float *accl;                 /* [T][latent] */
+    float *sh_h;                 /* [T][shared_inter] */
+    float *sh_out;               /* [T][hidden] */
+    int *err;                    /* device error word */
+    int *stats;                  /* device counters */
+};
+
+/* Stages of k3g_moe, for callers (the drop-in) that must act on the routing between
+ * them. idx/wt are device arrays [T][topk]; entries with idx < 0 are skipped. */
+int k3g_route(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx, float *wt,
+              hipStream_t st);
+int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
+                const float *wt, float *out, hipStream_t st);
+
+#endif /* K3G_CTX_H */

@@ -1,0 +1,112 @@
+/* k3g_dev.h - device-side helpers shared by the gfx950 kernels. */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define K3G_WAVE 64
+
+typedef float k3v2f __attribute__((ext_vector_type(2)));
+
+/* Error codes a kernel may raise into the context's device error word. The host reads
+ * it in k3g_sync() and reports it. */
+enum {
+    K3G_ERR_NONE = 0,
+    K3G_ERR_EXPERT_RANGE = 1,   /* a routed index outside [0, n_experts) reached a kernel */
+    K3G_ERR_WAIT = 2,           /* a bounded device wait ran out */
+};
+
+__device__ __forceinline__ void k3d_raise(int *err, int code)
+{
+    if (err) atomicCAS(err, 0, code);
+}
+
+/* E8M0 byte -> 2^(b-127) as fp32; 255 (NaN by the OCP spec) -> 0, matching the engine's
+ * table (src/core/k3_ops.c:1315-1322). b = 0 gives the denormal 2^-127. */
+__device__ __forceinline__ float k3d_e8m0(uint32_t b)
+{
+    return b == 255u ? 0.0f
+         : (b == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(b << 23));
+}
+
+/* Eight E2M1 values from one 32-bit word (bytes in memory order; low nibble is the even
+ * element), each times `scale`, using gfx950's v_cvt_scalef32_pk_f32_fp4. The product
+ * with a power-of-two scale is exact. */
+__device__ __forceinline__ void k3d_fp4x8(uint32_t w, float scale, float *o)
+{
+    k3v2f a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 0);
+    k3v2f b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 1);
+    k3v2f c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 2);
+    k3v2f d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, scale, 3);
+    o[0] = a.x; o[1] = a.y; o[2] = b.x; o[3] = b.y;
+    o[4] = c.x; o[5] = c.y; o[6] = d.x; o[7] = d.y;
+}
+
+__device__ __forceinline__ float k3d_bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float k3d_bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+/* Wave-wide sum, every lane gets the total. */
+__device__ __forceinline__ float k3d_wave_sum(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, K3G_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ double k3d_wave_sumd(double v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, K3G_WAVE);
+    return v;
+}
+
+/* Transposed wave reduction of V partial sums per lane (V a power of two, <= 64).
+ * Afterwards lane l holds the full 64-lane sum of value index (l >> (6 - log2 V)) in
+ * v[0]. Each halving round trades half the values with the partner lane, so the whole
+ * reduction costs about V shuffles instead of 6*V. */
+template <int V>
+__device__ __forceinline__ void k3d_transpose_reduce(float *v, int lane)
+{
+    int n = V;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        if (n > 1) {
+            const int h = n >> 1;
+            const bool upper = (lane & m) != 0;
+#pragma unroll
+            for (int i = 0; i < V / 2; ++i) {
+                if (i < h) {
+                    const float send = upper ? v[i] : v[i + h];
+                    const float keep = upper ? v[i + h] : v[i];
+                    v[i] = keep + __shfl_xor(send, m, K3G_WAVE);
+                }
+            }
+            n = h;
+        } else {
+            v[0] += __shfl_xor(v[0], m, K3G_WAVE);
+        }
+    }
+}
+
+template <>
+__device__ __forceinline__ void k3d_transpose_reduce<1>(float *v, int lane)
+{
+    (void)lane;
+    v[0] = k3d_wave_sum(v[0]);
+}
+
+/* SiTU-GLU on one (gate, up) pair, src/core/k3_ops.c:110-123:
+ *   a = b1*tanh(g/b1)*sigmoid(g), u = b2*tanh(up/b2), y = a*u.
+ * A cap >= 2^64 is treated as absent, the exact limit the engine reaches for its
+ * SwiGLU setting b = 2^100 (tanh(t) = t for tiny t, and scaling by a power of two is
+ * exact): a = g*sigmoid(g), u = up. The sigmoid takes the uncapped gate. */
+__device__ __forceinline__ float k3d_act(float g, float up, float b1, float b2)
+{
+    const float sg = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+    float a, u;
+    if (b1 >= 18446744073709551616.0f) a = __fmul_rn(g, sg);
+    else a = __fmul_rn(__fmul_rn(b1, tanhf(__fdiv_rn(g, b1))), sg);
+    if (b2 >= 18446744073709551616.0f) u = up;
+    else u = __fmul_rn(b2, tanhf(__fdiv_rn(up, b2)));
+    return __fmul_rn(a, u);
+}

@@ -1,0 +1,92 @@
+/* k3g_kernels.h - launchers of the gfx950 kernels, callable from the C99 host code.
+ * Every launcher enqueues on the given stream and returns 0, or -1 when the arguments
+ * are outside what the kernel supports (nothing is launched then). */
+#ifndef K3G_KERNELS_H
+#define K3G_KERNELS_H
+
+#include <stdint.h>
+#ifndef __HIPCC__
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#endif
+#include <hip/hip_runtime_api.h>
+
+#include "../../include/k3moe.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define K3G_MAX_TOPK 64
+
+/* weight formats */
+enum { K3K_MXFP4 = 0, K3K_F32 = 1, K3K_BF16 = 2 };
+
+/* Everything the routed-expert kernels read, device pointers. */
+typedef struct {
+    int fmt;                          /* K3K_MXFP4: eq table; K3K_F32: w1/w3/w2 bank */
+    const K3ExpertQ *eq;              /* [n_experts] */
+    const float *w1, *w3, *w2;        /* [n_experts][inter][latent], [..][latent][inter] */
+    const int32_t *act, *nact;        /* active experts, ascending, and their count */
+    const int32_t *off;               /* [n_experts + 1] pair ranges per expert */
+    const int32_t *perm;              /* pair ids p = t*topk + j, grouped by expert */
+    int topk, inter, latent;
+    const float *z;                   /* [T][latent] routed input */
+    float *h;                         /* [T*topk][inter] after the activation */
+    float *contrib;                   /* [T*topk][latent] per-slot expert outputs */
+    float b1, b2;                     /* SiTU caps (>= 2^64: uncapped) */
+    int *err;
+} K3kRouted;
+
+int k3k_router(const float *x, int T, const float *W, const float *bias, int d, int E,
+               int k, int renorm, float routed_scale, double *logit, double *asum,
+               int32_t *idx, float *wt, int force, int *stats, hipStream_t st);
+
+/* Stable counting sort of the T*k (token, slot) pairs by expert. cnt/base are
+ * [ceil(P/256)][E] ints of workspace. */
+int k3k_dispatch(const int32_t *idx, int P, int E, int32_t *cnt, int32_t *base,
+                 int32_t *off, int32_t *act, int32_t *nact, int32_t *perm, int *err,
+                 hipStream_t st);
+
+/* h = act(W1 z, W3 z) and contrib = W2 h for every active expert's pairs. maxU bounds
+ * the number of active experts (min(E, T*k)); maxtok bounds tokens per expert. */
+int k3k_routed_gateup(const K3kRouted *a, int maxU, int maxtok, hipStream_t st);
+int k3k_routed_down(const K3kRouted *a, int maxU, int maxtok, hipStream_t st);
+
+/* y[t][r] = W[r] . x[t] (fmt K3K_F32 or K3K_BF16), or with Wb != NULL
+ * y[t][r] = act(Wa[r] . x[t], Wb[r] . x[t]). */
+int k3k_dense(int fmt, const void *Wa, const void *Wb, int rows, int in,
+              const float *x, int ldx, int T, float *y, int ldy, float b1, float b2,
+              hipStream_t st);
+
+/* out[t] = sum_j wt[t][j] * contrib[t*k+j] in slot order (float multiply, then add;
+ * slots with idx < 0 skipped), then + add[t] when add != NULL. */
+int k3k_combine(const float *contrib, const int32_t *idx, const float *wt, int T, int k,
+                int n, const float *add, float *out, hipStream_t st);
+
+/* y = w * x * (float)(1/sqrt(sum x^2 / n + eps)), double sum; one token per block. */
+int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
+                hipStream_t st);
+
+/* y += a, elementwise */
+int k3k_add(float *y, const float *a, size_t n, hipStream_t st);
+
+/* MXFP4 -> fp32, exact (k3_mxfp4_dequant semantics). */
+int k3k_dequant(float *out, const uint8_t *packed, const uint8_t *scales, int rows,
+                int pcols, int group, hipStream_t st);
+
+/* y[rows] = W x for one MXFP4 matrix (group 32), any even `in`. */
+int k3k_mxfp4_gemv(float *y, const float *x, const uint8_t *packed, const uint8_t *scales,
+                   int in, int rows, hipStream_t st);
+
+int k3k_fill_bytes(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream, uint64_t first,
+                   hipStream_t st);
+int k3k_fill_scales(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream,
+                    uint64_t first, int lo, int hi, hipStream_t st);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* K3G_KERNELS_H */

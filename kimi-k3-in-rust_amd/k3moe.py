@@ -1,0 +1,491 @@
+"""ctypes binding of libk3moe.so: the C ABI in include/k3moe.h, plus the seeded
+synthetic layers the tests and the benchmark drive it with.
+
+The binding mirrors the engine's own interface (include/k3/k3.h): K3Cfg, K3MoeW,
+K3ExpertQ and K3ExpertSrc are the engine's struct layouts, and k3_router / k3_moe /
+k3_moe_prefill / k3_matmul_mxfp4 / k3_mxfp4_dequant keep the engine's argument meaning.
+Device memory and timing go straight through the HIP runtime (libamdhip64); nothing here
+computes a result on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libk3moe.so")
+
+# ----------------------------------------------------------------- struct layouts ----
+
+
+class K3Cfg(C.Structure):
+    """include/k3/k3.h:73-120, field for field."""
+    _fields_ = [
+        ("hidden", C.c_int), ("n_layers", C.c_int), ("vocab", C.c_int), ("rms_eps", C.c_float),
+        ("kda_heads", C.c_int), ("kda_head_dim", C.c_int), ("conv_k", C.c_int),
+        ("gate_lb", C.c_float),
+        ("n_heads", C.c_int), ("q_lora", C.c_int), ("kv_lora", C.c_int), ("qk_nope", C.c_int),
+        ("qk_rope", C.c_int), ("v_head", C.c_int), ("mla_out_gate", C.c_int),
+        ("n_experts", C.c_int), ("topk", C.c_int), ("n_shared", C.c_int), ("latent", C.c_int),
+        ("moe_inter", C.c_int), ("routed_scale", C.c_float), ("moe_renorm", C.c_int),
+        ("latent_norm", C.c_int),
+        ("first_dense", C.c_int), ("dense_inter", C.c_int),
+        ("attn_res_block", C.c_int),
+        ("situ_b1", C.c_float), ("situ_b2", C.c_float),
+        ("n_full_attn", C.c_int), ("full_attn", C.POINTER(C.c_int)),
+    ]
+
+
+class K3ExpertQ(C.Structure):
+    """include/k3/k3.h:323-327."""
+    _fields_ = [("p1", C.c_void_p), ("s1", C.c_void_p), ("p3", C.c_void_p),
+                ("s3", C.c_void_p), ("p2", C.c_void_p), ("s2", C.c_void_p)]
+
+
+class K3ExpertSrc(C.Structure):
+    """include/k3/k3.h:332-355."""
+    _fields_ = [("get", C.c_void_p), ("getmany", C.c_void_p), ("resident", C.c_void_p),
+                ("ctx", C.c_void_p)]
+
+
+class K3MoeW(C.Structure):
+    """include/k3/k3.h:357-380."""
+    _fields_ = [
+        ("gate", C.c_void_p), ("bias", C.c_void_p),
+        ("w1", C.c_void_p), ("w3", C.c_void_p), ("w2", C.c_void_p),
+        ("latent_norm", C.c_void_p),
+        ("down", C.c_void_p), ("up", C.c_void_p),
+        ("sh1", C.c_void_p), ("sh3", C.c_void_p), ("sh2", C.c_void_p),
+        ("wdt", C.c_int),
+        ("src", C.c_void_p), ("layer", C.c_int), ("cache_only", C.c_int),
+    ]
+
+
+class K3gExpertLayout(C.Structure):
+    _fields_ = [("p1_off", C.c_int64), ("s1_off", C.c_int64), ("p2_off", C.c_int64),
+                ("s2_off", C.c_int64), ("p3_off", C.c_int64), ("s3_off", C.c_int64),
+                ("nbytes", C.c_int64)]
+
+
+class K3gLayer(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_int), ("n_experts", C.c_int), ("topk", C.c_int), ("inter", C.c_int),
+        ("shared_inter", C.c_int), ("latent", C.c_int),
+        ("renorm", C.c_int), ("routed_scale", C.c_float),
+        ("act_b1", C.c_float), ("act_b2", C.c_float), ("rms_eps", C.c_float),
+        ("gate", C.c_void_p), ("bias", C.c_void_p),
+        ("expert_fmt", C.c_int),
+        ("experts", C.c_void_p),
+        ("w1", C.c_void_p), ("w3", C.c_void_p), ("w2", C.c_void_p),
+        ("wdt", C.c_int),
+        ("sh1", C.c_void_p), ("sh3", C.c_void_p), ("sh2", C.c_void_p),
+        ("down", C.c_void_p), ("up", C.c_void_p),
+        ("latent_norm", C.c_void_p),
+    ]
+
+
+K3_WF32, K3_WBF16 = 0, 1
+SWIGLU_CAP = float(2.0 ** 100)   # the engine's SwiGLU setting of the SiTU caps
+
+# -------------------------------------------------------------------- libraries ----
+
+_lib = None
+_hip = None
+
+
+def lib() -> C.CDLL:
+    """libk3moe.so, loaded once. Raises when it has not been built: there is no CPU
+    fallback for anything in it."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        L = C.CDLL(LIB_PATH)
+        vp, i, f, sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+        u64 = C.c_uint64
+        L.k3_router.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, f]
+        L.k3_router.restype = None
+        L.k3_moe.argtypes = [vp, vp, C.POINTER(K3MoeW), C.POINTER(K3Cfg), i, vp, vp, vp]
+        L.k3_moe.restype = None
+        L.k3_moe_prefill.argtypes = L.k3_moe.argtypes
+        L.k3_moe_prefill.restype = None
+        L.k3_moe_scratch.argtypes = [C.POINTER(K3Cfg)]
+        L.k3_moe_scratch.restype = sz
+        L.k3_matmul_mxfp4.argtypes = [vp, vp, vp, vp, i, i, i]
+        L.k3_matmul_mxfp4.restype = None
+        L.k3_mxfp4_dequant.argtypes = [vp, vp, vp, i, i, i]
+        L.k3_mxfp4_dequant.restype = None
+        L.k3moe_forget_weights.argtypes = []
+        L.k3moe_forget_weights.restype = None
+        L.k3g_expert_layout.argtypes = [i, i]
+        L.k3g_expert_layout.restype = K3gExpertLayout
+        L.k3g_ctx_create.argtypes = [C.POINTER(vp), i, C.POINTER(K3gLayer), i]
+        L.k3g_ctx_create.restype = i
+        L.k3g_ctx_destroy.argtypes = [vp]
+        L.k3g_ctx_destroy.restype = None
+        L.k3g_ctx_stream.argtypes = [vp]
+        L.k3g_ctx_stream.restype = vp
+        L.k3g_ctx_stats.argtypes = [vp, C.POINTER(C.c_int64), i]
+        L.k3g_ctx_stats.restype = None
+        L.k3g_ctx_force_exact.argtypes = [vp, i]
+        L.k3g_ctx_force_exact.restype = None
+        L.k3g_router.argtypes = [vp, C.POINTER(K3gLayer), vp, i, vp, vp, vp]
+        L.k3g_router.restype = i
+        L.k3g_moe.argtypes = [vp, C.POINTER(K3gLayer), vp, i, vp, vp, vp, vp]
+        L.k3g_moe.restype = i
+        L.k3g_sync.argtypes = [vp, vp]
+        L.k3g_sync.restype = i
+        L.k3s_byte.argtypes = [u64, u64, u64]
+        L.k3s_byte.restype = C.c_uint8
+        L.k3s_fill_bytes.argtypes = [vp, sz, u64, u64, u64]
+        L.k3s_fill_bytes.restype = None
+        L.k3s_fill_scales.argtypes = [vp, sz, u64, u64, u64, i, i]
+        L.k3s_fill_scales.restype = None
+        L.k3s_fill_normal.argtypes = [vp, sz, u64, u64, u64, f, f, i]
+        L.k3s_fill_normal.restype = None
+        L.k3g_fill_bytes.argtypes = [vp, sz, u64, u64, u64, vp]
+        L.k3g_fill_bytes.restype = i
+        L.k3g_fill_scales.argtypes = [vp, sz, u64, u64, u64, i, i, vp]
+        L.k3g_fill_scales.restype = i
+        _lib = L
+    return _lib
+
+
+def hip() -> C.CDLL:
+    """The HIP runtime, for device memory, copies and events."""
+    global _hip
+    if _hip is None:
+        H = C.CDLL("libamdhip64.so", mode=C.RTLD_GLOBAL)
+        vp, sz, i = C.c_void_p, C.c_size_t, C.c_int
+        H.hipMalloc.argtypes = [C.POINTER(vp), sz]
+        H.hipFree.argtypes = [vp]
+        H.hipMemcpy.argtypes = [vp, vp, sz, i]
+        H.hipMemcpyAsync.argtypes = [vp, vp, sz, i, vp]
+        H.hipMemset.argtypes = [vp, i, sz]
+        H.hipDeviceSynchronize.argtypes = []
+        H.hipStreamSynchronize.argtypes = [vp]
+        H.hipGetDeviceCount.argtypes = [C.POINTER(i)]
+        H.hipSetDevice.argtypes = [i]
+        H.hipEventCreate.argtypes = [C.POINTER(vp)]
+        H.hipEventRecord.argtypes = [vp, vp]
+        H.hipEventSynchronize.argtypes = [vp]
+        H.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), vp, vp]
+        H.hipEventDestroy.argtypes = [vp]
+        H.hipGetErrorString.argtypes = [i]
+        H.hipGetErrorString.restype = C.c_char_p
+        H.hipHostMalloc.argtypes = [C.POINTER(vp), sz, C.c_uint]
+        H.hipHostFree.argtypes = [vp]
+        _hip = H
+    return _hip
+
+
+H2D, D2H, D2D = 1, 2, 3
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = hip().hipGetErrorString(rc)
+        raise RuntimeError(f"{what} failed: {msg.decode() if msg else rc}")
+
+
+def gpu_count() -> int:
+    n = C.c_int(0)
+    if hip().hipGetDeviceCount(C.byref(n)) != 0:
+        return 0
+    return n.value
+
+
+class DevBuf:
+    """A device allocation owned by Python."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        _check(hip().hipMalloc(C.byref(p), max(self.nbytes, 1)), f"hipMalloc({nbytes})")
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DevBuf":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        _check(hip().hipMemcpy(C.c_void_p(self.ptr + offset), a.ctypes.data_as(C.c_void_p),
+                               a.nbytes, H2D), "hipMemcpy H2D")
+
+    def download(self, dtype, count: int, offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        _check(hip().hipMemcpy(out.ctypes.data_as(C.c_void_p), C.c_void_p(self.ptr + offset),
+                               out.nbytes, D2H), "hipMemcpy D2H")
+        return out
+
+    def zero(self) -> None:
+        _check(hip().hipMemset(C.c_void_p(self.ptr), 0, self.nbytes), "hipMemset")
+
+    def free(self) -> None:
+        if self.ptr:
+            hip().hipFree(C.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def sync() -> None:
+    _check(hip().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class Timer:
+    """HIP events on a given stream (events on the stream the kernels run on)."""
+
+    def __init__(self, stream=None):
+        H = hip()
+        self.stream = stream
+        self.a, self.b = C.c_void_p(), C.c_void_p()
+        _check(H.hipEventCreate(C.byref(self.a)), "hipEventCreate")
+        _check(H.hipEventCreate(C.byref(self.b)), "hipEventCreate")
+
+    def start(self):
+        _check(hip().hipEventRecord(self.a, C.c_void_p(self.stream)), "hipEventRecord")
+
+    def stop(self) -> float:
+        H = hip()
+        _check(H.hipEventRecord(self.b, C.c_void_p(self.stream)), "hipEventRecord")
+        _check(H.hipEventSynchronize(self.b), "hipEventSynchronize")
+        ms = C.c_float()
+        _check(H.hipEventElapsedTime(C.byref(ms), self.a, self.b), "hipEventElapsedTime")
+        return float(ms.value)
+
+
+# ---------------------------------------------------------------- synthetic data ----
+
+def bf16_bits(a: np.ndarray) -> np.ndarray:
+    """fp32 values already rounded to bf16 -> their 16-bit patterns."""
+    return (np.ascontiguousarray(a, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def host_normal(n: int, seed: int, stream: int, mean=0.0, std=1.0, bf16=False,
+                first: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().k3s_fill_normal(out.ctypes.data_as(C.c_void_p), n, seed, stream, first, mean, std,
+                          1 if bf16 else 0)
+    return out
+
+
+def host_bytes(n: int, seed: int, stream: int, first: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint8)
+    lib().k3s_fill_bytes(out.ctypes.data_as(C.c_void_p), n, seed, stream, first)
+    return out
+
+
+def host_scales(n: int, seed: int, stream: int, lo: int, hi: int, first: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint8)
+    lib().k3s_fill_scales(out.ctypes.data_as(C.c_void_p), n, seed, stream, first, lo, hi)
+    return out
+
+
+# stream ids: every tensor of every layer has its own hash stream
+S_GATE, S_BIAS, S_X, S_SH1, S_SH3, S_SH2 = 1, 2, 3, 4, 5, 6
+
+
+def expert_stream(layer: int, e: int, mat: int, scale: bool) -> int:
+    """Hash stream of matrix mat (0 = w1, 1 = w2, 2 = w3) of expert e: packed or scales."""
+    return 1_000_000 + ((layer * 4096 + e) * 4 + mat) * 2 + (1 if scale else 0)
+
+
+@dataclass
+class Shape:
+    name: str
+    hidden: int
+    n_experts: int
+    topk: int
+    inter: int
+    n_shared: int = 1
+    routed_scale: float = 2.5
+    renorm: int = 1
+    x_bf16: bool = True
+    scale_lo: int = -4
+    scale_hi: int = 2
+    zipf_s: float = 0.0        # selection-bias skew (0 = none)
+    zipf_alpha: float = 0.0
+
+
+# The workloads: (c0) tiny layer on the CPU-runnable path, (c1) Kimi-K2-scale layer.
+TINY = Shape("tiny d=256 E=16 k=4 I=128", 256, 16, 4, 128, x_bf16=False)
+K2 = Shape("K2 d=7168 E=384 k=8 I=2048", 7168, 384, 8, 2048)
+
+
+class SynthLayer:
+    """A seeded K2-shaped MoE layer (no latent projection, SwiGLU, one bf16 shared
+    expert, MXFP4 routed experts): host copies of the small tensors, the whole layer in
+    HBM, and on-demand host regeneration of any expert for a CPU check."""
+
+    def __init__(self, shape: Shape, seed: int, layer: int = 0, device: bool = True,
+                 zipf_perm_seed: int | None = None):
+        self.shape, self.seed, self.layer = shape, seed, layer
+        d, E, I = shape.hidden, shape.n_experts, shape.inter
+        SI = I * shape.n_shared
+        self.SI = SI
+        self.geo = lib().k3g_expert_layout(d, I)
+        self.gate = host_normal(E * d, seed, S_GATE + 100 * layer, 0.0, 0.02)
+        self.bias = host_normal(E, seed, S_BIAS + 100 * layer, 0.0, 0.01)
+        if shape.zipf_alpha:
+            # selection-only skew: alpha * log p_rank(e), p_rank Zipf(s) over a seeded
+            # permutation of the experts
+            rng = np.random.default_rng(seed if zipf_perm_seed is None else zipf_perm_seed)
+            perm = rng.permutation(E)
+            ranks = np.empty(E, dtype=np.int64)
+            ranks[perm] = np.arange(1, E + 1)
+            p = ranks.astype(np.float64) ** (-shape.zipf_s)
+            p /= p.sum()
+            self.bias = (self.bias + shape.zipf_alpha * np.log(p)).astype(np.float32)
+        sh = []
+        for s in (S_SH1, S_SH3, S_SH2):
+            v = host_normal(SI * d, seed, s + 100 * layer, 0.0, 0.02, bf16=True)
+            sh.append(bf16_bits(v))
+        self.sh1, self.sh3, self.sh2 = sh
+        self.dev = None
+        if device:
+            self.to_device()
+
+    # -- experts -------------------------------------------------------------------
+    def expert_host(self, e: int) -> np.ndarray:
+        """Expert e's run (w1p w1s w2p w2s w3p w3s), regenerated on the host."""
+        g, d, I = self.geo, self.shape.hidden, self.shape.inter
+        out = np.empty(g.nbytes, dtype=np.uint8)
+        lo, hi = self.shape.scale_lo, self.shape.scale_hi
+        parts = [(0, g.p1_off, I * d // 2, g.s1_off, I * ((d + 31) // 32)),
+                 (1, g.p2_off, d * I // 2, g.s2_off, d * ((I + 31) // 32)),
+                 (2, g.p3_off, I * d // 2, g.s3_off, I * ((d + 31) // 32))]
+        for m, po, pn, so, sn in parts:
+            out[po:po + pn] = host_bytes(pn, self.seed, expert_stream(self.layer, e, m, False))
+            out[so:so + sn] = host_scales(sn, self.seed, expert_stream(self.layer, e, m, True),
+                                          lo, hi)
+        return out
+
+    def fill_expert_device(self, base_ptr: int, e: int, stream=None) -> None:
+        g, d, I = self.geo, self.shape.hidden, self.shape.inter
+        lo, hi = self.shape.scale_lo, self.shape.scale_hi
+        parts = [(0, g.p1_off, I * d // 2, g.s1_off, I * ((d + 31) // 32)),
+                 (1, g.p2_off, d * I // 2, g.s2_off, d * ((I + 31) // 32)),
+                 (2, g.p3_off, I * d // 2, g.s3_off, I * ((d + 31) // 32))]
+        L = lib()
+        for m, po, pn, so, sn in parts:
+            _check(L.k3g_fill_bytes(C.c_void_p(base_ptr + po), pn, self.seed,
+                                    expert_stream(self.layer, e, m, False), 0, stream),
+                   "k3g_fill_bytes")
+            _check(L.k3g_fill_scales(C.c_void_p(base_ptr + so), sn, self.seed,
+                                     expert_stream(self.layer, e, m, True), 0, lo, hi, stream),
+                   "k3g_fill_scales")
+
+    def expert_table(self, bank_ptr: int) -> list:
+        g = self.geo
+        tab = (K3ExpertQ * self.shape.n_experts)()
+        for e in range(self.shape.n_experts):
+            b = bank_ptr + e * g.nbytes
+            tab[e] = K3ExpertQ(b + g.p1_off, b + g.s1_off, b + g.p3_off, b + g.s3_off,
+                               b + g.p2_off, b + g.s2_off)
+        return tab
+
+    def to_device(self) -> None:
+        E = self.shape.n_experts
+        self.bank = DevBuf(E * self.geo.nbytes)
+        for e in range(E):
+            self.fill_expert_device(self.bank.ptr + e * self.geo.nbytes, e)
+        sync()
+        tab = self.expert_table(self.bank.ptr)
+        self.d_table = DevBuf(C.sizeof(tab))
+        _check(hip().hipMemcpy(C.c_void_p(self.d_table.ptr), C.cast(tab, C.c_void_p),
+                               C.sizeof(tab), H2D), "table upload")
+        self.d_gate = DevBuf.from_array(self.gate)
+        self.d_bias = DevBuf.from_array(self.bias)
+        self.d_sh1 = DevBuf.from_array(self.sh1)
+        self.d_sh3 = DevBuf.from_array(self.sh3)
+        self.d_sh2 = DevBuf.from_array(self.sh2)
+        self.dev = self.k3g_layer()
+
+    def k3g_layer(self) -> K3gLayer:
+        s = self.shape
+        L = K3gLayer()
+        L.hidden, L.n_experts, L.topk, L.inter = s.hidden, s.n_experts, s.topk, s.inter
+        L.shared_inter, L.latent = self.SI, s.hidden
+        L.renorm, L.routed_scale = s.renorm, s.routed_scale
+        L.act_b1 = L.act_b2 = SWIGLU_CAP
+        L.rms_eps = 1e-5
+        L.gate, L.bias = self.d_gate.ptr, self.d_bias.ptr
+        L.expert_fmt = 0
+        L.experts = self.d_table.ptr
+        L.wdt = K3_WBF16
+        if self.SI:
+            L.sh1, L.sh3, L.sh2 = self.d_sh1.ptr, self.d_sh3.ptr, self.d_sh2.ptr
+        return L
+
+    def cfg(self) -> K3Cfg:
+        s = self.shape
+        c = K3Cfg()
+        c.hidden, c.latent, c.moe_inter = s.hidden, s.hidden, s.inter
+        c.n_experts, c.topk, c.n_shared = s.n_experts, s.topk, s.n_shared
+        c.routed_scale, c.moe_renorm, c.latent_norm = s.routed_scale, s.renorm, 0
+        c.rms_eps = 1e-5
+        c.situ_b1 = c.situ_b2 = SWIGLU_CAP
+        c.n_layers = 1
+        return c
+
+    def tokens(self, T: int, stream_base: int = 0) -> np.ndarray:
+        x = host_normal(T * self.shape.hidden, self.seed, S_X + 100 * self.layer + stream_base,
+                        0.0, 1.0, bf16=self.shape.x_bf16)
+        return x.reshape(T, self.shape.hidden)
+
+
+class Ctx:
+    """A k3g context sized for a layer shape and token budget."""
+
+    def __init__(self, layer: K3gLayer, max_tokens: int, device: int = 0):
+        self.ptr = C.c_void_p()
+        rc = lib().k3g_ctx_create(C.byref(self.ptr), device, C.byref(layer), max_tokens)
+        if rc != 0:
+            raise RuntimeError("k3g_ctx_create failed")
+        self.stream = lib().k3g_ctx_stream(self.ptr)
+
+    def moe(self, layer: K3gLayer, x_ptr: int, T: int, out_ptr: int, idx_ptr=None,
+            wt_ptr=None) -> None:
+        rc = lib().k3g_moe(self.ptr, C.byref(layer), C.c_void_p(x_ptr), T, C.c_void_p(out_ptr),
+                           C.c_void_p(idx_ptr) if idx_ptr else None,
+                           C.c_void_p(wt_ptr) if wt_ptr else None, None)
+        if rc != 0:
+            raise RuntimeError("k3g_moe launch failed")
+
+    def router(self, layer: K3gLayer, x_ptr: int, T: int, idx_ptr: int, wt_ptr: int) -> None:
+        rc = lib().k3g_router(self.ptr, C.byref(layer), C.c_void_p(x_ptr), T,
+                              C.c_void_p(idx_ptr), C.c_void_p(wt_ptr), None)
+        if rc != 0:
+            raise RuntimeError("k3g_router launch failed")
+
+    def sync(self) -> None:
+        rc = lib().k3g_sync(self.ptr, None)
+        if rc != 0:
+            raise RuntimeError(f"device error {rc}")
+
+    def force_exact(self, mode: int) -> None:
+        lib().k3g_ctx_force_exact(self.ptr, mode)
+
+    def stats(self) -> list:
+        out = (C.c_int64 * 4)()
+        lib().k3g_ctx_stats(self.ptr, out, 4)
+        return list(out)
+
+    def destroy(self) -> None:
+        if self.ptr:
+            lib().k3g_ctx_destroy(self.ptr)
+            self.ptr = C.c_void_p()
