@@ -27,6 +27,7 @@ static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
 typedef struct {
     const void *host;
     size_t bytes;
+    uint64_t print;              /* sampled fingerprint of the host bytes at upload */
     void *dev;
 } Mirror;
 
@@ -55,12 +56,38 @@ static DevState *dev_state(void)
     return &g_dev[d];
 }
 
-/* Device copy of `bytes` of host memory at `host`, uploaded on first use. */
+/* FNV-1a over 64 eight-byte samples spread across the buffer (all of it when short):
+ * cheap enough to check on every call, and it catches a buffer that was freed and
+ * reused for other weights at the same address. */
+static uint64_t fingerprint(const void *host, size_t bytes)
+{
+    const unsigned char *b = (const unsigned char *)host;
+    uint64_t h = 1469598103934665603ull;
+    if (bytes <= 512) {
+        for (size_t i = 0; i < bytes; i++) { h ^= b[i]; h *= 1099511628211ull; }
+        return h;
+    }
+    for (int k = 0; k < 64; k++) {
+        const size_t at = (size_t)k * ((bytes - 8) / 63);
+        for (int i = 0; i < 8; i++) { h ^= b[at + i]; h *= 1099511628211ull; }
+    }
+    return h;
+}
+
+/* Device copy of `bytes` of host memory at `host`, uploaded on first use and again
+ * whenever the sampled fingerprint shows the host bytes changed. */
 static const void *mirror(DevState *s, const void *host, size_t bytes)
 {
     if (!host || !bytes) return NULL;
+    const uint64_t fp = fingerprint(host, bytes);
     for (int i = 0; i < s->nmir; i++)
-        if (s->mir[i].host == host && s->mir[i].bytes == bytes) return s->mir[i].dev;
+        if (s->mir[i].host == host && s->mir[i].bytes == bytes) {
+            if (s->mir[i].print != fp) {
+                K3G_CHECK(hipMemcpy(s->mir[i].dev, host, bytes, hipMemcpyHostToDevice));
+                s->mir[i].print = fp;
+            }
+            return s->mir[i].dev;
+        }
     if (s->nmir == s->capmir) {
         const int nc = s->capmir ? 2 * s->capmir : 32;
         Mirror *m = (Mirror *)realloc(s->mir, (size_t)nc * sizeof *m);
@@ -73,6 +100,7 @@ static const void *mirror(DevState *s, const void *host, size_t bytes)
     K3G_CHECK(hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice));
     s->mir[s->nmir].host = host;
     s->mir[s->nmir].bytes = bytes;
+    s->mir[s->nmir].print = fp;
     s->mir[s->nmir].dev = dev;
     s->nmir++;
     return dev;

@@ -64,8 +64,8 @@ __device__ __forceinline__ double k3d_wave_sumd(double v)
  * Afterwards lane l holds the full 64-lane sum of value index (l >> (6 - log2 V)) in
  * v[0]. Each halving round trades half the values with the partner lane, so the whole
  * reduction costs about V shuffles instead of 6*V. */
-template <int V>
-__device__ __forceinline__ void k3d_transpose_reduce(float *v, int lane)
+template <int V, typename A>
+__device__ __forceinline__ void k3d_transpose_reduce(A *v, int lane)
 {
     int n = V;
 #pragma unroll
@@ -76,8 +76,8 @@ __device__ __forceinline__ void k3d_transpose_reduce(float *v, int lane)
 #pragma unroll
             for (int i = 0; i < V / 2; ++i) {
                 if (i < h) {
-                    const float send = upper ? v[i] : v[i + h];
-                    const float keep = upper ? v[i + h] : v[i];
+                    const A send = upper ? v[i] : v[i + h];
+                    const A keep = upper ? v[i + h] : v[i];
                     v[i] = keep + __shfl_xor(send, m, K3G_WAVE);
                 }
             }
@@ -88,25 +88,30 @@ __device__ __forceinline__ void k3d_transpose_reduce(float *v, int lane)
     }
 }
 
-template <>
-__device__ __forceinline__ void k3d_transpose_reduce<1>(float *v, int lane)
+/* Float expf, correctly rounded except for ~2^-28 of inputs: the double exp is within an
+ * ulp of double, far inside a float rounding interval. glibc's expf is within 0.502 ulp,
+ * so the two agree but on a vanishing set of near-midpoint inputs. */
+__device__ __forceinline__ float k3d_expf_cr(float v) { return (float)exp((double)v); }
+__device__ __forceinline__ float k3d_tanhf_cr(float v) { return (float)tanh((double)v); }
+
+/* 1/(1+expf(-v)) with the engine's float operation order (src/core/k3_ops.c:105) */
+__device__ __forceinline__ float k3d_sigmoid(float v)
 {
-    (void)lane;
-    v[0] = k3d_wave_sum(v[0]);
+    return __fdiv_rn(1.0f, __fadd_rn(1.0f, k3d_expf_cr(-v)));
 }
 
-/* SiTU-GLU on one (gate, up) pair, src/core/k3_ops.c:110-123:
- *   a = b1*tanh(g/b1)*sigmoid(g), u = b2*tanh(up/b2), y = a*u.
- * A cap >= 2^64 is treated as absent, the exact limit the engine reaches for its
- * SwiGLU setting b = 2^100 (tanh(t) = t for tiny t, and scaling by a power of two is
- * exact): a = g*sigmoid(g), u = up. The sigmoid takes the uncapped gate. */
+/* SiTU-GLU on one (gate, up) pair, src/core/k3_ops.c:110-123, in the engine's float
+ * operation order: a = (b1 * tanh(g / b1)) * sigmoid(g), u = b2 * tanh(up / b2), y = a * u.
+ * A cap >= 2^64 is treated as absent, the exact limit the engine reaches for its SwiGLU
+ * setting b = 2^100 (tanh(t) = t for tiny t, and scaling by a power of two is exact):
+ * a = g * sigmoid(g), u = up. The sigmoid takes the uncapped gate. */
 __device__ __forceinline__ float k3d_act(float g, float up, float b1, float b2)
 {
-    const float sg = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+    const float sg = k3d_sigmoid(g);
     float a, u;
     if (b1 >= 18446744073709551616.0f) a = __fmul_rn(g, sg);
-    else a = __fmul_rn(__fmul_rn(b1, tanhf(__fdiv_rn(g, b1))), sg);
+    else a = __fmul_rn(__fmul_rn(b1, k3d_tanhf_cr(__fdiv_rn(g, b1))), sg);
     if (b2 >= 18446744073709551616.0f) u = up;
-    else u = __fmul_rn(b2, tanhf(__fdiv_rn(up, b2)));
+    else u = __fmul_rn(b2, k3d_tanhf_cr(__fdiv_rn(up, b2)));
     return __fmul_rn(a, u);
 }

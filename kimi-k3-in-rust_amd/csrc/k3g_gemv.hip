@@ -82,15 +82,26 @@ struct K3Log2 { static constexpr int v = 1 + K3Log2<V / 2>::v; };
 template <>
 struct K3Log2<1> { static constexpr int v = 0; };
 
+/* Accumulator type: fp32 for the streamed formats (MXFP4, bf16), double for fp32
+ * weights, whose products are exact in double as in the engine's fixture path. */
+template <int FMT> struct K3Acc { typedef float T; };
+template <> struct K3Acc<K3K_F32> { typedef double T; };
+
+__device__ __forceinline__ float k3d_fma(float w, float x, float a) { return fmaf(w, x, a); }
+__device__ __forceinline__ double k3d_fma(float w, float x, double a)
+{
+    return fma((double)w, (double)x, a);
+}
+
 /* Tile core: NRT rows (rows[] pointers, NULL = out of range) x NT tokens (xr[] rows,
  * NULL = absent), accumulated into acc[r*NT + t] over all column blocks. */
-template <int FMT, int NRT, int NT>
+template <int FMT, int NRT, int NT, typename A>
 __device__ __forceinline__ void k3d_tile(const void *const *rows, const uint8_t *const *srows,
                                          const float *const *xr, int in, int lane,
-                                         float *acc)
+                                         A *acc)
 {
 #pragma unroll
-    for (int i = 0; i < NRT * NT; ++i) acc[i] = 0.0f;
+    for (int i = 0; i < NRT * NT; ++i) acc[i] = (A)0;
     for (int cb = 0; cb < in; cb += K3G_CB) {
         const int col = cb + lane * 16;
         if (col >= in) continue;
@@ -104,9 +115,9 @@ __device__ __forceinline__ void k3d_tile(const void *const *rows, const uint8_t 
             k3d_load16<FMT>(rows[r], srows[r], col, w);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                float a = acc[r * NT + t];
+                A a = acc[r * NT + t];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) a = fmaf(w[i], xv[t][i], a);
+                for (int i = 0; i < 16; ++i) a = k3d_fma(w[i], xv[t][i], a);
                 acc[r * NT + t] = a;
             }
         }
@@ -159,10 +170,11 @@ k_routed_gateup(K3kRouted a)
             pr[t] = c0 + t < end ? a.perm[c0 + t] : -1;
             xr[t] = pr[t] >= 0 ? a.z + (size_t)(pr[t] / a.topk) * L : nullptr;
         }
-        float acc[V];
+        typename K3Acc<FMT>::T acc[V];
         k3d_tile<FMT, 2 * NR, NT>(rows, srows, xr, L, lane, acc);
         k3d_transpose_reduce<V>(acc, lane);
-        const float upv = __shfl_xor(acc[0], 32, K3G_WAVE);
+        const float gv = (float)acc[0];
+        const float upv = __shfl_xor(gv, 32, K3G_WAVE);
         const int v = lane >> SH;
         if ((lane & ((1 << SH) - 1)) == 0 && v < NR * NT) {
             const int r = v / NT, t = v % NT;
@@ -170,7 +182,7 @@ k_routed_gateup(K3kRouted a)
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt) if (tt == t) p = pr[tt];
             if (row0 + r < I && p >= 0)
-                a.h[(size_t)p * I + row0 + r] = k3d_act(acc[0], upv, a.b1, a.b2);
+                a.h[(size_t)p * I + row0 + r] = k3d_act(gv, upv, a.b1, a.b2);
         }
     }
 }
@@ -215,7 +227,7 @@ k_routed_down(K3kRouted a)
             pr[t] = c0 + t < end ? a.perm[c0 + t] : -1;
             xr[t] = pr[t] >= 0 ? a.h + (size_t)pr[t] * I : nullptr;
         }
-        float acc[V];
+        typename K3Acc<FMT>::T acc[V];
         k3d_tile<FMT, NR, NT>(rows, srows, xr, I, lane, acc);
         k3d_transpose_reduce<V>(acc, lane);
         const int v = lane >> SH;
@@ -224,7 +236,7 @@ k_routed_down(K3kRouted a)
             int p = -1;
 #pragma unroll
             for (int tt = 0; tt < NT; ++tt) if (tt == t) p = pr[tt];
-            if (row0 + r < L && p >= 0) a.contrib[(size_t)p * L + row0 + r] = acc[0];
+            if (row0 + r < L && p >= 0) a.contrib[(size_t)p * L + row0 + r] = (float)acc[0];
         }
     }
 }
@@ -259,22 +271,23 @@ k_dense(const void *Wa, const void *Wb, const uint8_t *Sa, const uint8_t *Sb, in
     for (int t = 0; t < NT; ++t) xr[t] = t0 + t < T ? x + (size_t)(t0 + t) * ldx : nullptr;
     constexpr int V = NRT * NT;
     constexpr int SH = 6 - K3Log2<V>::v;
-    float acc[V];
+    typename K3Acc<FMT>::T acc[V];
     k3d_tile<FMT, NRT, NT>(rows, srows, xr, in, lane, acc);
     k3d_transpose_reduce<V>(acc, lane);
     const int v = lane >> SH;
+    const float av = (float)acc[0];
     if constexpr (PAIR) {
-        const float bv = __shfl_xor(acc[0], 32, K3G_WAVE);
+        const float bv = __shfl_xor(av, 32, K3G_WAVE);
         if ((lane & ((1 << SH) - 1)) == 0 && v < NR * NT) {
             const int r = v / NT, t = v % NT;
             if (row0 + r < nrows && t0 + t < T)
-                y[(size_t)(t0 + t) * ldy + row0 + r] = k3d_act(acc[0], bv, b1, b2);
+                y[(size_t)(t0 + t) * ldy + row0 + r] = k3d_act(av, bv, b1, b2);
         }
     } else {
         if ((lane & ((1 << SH) - 1)) == 0 && v < V) {
             const int r = v / NT, t = v % NT;
             if (row0 + r < nrows && t0 + t < T)
-                y[(size_t)(t0 + t) * ldy + row0 + r] = acc[0];
+                y[(size_t)(t0 + t) * ldy + row0 + r] = av;
         }
     }
 }

@@ -25,15 +25,6 @@
 
 #include <math.h>
 
-/* float expf, correctly rounded but for ~2^-28 of inputs: the double exp is within an
- * ulp of double, far inside a float rounding interval. */
-__device__ __forceinline__ float k3d_expf_cr(float v) { return (float)exp((double)v); }
-
-__device__ __forceinline__ float k3d_sigmoid(float v)
-{
-    return __fdiv_rn(1.0f, __fadd_rn(1.0f, k3d_expf_cr(-v)));
-}
-
 /* ------------------------------------------------------------------ logits ---- */
 /* grid (n_experts, ceil(T / RT)), block = one wave. Lane l reads float4 column chunks
  * 4l, 4l+256, ... of the expert row and of each token's x. */

@@ -1,0 +1,316 @@
+"""GPU parity: the HIP path against the CPU oracle on identical seeded inputs.
+
+Bars: routing indices bit-exact (in order); MXFP4 dequantisation bit-exact; layer
+outputs within rel-L2 1e-3 (fp32 accumulation). Each test prints the case it runs
+before touching the GPU.
+"""
+import ctypes as C
+import json
+import os
+
+import numpy as np
+import pytest
+
+import k3moe
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+REL_L2 = 1e-3
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - np.asarray(b, np.float64)) /
+                 max(np.linalg.norm(np.asarray(b, np.float64)), 1e-30))
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def run_layer(layer, x, ctx=None, force=0):
+    T, d, k = x.shape[0], layer.shape.hidden, layer.shape.topk
+    own = ctx is None
+    ctx = ctx or k3moe.Ctx(layer.dev, max_tokens=T)
+    ctx.force_exact(force)
+    dx = k3moe.DevBuf.from_array(x)
+    dout, didx, dwt = k3moe.DevBuf(T * d * 4), k3moe.DevBuf(T * k * 4), k3moe.DevBuf(T * k * 4)
+    ctx.moe(layer.dev, dx.ptr, T, dout.ptr, didx.ptr, dwt.ptr)
+    ctx.sync()
+    res = (dout.download(np.float32, T * d).reshape(T, d),
+           didx.download(np.int32, T * k).reshape(T, k),
+           dwt.download(np.float32, T * k).reshape(T, k))
+    ctx.force_exact(0)
+    if own:
+        ctx.destroy()
+    return res
+
+
+def oracle_tokens(layer, x):
+    outs, idxs, wts = [], [], []
+    for t in range(x.shape[0]):
+        o, i, w = O.k2_forward(layer, x[t:t + 1])
+        outs.append(o[0]); idxs.append(i); wts.append(w)
+    return np.stack(outs), np.stack(idxs), np.stack(wts)
+
+
+# ------------------------------------------------------------------ synthetic data ----
+
+def test_device_fill_matches_host(gpu):
+    say("case: k3g_fill_bytes / k3g_fill_scales vs host fills, 3 streams, odd offsets")
+    L = k3moe.lib()
+    for stream, first, n in [(11, 0, 4096), (12, 5, 1000), (1_000_007, 123457, 77777)]:
+        buf = k3moe.DevBuf(n)
+        assert L.k3g_fill_bytes(C.c_void_p(buf.ptr), n, 99, stream, first, None) == 0
+        k3moe.sync()
+        assert np.array_equal(buf.download(np.uint8, n), k3moe.host_bytes(n, 99, stream, first))
+        assert L.k3g_fill_scales(C.c_void_p(buf.ptr), n, 99, stream, first, -4, 2, None) == 0
+        k3moe.sync()
+        dev = buf.download(np.uint8, n)
+        assert np.array_equal(dev, k3moe.host_scales(n, 99, stream, -4, 2, first))
+        assert dev.min() >= 123 and dev.max() <= 129
+
+
+# ------------------------------------------------------------------ MXFP4 kernels ----
+
+def test_dequant_real_checkpoint_bytes(gpu):
+    say("case: k3_mxfp4_dequant on tests/fixtures/mxfp4.json (64 x 3584), exact")
+    m = np.load(os.path.join(GOLDEN, "mxfp4.npz"))
+    rows, pc = int(m["rows"]), int(m["packed_cols"])
+    packed = np.ascontiguousarray(m["packed"])
+    scales = np.ascontiguousarray(m["scales"])
+    expected = np.ascontiguousarray(m["expected"], np.float32).ravel()
+    out = np.zeros(rows * pc * 2, np.float32)
+    k3moe.lib().k3_mxfp4_dequant(out.ctypes.data, packed.ctypes.data, scales.ctypes.data,
+                                 rows, pc, 32)
+    assert np.array_equal(out.view(np.uint32), expected.view(np.uint32))
+    assert not np.array_equal(out[:64], m["swapped_first64"])
+
+
+def test_matmul_mxfp4_kat(gpu):
+    say("case: k3_matmul_mxfp4 3072x3584 on the bench_kernels known-answer inputs")
+    pk = O.kat_b(3072 * 1792, 777)
+    sc = np.full(3072 * 112, 127, np.uint8)
+    x = O.kat_f(3584, 4242)
+    y = np.zeros(3072, np.float32)
+    k3moe.lib().k3_matmul_mxfp4(y.ctypes.data, x.ctypes.data, pk.ctypes.data, sc.ctypes.data,
+                                3584, 3072, 32)
+    ref = O.oracle().matmul_mxfp4(x, pk, sc, 3072)
+    assert O.fnv1a(ref) == "a231061237b5579d"
+    assert rel_l2(y, ref) < 1e-6
+    # fp32 accumulation: every row within 1e-5 of the output's RMS
+    assert np.max(np.abs(y - ref)) <= 1e-5 * np.sqrt(np.mean(ref.astype(np.float64) ** 2))
+
+
+@pytest.mark.parametrize("rows,inn,lo,hi", [(129, 48, -4, 2), (70, 40, -20, 20), (33, 2048, -4, 2),
+                                           (17, 7168, 100, 110)])
+def test_matmul_mxfp4_shapes(gpu, rows, inn, lo, hi):
+    say(f"case: k3_matmul_mxfp4 rows={rows} in={inn} scales 127+[{lo},{hi}] incl. byte 255")
+    ng = (inn + 31) // 32
+    pk = k3moe.host_bytes(rows * inn // 2, 5, 900 + inn)
+    sc = k3moe.host_scales(rows * ng, 5, 901 + inn, lo, hi)
+    sc[3] = 255
+    x = k3moe.host_normal(inn, 5, 902 + inn)
+    y = np.zeros(rows, np.float32)
+    k3moe.lib().k3_matmul_mxfp4(y.ctypes.data, x.ctypes.data, pk.ctypes.data, sc.ctypes.data,
+                                inn, rows, 32)
+    ref = O.oracle().matmul_mxfp4(x, pk, sc, rows)
+    assert rel_l2(y, ref) < 1e-6
+
+
+# ------------------------------------------------------------------------ router ----
+
+def test_router_golden(gpu):
+    say("case: k3_router on tests/fixtures/ops/router.json (d=128, 8 experts, top-2, 6 rows)")
+    d = np.load(os.path.join(GOLDEN, "router.npz"))
+    tol = json.load(open(os.path.join(GOLDEN, "tolerance.json")))["tolerance"]
+    E, K = int(d["n_experts"]), int(d["top_k"])
+    W = np.ascontiguousarray(d["gate_weight"].reshape(E, -1))
+    x = d["x"].reshape(-1, W.shape[1])
+    bias = np.ascontiguousarray(d["bias"])
+    for r in range(x.shape[0]):
+        idx = np.zeros(K, np.int32)
+        w = np.zeros(K, np.float32)
+        xr = np.ascontiguousarray(x[r])
+        k3moe.lib().k3_router(idx.ctypes.data, w.ctypes.data, xr.ctypes.data, W.ctypes.data,
+                              bias.ctypes.data, W.shape[1], E, K, 1, 1.0)
+        oi, ow = O.oracle().router(xr, W, bias, E, K, 1, 1.0)
+        assert np.array_equal(idx, oi), (r, idx, oi)
+        exp_i = d["topk_idx"].reshape(-1, K)[r]
+        exp_w = d["topk_weight"].reshape(-1, K)[r]
+        assert set(idx.tolist()) == set(exp_i.tolist())
+        for a in range(K):
+            b = list(exp_i).index(idx[a])
+            assert abs(w[a] - exp_w[b]) <= tol["fp32_abs"] + tol["fp32_rel"] * abs(exp_w[b])
+
+
+@pytest.fixture(scope="module")
+def k2_layer(gpu):
+    say("setup: Kimi-K2-scale layer (d=7168, 384 experts, top-8, I=2048), seed 2024, 9 GB bank")
+    layer = k3moe.SynthLayer(k3moe.K2, seed=2024)
+    yield layer
+
+
+@pytest.mark.parametrize("force", [0, 1, 2])
+def test_router_k2_bitexact(k2_layer, force):
+    T = 24 if force < 2 else 2
+    say(f"case: k3g_router d=7168 E=384 k=8, {T} tokens, force_exact={force}")
+    layer = k2_layer
+    x = layer.tokens(T, stream_base=7)
+    ctx = k3moe.Ctx(layer.dev, max_tokens=T)
+    ctx.force_exact(force)
+    dx = k3moe.DevBuf.from_array(x)
+    didx, dwt = k3moe.DevBuf(T * 8 * 4), k3moe.DevBuf(T * 8 * 4)
+    ctx.router(layer.dev, dx.ptr, T, didx.ptr, dwt.ptr)
+    ctx.sync()
+    idx = didx.download(np.int32, T * 8).reshape(T, 8)
+    wt = dwt.download(np.float32, T * 8).reshape(T, 8)
+    for t in range(T):
+        oi, ow = O.oracle().router(x[t], layer.gate, layer.bias, 384, 8, 1, 2.5)
+        assert np.array_equal(idx[t], oi), (t, idx[t], oi)
+        np.testing.assert_allclose(wt[t], ow, rtol=1e-6, atol=0)
+    if force:
+        assert ctx.stats()[0] >= T
+    ctx.destroy()
+
+
+def test_router_ties_and_degenerate(gpu):
+    say("case: router with exact ties (zero input, equal biases) and k > distinct values")
+    E, d, k = 16, 64, 4
+    W = np.ascontiguousarray(k3moe.host_normal(E * d, 3, 77, 0, 0.02).reshape(E, d))
+    bias = np.zeros(E, np.float32)
+    bias[5] = bias[9] = 0.25
+    x = np.zeros(d, np.float32)
+    idx = np.zeros(k, np.int32)
+    w = np.zeros(k, np.float32)
+    k3moe.lib().k3_router(idx.ctypes.data, w.ctypes.data, x.ctypes.data, W.ctypes.data,
+                          bias.ctypes.data, d, E, k, 1, 2.5)
+    oi, ow = O.oracle().router(x, W, bias, E, k, 1, 2.5)
+    assert np.array_equal(idx, oi), (idx, oi)
+    np.testing.assert_array_equal(w, ow)
+
+
+# ------------------------------------------------------------------------- layer ----
+
+def test_layer_tiny_decode(gpu):
+    say("case: k3g_moe tiny layer (d=256, E=16, k=4, I=128), 4 tokens")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=1234)
+    x = layer.tokens(4)
+    out, idx, wt = run_layer(layer, x)
+    ro, ri, rw = oracle_tokens(layer, x)
+    assert np.array_equal(idx, ri)
+    np.testing.assert_allclose(wt, rw, rtol=1e-6)
+    assert rel_l2(out, ro) <= REL_L2
+
+
+def test_layer_k2_decode_one_token(k2_layer):
+    say("case: k3g_moe K2 layer, 1-token decode, 3 different tokens")
+    layer = k2_layer
+    for s in range(3):
+        x = layer.tokens(1, stream_base=20 + s)
+        out, idx, _ = run_layer(layer, x)
+        ro, ri, _ = oracle_tokens(layer, x)
+        assert np.array_equal(idx, ri)
+        r = rel_l2(out, ro)
+        say(f"  token {s}: rel-L2 {r:.3e}")
+        assert r <= REL_L2
+
+
+def test_layer_k2_batch(k2_layer):
+    say("case: k3g_moe K2 layer, 12 tokens in one call")
+    layer = k2_layer
+    x = layer.tokens(12, stream_base=40)
+    out, idx, _ = run_layer(layer, x)
+    ro, ri, _ = oracle_tokens(layer, x)
+    assert np.array_equal(idx, ri)
+    assert rel_l2(out, ro) <= REL_L2
+
+
+# --------------------------------------------------------------------- drop-in ABI ----
+
+def _moe_json_weights():
+    d = np.load(os.path.join(GOLDEN, "moe.npz"))
+    cfg = k3moe.K3Cfg()
+    cfg.hidden, cfg.latent, cfg.moe_inter = int(d["hidden"]), int(d["latent"]), int(d["moe_inter"])
+    cfg.n_experts, cfg.topk, cfg.n_shared = int(d["n_experts"]), int(d["top_k"]), int(d["n_shared"])
+    cfg.routed_scale, cfg.moe_renorm = float(d["routed_scale"]), int(d["renorm"])
+    cfg.latent_norm, cfg.rms_eps = int(d["latent_norm"]), float(d["rms_eps"])
+    cfg.situ_b1, cfg.situ_b2 = float(d["situ_b1"]), float(d["situ_b2"])
+    keep = {k: np.ascontiguousarray(d[k], np.float32) for k in d.files
+            if d[k].dtype == np.float32 and d[k].ndim > 0}
+    w = k3moe.K3MoeW()
+    w.gate, w.bias = keep["gate_weight"].ctypes.data, keep["e_score_correction_bias"].ctypes.data
+    w.w1, w.w3, w.w2 = keep["w1"].ctypes.data, keep["w3"].ctypes.data, keep["w2"].ctypes.data
+    w.latent_norm = keep["norm_weight"].ctypes.data
+    w.down, w.up = keep["down_weight"].ctypes.data, keep["up_weight"].ctypes.data
+    w.sh1, w.sh3 = keep["shared_w1_weight"].ctypes.data, keep["shared_w3_weight"].ctypes.data
+    w.sh2 = keep["shared_w2_weight"].ctypes.data
+    return w, cfg, keep
+
+
+def test_dropin_moe_json(gpu):
+    say("case: k3_moe on tests/fixtures/ops/moe.json (LatentMoE, SiTU(4,25), fp32 bank)")
+    w, cfg, keep = _moe_json_weights()
+    tol = json.load(open(os.path.join(GOLDEN, "tolerance.json")))["tolerance"]
+    x = keep["in"].reshape(-1, cfg.hidden)
+    T = x.shape[0]
+    out = np.zeros_like(x)
+    idx = np.zeros(cfg.topk, np.int32)
+    wt = np.zeros(cfg.topk, np.float32)
+    k3moe.lib().k3_moe(out.ctypes.data, x.ctypes.data, C.byref(w), C.byref(cfg), T,
+                       idx.ctypes.data, wt.ctypes.data, None)
+    exp = keep["out"].reshape(out.shape)
+    worst = np.max(np.abs(out - exp) / (tol["fp32_abs"] + tol["fp32_rel"] * np.abs(exp)))
+    say(f"  worst {worst:.2f}x tolerance")
+    assert worst <= 1.0
+    oo, oi, ow = O.oracle().moe(w, cfg, x)
+    assert np.array_equal(idx, oi)
+    assert rel_l2(out, oo) <= 1e-5
+
+
+@pytest.mark.parametrize("prefill,T", [(False, 5), (True, 70), (True, 65)])
+def test_dropin_k3_moe_host_source(gpu, prefill, T):
+    say(f"case: {'k3_moe_prefill' if prefill else 'k3_moe'} tiny K2 layer, T={T}, host expert source")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=99, device=False)
+    x = layer.tokens(T)
+    experts = list(range(layer.shape.n_experts))
+    w, cfg, keep = O.k2_weights(layer, experts)
+    out = np.zeros_like(x)
+    idx = np.full(cfg.topk, -7, np.int32)
+    wt = np.zeros(cfg.topk, np.float32)
+    f = k3moe.lib().k3_moe_prefill if prefill else k3moe.lib().k3_moe
+    f(out.ctypes.data, x.ctypes.data, C.byref(w), C.byref(cfg), T, idx.ctypes.data,
+      wt.ctypes.data, None)
+    gets_gpu = keep[1].s.gets
+    w2, cfg2, keep2 = O.k2_weights(layer, experts)
+    oo, oi, ow = O.oracle().moe(w2, cfg2, x, prefill=prefill)
+    assert rel_l2(out, oo) <= REL_L2
+    assert gets_gpu == keep2[1].s.gets, "expert source saw a different request pattern"
+    if not prefill or (T - 1) % 64 == 0:
+        assert np.array_equal(idx, oi)
+        np.testing.assert_allclose(wt, ow, rtol=1e-6)
+    else:
+        assert np.all(idx == -7), "batched prefill must leave idx/wt untouched"
+
+
+def test_dropin_expert_drop(gpu):
+    say("case: k3_moe with a source that fails one expert: drop counted, slot skipped")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=5, device=False)
+    x = layer.tokens(6)
+    O_ = O.oracle()
+    union = O.routed_union(layer, x)
+    missing = union[0]
+    experts = [e for e in range(layer.shape.n_experts) if e != missing]
+    w, cfg, keep = O.k2_weights(layer, experts)
+    drops0 = C.c_long.in_dll(k3moe.lib(), "k3_expert_drops").value
+    out = np.zeros_like(x)
+    idx = np.zeros(cfg.topk, np.int32)
+    wt = np.zeros(cfg.topk, np.float32)
+    k3moe.lib().k3_moe(out.ctypes.data, x.ctypes.data, C.byref(w), C.byref(cfg), 6,
+                       idx.ctypes.data, wt.ctypes.data, None)
+    drops = C.c_long.in_dll(k3moe.lib(), "k3_expert_drops").value - drops0
+    w2, cfg2, keep2 = O.k2_weights(layer, experts)
+    od0 = O_.drops.value
+    oo, _, _ = O_.moe(w2, cfg2, x)
+    assert drops == O_.drops.value - od0 and drops > 0
+    assert rel_l2(out, oo) <= REL_L2
