@@ -218,6 +218,14 @@ void *k3g_ctx_stream(K3gCtx *ctx);   /* the context's compute stream (hipStream_
  * failed and were re-routed in the engine's serial order. */
 void k3g_ctx_stats(K3gCtx *ctx, int64_t *out, int n);
 
+/* Per-stage timing with HIP events on the call's stream (off by default; turning it on
+ * or off clears the totals). Stages: 0 router, 1 dispatch, 2 routed gate/up, 3 routed
+ * down, 4 shared gate/up, 5 shared down, 6 combine, 7 latent projections. */
+void k3g_ctx_profile(K3gCtx *ctx, int on);
+/* Totals since profiling was turned on: milliseconds and call counts per stage. Returns
+ * the number of stages. */
+int  k3g_ctx_stage_ms(K3gCtx *ctx, double *ms, int64_t *count, int n);
+
 /* Force the router's exact re-routing path: 0 normal, 1 every token re-routes its
  * candidate set, 2 every token recomputes every expert serially (testing only). */
 void k3g_ctx_force_exact(K3gCtx *ctx, int mode);

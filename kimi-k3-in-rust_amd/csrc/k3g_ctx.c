@@ -125,11 +125,81 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     return 0;
 }
 
+/* Stage timing: each stage owns a ring of K3G_RING event pairs. A pair is harvested
+ * (its elapsed time added to the stage total) only when the ring comes back to it or
+ * the totals are read, so a timed loop of up to K3G_RING calls never blocks on its own
+ * events. */
+static void harvest_one(K3gCtx *c, int s, int i)
+{
+    float ms = 0.0f;
+    K3G_CHECK(hipEventSynchronize(c->ev[s][i][1]));
+    K3G_CHECK(hipEventElapsedTime(&ms, c->ev[s][i][0], c->ev[s][i][1]));
+    c->stage_ms[s] += ms;
+    c->stage_n[s]++;
+}
+
+static void harvest(K3gCtx *c, int s)
+{
+    const int n = c->ev_used[s];
+    for (int k = 0; k < n; k++)
+        harvest_one(c, s, (c->ev_head[s] - n + k + K3G_RING) % K3G_RING);
+    c->ev_used[s] = 0;
+}
+
+void k3g_stage_begin(K3gCtx *c, int s, hipStream_t st)
+{
+    if (!c->prof) return;
+    const int i = c->ev_head[s];
+    if (!c->ev[s][i][0]) {
+        K3G_CHECK(hipEventCreate(&c->ev[s][i][0]));
+        K3G_CHECK(hipEventCreate(&c->ev[s][i][1]));
+    }
+    if (c->ev_used[s] == K3G_RING) {        /* the oldest pair is this one */
+        harvest_one(c, s, i);
+        c->ev_used[s]--;
+    }
+    K3G_CHECK(hipEventRecord(c->ev[s][i][0], st));
+}
+
+void k3g_stage_end(K3gCtx *c, int s, hipStream_t st)
+{
+    if (!c->prof) return;
+    const int i = c->ev_head[s];
+    K3G_CHECK(hipEventRecord(c->ev[s][i][1], st));
+    c->ev_head[s] = (i + 1) % K3G_RING;
+    c->ev_used[s]++;
+}
+
+void k3g_ctx_profile(K3gCtx *c, int on)
+{
+    if (!c) return;
+    for (int s = 0; s < K3G_NSTAGE; s++) harvest(c, s);
+    c->prof = on;
+    for (int s = 0; s < K3G_NSTAGE; s++) { c->stage_ms[s] = 0.0; c->stage_n[s] = 0; }
+}
+
+int k3g_ctx_stage_ms(K3gCtx *c, double *ms, int64_t *count, int n)
+{
+    if (!c) return 0;
+    for (int s = 0; s < K3G_NSTAGE; s++) harvest(c, s);
+    for (int s = 0; s < n && s < K3G_NSTAGE; s++) {
+        if (ms) ms[s] = c->stage_ms[s];
+        if (count) count[s] = c->stage_n[s];
+    }
+    return K3G_NSTAGE;
+}
+
 void k3g_ctx_destroy(K3gCtx *c)
 {
     if (!c) return;
     hipSetDevice(c->device);
     hipStreamSynchronize(c->stream);
+    for (int s = 0; s < K3G_NSTAGE; s++)
+        for (int i = 0; i < K3G_RING; i++)
+            if (c->ev[s][i][0]) {
+                hipEventDestroy(c->ev[s][i][0]);
+                hipEventDestroy(c->ev[s][i][1]);
+            }
     hipFree(c->ws);
     hipStreamDestroy(c->stream);
     free(c);
@@ -170,9 +240,12 @@ int k3g_route(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx,
               hipStream_t st)
 {
     if (!fits(c, L, T)) return -1;
-    return k3k_router(x, T, L->gate, L->bias, L->hidden, L->n_experts, L->topk, L->renorm,
-                      L->routed_scale, c->logit, c->asum, idx, wt, c->force_exact,
-                      c->stats, st);
+    k3g_stage_begin(c, K3G_ST_ROUTER, st);
+    const int rc = k3k_router(x, T, L->gate, L->bias, L->hidden, L->n_experts, L->topk,
+                              L->renorm, L->routed_scale, c->logit, c->asum, idx, wt,
+                              c->force_exact, c->stats, st);
+    k3g_stage_end(c, K3G_ST_ROUTER, st);
+    return rc;
 }
 
 int k3g_router(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx, float *wt,
@@ -194,11 +267,15 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     const int projected = L->down != NULL;
     int rc = 0;
 
+    k3g_stage_begin(c, K3G_ST_DISPATCH, st);
     rc |= k3k_dispatch(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm, c->err,
                        st);
+    k3g_stage_end(c, K3G_ST_DISPATCH, st);
     const float *z = x;
     if (projected) {
+        k3g_stage_begin(c, K3G_ST_LATENT, st);
         rc |= k3k_dense(wfmt(L->wdt), L->down, NULL, lat, d, x, d, T, c->z, lat, 0.f, 0.f, st);
+        k3g_stage_end(c, K3G_ST_LATENT, st);
         z = c->z;
     }
     K3kRouted a;
@@ -222,16 +299,26 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     a.b2 = L->act_b2;
     a.err = c->err;
     const int maxU = P < E ? P : E;
+    k3g_stage_begin(c, K3G_ST_GATEUP, st);
     rc |= k3k_routed_gateup(&a, maxU, T, st);
+    k3g_stage_end(c, K3G_ST_GATEUP, st);
+    k3g_stage_begin(c, K3G_ST_DOWN, st);
     rc |= k3k_routed_down(&a, maxU, T, st);
+    k3g_stage_end(c, K3G_ST_DOWN, st);
     if (SI > 0) {
+        k3g_stage_begin(c, K3G_ST_SH_GATEUP, st);
         rc |= k3k_dense(wfmt(L->wdt), L->sh1, L->sh3, SI, d, x, d, T, c->sh_h, SI,
                         L->act_b1, L->act_b2, st);
+        k3g_stage_end(c, K3G_ST_SH_GATEUP, st);
+        k3g_stage_begin(c, K3G_ST_SH_DOWN, st);
         rc |= k3k_dense(wfmt(L->wdt), L->sh2, NULL, d, SI, c->sh_h, SI, T, c->sh_out, d,
                         0.f, 0.f, st);
+        k3g_stage_end(c, K3G_ST_SH_DOWN, st);
     }
     if (!projected && !L->up && !L->latent_norm) {
+        k3g_stage_begin(c, K3G_ST_COMBINE, st);
         rc |= k3k_combine(c->contrib, idx, wt, T, k, d, SI > 0 ? c->sh_out : NULL, out, st);
+        k3g_stage_end(c, K3G_ST_COMBINE, st);
     } else {
         rc |= k3k_combine(c->contrib, idx, wt, T, k, lat, NULL, c->accl, st);
         if (L->latent_norm) rc |= k3k_rmsnorm(c->accl, c->accl, L->latent_norm, lat, T,

@@ -15,6 +15,14 @@
 void k3g_fatal_hip(const char *what, hipError_t e, const char *file, int line);
 void k3g_fatal(const char *what);
 
+/* stages of a layer call, for the optional per-stage timing */
+enum {
+    K3G_ST_ROUTER = 0, K3G_ST_DISPATCH, K3G_ST_GATEUP, K3G_ST_DOWN, K3G_ST_SH_GATEUP,
+    K3G_ST_SH_DOWN, K3G_ST_COMBINE, K3G_ST_LATENT, K3G_NSTAGE
+};
+
+#define K3G_RING 256
+
 struct K3gCtx {
     int device;
     hipStream_t stream;
@@ -38,7 +46,17 @@ struct K3gCtx {
     float *sh_out;               /* [T][hidden] */
     int *err;                    /* device error word */
     int *stats;                  /* device counters */
+    /* optional per-stage timing: a ring of event pairs around each stage of a call,
+     * harvested only when the ring wraps or the totals are read */
+    int prof;
+    hipEvent_t ev[K3G_NSTAGE][K3G_RING][2];
+    int ev_head[K3G_NSTAGE], ev_used[K3G_NSTAGE];
+    double stage_ms[K3G_NSTAGE];
+    int64_t stage_n[K3G_NSTAGE];
 };
+
+void k3g_stage_begin(K3gCtx *c, int stage, hipStream_t st);
+void k3g_stage_end(K3gCtx *c, int stage, hipStream_t st);
 
 /* Stages of k3g_moe, for callers (the drop-in) that must act on the routing between
  * them. idx/wt are device arrays [T][topk]; entries with idx < 0 are skipped. */
