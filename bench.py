@@ -116,7 +116,6 @@ def main():
     dout = k3moe.DevBuf(n_tok * D * 4)
     didx = k3moe.DevBuf(n_tok * K * 4)
     dwt = k3moe.DevBuf(n_tok * K * 4)
-    L = k3moe.lib()
 
     def step(i):
         ctx.moe(layers[i % a.layers].dev, dx.ptr + i * D * 4, 1, dout.ptr + i * D * 4,
@@ -126,10 +125,7 @@ def main():
     for i in range(a.warmup):
         step(i)
     ctx.sync()
-    L.k3g_ctx_profile.argtypes = [k3moe.C.c_void_p, k3moe.C.c_int]
-    L.k3g_ctx_stage_ms.argtypes = [k3moe.C.c_void_p, k3moe.C.c_void_p, k3moe.C.c_void_p,
-                                   k3moe.C.c_int]
-    L.k3g_ctx_profile(ctx.ptr, 1)
+    ctx.profile(True)
     log(f"bench: timing {a.steps} steps")
     k3moe.sync()
     t0 = time.perf_counter()
@@ -138,10 +134,8 @@ def main():
     k3moe.sync()
     t1 = time.perf_counter()
     ctx.sync()
-    ms_stage = np.zeros(8)
-    n_stage = np.zeros(8, np.int64)
-    L.k3g_ctx_stage_ms(ctx.ptr, ms_stage.ctypes.data, n_stage.ctypes.data, 8)
-    L.k3g_ctx_profile(ctx.ptr, 0)
+    ms_stage, n_stage = ctx.stage_ms()
+    ctx.profile(False)
     out = dout.download(np.float32, n_tok * D)
     assert np.isfinite(out).all()
 
@@ -149,12 +143,18 @@ def main():
     us_tok = ms_step * 1e3
     layer_bytes = K * B_EXPERT + B_SHARED + B_ROUTER + B_TOKEN
     names = ["router", "dispatch", "routed_gateup", "routed_down", "shared_gateup",
-             "shared_down", "combine", "latent"]
+             "shared_down", "combine", "latent", "fused_layer"]
     stage_us = {names[s]: round(1e3 * ms_stage[s] / max(n_stage[s], 1), 2)
-                for s in range(8) if n_stage[s]}
-    gu_us = 1e3 * ms_stage[2] / max(n_stage[2], 1)
-    gu_bytes = K * B_GATEUP_EXPERT
-    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+                for s in range(len(names)) if n_stage[s]}
+    if n_stage[8]:
+        kern = "k_decode_fused (whole layer: router, top-k, shared + routed MXFP4 GEMVs, combine)"
+        k_us = 1e3 * ms_stage[8] / n_stage[8]
+        k_bytes = layer_bytes
+    else:
+        kern = "k_routed_gateup (MXFP4 gate+up GEMV, SwiGLU epilogue)"
+        k_us = 1e3 * ms_stage[2] / max(n_stage[2], 1)
+        k_bytes = K * B_GATEUP_EXPERT
+    achieved = k_bytes / (k_us * 1e-6) / 1e9
     res = {
         "metric": METRIC,
         "value": round(1e6 / us_tok, 2),
@@ -177,11 +177,10 @@ def main():
         "hbm_frac": round(layer_bytes / (us_tok * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_token": layer_bytes,
         "stage_us": stage_us,
-        "roofline": {"kernel": "k_routed_gateup (MXFP4 gate+up GEMV, SwiGLU epilogue)",
-                     "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": gu_bytes,
-                     "avg_launch_us": round(gu_us, 2)},
+        "roofline": {"kernel": kern, "bound": "hbm", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": k_bytes,
+                     "avg_launch_us": round(k_us, 2)},
     }
     ctx.destroy()
     del layers

@@ -220,11 +220,21 @@ void k3g_ctx_stats(K3gCtx *ctx, int64_t *out, int n);
 
 /* Per-stage timing with HIP events on the call's stream (off by default; turning it on
  * or off clears the totals). Stages: 0 router, 1 dispatch, 2 routed gate/up, 3 routed
- * down, 4 shared gate/up, 5 shared down, 6 combine, 7 latent projections. */
+ * down, 4 shared gate/up, 5 shared down, 6 combine, 7 latent projections, 8 the fused
+ * decode kernel (the whole layer in one launch). */
 void k3g_ctx_profile(K3gCtx *ctx, int on);
 /* Totals since profiling was turned on: milliseconds and call counts per stage. Returns
  * the number of stages. */
 int  k3g_ctx_stage_ms(K3gCtx *ctx, double *ms, int64_t *count, int n);
+
+/* k3g_moe runs a Kimi-K2-shaped layer at up to 4 tokens as one fused persistent kernel
+ * (default on); off forces the staged kernels. No reference counterpart. */
+void k3g_ctx_set_fused(K3gCtx *ctx, int on);
+
+/* Instrumentation: with a device buffer of 2 * (tickets) uint64, the fused kernel writes
+ * each ticket's start and end wall-clock stamps (100 MHz counter). NULL turns it off.
+ * No reference counterpart. */
+void k3g_ctx_set_trace(K3gCtx *ctx, void *dev_buf);
 
 /* Force the router's exact re-routing path: 0 normal, 1 every token re-routes its
  * candidate set, 2 every token recomputes every expert serially (testing only). */

@@ -80,7 +80,8 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t L = (size_t)c->latent, I = (size_t)c->inter, SI = (size_t)c->shared_inter;
     const size_t d = (size_t)c->hidden;
     size_t at = 0;
-    const size_t o_logit = carve(&at, T * E * 8), o_asum = carve(&at, T * E * 8);
+    const size_t nrc = (d + 1023) / 1024;   /* router partial sums per token */
+    const size_t o_logit = carve(&at, nrc * T * E * 8), o_asum = carve(&at, nrc * T * E * 8);
     const size_t o_idx = carve(&at, P * 4), o_wt = carve(&at, P * 4);
     const size_t o_cnt = carve(&at, nch * E * 4), o_base = carve(&at, nch * E * 4);
     const size_t o_off = carve(&at, (E + 1) * 4), o_act = carve(&at, E * 4);
@@ -89,6 +90,7 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t o_contrib = carve(&at, P * L * 4), o_accl = carve(&at, T * L * 4);
     const size_t o_shh = carve(&at, T * (SI ? SI : 1) * 4), o_sho = carve(&at, T * d * 4);
     const size_t o_err = carve(&at, 4), o_stats = carve(&at, 16 * 4);
+    const size_t o_sync = carve(&at, K3G_SYNC_WORDS * 4);
     c->ws_bytes = at;
     if (hipMalloc(&c->ws, at) != hipSuccess) {
         fprintf(stderr, "k3moe: cannot allocate %.2f GB of device workspace\n", at / 1e9);
@@ -115,6 +117,8 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->sh_out = (float *)(b + o_sho);
     c->err = (int *)(b + o_err);
     c->stats = (int *)(b + o_stats);
+    c->sync = (int *)(b + o_sync);
+    c->fused = 1;
     if (hipMemset(c->ws, 0, at) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         hipFree(c->ws);
         hipStreamDestroy(c->stream);
@@ -208,6 +212,19 @@ void k3g_ctx_destroy(K3gCtx *c)
 void *k3g_ctx_stream(K3gCtx *c) { return c ? (void *)c->stream : NULL; }
 
 void k3g_ctx_force_exact(K3gCtx *c, int mode) { if (c) c->force_exact = mode; }
+
+void k3g_ctx_set_fused(K3gCtx *c, int on) { if (c) c->fused = on; }
+
+void k3g_ctx_set_trace(K3gCtx *c, void *dev_buf) { if (c) c->trace = (unsigned long long *)dev_buf; }
+
+/* The fused kernel covers the Kimi-K2 layer shape at decode token counts. */
+static int fusable(const K3gCtx *c, const K3gLayer *L, int T)
+{
+    const int lat = L->latent > 0 ? L->latent : L->hidden;
+    return c->fused && T <= 4 && L->expert_fmt == 0 && !L->down && !L->up &&
+           !L->latent_norm && lat == L->hidden && L->hidden % 32 == 0 && L->inter % 32 == 0 &&
+           (L->shared_inter == 0 || (L->wdt == K3_WBF16 && L->shared_inter % 16 == 0));
+}
 
 void k3g_ctx_stats(K3gCtx *c, int64_t *out, int n)
 {
@@ -340,6 +357,52 @@ int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int
     hipStream_t st = stream ? (hipStream_t)stream : c->stream;
     if (!idx) idx = c->idx;
     if (!wt) wt = c->wt;
+    if (!fits(c, L, T)) return -1;
+    if (fusable(c, L, T)) {
+        K3kDecode a;
+        memset(&a, 0, sizeof a);
+        a.T = T;
+        a.d = L->hidden;
+        a.E = L->n_experts;
+        a.k = L->topk;
+        a.I = L->inter;
+        a.SI = L->shared_inter;
+        a.renorm = L->renorm;
+        a.routed_scale = L->routed_scale;
+        a.b1 = L->act_b1;
+        a.b2 = L->act_b2;
+        a.gate = L->gate;
+        a.bias = L->bias;
+        a.eq = L->experts;
+        a.sh1 = (const uint16_t *)L->sh1;
+        a.sh3 = (const uint16_t *)L->sh3;
+        a.sh2 = (const uint16_t *)L->sh2;
+        a.x = x;
+        a.out = out;
+        a.idx = idx;
+        a.wt = wt;
+        a.plogit = c->logit;
+        a.pasum = c->asum;
+        a.h = c->h;
+        a.sh_h = c->sh_h;
+        a.contrib = c->contrib;
+        a.sh_out = c->sh_out;
+        a.sync = c->sync;
+        a.err = c->err;
+        a.stats = c->stats;
+        a.force = c->force_exact;
+        a.spin_limit = 1ll << 21;
+        if (c->epoch >= K3G_EPOCH_MAX) {
+            if (hipMemsetAsync(c->sync, 0, K3G_SYNC_WORDS * 4, st) != hipSuccess) return -1;
+            c->epoch = 0;
+        }
+        a.epoch = ++c->epoch;
+        a.trace = c->trace;
+        k3g_stage_begin(c, K3G_ST_FUSED, st);
+        const int rc = k3k_decode_fused(&a, st);
+        k3g_stage_end(c, K3G_ST_FUSED, st);
+        return rc;
+    }
     if (k3g_route(c, L, x, T, idx, wt, st) != 0) return -1;
     return k3g_experts(c, L, x, T, idx, wt, out, st);
 }
@@ -355,6 +418,9 @@ int k3g_sync(K3gCtx *c, void *stream)
                 e == 1 ? "routed expert index out of range" : "bounded wait ran out");
         int z = 0;
         hipMemcpy(c->err, &z, sizeof z, hipMemcpyHostToDevice);
+        /* a call cut short leaves the fused kernel's counters short: start over */
+        hipMemset(c->sync, 0, K3G_SYNC_WORDS * 4);
+        c->epoch = 0;
         return e;
     }
     return 0;

@@ -18,7 +18,7 @@ void k3g_fatal(const char *what);
 /* stages of a layer call, for the optional per-stage timing */
 enum {
     K3G_ST_ROUTER = 0, K3G_ST_DISPATCH, K3G_ST_GATEUP, K3G_ST_DOWN, K3G_ST_SH_GATEUP,
-    K3G_ST_SH_DOWN, K3G_ST_COMBINE, K3G_ST_LATENT, K3G_NSTAGE
+    K3G_ST_SH_DOWN, K3G_ST_COMBINE, K3G_ST_LATENT, K3G_ST_FUSED, K3G_NSTAGE
 };
 
 #define K3G_RING 256
@@ -46,6 +46,10 @@ struct K3gCtx {
     float *sh_out;               /* [T][hidden] */
     int *err;                    /* device error word */
     int *stats;                  /* device counters */
+    int *sync;                   /* fused-kernel counters */
+    int epoch;                   /* fused-kernel calls since the counters were cleared */
+    int fused;                   /* use the fused decode kernel when the layer allows */
+    unsigned long long *trace;   /* optional per-ticket timestamps of the fused kernel */
     /* optional per-stage timing: a ring of event pairs around each stage of a call,
      * harvested only when the ring wraps or the totals are read */
     int prof;

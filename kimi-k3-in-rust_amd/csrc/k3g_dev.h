@@ -21,6 +21,21 @@ __device__ __forceinline__ void k3d_raise(int *err, int code)
     if (err) atomicCAS(err, 0, code);
 }
 
+/* Device-coherent (sc1) 64-bit load and store, for values other waves exchange inside
+ * one kernel without a device-wide cache writeback. */
+__device__ __forceinline__ double k3d_ld_dev64(const double *p)
+{
+    const unsigned long long v = __hip_atomic_load((const unsigned long long *)p,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __longlong_as_double((long long)v);
+}
+
+__device__ __forceinline__ void k3d_st_dev64(double *p, double v)
+{
+    __hip_atomic_store((unsigned long long *)p, (unsigned long long)__double_as_longlong(v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 /* E8M0 byte -> 2^(b-127) as fp32; 255 (NaN by the OCP spec) -> 0, matching the engine's
  * table (src/core/k3_ops.c:1315-1322). b = 0 gives the denormal 2^-127. */
 __device__ __forceinline__ float k3d_e8m0(uint32_t b)

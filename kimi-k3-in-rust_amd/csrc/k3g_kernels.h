@@ -39,6 +39,37 @@ typedef struct {
     int *err;
 } K3kRouted;
 
+/* The fused decode kernel (k3g_decode.hip): the whole Kimi-K2-shaped layer for T <= 4
+ * tokens in one persistent launch. */
+typedef struct {
+    int T, d, E, k, I, SI;
+    int renorm;
+    float routed_scale, b1, b2;
+    const float *gate, *bias;
+    const K3ExpertQ *eq;
+    const uint16_t *sh1, *sh3, *sh2;
+    const float *x;
+    float *out;
+    int32_t *idx;
+    float *wt;
+    double *plogit, *pasum;       /* [ceil(d/1024)][T][E] partial logits */
+    float *h;                     /* [T*k][I] */
+    float *sh_h;                  /* [T][SI] */
+    float *contrib;               /* [T*k][d] per-slot expert outputs */
+    float *sh_out;                /* [T][d] shared-expert output */
+    int *sync;                    /* K3G_SYNC_WORDS counters, zero between launches */
+    int *err, *stats;
+    int force;
+    int epoch;                    /* call number since the counters were cleared, >= 1 */
+    long long spin_limit;
+    unsigned long long *trace;    /* optional: [ticket][2] start/end wall-clock stamps */
+} K3kDecode;
+
+#define K3G_SYNC_WORDS (600 * 32)
+#define K3G_EPOCH_MAX 100000      /* counters are cleared before they could overflow */
+
+int k3k_decode_fused(const K3kDecode *a, hipStream_t st);
+
 int k3k_router(const float *x, int T, const float *W, const float *bias, int d, int E,
                int k, int renorm, float routed_scale, double *logit, double *asum,
                int32_t *idx, float *wt, int force, int *stats, hipStream_t st);

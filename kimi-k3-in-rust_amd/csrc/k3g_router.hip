@@ -22,6 +22,7 @@
  */
 #include "k3g_dev.h"
 #include "k3g_kernels.h"
+#include "k3g_select.h"
 
 #include <math.h>
 
@@ -80,163 +81,17 @@ k_router_logits(const float *__restrict__ x, int T, const float *__restrict__ W,
 }
 
 /* ------------------------------------------------------------------ select ---- */
-#define K3G_MAX_E 1024
-
-/* (value, index) argmax with the engine's rule: larger value wins, equal values go to
- * the lower index. NaN and -inf never win (the engine's strict > against -inf). */
-__device__ __forceinline__ void k3d_argmax(float &v, int &i)
-{
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = __shfl_xor(v, m, K3G_WAVE);
-        const int oi = __shfl_xor(i, m, K3G_WAVE);
-        if (ov > v || (ov == v && oi >= 0 && (i < 0 || oi < i))) { v = ov; i = oi; }
-    }
-}
-
 /* One wave per token. */
 __global__ void __launch_bounds__(64)
 k_router_select(const double *__restrict__ logit, const double *__restrict__ asum,
                 const float *__restrict__ bias, const float *__restrict__ W,
                 const float *__restrict__ x, int d, int E, int k, int renorm,
                 float routed_scale, int32_t *__restrict__ idx, float *__restrict__ wt,
-                int force, int *__restrict__ stats)
+                int force, int *__restrict__ stats, int T)
 {
-    __shared__ float s_choice[K3G_MAX_E];
-    __shared__ float s_lo[K3G_MAX_E];
-    __shared__ float s_hi[K3G_MAX_E];
-    __shared__ float s_score[K3G_MAX_E];
-    __shared__ unsigned char s_taken[K3G_MAX_E];
-    __shared__ int s_sel[K3G_MAX_TOPK];
-    __shared__ int s_cand[K3G_MAX_E];
-    __shared__ int s_ncand;
-    __shared__ int s_cert;
-
-    const int t = blockIdx.x;
-    const int lane = threadIdx.x;
-    const double *lg = logit + (size_t)t * E;
-    const double *as = asum + (size_t)t * E;
-    const double kB = ((double)d * (1.0 + 1.0 / 64.0) + 16.0) * 0x1p-53 * 1.01;
-
-    for (int e = lane; e < E; e += 64) {
-        const double acc = lg[e];
-        const double B = kB * as[e] + fabs(acc) * 0x1p-51 + 0x1p-1000;
-        const float b = bias ? bias[e] : 0.0f;
-        const float s = k3d_sigmoid((float)acc);
-        float slo = k3d_sigmoid((float)(acc - B));
-        float shi = k3d_sigmoid((float)(acc + B));
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            slo = nextafterf(slo, -INFINITY);
-            shi = nextafterf(shi, INFINITY);
-        }
-        s_score[e] = s;
-        s_choice[e] = __fadd_rn(s, b);
-        s_lo[e] = __fadd_rn(slo, b);
-        s_hi[e] = __fadd_rn(shi, b);
-        s_taken[e] = 0;
-    }
-    __syncthreads();
-
-    /* top-k on the best guess */
-    for (int j = 0; j < k; ++j) {
-        float bv = -INFINITY;
-        int bi = -1;
-        for (int e = lane; e < E; e += 64) {
-            const float c = s_choice[e];
-            if (!s_taken[e] && c > bv) { bv = c; bi = e; }
-        }
-        k3d_argmax(bv, bi);
-        if (lane == 0) {
-            s_sel[j] = bi;
-            if (bi >= 0) s_taken[bi] = 1;
-        }
-        __syncthreads();
-    }
-
-    /* certificate: every selected lo strictly above the hi of everything ranked after */
-    float hrest = -INFINITY;
-    for (int e = lane; e < E; e += 64)
-        if (!s_taken[e] && s_hi[e] > hrest) hrest = s_hi[e];
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) hrest = fmaxf(hrest, __shfl_xor(hrest, m, K3G_WAVE));
-    if (lane == 0) {
-        int ok = force ? 0 : 1;
-        float M = hrest;
-        for (int j = k - 1; j >= 0 && ok; --j) {
-            const int e = s_sel[j];
-            if (e < 0) { ok = 0; break; }
-            if (!(s_lo[e] > M)) ok = 0;
-            M = fmaxf(M, s_hi[e]);
-        }
-        s_cert = ok;
-    }
-    __syncthreads();
-
-    if (!s_cert) {
-        /* candidates: every expert whose interval reaches the weakest selected lo */
-        if (lane == 0) {
-            float theta = INFINITY;
-            for (int j = 0; j < k; ++j) {
-                const int e = s_sel[j];
-                theta = e < 0 ? -INFINITY : fminf(theta, s_lo[e]);
-            }
-            int n = 0;
-            for (int e = 0; e < E; ++e)
-                if (force == 2 || s_hi[e] >= theta || s_taken[e]) s_cand[n++] = e;
-            s_ncand = n;
-            if (stats) atomicAdd(&stats[0], 1);
-        }
-        __syncthreads();
-        const int nc = s_ncand;
-        const float *xt = x + (size_t)t * d;
-        for (int c0 = 0; c0 < nc; c0 += 64) {
-            const int c = c0 + lane;
-            if (c < nc) {
-                const int e = s_cand[c];
-                const float *w = W + (size_t)e * d;
-                double acc = 0.0;
-                for (int i = 0; i < d; ++i) acc = fma((double)w[i], (double)xt[i], acc);
-                const float s = k3d_sigmoid((float)acc);
-                s_score[e] = s;
-                s_choice[e] = __fadd_rn(s, bias ? bias[e] : 0.0f);
-            }
-        }
-        __syncthreads();
-        for (int c = lane; c < nc; c += 64) s_taken[s_cand[c]] = 0;
-        __syncthreads();
-        for (int j = 0; j < k; ++j) {
-            float bv = -INFINITY;
-            int bi = -1;
-            for (int c = lane; c < nc; c += 64) {
-                const int e = s_cand[c];
-                const float v = s_choice[e];
-                if (!s_taken[e] && (v > bv || (v == bv && bi >= 0 && e < bi))) { bv = v; bi = e; }
-            }
-            k3d_argmax(bv, bi);
-            if (lane == 0) {
-                s_sel[j] = bi;
-                if (bi >= 0) s_taken[bi] = 1;
-            }
-            __syncthreads();
-        }
-    }
-
-    /* weights from the unbiased scores, renormalised in double, then scaled */
-    if (lane == 0) {
-        float w[K3G_MAX_TOPK];
-        for (int j = 0; j < k; ++j) w[j] = s_sel[j] >= 0 ? s_score[s_sel[j]] : 0.0f;
-        if (renorm && k > 1) {
-            double s = 0.0;
-            for (int j = 0; j < k; ++j) s += (double)w[j];
-            const float inv = (float)(1.0 / (s + 1e-20));
-            for (int j = 0; j < k; ++j) w[j] = __fmul_rn(w[j], inv);
-        }
-        for (int j = 0; j < k; ++j) {
-            idx[(size_t)t * k + j] = s_sel[j] >= 0 ? s_sel[j] : 0;
-            wt[(size_t)t * k + j] = __fmul_rn(w[j], routed_scale);
-        }
-    }
+    __shared__ K3SelectLds lds;
+    k3d_select_token(&lds, blockIdx.x, T, 1, logit, asum, bias, W, x, d, E, k, renorm,
+                     routed_scale, idx, wt, force, stats, threadIdx.x);
 }
 
 extern "C" int k3k_router(const float *x, int T, const float *W, const float *bias, int d,
@@ -245,6 +100,7 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
                           hipStream_t st)
 {
     if (E > K3G_MAX_E || k > K3G_MAX_TOPK || k < 1 || T < 1 || d < 1) return -1;
+    /* logits of token t live at [t][E] (one partial sum) */
     /* float4 loads need 16-byte aligned rows; anything else takes the scalar loop */
     const int vec = ((((uintptr_t)x | (uintptr_t)W) & 15) == 0) && ((d & 3) == 0);
     if (T >= 4) {
@@ -255,6 +111,6 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
                            x, T, W, d, vec, logit, asum, E);
     }
     hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), 0, st, logit, asum, bias, W, x,
-                       d, E, k, renorm, routed_scale, idx, wt, force, stats);
+                       d, E, k, renorm, routed_scale, idx, wt, force, stats, T);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -132,6 +132,12 @@ def lib() -> C.CDLL:
         L.k3g_ctx_stats.restype = None
         L.k3g_ctx_force_exact.argtypes = [vp, i]
         L.k3g_ctx_force_exact.restype = None
+        L.k3g_ctx_set_fused.argtypes = [vp, i]
+        L.k3g_ctx_set_fused.restype = None
+        L.k3g_ctx_profile.argtypes = [vp, i]
+        L.k3g_ctx_profile.restype = None
+        L.k3g_ctx_stage_ms.argtypes = [vp, vp, vp, i]
+        L.k3g_ctx_stage_ms.restype = i
         L.k3g_router.argtypes = [vp, C.POINTER(K3gLayer), vp, i, vp, vp, vp]
         L.k3g_router.restype = i
         L.k3g_moe.argtypes = [vp, C.POINTER(K3gLayer), vp, i, vp, vp, vp, vp]
@@ -479,6 +485,18 @@ class Ctx:
 
     def force_exact(self, mode: int) -> None:
         lib().k3g_ctx_force_exact(self.ptr, mode)
+
+    def set_fused(self, on: bool) -> None:
+        lib().k3g_ctx_set_fused(self.ptr, 1 if on else 0)
+
+    def profile(self, on: bool) -> None:
+        lib().k3g_ctx_profile(self.ptr, 1 if on else 0)
+
+    def stage_ms(self):
+        ms = np.zeros(16)
+        n = np.zeros(16, np.int64)
+        ns = lib().k3g_ctx_stage_ms(self.ptr, ms.ctypes.data, n.ctypes.data, 16)
+        return ms[:ns], n[:ns]
 
     def stats(self) -> list:
         out = (C.c_int64 * 4)()

@@ -28,11 +28,12 @@ def say(msg):
     print(msg, flush=True)
 
 
-def run_layer(layer, x, ctx=None, force=0):
+def run_layer(layer, x, ctx=None, force=0, fused=True):
     T, d, k = x.shape[0], layer.shape.hidden, layer.shape.topk
     own = ctx is None
     ctx = ctx or k3moe.Ctx(layer.dev, max_tokens=T)
     ctx.force_exact(force)
+    ctx.set_fused(fused)
     dx = k3moe.DevBuf.from_array(x)
     dout, didx, dwt = k3moe.DevBuf(T * d * 4), k3moe.DevBuf(T * k * 4), k3moe.DevBuf(T * k * 4)
     ctx.moe(layer.dev, dx.ptr, T, dout.ptr, didx.ptr, dwt.ptr)
@@ -192,28 +193,44 @@ def test_router_ties_and_degenerate(gpu):
 
 # ------------------------------------------------------------------------- layer ----
 
-def test_layer_tiny_decode(gpu):
-    say("case: k3g_moe tiny layer (d=256, E=16, k=4, I=128), 4 tokens")
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 7])
+def test_layer_tiny_decode(gpu, T, fused):
+    say(f"case: k3g_moe tiny layer (d=256, E=16, k=4, I=128), {T} tokens, fused={fused}")
     layer = k3moe.SynthLayer(k3moe.TINY, seed=1234)
-    x = layer.tokens(4)
-    out, idx, wt = run_layer(layer, x)
+    x = layer.tokens(T)
+    out, idx, wt = run_layer(layer, x, fused=fused)
     ro, ri, rw = oracle_tokens(layer, x)
     assert np.array_equal(idx, ri)
     np.testing.assert_allclose(wt, rw, rtol=1e-6)
     assert rel_l2(out, ro) <= REL_L2
 
 
-def test_layer_k2_decode_one_token(k2_layer):
-    say("case: k3g_moe K2 layer, 1-token decode, 3 different tokens")
+@pytest.mark.parametrize("fused", [False, True])
+def test_layer_k2_decode_one_token(k2_layer, fused):
+    say(f"case: k3g_moe K2 layer, 1-token decode, 3 different tokens, fused={fused}")
     layer = k2_layer
     for s in range(3):
         x = layer.tokens(1, stream_base=20 + s)
-        out, idx, _ = run_layer(layer, x)
+        out, idx, _ = run_layer(layer, x, fused=fused)
         ro, ri, _ = oracle_tokens(layer, x)
         assert np.array_equal(idx, ri)
         r = rel_l2(out, ro)
         say(f"  token {s}: rel-L2 {r:.3e}")
         assert r <= REL_L2
+
+
+def test_layer_k2_fused_repeat_and_force(k2_layer):
+    say("case: fused K2 decode: 4 tokens in one call, forced re-routing, 5 repeated launches")
+    layer = k2_layer
+    x = layer.tokens(4, stream_base=60)
+    ro, ri, _ = oracle_tokens(layer, x)
+    ctx = k3moe.Ctx(layer.dev, max_tokens=4)
+    for rep in range(5):
+        out, idx, _ = run_layer(layer, x, ctx=ctx, force=1 if rep == 2 else 0)
+        assert np.array_equal(idx, ri), rep
+        assert rel_l2(out, ro) <= REL_L2, rep
+    ctx.destroy()
 
 
 def test_layer_k2_batch(k2_layer):
