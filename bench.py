@@ -108,7 +108,8 @@ def main():
     import k3moe
 
     log(f"bench: building {a.layers} K2 layers (d={D}, E={E}, top-{K}, I={I}) in HBM")
-    layers = [k3moe.SynthLayer(k3moe.K2, seed=a.seed, layer=l) for l in range(a.layers)]
+    layers = [k3moe.SynthLayer(k3moe.K2, seed=a.seed, layer=l, layout="tiled")
+              for l in range(a.layers)]
     n_tok = a.warmup + a.steps
     xs = layers[0].tokens(n_tok, stream_base=900)
     ctx = k3moe.Ctx(layers[0].dev, max_tokens=1)

@@ -186,8 +186,13 @@ K3gExpertLayout k3g_expert_layout(int hidden, int inter);
  *                   pointers to MXFP4 matrices (entries of unrouted experts unused)
  *     expert_fmt 1: the fp32 resident bank w1/w3 [n_experts][inter][latent] and
  *                   w2 [n_experts][latent][inter] (the engine's fixture path)
+ *     expert_fmt 2: as 0, but p1/p3/p2 point at matrices in the tiled MXFP4 layout
+ *                   k3g_tile_mxfp4 writes (they carry their own scales; s1/s3/s2
+ *                   unused). The fused decode kernel streams this layout at full line
+ *                   granularity into the matrix cores; it serves up to 4 tokens a call.
  *   shared expert, tagged by wdt (K3_WF32 or K3_WBF16): sh1/sh3 [shared_inter][hidden],
- *     sh2 [hidden][shared_inter]; shared_inter == 0 means none
+ *     sh2 [hidden][shared_inter]; shared_inter == 0 means none. shared_fmt 0: row-major;
+ *     1: bf16 in the tiled layout k3g_tile_bf16 writes (goes with expert_fmt 2)
  *   latent projections, tagged by wdt: down [latent][hidden], up [hidden][latent];
  *     NULL for the Kimi-K2 shape (latent == hidden). latent_norm [latent] or NULL.
  *   act_b1/act_b2: SiTU caps; a value >= 2^64 means uncapped (SwiGLU). */
@@ -205,7 +210,23 @@ typedef struct {
     const void *sh1, *sh3, *sh2;
     const void *down, *up;
     const float *latent_norm;
+    int shared_fmt;
 } K3gLayer;
+
+enum { K3G_EXPERT_MXFP4 = 0, K3G_EXPERT_F32 = 1, K3G_EXPERT_MXFP4_TILED = 2 };
+
+/* Repack a device matrix from the checkpoint layout into the tiled layout the matrix
+ * cores stream (asynchronous on `stream`; dst must not overlap the source).
+ * MXFP4: rows % 16 == 0, cols % 32 == 0, packed [rows][cols/2] + scales [rows][cols/32]
+ * (group 32); the tiled matrix takes k3g_tiled_mxfp4_bytes (cols padded to a multiple of
+ * 512). bf16: rows % 16 == 0, cols % 32 == 0, [rows][cols] -> the same number of bytes.
+ * Sizes are 0 and the calls return -1 for other shapes. No reference counterpart: the
+ * engine reads the checkpoint layout in place. */
+size_t k3g_tiled_mxfp4_bytes(int rows, int cols);
+int  k3g_tile_mxfp4(void *dst, const void *packed, const void *scales, int rows, int cols,
+                    void *stream);
+size_t k3g_tiled_bf16_bytes(int rows, int cols);
+int  k3g_tile_bf16(void *dst, const void *src, int rows, int cols, void *stream);
 
 /* Create a context on `device` for layers of this shape (only the size fields of
  * `shape` are read) and up to max_tokens tokens per call. Allocates the whole workspace
@@ -231,9 +252,10 @@ int  k3g_ctx_stage_ms(K3gCtx *ctx, double *ms, int64_t *count, int n);
  * (default on); off forces the staged kernels. No reference counterpart. */
 void k3g_ctx_set_fused(K3gCtx *ctx, int on);
 
-/* Instrumentation: with a device buffer of 2 * (tickets) uint64, the fused kernel writes
- * each ticket's start and end wall-clock stamps (100 MHz counter). NULL turns it off.
- * No reference counterpart. */
+/* Instrumentation: with a device buffer of 2 * tickets + 2 uint64, the fused kernel writes
+ * each ticket's start and end wall-clock stamps (100 MHz counter), then the top-k ticket's
+ * stamps after its wait and after its selection. NULL turns it off. No reference
+ * counterpart. */
 void k3g_ctx_set_trace(K3gCtx *ctx, void *dev_buf);
 
 /* Force the router's exact re-routing path: 0 normal, 1 every token re-routes its

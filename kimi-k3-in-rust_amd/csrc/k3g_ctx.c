@@ -44,6 +44,22 @@ K3gExpertLayout k3g_expert_layout(int hidden, int inter)
     return l;
 }
 
+size_t k3g_tiled_mxfp4_bytes(int rows, int cols) { return k3k_tiled_mxfp4_bytes(rows, cols); }
+size_t k3g_tiled_bf16_bytes(int rows, int cols) { return k3k_tiled_bf16_bytes(rows, cols); }
+
+int k3g_tile_mxfp4(void *dst, const void *packed, const void *scales, int rows, int cols,
+                   void *stream)
+{
+    return k3k_tile_mxfp4((uint8_t *)dst, (const uint8_t *)packed, (const uint8_t *)scales,
+                          rows, cols, (hipStream_t)stream);
+}
+
+int k3g_tile_bf16(void *dst, const void *src, int rows, int cols, void *stream)
+{
+    return k3k_tile_bf16((uint16_t *)dst, (const uint16_t *)src, rows, cols,
+                         (hipStream_t)stream);
+}
+
 static size_t carve(size_t *at, size_t bytes)
 {
     const size_t o = *at;
@@ -80,8 +96,7 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t L = (size_t)c->latent, I = (size_t)c->inter, SI = (size_t)c->shared_inter;
     const size_t d = (size_t)c->hidden;
     size_t at = 0;
-    const size_t nrc = (d + 1023) / 1024;   /* router partial sums per token */
-    const size_t o_logit = carve(&at, nrc * T * E * 8), o_asum = carve(&at, nrc * T * E * 8);
+    const size_t o_rs = carve(&at, T * E * 16);
     const size_t o_idx = carve(&at, P * 4), o_wt = carve(&at, P * 4);
     const size_t o_cnt = carve(&at, nch * E * 4), o_base = carve(&at, nch * E * 4);
     const size_t o_off = carve(&at, (E + 1) * 4), o_act = carve(&at, E * 4);
@@ -90,7 +105,21 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t o_contrib = carve(&at, P * L * 4), o_accl = carve(&at, T * L * 4);
     const size_t o_shh = carve(&at, T * (SI ? SI : 1) * 4), o_sho = carve(&at, T * d * 4);
     const size_t o_err = carve(&at, 4), o_stats = carve(&at, 16 * 4);
-    const size_t o_sync = carve(&at, K3G_SYNC_WORDS * 4);
+    /* the fused decode kernel's buffers, for up to 4 tokens */
+    const int T4 = max_tokens < 4 ? max_tokens : 4;
+    const size_t P4 = (size_t)T4 * k;
+    const size_t nQd = (d + 511) / 512, nQi = (I + 511) / 512;
+    const size_t o_xq8 = carve(&at, (size_t)T4 * nQd * 8448), o_hq8 = carve(&at, P4 * nQi * 8448);
+    const size_t o_xq16 = carve(&at, (d / 32) * 1024), o_hq16 = carve(&at, (SI / 32 + 1) * 1024);
+    const size_t o_gpart = carve(&at, P4 * K3G_KS_G * 2 * I * 4);
+    const size_t o_sgpart = carve(&at, (size_t)K3G_KS_SG * T4 * 2 * (SI ? SI : 1) * 4);
+    const size_t o_shpart = carve(&at, (size_t)K3G_KS_SD * T4 * d * 4);
+    const size_t o_rpart = carve(&at, (size_t)T4 * E * K3G_KS_R * 16);
+    const size_t o_dcontrib = carve(&at, P4 * K3G_KS_D * d * 4);
+    /* two banks of counters, one per call in turn; each a multiple of 256 bytes */
+    c->sync_bytes = (k3k_decode_sync_bytes(T4, (int)d, (int)E, (int)k, (int)I, (int)SI) + 255) &
+                    ~(size_t)255;
+    const size_t o_sync = carve(&at, 2 * c->sync_bytes);
     c->ws_bytes = at;
     if (hipMalloc(&c->ws, at) != hipSuccess) {
         fprintf(stderr, "k3moe: cannot allocate %.2f GB of device workspace\n", at / 1e9);
@@ -99,8 +128,7 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
         return -1;
     }
     char *b = (char *)c->ws;
-    c->logit = (double *)(b + o_logit);
-    c->asum = (double *)(b + o_asum);
+    c->rs = (float *)(b + o_rs);
     c->idx = (int32_t *)(b + o_idx);
     c->wt = (float *)(b + o_wt);
     c->cnt = (int32_t *)(b + o_cnt);
@@ -117,6 +145,15 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->sh_out = (float *)(b + o_sho);
     c->err = (int *)(b + o_err);
     c->stats = (int *)(b + o_stats);
+    c->xq8 = (uint8_t *)(b + o_xq8);
+    c->hq8 = (uint8_t *)(b + o_hq8);
+    c->xq16 = (uint16_t *)(b + o_xq16);
+    c->hq16 = (uint16_t *)(b + o_hq16);
+    c->gpart = (float *)(b + o_gpart);
+    c->sgpart = (float *)(b + o_sgpart);
+    c->shpart = (float *)(b + o_shpart);
+    c->rpart = (double *)(b + o_rpart);
+    c->dcontrib = (float *)(b + o_dcontrib);
     c->sync = (int *)(b + o_sync);
     c->fused = 1;
     if (hipMemset(c->ws, 0, at) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
@@ -217,13 +254,16 @@ void k3g_ctx_set_fused(K3gCtx *c, int on) { if (c) c->fused = on; }
 
 void k3g_ctx_set_trace(K3gCtx *c, void *dev_buf) { if (c) c->trace = (unsigned long long *)dev_buf; }
 
-/* The fused kernel covers the Kimi-K2 layer shape at decode token counts. */
+/* The fused kernel covers the Kimi-K2 layer shape at decode token counts, with the
+ * routed experts and the shared expert in the tiled layouts. */
 static int fusable(const K3gCtx *c, const K3gLayer *L, int T)
 {
     const int lat = L->latent > 0 ? L->latent : L->hidden;
-    return c->fused && T <= 4 && L->expert_fmt == 0 && !L->down && !L->up &&
-           !L->latent_norm && lat == L->hidden && L->hidden % 32 == 0 && L->inter % 32 == 0 &&
-           (L->shared_inter == 0 || (L->wdt == K3_WBF16 && L->shared_inter % 16 == 0));
+    return c->fused && T <= 4 && L->expert_fmt == K3G_EXPERT_MXFP4_TILED && !L->down &&
+           !L->up && !L->latent_norm && lat == L->hidden && L->hidden % 32 == 0 &&
+           L->inter % 32 == 0 &&
+           (L->shared_inter == 0 || (L->wdt == K3_WBF16 && L->shared_fmt == 1 &&
+                                     L->shared_inter % 32 == 0));
 }
 
 void k3g_ctx_stats(K3gCtx *c, int64_t *out, int n)
@@ -259,8 +299,8 @@ int k3g_route(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx,
     if (!fits(c, L, T)) return -1;
     k3g_stage_begin(c, K3G_ST_ROUTER, st);
     const int rc = k3k_router(x, T, L->gate, L->bias, L->hidden, L->n_experts, L->topk,
-                              L->renorm, L->routed_scale, c->logit, c->asum, idx, wt,
-                              c->force_exact, c->stats, st);
+                              L->renorm, L->routed_scale, c->rs, idx, wt, c->force_exact,
+                              c->stats, st);
     k3g_stage_end(c, K3G_ST_ROUTER, st);
     return rc;
 }
@@ -283,6 +323,11 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     const int P = T * k;
     const int projected = L->down != NULL;
     int rc = 0;
+    if (L->expert_fmt == K3G_EXPERT_MXFP4_TILED || L->shared_fmt != 0) {
+        fprintf(stderr, "k3moe: tiled experts run on the fused decode kernel only (up to 4 "
+                        "tokens, no latent projection)\n");
+        return -1;
+    }
 
     k3g_stage_begin(c, K3G_ST_DISPATCH, st);
     rc |= k3k_dispatch(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm, c->err,
@@ -381,26 +426,29 @@ int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int
         a.out = out;
         a.idx = idx;
         a.wt = wt;
-        a.plogit = c->logit;
-        a.pasum = c->asum;
-        a.h = c->h;
-        a.sh_h = c->sh_h;
-        a.contrib = c->contrib;
-        a.sh_out = c->sh_out;
-        a.sync = c->sync;
+        a.rs = c->rs;
+        a.xq8 = c->xq8;
+        a.xq16 = c->xq16;
+        a.gpart = c->gpart;
+        a.hq8 = c->hq8;
+        a.sgpart = c->sgpart;
+        a.hq16 = c->hq16;
+        a.contrib = c->dcontrib;
+        a.shpart = c->shpart;
+        a.rpart = c->rpart;
+        const int words = (int)(c->sync_bytes / 4);
+        a.sync = c->sync + (size_t)(c->epoch & 1) * words;
+        a.sync_clear = c->sync + (size_t)((c->epoch & 1) ^ 1) * words;
+        a.sync_words = words;
         a.err = c->err;
         a.stats = c->stats;
         a.force = c->force_exact;
         a.spin_limit = 1ll << 21;
-        if (c->epoch >= K3G_EPOCH_MAX) {
-            if (hipMemsetAsync(c->sync, 0, K3G_SYNC_WORDS * 4, st) != hipSuccess) return -1;
-            c->epoch = 0;
-        }
-        a.epoch = ++c->epoch;
         a.trace = c->trace;
         k3g_stage_begin(c, K3G_ST_FUSED, st);
         const int rc = k3k_decode_fused(&a, st);
         k3g_stage_end(c, K3G_ST_FUSED, st);
+        if (rc == 0) c->epoch = (c->epoch + 1) & 0x3fffffff;   /* the next call's bank */
         return rc;
     }
     if (k3g_route(c, L, x, T, idx, wt, st) != 0) return -1;
@@ -419,7 +467,7 @@ int k3g_sync(K3gCtx *c, void *stream)
         int z = 0;
         hipMemcpy(c->err, &z, sizeof z, hipMemcpyHostToDevice);
         /* a call cut short leaves the fused kernel's counters short: start over */
-        hipMemset(c->sync, 0, K3G_SYNC_WORDS * 4);
+        hipMemset(c->sync, 0, 2 * c->sync_bytes);
         c->epoch = 0;
         return e;
     }

@@ -32,7 +32,7 @@ struct K3gCtx {
     /* one device allocation, carved below */
     void *ws;
     size_t ws_bytes;
-    double *logit, *asum;        /* [T][E] */
+    float *rs;                   /* [T][E][4] router score intervals */
     int32_t *idx;                /* [T][k] when the caller passes none */
     float *wt;
     int32_t *cnt, *base;         /* [nch][E] */
@@ -46,8 +46,14 @@ struct K3gCtx {
     float *sh_out;               /* [T][hidden] */
     int *err;                    /* device error word */
     int *stats;                  /* device counters */
-    int *sync;                   /* fused-kernel counters */
-    int epoch;                   /* fused-kernel calls since the counters were cleared */
+    /* fused decode kernel: activation pieces, partial sums, counters */
+    uint8_t *xq8, *hq8;
+    uint16_t *xq16, *hq16;
+    float *gpart, *sgpart, *shpart, *dcontrib;
+    double *rpart;
+    int *sync;
+    size_t sync_bytes;
+    int epoch;                   /* fused-kernel calls; its parity picks the counter bank */
     int fused;                   /* use the fused decode kernel when the layer allows */
     unsigned long long *trace;   /* optional per-ticket timestamps of the fused kernel */
     /* optional per-stage timing: a ring of event pairs around each stage of a call,

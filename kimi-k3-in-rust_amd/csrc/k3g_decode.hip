@@ -1,69 +1,143 @@
 /* k3g_decode.hip - the whole decode-sized MoE layer (Kimi-K2 shape: no latent, MXFP4
- * routed experts, bf16 shared expert) as ONE persistent kernel.
+ * routed experts, bf16 shared expert) as ONE persistent kernel on the matrix cores.
  *
- * Why one kernel. At one token the layer streams ~286 MB and does almost no arithmetic,
- * so it is a pure HBM-streaming problem, and a chain of separate kernels loses the
- * machine at every boundary: each launch ramps up, drains, and waits for its slowest
- * wave. Here the work is cut into tickets, ordered so that whatever a ticket depends on
- * has a smaller ticket, and wave w of a co-resident persistent grid of W waves takes
- * tickets w, w + W, w + 2W, ... in order (a shared ticket counter costs one contended
- * device atomic per ticket, which at ~10^4 tickets per call is the bottleneck itself):
+ * At one token the layer streams ~286 MB and does almost no arithmetic, so it is an
+ * HBM-streaming problem. Two things decide the speed: every wave must keep bytes in
+ * flight all the time, and no phase boundary may drain the machine. So:
  *
- *   R   router logits: (expert, 1024-column chunk) per ticket, fp64 partial sums
- *   S   the certified top-k for every token (one ticket); waits for all R
- *   SG  shared-expert gate/up, 4 row pairs per ticket, SwiGLU/SiTU epilogue
- *   G   routed gate/up of one (token, slot) pair, 8 row pairs per ticket; waits for
- *       the routing
- *   SD  shared-expert down, 8 output rows per ticket; waits for all SG
- *   D   routed down of one pair, 16 output rows per ticket; waits for that pair's G
- *   C   combine, 256 output rows per ticket: slots in the engine's order (float
- *       multiply, then add), then + shared; waits for every D and SD
+ * 1. The weights are consumed by MFMAs straight from the load registers. Routed experts
+ *    are in the tiled MXFP4 layout (k3g_tile.hip) and go to
+ *    v_mfma_scale_f32_16x16x128_f8f6f4 as FP4 A operands with their own E8M0 scales;
+ *    the shared expert is in the tiled bf16 layout and goes to v_mfma_f32_16x16x32_bf16.
+ *    The activations are the B operand, split into pieces so the products keep fp32
+ *    accuracy: for FP4 x FP8, v = sum of 6 E4M3 pieces, each with its own per-32-block
+ *    E8M0 scale (B columns 0..5); for bf16, v = sum of 3 bf16 pieces (columns 3t..3t+2 of
+ *    token t). A GEMV row is the sum of its piece columns. Products of an E2M1 and an
+ *    E4M3 (or two bf16) are exact in fp32, so the only error left is the pieces' residual
+ *    (below 2^-24 of the block maximum) and fp32 accumulation.
+ *    No weight is ever decoded by the vector ALUs.
  *
- * The shared expert does not depend on the routing, so it streams while the top-k is
- * being chosen, and the G tickets of slot 0 finish first, so its D tickets start while
- * later slots still stream their gate/up rows.
+ * 2. The work is cut into tickets, ordered so that whatever a ticket depends on has a
+ *    smaller ticket, and wave w of a co-resident persistent grid of W waves takes
+ *    tickets w, w + W, w + 2W, ... (a shared ticket counter would cost one contended
+ *    device atomic per ticket):
  *
- * Cross-wave data (partial logits, the routing, h, per-slot outputs) is written and read
- * at device coherence (sc1 stores and loads), and a producer waits for its stores to
- * complete before it bumps a counter, so no device-wide cache writeback or invalidate is
- * ever issued and the L2s keep streaming.
+ *      X   x -> FP8 pieces (per token, per 512 columns) and bf16 pieces
+ *      R   router logits of one expert row (all tokens), fp64 with an error bound
+ *      S   the certified top-k for every token (one ticket); waits for all R
+ *      SG  shared gate/up: 16 rows x a K slice; the last slice of a row tile (found
+ *          with a returning atomic) sums the slices in slice order, applies the
+ *          activation and writes the shared h as bf16 pieces
+ *      G   routed gate/up of one (token, slot) pair: 32 rows x a K slice of 512-column
+ *          quads; the last slice of a tile sums, activates and writes h's FP8 pieces
+ *      SD  shared down: 32 rows x a K slice, partial sums per slice
+ *      D   routed down of one pair: 32 output rows, all of K; waits for that pair's h
+ *      C   combine, 256 output rows: slots in the engine's order (float multiply,
+ *          then add), then + the shared output (its slices summed in slice order)
  *
- * Completion counters are spread over separate cache lines (sub-counters per ticket
- * class, summed by the waiter) and never reset: launch n waits for n times the per-call
- * count (the host passes n as the epoch and clears the counters when it wraps or after
- * a device error).
+ *    The shared expert needs no routing, so SG streams while the router and top-k run.
  *
- * Deadlock freedom: a ticket only waits on smaller tickets; the owner of a smaller ticket
- * reaches it after its own even smaller tickets, all waves are resident at once (the grid
- * is sized by the occupancy calculator), and every wait is bounded (an exhausted wait
- * raises K3G_ERR_WAIT and the wave moves on, so every wave reaches the exit).
+ * Cross-wave data (logits, routing, partial sums, pieces, per-slot outputs) is written
+ * and read at device coherence (sc1 stores and loads) and a producer waits for its stores
+ * to complete before it bumps a counter, so no device-wide cache writeback or invalidate
+ * is ever issued. Completion counters sit on separate 128-byte lines. They come in two
+ * banks that calls alternate between: a call counts from zero in its bank and, at its
+ * start, zeroes the other bank (which the previous call used and, the launches being
+ * ordered on the stream, has finished with) for the next call. So the per-call counts
+ * may change from call to call (a different token count or layer).
+ *
+ * Deadlock freedom: a ticket only waits on smaller tickets, all waves are resident at
+ * once (the grid is sized by the occupancy calculator), and every wait is bounded (an
+ * exhausted wait raises K3G_ERR_WAIT and the wave moves on, so every wave reaches the
+ * exit).
  */
 #include "k3g_dev.h"
 #include "k3g_kernels.h"
 #include "k3g_select.h"
 
-/* counter layout: every counter on its own 128-byte line (32 ints) */
-#define SY_LINE 32
-#define NSUB 16           /* sub-counters per ticket class */
-enum { SY_R = 0, SY_SEL = SY_R + NSUB, SY_SG = SY_SEL + 1, SY_SD = SY_SG + NSUB,
-       SY_G = SY_SD + NSUB, SY_D = SY_G + 256, SY_NLINES = SY_D + 256 };
+#include <stdlib.h>
 
-#define R_CHUNK 1024      /* router columns per ticket: 64 lanes x 16 */
-#define SG_PAIRS 4        /* shared gate/up row pairs per ticket */
-#define G_PAIRS 8         /* routed gate/up row pairs per ticket */
-#define SD_ROWS 8         /* shared down rows per ticket */
-#define D_ROWS 16         /* routed down rows per ticket */
+typedef int k3v8i __attribute__((ext_vector_type(8)));
+typedef float k3v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 k3v8bf __attribute__((ext_vector_type(8)));
+typedef unsigned int k3v4u __attribute__((ext_vector_type(4)));
+
+#define K3G_QT 4352       /* MXFP4 quad tile: 4 x 1 KB chunks + 256 B of scales */
+#define K3G_BQ 8448       /* FP8 B quad: 4 x 2 KB chunks + 256 B of scales */
+#define NPC8 6            /* FP8 pieces per value */
+#define NPC16 3           /* bf16 pieces per value */
 #define C_ROWS 256        /* combine rows per ticket: 64 lanes x 4 */
+
+#define SY_LINE 32        /* ints per counter line (128 bytes) */
+#define NSUB 16           /* sub-counters per ticket class with many signalers */
+/* An event that thousands of waves wait for is published as NREP flag copies, 512 bytes
+ * apart, and each waiter polls the copy its ticket number picks: one hot line polled by
+ * every waiting wave would serialise at one memory channel and slow every other access
+ * to it. */
+#define NREP 16
+#define REP_STRIDE 4      /* lines between copies */
+#define K3_EVLINES (NREP * REP_STRIDE)
+
+/* ------------------------------------------------------------ geometry ---- */
+struct K3Geo {
+    int T, P, nQd, nCd, nQi, nCsi;
+    int KSS, KSG, KSD, KSR, KSDN; /* K slices of SG, G, SD, R, D tickets */
+    int nRc;                     /* router 1024-column chunks */
+    int nSGt, nGt, nSDt, nDt;    /* row tiles */
+    int nX, nR, nSG, nG, nSD, nD, nC, total;
+    /* counter lines */
+    int lR, lSD, lD, lTSG, lTG, lRE, cX, cSGF, cGF, eX, eSEL, eSGF, eGF, nlines;
+};
+
+__host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int SI)
+{
+    K3Geo g;
+    g.T = T;
+    g.P = T * k;
+    g.nQd = (d + 511) / 512;
+    g.nCd = d / 32;
+    g.nQi = (I + 511) / 512;
+    g.nCsi = SI / 32;
+    g.KSS = SI > 0 ? (K3G_KS_SG < g.nCd ? K3G_KS_SG : g.nCd) : 0;
+    g.KSG = K3G_KS_G < g.nQd ? K3G_KS_G : g.nQd;
+    g.KSD = SI > 0 ? (K3G_KS_SD < g.nCsi ? K3G_KS_SD : g.nCsi) : 0;
+    g.nRc = (d + 1023) / 1024;
+    g.KSR = K3G_KS_R < g.nRc ? K3G_KS_R : g.nRc;
+    g.KSDN = K3G_KS_D < g.nQi ? K3G_KS_D : g.nQi;
+    g.nSGt = SI / 16;
+    g.nGt = I / 32;
+    g.nSDt = SI > 0 ? d / 32 : 0;
+    g.nDt = d / 32;
+    g.nX = T * ((g.nCd + 1) / 2);
+    g.nR = E * g.KSR;
+    g.nSG = g.nSGt * g.KSS;
+    g.nG = g.P * g.nGt * g.KSG;
+    g.nSD = g.nSDt * g.KSD;
+    g.nD = g.P * g.nDt * g.KSDN;
+    g.nC = (d + C_ROWS - 1) / C_ROWS;
+    g.total = g.nX + g.nR + 1 + g.nSG + g.nG + g.nSD + g.nD + g.nC;
+    /* counters: one 128-byte line each; events: a counter plus NREP replicated flags */
+    g.lR = 0;
+    g.lSD = g.lR + NSUB;
+    g.lD = g.lSD + NSUB;
+    g.lTSG = g.lD + g.P;
+    g.lTG = g.lTSG + g.nSGt;
+    g.lRE = g.lTG + g.P * g.nGt;
+    g.cX = g.lRE + E;
+    g.cSGF = g.cX + 1;
+    g.cGF = g.cSGF + 1;
+    g.eX = g.cGF + g.P;
+    g.eSEL = g.eX + K3_EVLINES;
+    g.eSGF = g.eSEL + K3_EVLINES;
+    g.eGF = g.eSGF + K3_EVLINES;
+    g.nlines = g.eGF + g.P * K3_EVLINES;
+    return g;
+}
 
 /* ------------------------------------------------------------ coherence ---- */
 __device__ __forceinline__ int k3d_ld_relaxed(const int *p)
 {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void k3d_st_dev(float *p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ int *k3d_line(int *sync, int i) { return sync + (size_t)i * SY_LINE; }
@@ -75,6 +149,20 @@ __device__ __forceinline__ void k3d_signal(int *ctr, int lane)
     asm volatile("" ::: "memory");
     if (lane == 0)
         __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* All of this wave's memory operations complete, then it arrives at a tile counter;
+ * true (in every lane) for the arrival that completes the tile in this call. */
+__device__ __forceinline__ bool k3d_arrive(int *ctr, int last_old, int lane)
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
+    int old = 0;
+    if (lane == 0)
+        old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    asm volatile("" ::: "memory");
+    return old == last_old;
 }
 
 /* Wait until the counters line(first) .. line(first + n - 1) sum to at least target.
@@ -98,11 +186,46 @@ __device__ __forceinline__ bool k3d_wait_sum(int *sync, int first, int n, long l
     return true;
 }
 
-/* ----------------------------------------------------------- buffer loads ---- */
-/* Every weight row is read through a raw buffer descriptor: the matrix base lives in
- * scalar registers, each row is a scalar offset, and only the lane's column offset is a
- * vector register, so a tile of 16 rows costs 16 scalar offsets instead of 16 vector
- * pointer pairs. Out-of-range offsets read zero (the descriptor's byte bound). */
+/* Wait until the event's flag copy picked by `who` is set. Bounded like k3d_wait_sum. */
+__device__ __forceinline__ bool k3d_wait_event(int *sync, int ev, int who, long long limit,
+                                               int *err, int lane)
+{
+    const int *f = k3d_line(sync, ev + (who % NREP) * REP_STRIDE);
+    long long spins = 0;
+    for (;;) {
+        int v = lane == 0 ? k3d_ld_relaxed(f) : 0;
+        if (__builtin_amdgcn_readfirstlane(v)) break;
+        __builtin_amdgcn_s_sleep(8);
+        if (++spins > limit) {
+            k3d_raise(err, K3G_ERR_WAIT);
+            return false;
+        }
+    }
+    asm volatile("" ::: "memory");
+    return true;
+}
+
+/* Set every flag copy of an event (after this wave's stores completed). */
+__device__ __forceinline__ void k3d_set_event(int *sync, int ev, int lane)
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("" ::: "memory");
+    if (lane < NREP)
+        __hip_atomic_store(k3d_line(sync, ev + lane * REP_STRIDE), 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+/* Arrive at an event's counter; the arrival that completes the count sets the event. */
+__device__ __forceinline__ void k3d_arrive_event(int *sync, int ctr, int count, int ev, int lane)
+{
+    if (k3d_arrive(k3d_line(sync, ctr), count - 1, lane)) k3d_set_event(sync, ev, lane);
+}
+
+/* ----------------------------------------------------------- buffer access ---- */
+/* Weights and pieces are read through raw buffer descriptors: the base lives in scalar
+ * registers and each lane adds its own byte offset. An offset at or past the
+ * descriptor's size reads zero without touching memory, which is how unused B columns
+ * are skipped. */
 typedef __amdgpu_buffer_rsrc_t K3Rsrc;
 
 __device__ __forceinline__ K3Rsrc k3d_rsrc(const void *p, size_t bytes)
@@ -112,63 +235,48 @@ __device__ __forceinline__ K3Rsrc k3d_rsrc(const void *p, size_t bytes)
                                              0x00020000);
 }
 
-#define K3_SC1 16   /* cache policy: device-coherent load */
+#define K3_SC1 16   /* cache policy: device-coherent access */
+/* Cache policy of the loads of activation pieces and per-slot outputs (xq8, xq16, hq8,
+ * hq16, contrib, shpart): ordinary cached loads. Each of those lines is written once per
+ * launch and read only after the counter that covers all of its writers has moved, and
+ * every launch starts with the L2s invalidated, so no XCD can hold a stale copy; cached
+ * loads keep these small, hot arrays in each XCD's L2 instead of going to memory for
+ * every read. (sgpart lines span two row tiles that finish at different times, and the
+ * router scores are read once; those stay device-coherent.) */
+#define K3_BPOL 0
+#define K3_OOB 0x7ffffff0
 
 template <int AUX = 0>
-__device__ __forceinline__ uint4 k3d_b128(K3Rsrc r, int voff, int soff)
+__device__ __forceinline__ uint4 k3d_b128(K3Rsrc r, int voff)
 {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX));
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, AUX));
 }
 
-__device__ __forceinline__ uint32_t k3d_b8(K3Rsrc r, int voff, int soff)
-{
-    return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
-}
-
-/* n4 float4 (16-byte) loads at byte offset voff + soff */
 template <int AUX = 0>
-__device__ __forceinline__ void k3d_bx(K3Rsrc r, int voff, int soff, float *x, int n4)
+__device__ __forceinline__ uint32_t k3d_b32(K3Rsrc r, int voff)
 {
-    for (int i = 0; i < n4; ++i) {
-        const uint4 v = k3d_b128<AUX>(r, voff + 16 * i, soff);
-        x[4 * i] = __uint_as_float(v.x); x[4 * i + 1] = __uint_as_float(v.y);
-        x[4 * i + 2] = __uint_as_float(v.z); x[4 * i + 3] = __uint_as_float(v.w);
-    }
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, AUX);
 }
 
-/* acc + the 32 products of one MXFP4 group (16 bytes, scale byte s), decoding one
- * 8-element word at a time */
-__device__ __forceinline__ float k3d_dot32(uint4 q, uint32_t s, const float *x, float acc)
+__device__ __forceinline__ float k3d_f32_sc1(K3Rsrc r, int voff)
 {
-    const float sc = k3d_e8m0(s);
-    const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-        float w[8];
-        k3d_fp4x8(wd[h], sc, w);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(w[i], x[8 * h + i], acc);
-    }
-    return acc;
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, K3_SC1));
 }
 
-/* 16 bf16 weights (32 bytes) dotted with 16 x values */
-__device__ __forceinline__ float k3d_dot16bf(const uint4 &a, const uint4 &b, const float *x,
-                                             float s)
+__device__ __forceinline__ void k3d_st4_sc1(K3Rsrc r, int voff, k3v4f v)
 {
-    const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        s = fmaf(k3d_bf16lo(wd[i]), x[2 * i], s);
-        s = fmaf(k3d_bf16hi(wd[i]), x[2 * i + 1], s);
-    }
-    return s;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(k3v4u, v), r, voff, 0, K3_SC1);
 }
 
-template <int V>
-struct K3L2 { static constexpr int v = 1 + K3L2<V / 2>::v; };
-template <>
-struct K3L2<1> { static constexpr int v = 0; };
+__device__ __forceinline__ void k3d_st8_sc1(K3Rsrc r, int voff, uint32_t v)
+{
+    __builtin_amdgcn_raw_buffer_store_b8((uint8_t)v, r, voff, 0, K3_SC1);
+}
+
+__device__ __forceinline__ void k3d_st16_sc1(K3Rsrc r, int voff, uint32_t v)
+{
+    __builtin_amdgcn_raw_buffer_store_b16((uint16_t)v, r, voff, 0, K3_SC1);
+}
 
 __device__ __forceinline__ int k3d_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -183,268 +291,556 @@ __device__ __forceinline__ P *k3d_uniform_ptr(P *p)
     return (P *)(((uint64_t)hi << 32) | lo);
 }
 
-__device__ __forceinline__ K3ExpertQ k3d_expert(const K3ExpertQ *eq, int e)
+/* ----------------------------------------------------------- MFMA helpers ---- */
+__device__ __forceinline__ k3v8i k3d_a4(uint4 a) { return k3v8i{(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0}; }
+
+__device__ __forceinline__ k3v8i k3d_b8(uint4 lo, uint4 hi)
 {
-    const K3ExpertQ q = eq[e];
-    K3ExpertQ u;
-    u.p1 = k3d_uniform_ptr(q.p1); u.s1 = k3d_uniform_ptr(q.s1);
-    u.p3 = k3d_uniform_ptr(q.p3); u.s3 = k3d_uniform_ptr(q.s3);
-    u.p2 = k3d_uniform_ptr(q.p2); u.s2 = k3d_uniform_ptr(q.s2);
-    return u;
+    return k3v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+}
+
+/* acc += A(FP4, scale byte J of sa) x B(FP8, scale byte J of sb) */
+template <int J>
+__device__ __forceinline__ k3v4f k3d_mma4(uint4 a, k3v8i b, k3v4f acc, uint32_t sa, uint32_t sb)
+{
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k3d_a4(a), b, acc, 4, 0, J, (int)sa,
+                                                            J, (int)sb);
+}
+
+__device__ __forceinline__ k3v4f k3d_mma16(uint4 a, uint4 b, k3v4f acc)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(k3v8bf, a),
+                                                   __builtin_bit_cast(k3v8bf, b), acc, 0, 0, 0);
+}
+
+/* Sum of the 16 columns of a 16x16 accumulator: afterwards the lanes of column 0
+ * (lane & 15 == 0) hold, in register i, row 4 (lane >> 4) + i. */
+__device__ __forceinline__ k3v4f k3d_colsum(k3v4f v)
+{
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+        v[0] += __shfl_xor(v[0], m, K3G_WAVE);
+        v[1] += __shfl_xor(v[1], m, K3G_WAVE);
+        v[2] += __shfl_xor(v[2], m, K3G_WAVE);
+        v[3] += __shfl_xor(v[3], m, K3G_WAVE);
+    }
+    return v;
+}
+
+/* Token t = lane & 15's sum of columns 3t, 3t+1, 3t+2 (lanes with t >= T get junk). */
+__device__ __forceinline__ k3v4f k3d_colsum3(k3v4f v, int lane)
+{
+    const int base = (lane & 48) + 3 * (lane & 15);
+    k3v4f r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = __shfl(v[i], base & 63, K3G_WAVE);
+        const float b = __shfl(v[i], (base + 1) & 63, K3G_WAVE);
+        const float c = __shfl(v[i], (base + 2) & 63, K3G_WAVE);
+        r[i] = (a + b) + c;
+    }
+    return r;
+}
+
+/* E8M0 exponent s such that max / 2^s <= 448 (the largest E4M3 value), for max > 0. */
+__device__ __forceinline__ int k3d_fp8_scale(float m)
+{
+    if (!(m > 0.0f)) return -127;
+    int e;
+    const float f = frexpf(m, &e);        /* m = f 2^e, f in [0.5, 1) */
+    int s = f <= 0.875f ? e - 9 : e - 8;  /* 448 = 0.875 * 2^9 */
+    return s < -127 ? -127 : (s > 127 ? 127 : s);
+}
+
+/* One FP8 piece of r (a block of 32 lanes shares the scale): returns the E4M3 byte,
+ * sets *sx to the block's scale exponent and removes the piece from r (exactly). */
+__device__ __forceinline__ uint32_t k3d_fp8_piece(float &r, int &sx)
+{
+    float m = fabsf(r);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, K3G_WAVE));
+    sx = k3d_fp8_scale(m);
+    const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(r, -sx), 0.0f, 0, false);
+    r = r - ldexpf(__builtin_amdgcn_cvt_f32_fp8(pk, 0), sx);
+    return (uint32_t)pk & 0xffu;
+}
+
+/* bf16 nearest-even of v (finite v) as bits, and its value */
+__device__ __forceinline__ uint32_t k3d_bf16_rn(float v, float &back)
+{
+    uint32_t u = __float_as_uint(v);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    back = __uint_as_float(u);
+    return u >> 16;
+}
+
+/* Byte offset inside an FP8 B quad of element e (0..31) of MX block b (of the whole
+ * vector) for piece column pc, and of that block's scale byte. The B operand pairs with
+ * the tiled A layout: chunk j = (b % 16) / 4 holds blocks 16Q + 4j + g in lane group g,
+ * and the MFMA pairs A group g's nibbles 0-15 / 16-31 with B lanes 16 (2 (g & 1)) + c /
+ * 16 (2 (g & 1) + 1) + c, bytes 16 (g >> 1) .. + 16 of column c. */
+__device__ __forceinline__ int k3d_bq_data(int b, int e, int pc)
+{
+    const int j = (b & 15) >> 2, g = b & 3;
+    const int M = 16 * (2 * (g & 1) + (e >> 4)) + pc;
+    return j * 2048 + M * 32 + 16 * (g >> 1) + (e & 15);
+}
+
+__device__ __forceinline__ int k3d_bq_scale(int b, int pc)
+{
+    const int j = (b & 15) >> 2, g = b & 3;
+    return 8192 + (16 * g + pc) * 4 + j;
+}
+
+/* Byte offset in a bf16 B array (chunks of 32 values, 1 KB each) of value k, column col */
+__device__ __forceinline__ int k3d_b16_off(int k, int col)
+{
+    return (k >> 5) * 1024 + (16 * ((k & 31) >> 3) + col) * 16 + 2 * (k & 7);
+}
+
+/* The kernel's arguments, addressed in the constant address space: a phase function
+ * moves the pointer to scalar registers and every field it reads comes back in scalar
+ * registers (scalar loads), so buffer descriptors and loop bounds never become per-lane
+ * values (which would turn each buffer load into a loop over lanes). */
+#ifdef __HIP_DEVICE_COMPILE__
+typedef const __attribute__((address_space(4))) K3kDecode *K3ArgPtr;
+#else
+typedef const K3kDecode *K3ArgPtr;   /* the host pass only parses the device code */
+#endif
+
+__device__ __forceinline__ K3ArgPtr k3d_uniform_cptr(K3ArgPtr p)
+{
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (K3ArgPtr)(((uint64_t)hi << 32) | lo);
 }
 
 template <int NT>
 struct K3Dec {
-    /* ----------------------------------------------------------------- R ---- */
-    static __device__ void router(const K3kDecode &a, int tk, int lane)
+    /* ----------------------------------------------------------------- X ---- */
+    static __device__ __noinline__ void prep(K3ArgPtr ap, int tk_, int lane)
     {
-        const int nch = (a.d + R_CHUNK - 1) / R_CHUNK;
-        const int e = tk / nch, c = tk - e * nch;
-        const int col = c * R_CHUNK + lane * 16;
-        const K3Rsrc rg = k3d_rsrc(a.gate, (size_t)a.E * a.d * 4);
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const int npair = (G.nCd + 1) / 2;
+        const int t = tk / npair, i = tk - t * npair;
+        const K3Rsrc r8 = k3d_rsrc(a.xq8 + (size_t)t * G.nQd * K3G_BQ, (size_t)G.nQd * K3G_BQ);
+        const K3Rsrc r16 = k3d_rsrc(a.xq16, (size_t)G.nCd * 1024);
+        /* lanes 0-31: block 2i, lanes 32-63: block 2i + 1 (absent when nCd is odd) */
+        const int b = 2 * i + (lane >> 5), e = lane & 31;
+        const int col = 32 * b + e;
+        const bool on = col < a.d;
+        const float v = on ? a.x[(size_t)t * a.d + col] : 0.0f;
+        const int Q = b >> 4;
+        float r = v;
+#pragma unroll
+        for (int pc = 0; pc < NPC8; ++pc) {
+            int sx;
+            const uint32_t q = k3d_fp8_piece(r, sx);
+            if (on) {
+                k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_data(b, e, pc), q);
+                if (e == 0) k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_scale(b, pc), sx + 127);
+            }
+        }
+        float r2 = v;
+#pragma unroll
+        for (int pc = 0; pc < NPC16; ++pc) {
+            float back;
+            const uint32_t h = k3d_bf16_rn(r2, back);
+            r2 -= back;
+            if (on) k3d_st16_sc1(r16, k3d_b16_off(col, NPC16 * t + pc), h);
+        }
+        k3d_arrive_event(a.sync, G.cX, G.nX, G.eX, lane);
+    }
+
+    /* ----------------------------------------------------------------- R ---- */
+    static __device__ __noinline__ void router(K3ArgPtr ap, int tk_, int lane)
+    {
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const int e = tk / G.KSR, r = tk - e * G.KSR;
+        const int ch0 = r * G.nRc / G.KSR, ch1 = (r + 1) * G.nRc / G.KSR;
+        const K3Rsrc rg = k3d_rsrc(a.gate + (size_t)e * a.d, (size_t)a.d * 4);
         const K3Rsrc rx = k3d_rsrc(a.x, (size_t)a.T * a.d * 4);
         double acc[NT], ab[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) { acc[t] = 0.0; ab[t] = 0.0; }
-        float w[16];
-        k3d_bx(rg, col * 4, e * a.d * 4, w, 4);
-        const bool on = col < a.d;     /* lanes past the row end read the next row */
+        for (int cb = ch0; cb < ch1; cb += 2) {
+            /* two 1024-column chunks per batch; columns past the slice or the row read
+             * zero */
+            uint4 W[8];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (t < a.T && on) {
-                float xv[16];
-                k3d_bx(rx, col * 4, t * a.d * 4, xv, 4);
+            for (int h = 0; h < 2; ++h) {
+                const int col = (cb + h) * 1024 + lane * 16;
+                const bool on = cb + h < ch1 && col < a.d;
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    acc[t] = fma((double)w[i], (double)xv[i], acc[t]);
-                    ab[t] = fma(fabs((double)w[i]), fabs((double)xv[i]), ab[t]);
+                for (int i = 0; i < 4; ++i) W[4 * h + i] = k3d_b128(rg, on ? col * 4 + 16 * i : K3_OOB);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (t < a.T) {
+                    uint4 X[8];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int col = (cb + h) * 1024 + lane * 16;
+                        const bool on = cb + h < ch1 && col < a.d;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            X[4 * h + i] = k3d_b128(rx, on ? (t * a.d + col) * 4 + 16 * i : K3_OOB);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float w4[4] = {__uint_as_float(W[i].x), __uint_as_float(W[i].y),
+                                             __uint_as_float(W[i].z), __uint_as_float(W[i].w)};
+                        const float x4[4] = {__uint_as_float(X[i].x), __uint_as_float(X[i].y),
+                                             __uint_as_float(X[i].z), __uint_as_float(X[i].w)};
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            acc[t] = fma((double)w4[q], (double)x4[q], acc[t]);
+                            ab[t] = fma(fabs((double)w4[q]), fabs((double)x4[q]), ab[t]);
+                        }
+                    }
                 }
             }
         }
+        /* the slice's partial sums, [t][e][slice] {sum, sum|w x|} */
+        const K3Rsrc rp = k3d_rsrc(a.rpart, (size_t)a.T * a.E * G.KSR * 16);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const double s = k3d_wave_sumd(acc[t]);
-            const double b = k3d_wave_sumd(ab[t]);
-            if (lane == 0 && t < a.T) {
-                k3d_st_dev64(&a.plogit[((size_t)c * a.T + t) * a.E + e], s);
-                k3d_st_dev64(&a.pasum[((size_t)c * a.T + t) * a.E + e], b);
-            }
+            const double sv = k3d_wave_sumd(acc[t]);
+            const double bv = k3d_wave_sumd(ab[t]);
+            if (lane == 0 && t < a.T)
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(k3v4u, make_double2(sv, bv)), rp,
+                    ((t * a.E + e) * G.KSR + r) * 16, 0, K3_SC1);
         }
-        k3d_signal(k3d_line(a.sync, SY_R + tk % NSUB), lane);
+        if (!k3d_arrive(k3d_line(a.sync, G.lRE + e), G.KSR - 1, lane)) return;
+        /* the last slice of the row: the slices summed in slice order, then the score
+         * interval (any summation order is inside the interval's bound) */
+        if (lane < a.T) {
+            double sv = 0.0, bv = 0.0;
+            for (int q = 0; q < G.KSR; ++q) {
+                const double2 v = __builtin_bit_cast(
+                    double2, __builtin_amdgcn_raw_buffer_load_b128(rp, ((lane * a.E + e) * G.KSR + q) * 16,
+                                                                   0, K3_SC1));
+                sv += v.x;
+                bv += v.y;
+            }
+            const K3Rsrc rr = k3d_rsrc(a.rs, (size_t)a.T * a.E * 16);
+            const float4 v = k3d_route_score(sv, bv, a.bias ? a.bias[e] : 0.0f, a.d);
+            k3d_st4_sc1(rr, (lane * a.E + e) * 16, k3v4f{v.x, v.y, v.z, v.w});
+        }
+        k3d_signal(k3d_line(a.sync, G.lR + e % NSUB), lane);
     }
 
     /* ----------------------------------------------------------------- S ---- */
-    static __device__ void select(const K3kDecode &a, int lane, K3SelectLds *lds, int nR)
+    static __device__ __noinline__ void select(K3ArgPtr ap, int lane, K3SelectLds *lds)
     {
-        const int nch = (a.d + R_CHUNK - 1) / R_CHUNK;
-        if (!k3d_wait_sum(a.sync, SY_R, NSUB, (long long)a.epoch * nR, a.spin_limit, a.err,
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        if (!k3d_wait_sum(a.sync, G.lR, NSUB, a.E, a.spin_limit, a.err,
                           lane))
             return;
+        /* instrumentation: after the trace's [ticket][2] stamps, the select's own phases */
+        if (a.trace && lane == 0) a.trace[2 * G.total] = wall_clock64();
+        /* everything routed waits for this wave: let it issue ahead of its SIMD's others */
+        __builtin_amdgcn_s_setprio(3);
         for (int t = 0; t < a.T; ++t)
-            k3d_select_token(lds, t, a.T, nch, a.plogit, a.pasum, a.bias, a.gate, a.x, a.d,
-                             a.E, a.k, a.renorm, a.routed_scale, a.idx, a.wt, a.force,
-                             a.stats, lane);
-        __builtin_amdgcn_s_waitcnt(0);
-        asm volatile("" ::: "memory");
-        if (lane == 0)
-            __hip_atomic_store(k3d_line(a.sync, SY_SEL), a.epoch, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            k3d_select_token(lds, t, (const float4 *)a.rs, a.bias, a.gate, a.x, a.d, a.E, a.k,
+                             a.renorm, a.routed_scale, a.idx, a.wt, a.force, a.stats, lane,
+                             a.trace && t == 0 ? a.trace + 2 * G.total + 2 : nullptr);
+        if (a.trace && lane == 0) a.trace[2 * G.total + 1] = wall_clock64();
+        /* the routed tickets also need x's pieces: publish the routing once both exist */
+        if (!k3d_wait_event(a.sync, G.eX, 0, a.spin_limit, a.err, lane)) return;
+        k3d_set_event(a.sync, G.eSEL, lane);
+        __builtin_amdgcn_s_setprio(0);
     }
 
     /* ---------------------------------------------------------------- SG ---- */
-    static __device__ void shared_gateup(const K3kDecode &a, int tk, int lane)
+    static __device__ __noinline__ void shared_gateup(K3ArgPtr ap, int tk_, int lane)
     {
-        const int r0 = tk * SG_PAIRS;
-        constexpr int V = 2 * SG_PAIRS * NT;
-        constexpr int SH = 6 - K3L2<V>::v;
-        const K3Rsrc r1 = k3d_rsrc(a.sh1, (size_t)a.SI * a.d * 2);
-        const K3Rsrc r3 = k3d_rsrc(a.sh3, (size_t)a.SI * a.d * 2);
-        const K3Rsrc rx = k3d_rsrc(a.x, (size_t)a.T * a.d * 4);
-        const int rowb = a.d * 2;
-        float acc[V];
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const int st = tk / G.KSS, ks = tk - st * G.KSS;
+        const int c0 = ks * G.nCd / G.KSS, c1 = (ks + 1) * G.nCd / G.KSS;
+        if (!k3d_wait_event(a.sync, G.eX, tk, a.spin_limit, a.err, lane)) return;
+        const size_t mb = (size_t)a.SI * a.d * 2;
+        const K3Rsrc r1 = k3d_rsrc(a.sh1, mb), r3 = k3d_rsrc(a.sh3, mb);
+        const K3Rsrc rb = k3d_rsrc(a.xq16, (size_t)G.nCd * 1024);
+        const bool bon = (lane & 15) < NPC16 * a.T;
+        k3v4f g = {0, 0, 0, 0}, u = {0, 0, 0, 0};
+        const int abase = st * G.nCd * 1024 + lane * 16;
+        for (int cb = c0; cb < c1; cb += 8) {
+            uint4 A1[8], A3[8], B[8];
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-        for (int cb = 0; cb < a.d; cb += 1024) {
-            const int col = cb + lane * 16;
-            uint4 q[2 * SG_PAIRS][2];
-#pragma unroll
-            for (int r = 0; r < SG_PAIRS; ++r) {
-                q[r][0] = k3d_b128(r1, col * 2, (r0 + r) * rowb);
-                q[r][1] = k3d_b128(r1, col * 2 + 16, (r0 + r) * rowb);
-                q[SG_PAIRS + r][0] = k3d_b128(r3, col * 2, (r0 + r) * rowb);
-                q[SG_PAIRS + r][1] = k3d_b128(r3, col * 2 + 16, (r0 + r) * rowb);
+            for (int i = 0; i < 8; ++i) {
+                const int c = cb + i;
+                A1[i] = k3d_b128(r1, c < c1 ? abase + c * 1024 : K3_OOB);
+                A3[i] = k3d_b128(r3, c < c1 ? abase + c * 1024 : K3_OOB);
+                B[i] = k3d_b128<K3_BPOL>(rb, bon && c < c1 ? c * 1024 + lane * 16 : K3_OOB);
             }
-            if (col >= a.d) continue;   /* lanes past the row end read the next row */
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                float xv[16];
-                k3d_bx(rx, col * 4, (t < a.T ? t : 0) * a.d * 4, xv, 4);
-#pragma unroll
-                for (int r = 0; r < 2 * SG_PAIRS; ++r)
-                    acc[r * NT + t] = k3d_dot16bf(q[r][0], q[r][1], xv, acc[r * NT + t]);
+            for (int i = 0; i < 8; ++i) {
+                g = k3d_mma16(A1[i], B[i], g);
+                u = k3d_mma16(A3[i], B[i], u);
             }
         }
-        k3d_transpose_reduce<V>(acc, lane);
-        const float upv = __shfl_xor(acc[0], 32, K3G_WAVE);
-        const int v = lane >> SH;
-        if ((lane & ((1 << SH) - 1)) == 0 && v < SG_PAIRS * NT) {
-            const int r = v / NT, t = v % NT;
-            if (r0 + r < a.SI && t < a.T)
-                k3d_st_dev(&a.sh_h[(size_t)t * a.SI + r0 + r], k3d_act(acc[0], upv, a.b1, a.b2));
+        g = k3d_colsum3(g, lane);
+        u = k3d_colsum3(u, lane);
+        const int t = lane & 15;
+        const K3Rsrc rp = k3d_rsrc(a.sgpart, (size_t)G.KSS * a.T * 2 * a.SI * 4);
+        if (t < a.T) {
+            const int row = 16 * st + 4 * (lane >> 4);
+            k3d_st4_sc1(rp, (((ks * a.T + t) * 2 + 0) * a.SI + row) * 4, g);
+            k3d_st4_sc1(rp, (((ks * a.T + t) * 2 + 1) * a.SI + row) * 4, u);
         }
-        k3d_signal(k3d_line(a.sync, SY_SG + tk % NSUB), lane);
+        if (!k3d_arrive(k3d_line(a.sync, G.lTSG + st), G.KSS - 1, lane)) return;
+        /* last slice of the tile: h = act(gate, up) for 16 rows x T tokens -> bf16 pieces */
+        const int tt = lane >> 4, row = 16 * st + (lane & 15);
+        if (tt < a.T) {
+            float gs = 0.0f, us = 0.0f;
+            for (int q = 0; q < G.KSS; ++q) {
+                gs += k3d_f32_sc1(rp, (((q * a.T + tt) * 2 + 0) * a.SI + row) * 4);
+                us += k3d_f32_sc1(rp, (((q * a.T + tt) * 2 + 1) * a.SI + row) * 4);
+            }
+            float r2 = k3d_act(gs, us, a.b1, a.b2);
+            const K3Rsrc rh = k3d_rsrc(a.hq16, (size_t)G.nCsi * 1024);
+#pragma unroll
+            for (int pc = 0; pc < NPC16; ++pc) {
+                float back;
+                const uint32_t h = k3d_bf16_rn(r2, back);
+                r2 -= back;
+                k3d_st16_sc1(rh, k3d_b16_off(row, NPC16 * tt + pc), h);
+            }
+        }
+        k3d_arrive_event(a.sync, G.cSGF, G.nSGt, G.eSGF, lane);
     }
 
     /* ----------------------------------------------------------------- G ---- */
-    static __device__ void routed_gateup(const K3kDecode &a, int tk, int lane)
+    static __device__ __noinline__ void routed_gateup(K3ArgPtr ap, int tk_, int lane)
     {
-        const int tiles = (a.I + G_PAIRS - 1) / G_PAIRS;
-        const int p = tk / tiles, g = tk - p * tiles;
-        const int r0 = g * G_PAIRS;
-        if (!k3d_wait_sum(a.sync, SY_SEL, 1, a.epoch, a.spin_limit, a.err, lane)) return;
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const int per = G.nGt * G.KSG;
+        const int p = tk / per, rem = tk - p * per;
+        const int gt = rem / G.KSG, ks = rem - gt * G.KSG;
+        const int q0 = ks * G.nQd / G.KSG, q1 = (ks + 1) * G.nQd / G.KSG;
+        if (!k3d_wait_event(a.sync, G.eSEL, tk, a.spin_limit, a.err, lane)) return;
         const int e = k3d_uniform(__hip_atomic_load(&a.idx[p], __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT));
+        const int t = p / a.k;
+        k3v4f acc[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
         if (e >= 0 && e < a.E) {
-            const K3ExpertQ q = k3d_expert(a.eq, e);
-            const int t = p / a.k;
-            const int pc = a.d >> 1, sc = (a.d + 31) >> 5;
-            const K3Rsrc rp1 = k3d_rsrc(q.p1, (size_t)a.I * pc), rs1 = k3d_rsrc(q.s1, (size_t)a.I * sc);
-            const K3Rsrc rp3 = k3d_rsrc(q.p3, (size_t)a.I * pc), rs3 = k3d_rsrc(q.s3, (size_t)a.I * sc);
-            const K3Rsrc rx = k3d_rsrc(a.x, (size_t)a.T * a.d * 4);
-            float acc[2 * G_PAIRS];
+            const uint8_t *w1 = k3d_uniform_ptr((const uint8_t *)a.eq[e].p1);
+            const uint8_t *w3 = k3d_uniform_ptr((const uint8_t *)a.eq[e].p3);
+            const size_t mb = (size_t)(a.I / 16) * G.nQd * K3G_QT;
+            const K3Rsrc r1 = k3d_rsrc(w1, mb), r3 = k3d_rsrc(w3, mb);
+            const K3Rsrc rb = k3d_rsrc(a.xq8 + (size_t)t * G.nQd * K3G_BQ, (size_t)G.nQd * K3G_BQ);
+            const bool bon = (lane & 15) < NPC8;
+            const int rs = G.nQd * K3G_QT;                    /* bytes per row block */
+            const int o0 = 2 * gt * rs + lane * 16, o1 = o0 + rs;
+            for (int Q = q0; Q < q1; ++Q) {
+                const int qo = Q * K3G_QT;
+                uint4 A[4][4];
 #pragma unroll
-            for (int i = 0; i < 2 * G_PAIRS; ++i) acc[i] = 0.0f;
-            for (int cb = 0; cb < a.d; cb += 2048) {
-                const int col = cb + lane * 32;
-                const bool on = col < a.d;
-                uint4 w[2 * G_PAIRS];
-                uint32_t s[2 * G_PAIRS];
-#pragma unroll
-                for (int r = 0; r < G_PAIRS; ++r) {
-                    w[r] = k3d_b128(rp1, col >> 1, (r0 + r) * pc);
-                    s[r] = k3d_b8(rs1, col >> 5, (r0 + r) * sc);
-                    w[G_PAIRS + r] = k3d_b128(rp3, col >> 1, (r0 + r) * pc);
-                    s[G_PAIRS + r] = k3d_b8(rs3, col >> 5, (r0 + r) * sc);
+                for (int j = 0; j < 4; ++j) {
+                    A[0][j] = k3d_b128(r1, o0 + qo + 1024 * j);
+                    A[1][j] = k3d_b128(r1, o1 + qo + 1024 * j);
+                    A[2][j] = k3d_b128(r3, o0 + qo + 1024 * j);
+                    A[3][j] = k3d_b128(r3, o1 + qo + 1024 * j);
                 }
-                float xv[32];
-                k3d_bx(rx, col * 4, t * a.d * 4, xv, 8);
-                if (on) {
+                const int so = qo + 4096 + lane * 4 - lane * 16;
+                const uint32_t s0 = k3d_b32(r1, o0 + so), s1 = k3d_b32(r1, o1 + so);
+                const uint32_t s2 = k3d_b32(r3, o0 + so), s3 = k3d_b32(r3, o1 + so);
+                uint4 B[4][2];
 #pragma unroll
-                    for (int r = 0; r < 2 * G_PAIRS; ++r) acc[r] = k3d_dot32(w[r], s[r], xv, acc[r]);
+                for (int j = 0; j < 4; ++j) {
+                    B[j][0] = k3d_b128<K3_BPOL>(rb, bon ? Q * K3G_BQ + j * 2048 + lane * 32 : K3_OOB);
+                    B[j][1] = k3d_b128<K3_BPOL>(rb, bon ? Q * K3G_BQ + j * 2048 + lane * 32 + 16 : K3_OOB);
                 }
+                const uint32_t sb = k3d_b32<K3_BPOL>(rb, Q * K3G_BQ + 8192 + lane * 4);
+                const k3v8i b0 = k3d_b8(B[0][0], B[0][1]), b1 = k3d_b8(B[1][0], B[1][1]);
+                const k3v8i b2 = k3d_b8(B[2][0], B[2][1]), b3 = k3d_b8(B[3][0], B[3][1]);
+                acc[0] = k3d_mma4<0>(A[0][0], b0, acc[0], s0, sb);
+                acc[1] = k3d_mma4<0>(A[1][0], b0, acc[1], s1, sb);
+                acc[2] = k3d_mma4<0>(A[2][0], b0, acc[2], s2, sb);
+                acc[3] = k3d_mma4<0>(A[3][0], b0, acc[3], s3, sb);
+                acc[0] = k3d_mma4<1>(A[0][1], b1, acc[0], s0, sb);
+                acc[1] = k3d_mma4<1>(A[1][1], b1, acc[1], s1, sb);
+                acc[2] = k3d_mma4<1>(A[2][1], b1, acc[2], s2, sb);
+                acc[3] = k3d_mma4<1>(A[3][1], b1, acc[3], s3, sb);
+                acc[0] = k3d_mma4<2>(A[0][2], b2, acc[0], s0, sb);
+                acc[1] = k3d_mma4<2>(A[1][2], b2, acc[1], s1, sb);
+                acc[2] = k3d_mma4<2>(A[2][2], b2, acc[2], s2, sb);
+                acc[3] = k3d_mma4<2>(A[3][2], b2, acc[3], s3, sb);
+                acc[0] = k3d_mma4<3>(A[0][3], b3, acc[0], s0, sb);
+                acc[1] = k3d_mma4<3>(A[1][3], b3, acc[1], s1, sb);
+                acc[2] = k3d_mma4<3>(A[2][3], b3, acc[2], s2, sb);
+                acc[3] = k3d_mma4<3>(A[3][3], b3, acc[3], s3, sb);
             }
-            k3d_transpose_reduce<2 * G_PAIRS>(acc, lane);
-            const float upv = __shfl_xor(acc[0], 32, K3G_WAVE);
-            const int v = lane >> 2;     /* V = 16: lane l holds row l >> 2 */
-            if ((lane & 3) == 0 && v < G_PAIRS && r0 + v < a.I)
-                k3d_st_dev(&a.h[(size_t)p * a.I + r0 + v], k3d_act(acc[0], upv, a.b1, a.b2));
         } else if (e >= a.E) {
             k3d_raise(a.err, K3G_ERR_EXPERT_RANGE);
         }
-        k3d_signal(k3d_line(a.sync, SY_G + p), lane);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[m] = k3d_colsum(acc[m]);
+        const K3Rsrc rp = k3d_rsrc(a.gpart, (size_t)G.P * G.KSG * 2 * a.I * 4);
+        if ((lane & 15) == 0) {
+            const int r4 = 32 * gt + 4 * (lane >> 4);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                k3d_st4_sc1(rp, (((p * G.KSG + ks) * 2 + (m >> 1)) * a.I + r4 + 16 * (m & 1)) * 4,
+                            acc[m]);
+        }
+        if (!k3d_arrive(k3d_line(a.sync, G.lTG + p * G.nGt + gt), G.KSG - 1, lane))
+            return;
+        /* last slice of the tile: 32 rows of h = act(gate, up) -> FP8 pieces (one block) */
+        const int r = lane & 31, row = 32 * gt + r;
+        float gs = 0.0f, us = 0.0f;
+        for (int q = 0; q < G.KSG; ++q) {
+            gs += k3d_f32_sc1(rp, (((p * G.KSG + q) * 2 + 0) * a.I + row) * 4);
+            us += k3d_f32_sc1(rp, (((p * G.KSG + q) * 2 + 1) * a.I + row) * 4);
+        }
+        float h = lane < 32 ? k3d_act(gs, us, a.b1, a.b2) : 0.0f;
+        const K3Rsrc rh = k3d_rsrc(a.hq8 + (size_t)p * G.nQi * K3G_BQ, (size_t)G.nQi * K3G_BQ);
+        const int Qh = gt >> 4;
+#pragma unroll
+        for (int pc = 0; pc < NPC8; ++pc) {
+            int sx;
+            const uint32_t q = k3d_fp8_piece(h, sx);
+            if (lane < 32) {
+                k3d_st8_sc1(rh, Qh * K3G_BQ + k3d_bq_data(gt, r, pc), q);
+                if (lane == 0) k3d_st8_sc1(rh, Qh * K3G_BQ + k3d_bq_scale(gt, pc), sx + 127);
+            }
+        }
+        k3d_arrive_event(a.sync, G.cGF + p, G.nGt, G.eGF + p * K3_EVLINES, lane);
     }
 
     /* ---------------------------------------------------------------- SD ---- */
-    static __device__ void shared_down(const K3kDecode &a, int tk, int lane, int nSG)
+    static __device__ __noinline__ void shared_down(K3ArgPtr ap, int tk_, int lane)
     {
-        const int r0 = tk * SD_ROWS;
-        if (!k3d_wait_sum(a.sync, SY_SG, NSUB, (long long)a.epoch * nSG, a.spin_limit, a.err,
-                          lane))
-            return;
-        constexpr int V = SD_ROWS * NT;
-        constexpr int SH = 6 - K3L2<V>::v;
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const int rt = tk / G.KSD, ks = tk - rt * G.KSD;
+        const int c0 = ks * G.nCsi / G.KSD, c1 = (ks + 1) * G.nCsi / G.KSD;
+        if (!k3d_wait_event(a.sync, G.eSGF, tk, a.spin_limit, a.err, lane)) return;
         const K3Rsrc r2 = k3d_rsrc(a.sh2, (size_t)a.d * a.SI * 2);
-        const K3Rsrc rh = k3d_rsrc(a.sh_h, (size_t)a.T * a.SI * 4);
-        const int rowb = a.SI * 2;
-        float acc[V];
+        const K3Rsrc rb = k3d_rsrc(a.hq16, (size_t)G.nCsi * 1024);
+        const bool bon = (lane & 15) < NPC16 * a.T;
+        k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
+        const int o0 = 2 * rt * G.nCsi * 1024 + lane * 16, o1 = o0 + G.nCsi * 1024;
+        for (int cb = c0; cb < c1; cb += 8) {
+            uint4 A0[8], A1[8], B[8];
 #pragma unroll
-        for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-        for (int cb = 0; cb < a.SI; cb += 1024) {
-            const int col = cb + lane * 16;
-            uint4 qv[SD_ROWS][2];
-#pragma unroll
-            for (int r = 0; r < SD_ROWS; ++r) {
-                qv[r][0] = k3d_b128(r2, col * 2, (r0 + r) * rowb);
-                qv[r][1] = k3d_b128(r2, col * 2 + 16, (r0 + r) * rowb);
+            for (int i = 0; i < 8; ++i) {
+                const int c = cb + i;
+                A0[i] = k3d_b128(r2, c < c1 ? o0 + c * 1024 : K3_OOB);
+                A1[i] = k3d_b128(r2, c < c1 ? o1 + c * 1024 : K3_OOB);
+                B[i] = k3d_b128<K3_BPOL>(rb, bon && c < c1 ? c * 1024 + lane * 16 : K3_OOB);
             }
-            if (col >= a.SI) continue;  /* lanes past the row end read the next row */
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                float xv[16];
-                k3d_bx<K3_SC1>(rh, col * 4, (t < a.T ? t : 0) * a.SI * 4, xv, 4);
-#pragma unroll
-                for (int r = 0; r < SD_ROWS; ++r)
-                    acc[r * NT + t] = k3d_dot16bf(qv[r][0], qv[r][1], xv, acc[r * NT + t]);
+            for (int i = 0; i < 8; ++i) {
+                y0 = k3d_mma16(A0[i], B[i], y0);
+                y1 = k3d_mma16(A1[i], B[i], y1);
             }
         }
-        k3d_transpose_reduce<V>(acc, lane);
-        const int v = lane >> SH;
-        if ((lane & ((1 << SH) - 1)) == 0 && v < V) {
-            const int r = v / NT, t = v % NT;
-            if (r0 + r < a.d && t < a.T) k3d_st_dev(&a.sh_out[(size_t)t * a.d + r0 + r], acc[0]);
+        y0 = k3d_colsum3(y0, lane);
+        y1 = k3d_colsum3(y1, lane);
+        const int t = lane & 15;
+        if (t < a.T) {
+            const K3Rsrc rp = k3d_rsrc(a.shpart, (size_t)G.KSD * a.T * a.d * 4);
+            const int row = 32 * rt + 4 * (lane >> 4);
+            k3d_st4_sc1(rp, ((ks * a.T + t) * a.d + row) * 4, y0);
+            k3d_st4_sc1(rp, ((ks * a.T + t) * a.d + row + 16) * 4, y1);
         }
-        k3d_signal(k3d_line(a.sync, SY_SD + tk % NSUB), lane);
+        k3d_signal(k3d_line(a.sync, G.lSD + tk % NSUB), lane);
     }
 
     /* ----------------------------------------------------------------- D ---- */
-    static __device__ void routed_down(const K3kDecode &a, int tk, int lane, int tilesG)
+    static __device__ __noinline__ void routed_down(K3ArgPtr ap, int tk_, int lane)
     {
-        const int tiles = (a.d + D_ROWS - 1) / D_ROWS;
-        const int p = tk / tiles, g = tk - p * tiles;
-        const int r0 = g * D_ROWS;
-        if (!k3d_wait_sum(a.sync, SY_G + p, 1, (long long)a.epoch * tilesG, a.spin_limit,
-                          a.err, lane))
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const int per = G.nDt * G.KSDN;
+        const int p = tk / per, rem = tk - p * per;
+        const int dt = rem / G.KSDN, ks = rem - dt * G.KSDN;
+        const int q0 = ks * G.nQi / G.KSDN, q1 = (ks + 1) * G.nQi / G.KSDN;
+        if (!k3d_wait_event(a.sync, G.eGF + p * K3_EVLINES, tk, a.spin_limit, a.err, lane))
             return;
         const int e = k3d_uniform(__hip_atomic_load(&a.idx[p], __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT));
+        k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
         if (e >= 0 && e < a.E) {
-            const K3ExpertQ q = k3d_expert(a.eq, e);
-            const int ipc = a.I >> 1, isc = (a.I + 31) >> 5;
-            const K3Rsrc rp = k3d_rsrc(q.p2, (size_t)a.d * ipc), rs = k3d_rsrc(q.s2, (size_t)a.d * isc);
-            const K3Rsrc rh = k3d_rsrc(a.h + (size_t)p * a.I, (size_t)a.I * 4);
-            float acc[D_ROWS];
+            const uint8_t *w2 = k3d_uniform_ptr((const uint8_t *)a.eq[e].p2);
+            const K3Rsrc r2 = k3d_rsrc(w2, (size_t)(a.d / 16) * G.nQi * K3G_QT);
+            const K3Rsrc rb = k3d_rsrc(a.hq8 + (size_t)p * G.nQi * K3G_BQ, (size_t)G.nQi * K3G_BQ);
+            const bool bon = (lane & 15) < NPC8;
+            const int rs = G.nQi * K3G_QT;
+            const int o0 = 2 * dt * rs + lane * 16, o1 = o0 + rs;
+            for (int Q = q0; Q < q1; ++Q) {
+                const int qo = Q * K3G_QT;
+                uint4 A[2][4];
 #pragma unroll
-            for (int i = 0; i < D_ROWS; ++i) acc[i] = 0.0f;
-            for (int cb = 0; cb < a.I; cb += 2048) {
-                const int col = cb + lane * 32;
-                const bool on = col < a.I;
-                uint4 w[D_ROWS];
-                uint32_t s[D_ROWS];
-#pragma unroll
-                for (int r = 0; r < D_ROWS; ++r) {
-                    w[r] = k3d_b128(rp, col >> 1, (r0 + r) * ipc);
-                    s[r] = k3d_b8(rs, col >> 5, (r0 + r) * isc);
+                for (int j = 0; j < 4; ++j) {
+                    A[0][j] = k3d_b128(r2, o0 + qo + 1024 * j);
+                    A[1][j] = k3d_b128(r2, o1 + qo + 1024 * j);
                 }
-                float xv[32];
-                k3d_bx<K3_SC1>(rh, col * 4, 0, xv, 8);
-                if (on) {
+                const int so = qo + 4096 + lane * 4 - lane * 16;
+                const uint32_t s0 = k3d_b32(r2, o0 + so), s1 = k3d_b32(r2, o1 + so);
+                uint4 B[4][2];
 #pragma unroll
-                    for (int r = 0; r < D_ROWS; ++r) acc[r] = k3d_dot32(w[r], s[r], xv, acc[r]);
+                for (int j = 0; j < 4; ++j) {
+                    B[j][0] = k3d_b128<K3_BPOL>(rb, bon ? Q * K3G_BQ + j * 2048 + lane * 32 : K3_OOB);
+                    B[j][1] = k3d_b128<K3_BPOL>(rb, bon ? Q * K3G_BQ + j * 2048 + lane * 32 + 16 : K3_OOB);
                 }
+                const uint32_t sb = k3d_b32<K3_BPOL>(rb, Q * K3G_BQ + 8192 + lane * 4);
+                const k3v8i b0 = k3d_b8(B[0][0], B[0][1]), b1 = k3d_b8(B[1][0], B[1][1]);
+                const k3v8i b2 = k3d_b8(B[2][0], B[2][1]), b3 = k3d_b8(B[3][0], B[3][1]);
+                y0 = k3d_mma4<0>(A[0][0], b0, y0, s0, sb);
+                y1 = k3d_mma4<0>(A[1][0], b0, y1, s1, sb);
+                y0 = k3d_mma4<1>(A[0][1], b1, y0, s0, sb);
+                y1 = k3d_mma4<1>(A[1][1], b1, y1, s1, sb);
+                y0 = k3d_mma4<2>(A[0][2], b2, y0, s0, sb);
+                y1 = k3d_mma4<2>(A[1][2], b2, y1, s1, sb);
+                y0 = k3d_mma4<3>(A[0][3], b3, y0, s0, sb);
+                y1 = k3d_mma4<3>(A[1][3], b3, y1, s1, sb);
             }
-            k3d_transpose_reduce<D_ROWS>(acc, lane);
-            const int v = lane >> 2;     /* V = 16: lane l holds row l >> 2 */
-            if ((lane & 3) == 0 && r0 + v < a.d)
-                k3d_st_dev(&a.contrib[(size_t)p * a.d + r0 + v], acc[0]);
         }
-        k3d_signal(k3d_line(a.sync, SY_D + p), lane);
+        y0 = k3d_colsum(y0);
+        y1 = k3d_colsum(y1);
+        if ((lane & 15) == 0) {
+            const K3Rsrc rc = k3d_rsrc(a.contrib, (size_t)G.P * G.KSDN * a.d * 4);
+            const int row = 32 * dt + 4 * (lane >> 4);
+            k3d_st4_sc1(rc, ((p * G.KSDN + ks) * a.d + row) * 4, y0);
+            k3d_st4_sc1(rc, ((p * G.KSDN + ks) * a.d + row + 16) * 4, y1);
+        }
+        k3d_signal(k3d_line(a.sync, G.lD + p), lane);
     }
 
     /* ----------------------------------------------------------------- C ---- */
-    static __device__ void combine(const K3kDecode &a, int tk, int lane, int nSD)
+    static __device__ __noinline__ void combine(K3ArgPtr ap, int tk_, int lane)
     {
-        const int P = a.T * a.k, tilesD = (a.d + D_ROWS - 1) / D_ROWS;
-        for (int p0 = 0; p0 < P; p0 += 64)
-            if (!k3d_wait_sum(a.sync, SY_D + p0, min(64, P - p0),
-                              (long long)a.epoch * tilesD * min(64, P - p0), a.spin_limit,
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        for (int p0 = 0; p0 < G.P; p0 += 64)
+            if (!k3d_wait_sum(a.sync, G.lD + p0, min(64, G.P - p0),
+                              (long long)G.nDt * G.KSDN * min(64, G.P - p0), a.spin_limit,
                               a.err, lane))
                 return;
-        if (a.SI > 0 && !k3d_wait_sum(a.sync, SY_SD, NSUB, (long long)a.epoch * nSD,
+        if (a.SI > 0 && !k3d_wait_sum(a.sync, G.lSD, NSUB, G.nSD,
                                       a.spin_limit, a.err, lane))
             return;
         const int row = tk * C_ROWS + lane * 4;
-        const K3Rsrc rc = k3d_rsrc(a.contrib, (size_t)a.T * a.k * a.d * 4);
-        const K3Rsrc rs = k3d_rsrc(a.sh_out, (size_t)a.T * a.d * 4);
+        const K3Rsrc rc = k3d_rsrc(a.contrib, (size_t)G.P * G.KSDN * a.d * 4);
+        const K3Rsrc rs = k3d_rsrc(a.shpart, (size_t)(G.KSD > 0 ? G.KSD : 1) * a.T * a.d * 4);
         for (int t = 0; t < a.T; ++t) {
             float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
             for (int j = 0; j < a.k; ++j) {
@@ -454,16 +850,28 @@ struct K3Dec {
                 if (e < 0 || e >= a.E) continue;
                 const float w = __hip_atomic_load(&a.wt[p], __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
-                const uint4 y = k3d_b128<K3_SC1>(rc, row * 4, p * a.d * 4);
-                c0 = __fadd_rn(c0, __fmul_rn(w, __uint_as_float(y.x)));
-                c1 = __fadd_rn(c1, __fmul_rn(w, __uint_as_float(y.y)));
-                c2 = __fadd_rn(c2, __fmul_rn(w, __uint_as_float(y.z)));
-                c3 = __fadd_rn(c3, __fmul_rn(w, __uint_as_float(y.w)));
+                float y0 = 0.0f, y1 = 0.0f, y2 = 0.0f, y3 = 0.0f;
+                for (int q = 0; q < G.KSDN; ++q) {
+                    const uint4 y = k3d_b128<K3_BPOL>(
+                        rc, row < a.d ? ((p * G.KSDN + q) * a.d + row) * 4 : K3_OOB);
+                    y0 += __uint_as_float(y.x); y1 += __uint_as_float(y.y);
+                    y2 += __uint_as_float(y.z); y3 += __uint_as_float(y.w);
+                }
+                c0 = __fadd_rn(c0, __fmul_rn(w, y0));
+                c1 = __fadd_rn(c1, __fmul_rn(w, y1));
+                c2 = __fadd_rn(c2, __fmul_rn(w, y2));
+                c3 = __fadd_rn(c3, __fmul_rn(w, y3));
             }
             if (a.SI > 0) {
-                const uint4 sv = k3d_b128<K3_SC1>(rs, row * 4, t * a.d * 4);
-                c0 = __fadd_rn(c0, __uint_as_float(sv.x)); c1 = __fadd_rn(c1, __uint_as_float(sv.y));
-                c2 = __fadd_rn(c2, __uint_as_float(sv.z)); c3 = __fadd_rn(c3, __uint_as_float(sv.w));
+                float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+                for (int q = 0; q < G.KSD; ++q) {
+                    const uint4 v = k3d_b128<K3_BPOL>(rs, row < a.d ? ((q * a.T + t) * a.d + row) * 4
+                                                                   : K3_OOB);
+                    s0 += __uint_as_float(v.x); s1 += __uint_as_float(v.y);
+                    s2 += __uint_as_float(v.z); s3 += __uint_as_float(v.w);
+                }
+                c0 = __fadd_rn(c0, s0); c1 = __fadd_rn(c1, s1);
+                c2 = __fadd_rn(c2, s2); c3 = __fadd_rn(c3, s3);
             }
             if (row < a.d)
                 *(float4 *)(a.out + (size_t)t * a.d + row) = make_float4(c0, c1, c2, c3);
@@ -472,42 +880,53 @@ struct K3Dec {
 };
 
 template <int NT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K3G_DEC_WAVES_PER_EU)))
 k_decode_fused(K3kDecode a)
 {
     __shared__ K3SelectLds lds;
     const int lane = threadIdx.x & 63;
-    const int P = a.T * a.k;
-    const int nch = (a.d + R_CHUNK - 1) / R_CHUNK;
-    const int nR = a.E * nch;
-    const int nSG = a.SI > 0 ? (a.SI + SG_PAIRS - 1) / SG_PAIRS : 0;
-    const int tilesG = (a.I + G_PAIRS - 1) / G_PAIRS;
-    const int nG = P * tilesG;
-    const int nSD = a.SI > 0 ? (a.d + SD_ROWS - 1) / SD_ROWS : 0;
-    const int nD = P * ((a.d + D_ROWS - 1) / D_ROWS);
-    const int nC = (a.d + C_ROWS - 1) / C_ROWS;
-    const int total = nR + 1 + nSG + nG + nSD + nD + nC;
+    const K3ArgPtr ap = (K3ArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
     const int W = gridDim.x * (blockDim.x >> 6);
     const int w = k3d_uniform(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
-    for (int tk = w; tk < total; tk += W) {
+    {
+        /* zero this wave's slice of the other counter bank for the next call */
+        const int per = (a.sync_words + W - 1) / W;
+        const int lo = w * per, hi = min(a.sync_words, lo + per);
+        for (int i = lo + lane; i < hi; i += 64) a.sync_clear[i] = 0;
+    }
+    for (int tk = w; tk < G.total; tk += W) {
         if (a.trace && lane == 0) a.trace[2 * tk] = wall_clock64();
         int t = tk;
-        if (t < nR) K3Dec<NT>::router(a, t, lane);
-        else if ((t -= nR) < 1) K3Dec<NT>::select(a, lane, &lds, nR);
-        else if ((t -= 1) < nSG) K3Dec<NT>::shared_gateup(a, t, lane);
-        else if ((t -= nSG) < nG) K3Dec<NT>::routed_gateup(a, t, lane);
-        else if ((t -= nG) < nSD) K3Dec<NT>::shared_down(a, t, lane, nSG);
-        else if ((t -= nSD) < nD) K3Dec<NT>::routed_down(a, t, lane, tilesG);
-        else K3Dec<NT>::combine(a, t - nD, lane, nSD);
+        if (t < G.nX) K3Dec<NT>::prep(ap, t, lane);
+        else if ((t -= G.nX) < G.nR) K3Dec<NT>::router(ap, t, lane);
+        else if ((t -= G.nR) < 1) K3Dec<NT>::select(ap, lane, &lds);
+        else if ((t -= 1) < G.nSG) K3Dec<NT>::shared_gateup(ap, t, lane);
+        else if ((t -= G.nSG) < G.nG) K3Dec<NT>::routed_gateup(ap, t, lane);
+        else if ((t -= G.nG) < G.nSD) K3Dec<NT>::shared_down(ap, t, lane);
+        else if ((t -= G.nSD) < G.nD) K3Dec<NT>::routed_down(ap, t, lane);
+        else K3Dec<NT>::combine(ap, t - G.nD, lane);
         if (a.trace && lane == 0) a.trace[2 * tk + 1] = wall_clock64();
     }
 }
 
+extern "C" size_t k3k_decode_sync_bytes(int T, int d, int E, int k, int I, int SI)
+{
+    const K3Geo G = k3_geo(T, d, E, k, I, SI);
+    return (size_t)G.nlines * SY_LINE * 4;
+}
+
+extern "C" int k3k_decode_tickets(int T, int d, int E, int k, int I, int SI)
+{
+    return k3_geo(T, d, E, k, I, SI).total;
+}
+
 extern "C" int k3k_decode_fused(const K3kDecode *a, hipStream_t st)
 {
-    if (a->T < 1 || a->T > 4 || a->d % 256 || a->I % 32 || (a->SI % 16) || a->k < 1 ||
-        a->k > K3G_MAX_TOPK || a->E < 1 || a->E > K3G_MAX_E ||
-        a->T * a->k > 256 || SY_NLINES * SY_LINE > K3G_SYNC_WORDS || a->epoch < 1)
+    if (a->T < 1 || a->T > 4 || a->d % 32 || a->I % 32 || a->SI % 32 || a->k < 1 ||
+        a->k > K3G_MAX_TOPK || a->E < 1 || a->E > K3G_MAX_E || a->T * a->k > 256 ||
+        !a->sync || !a->sync_clear ||
+        (size_t)a->sync_words * 4 < k3k_decode_sync_bytes(a->T, a->d, a->E, a->k, a->I, a->SI))
         return -1;
     static int grid[5] = {0, 0, 0, 0, 0};
     const int NT = a->T <= 1 ? 1 : a->T <= 2 ? 2 : 4;
@@ -519,7 +938,11 @@ extern "C" int k3k_decode_fused(const K3kDecode *a, hipStream_t st)
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, 256, 0) != hipSuccess)
             return -1;
-        grid[NT] = cus * (per > 0 ? per : 1);
+        if (per < 1) per = 1;
+        /* K3MOE_DECODE_BPC: blocks per CU, at most what fits at once (tuning knob) */
+        const char *env = getenv("K3MOE_DECODE_BPC");
+        const int want = env ? atoi(env) : 0;
+        grid[NT] = cus * (want > 0 && want < per ? want : per);
     }
     if (NT == 1) hipLaunchKernelGGL(k_decode_fused<1>, dim3(grid[1]), dim3(256), 0, st, *a);
     else if (NT == 2) hipLaunchKernelGGL(k_decode_fused<2>, dim3(grid[2]), dim3(256), 0, st, *a);

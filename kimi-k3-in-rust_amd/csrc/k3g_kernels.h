@@ -40,39 +40,62 @@ typedef struct {
 } K3kRouted;
 
 /* The fused decode kernel (k3g_decode.hip): the whole Kimi-K2-shaped layer for T <= 4
- * tokens in one persistent launch. */
+ * tokens in one persistent launch, on experts in the tiled MXFP4 layout and a shared
+ * expert in the tiled bf16 layout (k3g_tile.hip). */
 typedef struct {
     int T, d, E, k, I, SI;
     int renorm;
     float routed_scale, b1, b2;
     const float *gate, *bias;
-    const K3ExpertQ *eq;
-    const uint16_t *sh1, *sh3, *sh2;
+    const K3ExpertQ *eq;          /* p1/p3/p2: tiled MXFP4 w1, w3, w2; s* unused */
+    const uint16_t *sh1, *sh3, *sh2;   /* tiled bf16 */
     const float *x;
     float *out;
     int32_t *idx;
     float *wt;
-    double *plogit, *pasum;       /* [ceil(d/1024)][T][E] partial logits */
-    float *h;                     /* [T*k][I] */
-    float *sh_h;                  /* [T][SI] */
-    float *contrib;               /* [T*k][d] per-slot expert outputs */
-    float *sh_out;                /* [T][d] shared-expert output */
-    int *sync;                    /* K3G_SYNC_WORDS counters, zero between launches */
+    float *rs;                    /* [T][E][4] router {choice, lo, hi, score} */
+    double *rpart;                /* [T][E][K3G_KS_R][2] router slice sums */
+    uint8_t *xq8;                 /* [T][ceil(d/512)][8448]: x's FP8 pieces, B layout */
+    uint16_t *xq16;               /* [d/32][64][8]: x's bf16 pieces, column 3t + piece */
+    float *gpart;                 /* [T*k][K3G_KS_G][2][I] routed gate/up partial sums */
+    uint8_t *hq8;                 /* [T*k][ceil(I/512)][8448]: h's FP8 pieces */
+    float *sgpart;                /* [K3G_KS_SG][T][2][SI] shared gate/up partial sums */
+    uint16_t *hq16;               /* [SI/32][64][8]: shared h's bf16 pieces */
+    float *contrib;               /* [T*k][K3G_KS_D][d] per-slot expert output slices */
+    float *shpart;                /* [K3G_KS_SD][T][d] shared down partial sums */
+    int *sync;                    /* this call's counter bank, all zero */
+    int *sync_clear;              /* the other bank, zeroed by this call for the next */
+    int sync_words;               /* ints per bank */
     int *err, *stats;
     int force;
-    int epoch;                    /* call number since the counters were cleared, >= 1 */
     long long spin_limit;
     unsigned long long *trace;    /* optional: [ticket][2] start/end wall-clock stamps */
 } K3kDecode;
 
-#define K3G_SYNC_WORDS (600 * 32)
-#define K3G_EPOCH_MAX 100000      /* counters are cleared before they could overflow */
+/* K slices of the fused kernel's ticket classes (fewer when K is short) */
+#define K3G_KS_G 7                /* routed gate/up: over 512-column quads of d */
+#define K3G_KS_SG 7               /* shared gate/up: over 32-column chunks of d */
+#define K3G_KS_SD 2               /* shared down: over 32-column chunks of SI */
+#define K3G_KS_R 4                /* router: over 1024-column chunks of d */
+#define K3G_KS_D 2                /* routed down: over 512-column quads of I */
+#define K3G_DEC_WAVES_PER_EU 4
 
+/* bytes of counters and tickets per call of the fused kernel at this shape */
+size_t k3k_decode_sync_bytes(int T, int d, int E, int k, int I, int SI);
+int k3k_decode_tickets(int T, int d, int E, int k, int I, int SI);
 int k3k_decode_fused(const K3kDecode *a, hipStream_t st);
 
+/* Repack into the tiled layouts (k3g_tile.hip). Sizes are 0 for unsupported shapes. */
+size_t k3k_tiled_mxfp4_bytes(int rows, int cols);
+size_t k3k_tiled_bf16_bytes(int rows, int cols);
+int k3k_tile_mxfp4(uint8_t *dst, const uint8_t *packed, const uint8_t *scales, int rows,
+                   int cols, hipStream_t st);
+int k3k_tile_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols, hipStream_t st);
+
+/* rs: [T][E] float4 {choice, lo, hi, score} workspace */
 int k3k_router(const float *x, int T, const float *W, const float *bias, int d, int E,
-               int k, int renorm, float routed_scale, double *logit, double *asum,
-               int32_t *idx, float *wt, int force, int *stats, hipStream_t st);
+               int k, int renorm, float routed_scale, float *rs, int32_t *idx, float *wt,
+               int force, int *stats, hipStream_t st);
 
 /* Stable counting sort of the T*k (token, slot) pairs by expert. cnt/base are
  * [ceil(P/256)][E] ints of workspace. */

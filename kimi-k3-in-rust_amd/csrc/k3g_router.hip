@@ -32,7 +32,7 @@
 template <int RT>
 __global__ void __launch_bounds__(64)
 k_router_logits(const float *__restrict__ x, int T, const float *__restrict__ W,
-                int d, int vec, double *__restrict__ logit, double *__restrict__ asum,
+                const float *__restrict__ bias, int d, int vec, float4 *__restrict__ rs,
                 int E)
 {
     const int e = blockIdx.x;
@@ -73,44 +73,40 @@ k_router_logits(const float *__restrict__ x, int T, const float *__restrict__ W,
     for (int t = 0; t < RT; ++t) {
         const double s = k3d_wave_sumd(acc[t]);
         const double a = k3d_wave_sumd(ab[t]);
-        if (lane == 0 && t0 + t < T) {
-            logit[(size_t)(t0 + t) * E + e] = s;
-            asum[(size_t)(t0 + t) * E + e] = a;
-        }
+        if (lane == 0 && t0 + t < T)
+            rs[(size_t)(t0 + t) * E + e] = k3d_route_score(s, a, bias ? bias[e] : 0.0f, d);
     }
 }
 
 /* ------------------------------------------------------------------ select ---- */
 /* One wave per token. */
 __global__ void __launch_bounds__(64)
-k_router_select(const double *__restrict__ logit, const double *__restrict__ asum,
-                const float *__restrict__ bias, const float *__restrict__ W,
-                const float *__restrict__ x, int d, int E, int k, int renorm,
-                float routed_scale, int32_t *__restrict__ idx, float *__restrict__ wt,
-                int force, int *__restrict__ stats, int T)
+k_router_select(const float4 *__restrict__ rs, const float *__restrict__ bias,
+                const float *__restrict__ W, const float *__restrict__ x, int d, int E, int k,
+                int renorm, float routed_scale, int32_t *__restrict__ idx,
+                float *__restrict__ wt, int force, int *__restrict__ stats)
 {
     __shared__ K3SelectLds lds;
-    k3d_select_token(&lds, blockIdx.x, T, 1, logit, asum, bias, W, x, d, E, k, renorm,
-                     routed_scale, idx, wt, force, stats, threadIdx.x);
+    k3d_select_token(&lds, blockIdx.x, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
+                     force, stats, threadIdx.x);
 }
 
 extern "C" int k3k_router(const float *x, int T, const float *W, const float *bias, int d,
-                          int E, int k, int renorm, float routed_scale, double *logit,
-                          double *asum, int32_t *idx, float *wt, int force, int *stats,
-                          hipStream_t st)
+                          int E, int k, int renorm, float routed_scale, float *rs,
+                          int32_t *idx, float *wt, int force, int *stats, hipStream_t st)
 {
     if (E > K3G_MAX_E || k > K3G_MAX_TOPK || k < 1 || T < 1 || d < 1) return -1;
-    /* logits of token t live at [t][E] (one partial sum) */
+    /* the score intervals of token t live at [t][E] */
     /* float4 loads need 16-byte aligned rows; anything else takes the scalar loop */
     const int vec = ((((uintptr_t)x | (uintptr_t)W) & 15) == 0) && ((d & 3) == 0);
     if (T >= 4) {
         hipLaunchKernelGGL(k_router_logits<4>, dim3(E, (T + 3) / 4), dim3(64), 0, st,
-                           x, T, W, d, vec, logit, asum, E);
+                           x, T, W, bias, d, vec, (float4 *)rs, E);
     } else {
         hipLaunchKernelGGL(k_router_logits<1>, dim3(E, T), dim3(64), 0, st,
-                           x, T, W, d, vec, logit, asum, E);
+                           x, T, W, bias, d, vec, (float4 *)rs, E);
     }
-    hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), 0, st, logit, asum, bias, W, x,
-                       d, E, k, renorm, routed_scale, idx, wt, force, stats, T);
+    hipLaunchKernelGGL(k_router_select, dim3(T), dim3(64), 0, st, (const float4 *)rs, bias, W,
+                       x, d, E, k, renorm, routed_scale, idx, wt, force, stats);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

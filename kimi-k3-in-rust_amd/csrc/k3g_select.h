@@ -1,8 +1,14 @@
-/* k3g_select.h - certified top-k selection for one token, run by one wave. Shared by
- * the standalone router and the fused decode kernel.
+/* k3g_select.h - the router's score intervals and the certified top-k for one token, run
+ * by one wave. Shared by the standalone router and the fused decode kernel.
  *
- * Inputs are `nparts` partial fp64 logits and partial sum|w*x| per expert, laid out
- * [part][T][E] and added in part order. See k3g_router.hip for the certificate. */
+ * The engine's logit is a SEQUENTIAL double sum of exact products rounded to float,
+ * then sigmoid with float expf (src/core/k3_ops.c:419-478). A GPU sums in another order,
+ * so the kernels that form the logits (one wave per expert row) also form, per expert, an
+ * interval [lo, hi] guaranteed to hold the engine's choice score, and store
+ * {choice, lo, hi, score} per (token, expert). The selection then runs on the best
+ * guess and accepts it when every selected lo is strictly above the hi of every expert
+ * ranked after it; otherwise it recomputes the candidates in the engine's exact serial
+ * order. */
 #pragma once
 
 #include "k3g_dev.h"
@@ -19,7 +25,29 @@ struct K3SelectLds {
     int cand[K3G_MAX_E];
     int ncand;
     int cert;
+    double wsum;
 };
+
+/* {choice, lo, hi, score} of one expert from its fp64 logit sum `acc` over d products and
+ * sum|w*x| `ab`:
+ *   |acc - engine's double sum| <= B = (d (1 + 1/64) + 16) 2^-53 ab 1.01 + |acc| 2^-51,
+ * covering the rounding of both summation orders; the bound is pushed through the
+ * float rounding and the sigmoid (monotone) and widened by 4 ulp for a libm expf that
+ * differs from a correctly rounded one, then the bias is added (monotone again). */
+__device__ __forceinline__ float4 k3d_route_score(double acc, double ab, float bias, int d)
+{
+    const double kB = ((double)d * (1.0 + 1.0 / 64.0) + 16.0) * 0x1p-53 * 1.01;
+    const double B = kB * ab + fabs(acc) * 0x1p-51 + 0x1p-1000;
+    const float sc = k3d_sigmoid((float)acc);
+    float slo = k3d_sigmoid((float)(acc - B));
+    float shi = k3d_sigmoid((float)(acc + B));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        slo = nextafterf(slo, -INFINITY);
+        shi = nextafterf(shi, INFINITY);
+    }
+    return make_float4(__fadd_rn(sc, bias), __fadd_rn(slo, bias), __fadd_rn(shi, bias), sc);
+}
 
 /* (value, index) argmax with the engine's rule: larger value wins, equal values go to
  * the lower index. NaN and -inf never win (the engine's strict > against -inf). */
@@ -33,79 +61,140 @@ __device__ __forceinline__ void k3d_argmax(float &v, int &i)
     }
 }
 
-/* Selection for token t. Only this wave touches `s`; the wave synchronises itself with
- * wave-level barriers (LDS traffic within one wave is ordered by s_waitcnt). */
-__device__ __forceinline__ void
-k3d_select_token(K3SelectLds *s, int t, int T, int nparts, const double *logit,
-                 const double *asum, const float *bias, const float *W, const float *x,
-                 int d, int E, int k, int renorm, float routed_scale, int32_t *idx,
-                 float *wt, int force, int *stats, int lane)
+/* Wave-wide maximum with DPP row shifts and row broadcasts (no LDS round trips): every
+ * lane returns the maximum. */
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t k3d_dpp(uint32_t v)
 {
-    const double kB = ((double)d * (1.0 + 1.0 / 64.0) + 16.0) * 0x1p-53 * 1.01;
-    for (int e = lane; e < E; e += 64) {
-        double acc = 0.0, ab = 0.0;
-        for (int q = 0; q < nparts; ++q) {
-            acc += k3d_ld_dev64(&logit[((size_t)q * T + t) * E + e]);
-            ab += k3d_ld_dev64(&asum[((size_t)q * T + t) * E + e]);
-        }
-        const double B = kB * ab + fabs(acc) * 0x1p-51 + 0x1p-1000;
-        const float b = bias ? bias[e] : 0.0f;
-        const float sc = k3d_sigmoid((float)acc);
-        float slo = k3d_sigmoid((float)(acc - B));
-        float shi = k3d_sigmoid((float)(acc + B));
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            slo = nextafterf(slo, -INFINITY);
-            shi = nextafterf(shi, INFINITY);
-        }
-        s->score[e] = sc;
-        s->choice[e] = __fadd_rn(sc, b);
-        s->lo[e] = __fadd_rn(slo, b);
-        s->hi[e] = __fadd_rn(shi, b);
-        s->taken[e] = 0;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWS, 0xf, false);
+}
 
-    /* top-k on the best guess */
+__device__ __forceinline__ uint64_t k3d_wave_max_u64(uint64_t key)
+{
+    uint32_t lo = (uint32_t)key, hi = (uint32_t)(key >> 32);
+#define K3_MAX_STEP(C, R)                                                                    \
+    {                                                                                        \
+        const uint32_t ol = k3d_dpp<C, R>(lo), oh = k3d_dpp<C, R>(hi);                       \
+        if (oh > hi || (oh == hi && ol > lo)) { hi = oh; lo = ol; }                          \
+    }
+    K3_MAX_STEP(0x111, 0xf) K3_MAX_STEP(0x112, 0xf) K3_MAX_STEP(0x114, 0xf)
+    K3_MAX_STEP(0x118, 0xf) K3_MAX_STEP(0x142, 0xa) K3_MAX_STEP(0x143, 0xc)
+#undef K3_MAX_STEP
+    hi = __builtin_amdgcn_readlane(hi, 63);
+    lo = __builtin_amdgcn_readlane(lo, 63);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+/* fmaxf over the wave (NaN ignored, as fmaxf does) */
+__device__ __forceinline__ float k3d_wave_fmax(float v)
+{
+#define K3_FMAX_STEP(C, R) v = fmaxf(v, __uint_as_float(k3d_dpp<C, R>(__float_as_uint(v))));
+    K3_FMAX_STEP(0x111, 0xf) K3_FMAX_STEP(0x112, 0xf) K3_FMAX_STEP(0x114, 0xf)
+    K3_FMAX_STEP(0x118, 0xf) K3_FMAX_STEP(0x142, 0xa) K3_FMAX_STEP(0x143, 0xc)
+#undef K3_FMAX_STEP
+    return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
+}
+
+/* float -> uint32 with the same order (for finite and infinite values) */
+__device__ __forceinline__ uint32_t k3d_ordered(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* Selection for token t from rs [T][E] {choice, lo, hi, score} (read at device
+ * coherence: the fused kernel's router tickets write them in the same launch). Each lane
+ * owns experts lane, lane + 64, ... (NPL of them); all loads are issued before any is
+ * used. The top-k runs in registers: per round a lane proposes its best untaken choice and
+ * a DPP maximum over (ordered choice, ~index) keys picks the engine's winner (larger
+ * value, then lower index). The certificate is checked along the way: with the rounds in
+ * choice order, "every selected lo above the hi of everything ranked after it" is "each
+ * new hi below the smallest lo selected before it" plus "the smallest selected lo above
+ * the largest unselected hi". LDS is only used when the certificate fails. */
+template <int NPL>
+__device__ __noinline__ void
+k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
+                   const float *W, const float *x, int d, int E, int k, int renorm,
+                   float routed_scale, int32_t *idx, float *wt, int force, int *stats,
+                   int lane, unsigned long long *stamp)
+{
+    const int nb = (t + 1) * E * 16;
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float4 *>(rs), (short)0, nb, 0x00020000);
+    float4 v[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int e = lane + 64 * i;
+        /* experts past E read past the descriptor's bound: zero, no memory access */
+        const int off = e < E ? (t * E + e) * 16 : nb;
+        v[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 16));
+    }
+    if (stamp && lane == 0) stamp[0] = wall_clock64();
+
+    uint32_t taken = 0;
+    bool ok = !force;
+    float minlo = INFINITY;
+    double wsum = 0.0;
+    int my_sel = -1;          /* lane j: the j-th selected expert */
+    float my_score = 0.0f;
     for (int j = 0; j < k; ++j) {
         float bv = -INFINITY;
         int bi = -1;
-        for (int e = lane; e < E; e += 64) {
-            const float c = s->choice[e];
-            if (!s->taken[e] && c > bv) { bv = c; bi = e; }
+#pragma unroll
+        for (int i = 0; i < NPL; ++i)
+            if (lane + 64 * i < E && !((taken >> i) & 1u) && v[i].x > bv) {
+                bv = v[i].x;
+                bi = lane + 64 * i;
+            }
+        const uint64_t key = bi >= 0 ? ((uint64_t)k3d_ordered(bv) << 32) | (uint32_t)~bi : 0;
+        const uint64_t win = k3d_wave_max_u64(key);
+        const int w = win ? (int)~(uint32_t)win : -1;       /* uniform */
+        float wlo = 0.0f, whi = 0.0f, wsc = 0.0f;
+        if (w >= 0) {
+            const int slot = w >> 6, wl = w & 63;
+            float lo = 0.0f, hi = 0.0f, sc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NPL; ++i)
+                if (i == slot) { lo = v[i].y; hi = v[i].z; sc = v[i].w; }
+            wlo = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(lo), wl));
+            whi = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(hi), wl));
+            wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sc), wl));
+            if (lane == wl) taken |= 1u << slot;
+            if (j > 0 && !__builtin_isnan(whi) && !(whi < minlo)) ok = false;
+            if (__builtin_isnan(wlo)) ok = false;
+            minlo = fminf(minlo, wlo);
+            wsum += (double)wsc;
+        } else {
+            ok = false;
         }
-        k3d_argmax(bv, bi);
-        if (lane == 0) {
-            s->sel[j] = bi;
-            if (bi >= 0) s->taken[bi] = 1;
+        if (lane == j) { my_sel = w; my_score = w >= 0 ? wsc : 0.0f; }
+    }
+    float hrest = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+        if (lane + 64 * i < E && !((taken >> i) & 1u)) hrest = fmaxf(hrest, v[i].z);
+    hrest = k3d_wave_fmax(hrest);
+    if (!(minlo > hrest)) ok = false;
+    if (stamp && lane == 0) stamp[1] = wall_clock64();
+
+    if (!ok) {
+        /* the exact path: LDS copies, candidates (every expert whose interval reaches the
+         * weakest selected lo), their logits in the engine's serial order, and the
+         * engine's selection among them */
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int e = lane + 64 * i;
+            if (e < E) {
+                s->choice[e] = v[i].x;
+                s->lo[e] = v[i].y;
+                s->hi[e] = v[i].z;
+                s->score[e] = v[i].w;
+                s->taken[e] = (taken >> i) & 1u;
+            }
         }
+        if (lane < k) s->sel[lane] = my_sel;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
-    }
-
-    /* certificate: every selected lo strictly above the hi of everything ranked after */
-    float hrest = -INFINITY;
-    for (int e = lane; e < E; e += 64)
-        if (!s->taken[e] && s->hi[e] > hrest) hrest = s->hi[e];
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) hrest = fmaxf(hrest, __shfl_xor(hrest, m, K3G_WAVE));
-    if (lane == 0) {
-        int ok = force ? 0 : 1;
-        float M = hrest;
-        for (int j = k - 1; j >= 0 && ok; --j) {
-            const int e = s->sel[j];
-            if (e < 0) { ok = 0; break; }
-            if (!(s->lo[e] > M)) ok = 0;
-            M = fmaxf(M, s->hi[e]);
-        }
-        s->cert = ok;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-
-    if (!s->cert) {
-        /* candidates: every expert whose interval reaches the weakest selected lo */
         if (lane == 0) {
             float theta = INFINITY;
             for (int j = 0; j < k; ++j) {
@@ -144,8 +233,8 @@ k3d_select_token(K3SelectLds *s, int t, int T, int nparts, const double *logit,
             int bi = -1;
             for (int c = lane; c < nc; c += 64) {
                 const int e = s->cand[c];
-                const float v = s->choice[e];
-                if (!s->taken[e] && (v > bv || (v == bv && bi >= 0 && e < bi))) { bv = v; bi = e; }
+                const float cv = s->choice[e];
+                if (!s->taken[e] && (cv > bv || (cv == bv && bi >= 0 && e < bi))) { bv = cv; bi = e; }
             }
             k3d_argmax(bv, bi);
             if (lane == 0) {
@@ -155,25 +244,50 @@ k3d_select_token(K3SelectLds *s, int t, int T, int nparts, const double *logit,
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
             __builtin_amdgcn_wave_barrier();
         }
+        /* the engine's sequential double sum over the new selection */
+        if (lane == 0) {
+            double sum = 0.0;
+            for (int j = 0; j < k; ++j) sum += s->sel[j] >= 0 ? (double)s->score[s->sel[j]] : 0.0;
+            s->wsum = sum;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        wsum = s->wsum;
+        if (lane < k) {
+            my_sel = s->sel[lane];
+            my_score = my_sel >= 0 ? s->score[my_sel] : 0.0f;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
     }
 
-    /* weights from the unbiased scores, renormalised in double, then scaled */
-    if (lane == 0) {
-        float w[64];
-        for (int j = 0; j < k; ++j) w[j] = s->sel[j] >= 0 ? s->score[s->sel[j]] : 0.0f;
-        if (renorm && k > 1) {
-            double sum = 0.0;
-            for (int j = 0; j < k; ++j) sum += (double)w[j];
-            const float inv = (float)(1.0 / (sum + 1e-20));
-            for (int j = 0; j < k; ++j) w[j] = __fmul_rn(w[j], inv);
-        }
-        for (int j = 0; j < k; ++j) {
-            __hip_atomic_store(&idx[(size_t)t * k + j], s->sel[j] >= 0 ? s->sel[j] : 0,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&wt[(size_t)t * k + j], __fmul_rn(w[j], routed_scale),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+    /* weights from the unbiased scores, renormalised by the engine's sequential double
+     * sum (taken in selection order above), then scaled; lane j writes slot j */
+    if (stamp && lane == 0) stamp[2] = wall_clock64();
+    if (lane < k) {
+        float w = my_score;
+        if (renorm && k > 1) w = __fmul_rn(w, (float)(1.0 / (wsum + 1e-20)));
+        __hip_atomic_store(&idx[(size_t)t * k + lane], my_sel >= 0 ? my_sel : 0,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&wt[(size_t)t * k + lane], __fmul_rn(w, routed_scale),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
+}
+
+/* k3d_select_token_n with the per-lane count chosen for E (<= K3G_MAX_E). */
+__device__ __forceinline__ void
+k3d_select_token(K3SelectLds *s, int t, const float4 *rs, const float *bias, const float *W,
+                 const float *x, int d, int E, int k, int renorm, float routed_scale,
+                 int32_t *idx, float *wt, int force, int *stats, int lane,
+                 unsigned long long *stamp = nullptr)
+{
+    if (E <= 256)
+        k3d_select_token_n<4>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
+                              force, stats, lane, stamp);
+    else if (E <= 512)
+        k3d_select_token_n<8>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
+                              force, stats, lane, stamp);
+    else
+        k3d_select_token_n<16>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
+                               force, stats, lane, stamp);
 }

@@ -84,9 +84,11 @@ class K3gLayer(C.Structure):
         ("sh1", C.c_void_p), ("sh3", C.c_void_p), ("sh2", C.c_void_p),
         ("down", C.c_void_p), ("up", C.c_void_p),
         ("latent_norm", C.c_void_p),
+        ("shared_fmt", C.c_int),
     ]
 
 
+K3G_EXPERT_MXFP4, K3G_EXPERT_F32, K3G_EXPERT_MXFP4_TILED = 0, 1, 2
 K3_WF32, K3_WBF16 = 0, 1
 SWIGLU_CAP = float(2.0 ** 100)   # the engine's SwiGLU setting of the SiTU caps
 
@@ -156,6 +158,14 @@ def lib() -> C.CDLL:
         L.k3g_fill_bytes.restype = i
         L.k3g_fill_scales.argtypes = [vp, sz, u64, u64, u64, i, i, vp]
         L.k3g_fill_scales.restype = i
+        L.k3g_tiled_mxfp4_bytes.argtypes = [i, i]
+        L.k3g_tiled_mxfp4_bytes.restype = sz
+        L.k3g_tiled_bf16_bytes.argtypes = [i, i]
+        L.k3g_tiled_bf16_bytes.restype = sz
+        L.k3g_tile_mxfp4.argtypes = [vp, vp, vp, i, i, vp]
+        L.k3g_tile_mxfp4.restype = i
+        L.k3g_tile_bf16.argtypes = [vp, vp, i, i, vp]
+        L.k3g_tile_bf16.restype = i
         _lib = L
     return _lib
 
@@ -338,7 +348,13 @@ class SynthLayer:
     HBM, and on-demand host regeneration of any expert for a CPU check."""
 
     def __init__(self, shape: Shape, seed: int, layer: int = 0, device: bool = True,
-                 zipf_perm_seed: int | None = None):
+                 zipf_perm_seed: int | None = None, layout: str = "engine"):
+        """layout: "engine" keeps the experts and the shared expert in the checkpoint
+        layout (self.dev); "tiled" only in the tiled layouts the fused decode kernel
+        streams (self.dev is then that layer); "both" keeps both (self.dev engine,
+        self.dev_tiled tiled)."""
+        assert layout in ("engine", "tiled", "both")
+        self.layout = layout
         self.shape, self.seed, self.layer = shape, seed, layer
         d, E, I = shape.hidden, shape.n_experts, shape.inter
         SI = I * shape.n_shared
@@ -404,24 +420,70 @@ class SynthLayer:
                                b + g.p2_off, b + g.s2_off)
         return tab
 
+    def tiled_sizes(self):
+        """(w1/w3 bytes, w2 bytes, expert bytes) of one expert in the tiled layout"""
+        d, I = self.shape.hidden, self.shape.inter
+        t13 = lib().k3g_tiled_mxfp4_bytes(I, d)
+        t2 = lib().k3g_tiled_mxfp4_bytes(d, I)
+        if not t13 or not t2:
+            raise ValueError(f"shape d={d} I={I} has no tiled layout")
+        return t13, t2, 2 * t13 + t2
+
+    def _upload_table(self, tab) -> "DevBuf":
+        buf = DevBuf(C.sizeof(tab))
+        _check(hip().hipMemcpy(C.c_void_p(buf.ptr), C.cast(tab, C.c_void_p), C.sizeof(tab),
+                               H2D), "table upload")
+        return buf
+
     def to_device(self) -> None:
-        E = self.shape.n_experts
-        self.bank = DevBuf(E * self.geo.nbytes)
-        for e in range(E):
-            self.fill_expert_device(self.bank.ptr + e * self.geo.nbytes, e)
-        sync()
-        tab = self.expert_table(self.bank.ptr)
-        self.d_table = DevBuf(C.sizeof(tab))
-        _check(hip().hipMemcpy(C.c_void_p(self.d_table.ptr), C.cast(tab, C.c_void_p),
-                               C.sizeof(tab), H2D), "table upload")
+        E, g = self.shape.n_experts, self.geo
+        d, I = self.shape.hidden, self.shape.inter
+        L = lib()
+        keep_engine = self.layout in ("engine", "both")
+        if keep_engine:
+            self.bank = DevBuf(E * g.nbytes)
+            for e in range(E):
+                self.fill_expert_device(self.bank.ptr + e * g.nbytes, e)
+            sync()
+            self.d_table = self._upload_table(self.expert_table(self.bank.ptr))
         self.d_gate = DevBuf.from_array(self.gate)
         self.d_bias = DevBuf.from_array(self.bias)
         self.d_sh1 = DevBuf.from_array(self.sh1)
         self.d_sh3 = DevBuf.from_array(self.sh3)
         self.d_sh2 = DevBuf.from_array(self.sh2)
-        self.dev = self.k3g_layer()
+        if self.layout in ("tiled", "both"):
+            t13, t2, te = self.tiled_sizes()
+            self.tbank = DevBuf(E * te)
+            scratch = None if keep_engine else DevBuf(g.nbytes)
+            tab = (K3ExpertQ * E)()
+            for e in range(E):
+                src = self.bank.ptr + e * g.nbytes if keep_engine else scratch.ptr
+                if not keep_engine:
+                    self.fill_expert_device(src, e)
+                tb = self.tbank.ptr + e * te
+                for dst, po, so, rows, cols in ((tb, g.p1_off, g.s1_off, I, d),
+                                                (tb + t13, g.p3_off, g.s3_off, I, d),
+                                                (tb + 2 * t13, g.p2_off, g.s2_off, d, I)):
+                    _check(L.k3g_tile_mxfp4(C.c_void_p(dst), C.c_void_p(src + po),
+                                            C.c_void_p(src + so), rows, cols, None),
+                           "k3g_tile_mxfp4")
+                tab[e] = K3ExpertQ(tb, None, tb + t13, None, tb + 2 * t13, None)
+            sync()
+            del scratch
+            self.d_ttable = self._upload_table(tab)
+            if self.SI:
+                self.d_tsh = []
+                for src, rows, cols in ((self.d_sh1, self.SI, d), (self.d_sh3, self.SI, d),
+                                        (self.d_sh2, d, self.SI)):
+                    t = DevBuf(L.k3g_tiled_bf16_bytes(rows, cols))
+                    _check(L.k3g_tile_bf16(C.c_void_p(t.ptr), C.c_void_p(src.ptr), rows, cols,
+                                           None), "k3g_tile_bf16")
+                    self.d_tsh.append(t)
+                sync()
+            self.dev_tiled = self.k3g_layer(tiled=True)
+        self.dev = self.k3g_layer() if keep_engine else self.dev_tiled
 
-    def k3g_layer(self) -> K3gLayer:
+    def k3g_layer(self, tiled: bool = False) -> K3gLayer:
         s = self.shape
         L = K3gLayer()
         L.hidden, L.n_experts, L.topk, L.inter = s.hidden, s.n_experts, s.topk, s.inter
@@ -430,11 +492,18 @@ class SynthLayer:
         L.act_b1 = L.act_b2 = SWIGLU_CAP
         L.rms_eps = 1e-5
         L.gate, L.bias = self.d_gate.ptr, self.d_bias.ptr
-        L.expert_fmt = 0
-        L.experts = self.d_table.ptr
         L.wdt = K3_WBF16
-        if self.SI:
-            L.sh1, L.sh3, L.sh2 = self.d_sh1.ptr, self.d_sh3.ptr, self.d_sh2.ptr
+        if tiled:
+            L.expert_fmt = K3G_EXPERT_MXFP4_TILED
+            L.experts = self.d_ttable.ptr
+            if self.SI:
+                L.sh1, L.sh3, L.sh2 = (t.ptr for t in self.d_tsh)
+                L.shared_fmt = 1
+        else:
+            L.expert_fmt = K3G_EXPERT_MXFP4
+            L.experts = self.d_table.ptr
+            if self.SI:
+                L.sh1, L.sh3, L.sh2 = self.d_sh1.ptr, self.d_sh3.ptr, self.d_sh2.ptr
         return L
 
     def cfg(self) -> K3Cfg:

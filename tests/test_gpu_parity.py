@@ -29,14 +29,17 @@ def say(msg):
 
 
 def run_layer(layer, x, ctx=None, force=0, fused=True):
+    """fused: the fused decode kernel on the tiled copy of the layer (up to 4 tokens);
+    otherwise the staged kernels on the checkpoint layout."""
     T, d, k = x.shape[0], layer.shape.hidden, layer.shape.topk
+    L = layer.dev_tiled if fused and T <= 4 else layer.dev
     own = ctx is None
-    ctx = ctx or k3moe.Ctx(layer.dev, max_tokens=T)
+    ctx = ctx or k3moe.Ctx(L, max_tokens=T)
     ctx.force_exact(force)
     ctx.set_fused(fused)
     dx = k3moe.DevBuf.from_array(x)
     dout, didx, dwt = k3moe.DevBuf(T * d * 4), k3moe.DevBuf(T * k * 4), k3moe.DevBuf(T * k * 4)
-    ctx.moe(layer.dev, dx.ptr, T, dout.ptr, didx.ptr, dwt.ptr)
+    ctx.moe(L, dx.ptr, T, dout.ptr, didx.ptr, dwt.ptr)
     ctx.sync()
     res = (dout.download(np.float32, T * d).reshape(T, d),
            didx.download(np.int32, T * k).reshape(T, k),
@@ -147,8 +150,9 @@ def test_router_golden(gpu):
 
 @pytest.fixture(scope="module")
 def k2_layer(gpu):
-    say("setup: Kimi-K2-scale layer (d=7168, 384 experts, top-8, I=2048), seed 2024, 9 GB bank")
-    layer = k3moe.SynthLayer(k3moe.K2, seed=2024)
+    say("setup: Kimi-K2-scale layer (d=7168, 384 experts, top-8, I=2048), seed 2024, 9 GB bank "
+        "in the checkpoint layout and 9 GB tiled")
+    layer = k3moe.SynthLayer(k3moe.K2, seed=2024, layout="both")
     yield layer
 
 
@@ -191,13 +195,65 @@ def test_router_ties_and_degenerate(gpu):
     np.testing.assert_array_equal(w, ow)
 
 
+# ------------------------------------------------------------------- tiled layouts ----
+
+def _tile_mxfp4_host(packed, scales, rows, cols):
+    """The tiled MXFP4 layout, written out block by block on the host."""
+    nq = (cols + 511) // 512
+    out = np.zeros((rows // 16) * nq * 4352, np.uint8)
+    for r in range(rows):
+        for b in range(nq * 16):
+            rb, Q, j, g = r // 16, b // 16, (b % 16) // 4, b % 4
+            L = 16 * g + r % 16
+            base = (rb * nq + Q) * 4352
+            live = 32 * b < cols and scales[r, b] != 255
+            out[base + 1024 * j + 16 * L: base + 1024 * j + 16 * L + 16] = (
+                packed[r, 16 * b:16 * b + 16] if live else 0)
+            out[base + 4096 + 4 * L + j] = scales[r, b] if live else 127
+    return out
+
+
+@pytest.mark.parametrize("rows,cols", [(32, 96), (16, 512), (48, 1056)])
+def test_tile_mxfp4_layout(gpu, rows, cols):
+    say(f"case: k3g_tile_mxfp4 rows={rows} cols={cols} (scale 255 blocks included)")
+    packed = k3moe.host_bytes(rows * cols // 2, 11, 1).reshape(rows, cols // 2)
+    scales = k3moe.host_scales(rows * cols // 32, 11, 2, -3, 3).reshape(rows, cols // 32)
+    scales[0, 0] = 255
+    scales[rows - 1, cols // 32 - 1] = 255
+    n = k3moe.lib().k3g_tiled_mxfp4_bytes(rows, cols)
+    dp, ds, dt = k3moe.DevBuf.from_array(packed), k3moe.DevBuf.from_array(scales), k3moe.DevBuf(n)
+    assert k3moe.lib().k3g_tile_mxfp4(dt.ptr, dp.ptr, ds.ptr, rows, cols, None) == 0
+    k3moe.sync()
+    got = dt.download(np.uint8, n)
+    assert np.array_equal(got, _tile_mxfp4_host(packed, scales, rows, cols))
+
+
+def test_tile_bf16_layout(gpu):
+    rows, cols = 48, 96
+    say(f"case: k3g_tile_bf16 rows={rows} cols={cols}")
+    src = k3moe.host_bytes(rows * cols * 2, 12, 1).view(np.uint16).reshape(rows, cols)
+    n = k3moe.lib().k3g_tiled_bf16_bytes(rows, cols)
+    ds, dt = k3moe.DevBuf.from_array(src), k3moe.DevBuf(n)
+    assert k3moe.lib().k3g_tile_bf16(dt.ptr, ds.ptr, rows, cols, None) == 0
+    k3moe.sync()
+    got = dt.download(np.uint16, rows * cols)
+    exp = np.zeros(rows * cols, np.uint16)
+    for rb in range(rows // 16):
+        for c in range(cols // 32):
+            for L in range(64):
+                o = ((rb * (cols // 32) + c) * 64 + L) * 8
+                exp[o:o + 8] = src[16 * rb + L % 16, 32 * c + 8 * (L // 16): 32 * c + 8 * (L // 16) + 8]
+    assert np.array_equal(got, exp)
+    assert k3moe.lib().k3g_tiled_bf16_bytes(40, 96) == 0
+
+
 # ------------------------------------------------------------------------- layer ----
 
 @pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("T", [1, 2, 3, 4, 7])
 def test_layer_tiny_decode(gpu, T, fused):
     say(f"case: k3g_moe tiny layer (d=256, E=16, k=4, I=128), {T} tokens, fused={fused}")
-    layer = k3moe.SynthLayer(k3moe.TINY, seed=1234)
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=1234, layout="both")
     x = layer.tokens(T)
     out, idx, wt = run_layer(layer, x, fused=fused)
     ro, ri, rw = oracle_tokens(layer, x)
@@ -218,6 +274,10 @@ def test_layer_k2_decode_one_token(k2_layer, fused):
         r = rel_l2(out, ro)
         say(f"  token {s}: rel-L2 {r:.3e}")
         assert r <= REL_L2
+        # the staged kernels accumulate in fp32 on the vector ALUs; the fused kernel's
+        # matrix cores see activations split into pieces (residual below 2^-24 of each
+        # block's maximum) and accumulate in their own order
+        assert r <= (1e-4 if fused else 1e-5)
 
 
 def test_layer_k2_fused_repeat_and_force(k2_layer):
@@ -230,6 +290,22 @@ def test_layer_k2_fused_repeat_and_force(k2_layer):
         out, idx, _ = run_layer(layer, x, ctx=ctx, force=1 if rep == 2 else 0)
         assert np.array_equal(idx, ri), rep
         assert rel_l2(out, ro) <= REL_L2, rep
+    ctx.destroy()
+
+
+def test_layer_k2_fused_consecutive_tokens(k2_layer):
+    say("case: fused K2 decode, 6 consecutive launches on one context, a new token each")
+    layer = k2_layer
+    ctx = k3moe.Ctx(layer.dev_tiled, max_tokens=2)
+    for i in range(6):
+        T = 1 + i % 2
+        x = layer.tokens(T, stream_base=80 + 3 * i)
+        out, idx, _ = run_layer(layer, x, ctx=ctx)
+        ro, ri, _ = oracle_tokens(layer, x)
+        assert np.array_equal(idx, ri), i
+        r = rel_l2(out, ro)
+        say(f"  launch {i} ({T} tokens): rel-L2 {r:.3e}")
+        assert r <= 1e-4, i
     ctx.destroy()
 
 

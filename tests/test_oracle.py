@@ -1,0 +1,315 @@
+"""The CPU oracle pinned before it is trusted (no GPU needed).
+
+Each function of the C restatement (oracle/k3_oracle.c) is checked against what fixes it
+independently of the restatement itself:
+  * the reference's own golden vectors (tests/golden/*.npz, exported from
+    tests/fixtures/ops/{router,moe,situ_glu}.json and tests/fixtures/mxfp4.json),
+  * the reference's known-answer hash for the MXFP4 kernel (benchmark inputs, FNV-1a),
+  * closed forms, invariants and brute force on small inputs,
+  * the engine's own compiled kernels (oracle/_ref, built from src/core/k3_ops.c) when
+    they are present,
+so that a plausible slip (a swapped nibble, a dropped scale, a tie broken the wrong way,
+the bias used for the weights) fails at least one of them.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import k3moe
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = json.load(open(os.path.join(GOLDEN, "tolerance.json")))["tolerance"]
+
+
+def _within_tol(got, exp):
+    got = np.asarray(got, np.float64)
+    exp = np.asarray(exp, np.float64)
+    return np.all(np.abs(got - exp) <= TOL["fp32_abs"] + TOL["fp32_rel"] * np.abs(exp))
+
+
+def _sigmoid32(v):
+    v = np.float32(v)
+    return np.float32(1.0) / (np.float32(1.0) + np.exp(-v, dtype=np.float32))
+
+
+# ------------------------------------------------------------------------- router ----
+
+def test_router_golden():
+    """tests/fixtures/ops/router.json: the selected sets and the weights."""
+    d = np.load(os.path.join(GOLDEN, "router.npz"))
+    E, K = int(d["n_experts"]), int(d["top_k"])
+    W = d["gate_weight"].reshape(E, -1)
+    x = d["x"].reshape(-1, W.shape[1])
+    exp_i = d["topk_idx"].reshape(-1, K)
+    exp_w = d["topk_weight"].reshape(-1, K)
+    o = O.oracle()
+    for t in range(x.shape[0]):
+        idx, w = o.router(x[t], W, d["bias"], E, K, 1, 1.0)
+        assert set(idx.tolist()) == set(exp_i[t].tolist()), t
+        for a, e in enumerate(idx):
+            b = list(exp_i[t]).index(e)
+            assert _within_tol(w[a], exp_w[t][b]), (t, a)
+    # the fixture includes rows where the bias changes the selection
+    assert int(d["rows_where_bias_changed_selection"]) > 0
+
+
+def _router_brute(x, W, bias, k, renorm, scale):
+    """Selection by a stable sort on (-choice, index); weights from unbiased scores."""
+    logit = np.array([float(np.sum(W[e].astype(np.float64) * x.astype(np.float64)))
+                      for e in range(W.shape[0])])
+    s = np.array([_sigmoid32(np.float32(l)) for l in logit], np.float32)
+    choice = (s + bias).astype(np.float32)
+    order = sorted(range(len(choice)), key=lambda e: (-float(choice[e]), e))[:k]
+    w = s[order].astype(np.float32)
+    if renorm and k > 1:
+        inv = np.float32(1.0 / (float(np.sum(w.astype(np.float64))) + 1e-20))
+        w = (w * inv).astype(np.float32)
+    return np.array(order, np.int32), (w * np.float32(scale)).astype(np.float32)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_router_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    E, d, k = 12, 40, 4
+    W = rng.normal(0, 0.3, (E, d)).astype(np.float32)
+    x = rng.normal(0, 1, d).astype(np.float32)
+    bias = rng.normal(0, 0.05, E).astype(np.float32)
+    if seed % 2:
+        bias[:] = 0.0
+        bias[3] = bias[7] = 0.125           # exact ties in the bias
+    idx, w = O.oracle().router(x, W, bias, E, k, 1, 2.5)
+    bi, bw = _router_brute(x, W, bias, k, 1, 2.5)
+    assert np.array_equal(idx, bi), (idx, bi)
+    np.testing.assert_allclose(w, bw, rtol=2e-7, atol=0)
+
+
+def test_router_ties_go_to_lowest_index():
+    E, d, k = 8, 16, 3
+    W = np.zeros((E, d), np.float32)
+    x = np.ones(d, np.float32)
+    bias = np.zeros(E, np.float32)
+    idx, w = O.oracle().router(x, W, bias, E, k, 0, 1.0)
+    assert idx.tolist() == [0, 1, 2]
+    assert np.all(w == np.float32(0.5))
+
+
+def test_router_bias_selects_but_does_not_weight():
+    """A large bias on expert 5 must select it; its weight stays its unbiased score."""
+    E, d, k = 8, 16, 2
+    rng = np.random.default_rng(3)
+    W = rng.normal(0, 0.5, (E, d)).astype(np.float32)
+    x = rng.normal(0, 1, d).astype(np.float32)
+    bias = np.zeros(E, np.float32)
+    bias[5] = 10.0
+    idx, w = O.oracle().router(x, W, bias, E, k, 0, 1.0)
+    assert idx[0] == 5
+    assert w[0] == _sigmoid32(np.float32(np.sum(W[5].astype(np.float64) * x.astype(np.float64))))
+    # renormalised: the weights sum to routed_scale * sum(s) / (sum(s) + 1e-20)
+    idx, w = O.oracle().router(x, W, bias, E, k, 1, 2.5)
+    assert abs(float(np.sum(w, dtype=np.float64)) - 2.5) < 1e-6
+
+
+# ------------------------------------------------------------------------- MXFP4 ----
+
+def test_mxfp4_dequant_golden_exact():
+    """tests/fixtures/mxfp4.json: real checkpoint bytes, exact."""
+    m = np.load(os.path.join(GOLDEN, "mxfp4.npz"))
+    packed, scales = m["packed"], m["scales"]
+    rows, pcols = int(m["rows"]), int(m["packed_cols"])
+    deq = O.oracle().dequant(packed, scales, rows, pcols)
+    assert np.array_equal(deq.ravel(), m["expected"].ravel().astype(np.float32))
+    # negative control: the fixture's nibble-swapped first row must NOT match
+    sw = packed.copy()
+    sw[0] = ((sw[0] & 0x0F) << 4) | (sw[0] >> 4)
+    deq_sw = O.oracle().dequant(sw, scales, rows, pcols)
+    assert np.array_equal(deq_sw[0, :64], m["swapped_first64"].astype(np.float32))
+    assert not np.array_equal(deq_sw[0, :64], m["expected"].reshape(rows, -1)[0, :64])
+
+
+def test_mxfp4_dequant_closed_form():
+    lut = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0., -.5, -1, -1.5, -2, -3, -4, -6], np.float32)
+    rng = np.random.default_rng(1)
+    rows, cols = 3, 96
+    packed = rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8)
+    scales = rng.integers(100, 150, (rows, cols // 32), dtype=np.uint8)
+    scales[1, 2] = 255                      # the engine's table maps 255 to 0
+    exp = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        for i in range(cols):
+            b = packed[r, i // 2]
+            code = (b >> 4) if i % 2 else (b & 15)
+            s = scales[r, i // 32]
+            exp[r, i] = 0.0 if s == 255 else lut[code] * np.float32(2.0 ** (int(s) - 127))
+    got = O.oracle().dequant(packed, scales, rows, cols // 2)
+    assert np.array_equal(got, exp)
+
+
+def test_mxfp4_gemv_kat_hash():
+    """The engine's MXFP4 benchmark inputs (xorshift bytes seed 777, x seed 4242, scale
+    byte 127, 3072 x 3584) hash to FNV-1a a231061237b5579d on its AVX2 flat path."""
+    pk = O.kat_b(3072 * 1792, 777)
+    sc = np.full(3072 * 112, 127, np.uint8)
+    x = O.kat_f(3584, 4242)
+    y = O.oracle().matmul_mxfp4(x, pk, sc, 3072)
+    assert O.fnv1a(y) == "a231061237b5579d"
+
+
+@pytest.mark.parametrize("rows,inn", [(7, 64), (33, 1056), (5, 7168)])
+def test_mxfp4_gemv_vs_exact_dequant(rows, inn):
+    """Contract (test_expert.c:227): within 1e-6 of exact dequant + an fp64 dot."""
+    rng = np.random.default_rng(rows)
+    packed = rng.integers(0, 256, rows * inn // 2, dtype=np.uint8)
+    scales = rng.integers(120, 132, rows * inn // 32, dtype=np.uint8)
+    x = rng.normal(0, 1, inn).astype(np.float32)
+    o = O.oracle()
+    W = o.dequant(packed, scales, rows, inn // 2).astype(np.float64)
+    exp = W @ x.astype(np.float64)
+    y = o.matmul_mxfp4(x, packed, scales, rows)
+    ab = np.abs(W) @ np.abs(x.astype(np.float64))
+    assert np.all(np.abs(y - exp) <= 1e-6 * ab + 1e-30)
+
+
+# -------------------------------------------------------------------------- SiTU ----
+
+def test_situ_golden_and_bound():
+    g = np.load(os.path.join(GOLDEN, "situ_glu.npz"))
+    beta = float(g["beta"])
+    x, y = g["x"], g["y"]
+    o = O.oracle()
+    for r in range(x.shape[0]):
+        got = o.situ(x[r], beta, float(g["linear_beta"]))
+        assert _within_tol(got, y[r]), r
+        assert np.all(np.abs(got) <= beta * float(g["linear_beta"]) * (1 + 1e-6))
+
+
+def test_swiglu_is_situ_at_2_100():
+    rng = np.random.default_rng(4)
+    n = 64
+    gu = rng.normal(0, 3, 2 * n).astype(np.float32)
+    y = O.oracle().situ(gu, k3moe.SWIGLU_CAP, k3moe.SWIGLU_CAP)
+    g, u = gu[:n], gu[n:]
+    # sigmoid with expf taken as the float rounding of the double exp (glibc's expf
+    # agrees with it to within an ulp), so allow one ulp of the product
+    sig = (1.0 / (1.0 + np.exp(-g.astype(np.float64)).astype(np.float32))).astype(np.float32)
+    exp = ((g * sig).astype(np.float32) * u).astype(np.float32)
+    np.testing.assert_allclose(y, exp, rtol=3e-7, atol=0)
+
+
+# --------------------------------------------------------------------------- MoE ----
+
+def _moe_golden():
+    d = np.load(os.path.join(GOLDEN, "moe.npz"))
+    cfg = k3moe.K3Cfg()
+    cfg.hidden, cfg.latent, cfg.moe_inter = int(d["hidden"]), int(d["latent"]), int(d["moe_inter"])
+    cfg.n_experts, cfg.topk, cfg.n_shared = int(d["n_experts"]), int(d["top_k"]), int(d["n_shared"])
+    cfg.routed_scale, cfg.moe_renorm = float(d["routed_scale"]), int(d["renorm"])
+    cfg.latent_norm, cfg.rms_eps = int(d["latent_norm"]), float(d["rms_eps"])
+    cfg.situ_b1, cfg.situ_b2 = float(d["situ_b1"]), float(d["situ_b2"])
+    keep = {k: np.ascontiguousarray(d[k], np.float32) for k in d.files
+            if d[k].dtype == np.float32 and d[k].ndim > 0}
+    w = k3moe.K3MoeW()
+    w.gate, w.bias = keep["gate_weight"].ctypes.data, keep["e_score_correction_bias"].ctypes.data
+    w.w1, w.w3, w.w2 = keep["w1"].ctypes.data, keep["w3"].ctypes.data, keep["w2"].ctypes.data
+    w.latent_norm = keep["norm_weight"].ctypes.data
+    w.down, w.up = keep["down_weight"].ctypes.data, keep["up_weight"].ctypes.data
+    w.sh1, w.sh3 = keep["shared_w1_weight"].ctypes.data, keep["shared_w3_weight"].ctypes.data
+    w.sh2 = keep["shared_w2_weight"].ctypes.data
+    return w, cfg, keep
+
+
+def test_moe_golden():
+    """tests/fixtures/ops/moe.json (LatentMoE: latent down/up, RMSNorm, SiTU, shared)."""
+    w, cfg, keep = _moe_golden()
+    x = keep["in"].reshape(-1, cfg.hidden)
+    out, _, _ = O.oracle().moe(w, cfg, x)
+    assert _within_tol(out, keep["out"].reshape(out.shape))
+    outp, _, _ = O.oracle().moe(w, cfg, x, prefill=True)
+    assert np.array_equal(out, outp)        # prefill is bit-identical per token
+
+
+def test_k2_weights_sum_to_routed_scale():
+    """Renormalised routing weights of the K2 layer sum to routed_scale."""
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=21, device=False)
+    x = layer.tokens(1)
+    out, idx, wt = O.k2_forward(layer, x)
+    assert wt.dtype == np.float32 and idx.shape == (layer.shape.topk,)
+    # the weights are the renormalised unbiased scores times routed_scale
+    assert abs(float(np.sum(wt, dtype=np.float64)) - layer.shape.routed_scale) < 1e-5
+    assert np.isfinite(out).all()
+
+
+# -------------------------------------------------------- against the engine itself ----
+
+ref = O.ref()
+needs_ref = pytest.mark.skipif(ref is None, reason="oracle/_ref not built (no reference "
+                                                   "sources on this machine)")
+
+
+@needs_ref
+def test_ref_router_bit_identical():
+    rng = np.random.default_rng(9)
+    E, d, k = 384, 7168, 8
+    W = rng.normal(0, 0.02, (E, d)).astype(np.float32)
+    b = rng.normal(0, 0.01, E).astype(np.float32)
+    for t in range(4):
+        x = rng.normal(0, 1, d).astype(np.float32)
+        a = O.oracle().router(x, W, b, E, k, 1, 2.5)
+        r = ref.router(x, W, b, E, k, 1, 2.5)
+        assert np.array_equal(a[0], r[0]) and np.array_equal(a[1], r[1])
+
+
+@needs_ref
+def test_ref_mxfp4_and_bf16_bit_identical():
+    pk = O.kat_b(257 * 1792, 5)
+    sc = (O.kat_b(257 * 112, 6) % 9 + 122).astype(np.uint8)
+    x = O.kat_f(3584, 7)
+    assert np.array_equal(O.oracle().matmul_mxfp4(x, pk, sc, 257), ref.matmul_mxfp4(x, pk, sc, 257))
+    Wb = O.kat_bf16(129 * 3584, 8)
+    assert np.array_equal(O.oracle().matmul_bf16(x, Wb, 129), ref.matmul_bf16(x, Wb, 129))
+
+
+@needs_ref
+def test_ref_moe_golden_bit_identical():
+    w, cfg, keep = _moe_golden()
+    x = keep["in"].reshape(-1, cfg.hidden)
+    assert np.array_equal(O.oracle().moe(w, cfg, x)[0], ref.moe(w, cfg, x)[0])
+
+
+@needs_ref
+def test_k2_layer_matches_engine_with_identity_latent():
+    """The K2 layer without latent projections equals the engine's k3_moe with bf16
+    identity down/up matrices, bit for bit, decode and prefill."""
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=1234, device=False)
+    x = layer.tokens(4)
+    a, ia, _ = O.k2_forward(layer, x)
+    b, ib, _ = O.k2_forward(layer, x, k=ref, identity=True)
+    assert np.array_equal(a, b) and np.array_equal(ia, ib)
+    ap, _, _ = O.k2_forward(layer, x, prefill=True)
+    assert np.array_equal(ap, a)
+
+
+# ------------------------------------------------------------------------- cache ----
+
+def test_lru_replay_of_the_real_routing_trace():
+    """docs/data/expert-cache-capacity.txt:23-28: LRU hit rates of the 100,096-request
+    K3 trace at 8/64/128/192 GB of 17,547,264-byte slots."""
+    pairs = np.load(os.path.join(GOLDEN, "expert_trace.npz"))["pairs"]
+    keys = (pairs[:, 0].astype(np.int64) * 896 + pairs[:, 1]).astype(np.int32)
+    n = keys.size
+    assert n == 100096
+    for gb, pct in ((8, 36.24), (64, 36.24), (128, 49.19), (192, 90.00)):
+        slots = int(gb * 1e9 // 17547264)
+        hits = O.lru_hits(keys, 93 * 896, slots)
+        assert abs(100.0 * hits / n - pct) < 0.005, (gb, hits)
+
+
+def test_lru_small_cases():
+    keys = np.array([0, 1, 2, 0, 1, 3, 0, 4, 1], np.int32)
+    # capacity 2: 0,1 miss; 2 miss (evict 0); 0 miss (evict 1); 1 miss; 3 miss; 0 miss; 4 miss; 1 miss
+    assert O.lru_hits(keys, 5, 2) == 0
+    # capacity 3: hits at the 2nd 0 and 1, then 0 again, 1 evicted by 4? 3 evicts 2
+    assert O.lru_hits(keys, 5, 3) == 3
+    assert O.lru_hits(keys, 5, 5) == keys.size - 5
