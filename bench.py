@@ -36,6 +36,12 @@ B_ROUTER = 4 * E * D + 4 * E               # 11,011,584: fp32 gate + bias
 B_TOKEN = D * 2 + D * 4                    # bf16-valued input, fp32 output
 B_GATEUP_EXPERT = 2 * (I * D // 2 + I * D // 32)   # w1 + w3 of one expert
 
+# HBM bytes per launch of the fused decode kernel on this workload, from two rocprofv3
+# --pmc runs (FETCH_SIZE x 1.9996 + WRITE_SIZE x 1.0, the factors that make a 256 MiB
+# device-to-device copy read 256 MiB); the run and the numbers are in
+# profiles/k_decode_fused_k2_decode.md. Re-measured whenever the kernel changes.
+TRAFFIC_FUSED = 294602314
+
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
@@ -95,6 +101,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one 256 MiB device-to-device copy (a counter calibration "
+                         "point for rocprofv3 --pmc runs), outside the timed region")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (this build runs "
@@ -122,6 +131,13 @@ def main():
         ctx.moe(layers[i % a.layers].dev, dx.ptr + i * D * 4, 1, dout.ptr + i * D * 4,
                 didx.ptr + i * K * 4, dwt.ptr + i * K * 4)
 
+    if a.calib_copy:
+        n = 256 << 20
+        src, dst = k3moe.DevBuf(n), k3moe.DevBuf(n)
+        k3moe._check(k3moe.hip().hipMemcpy(k3moe.C.c_void_p(dst.ptr), k3moe.C.c_void_p(src.ptr),
+                                           n, k3moe.D2D), "calibration copy")
+        k3moe.sync()
+        del src, dst
     log(f"bench: warmup {a.warmup} steps")
     for i in range(a.warmup):
         step(i)
@@ -151,10 +167,12 @@ def main():
         kern = "k_decode_fused (whole layer: router, top-k, shared + routed MXFP4 GEMVs, combine)"
         k_us = 1e3 * ms_stage[8] / n_stage[8]
         k_bytes = layer_bytes
+        traffic = TRAFFIC_FUSED
     else:
         kern = "k_routed_gateup (MXFP4 gate+up GEMV, SwiGLU epilogue)"
         k_us = 1e3 * ms_stage[2] / max(n_stage[2], 1)
         k_bytes = K * B_GATEUP_EXPERT
+        traffic = None
     achieved = k_bytes / (k_us * 1e-6) / 1e9
     res = {
         "metric": METRIC,
@@ -180,7 +198,7 @@ def main():
         "stage_us": stage_us,
         "roofline": {"kernel": kern, "bound": "hbm", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": k_bytes,
+                     "traffic": traffic, "bytes_per_launch": k_bytes,
                      "avg_launch_us": round(k_us, 2)},
     }
     ctx.destroy()
