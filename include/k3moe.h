@@ -252,10 +252,10 @@ int  k3g_ctx_stage_ms(K3gCtx *ctx, double *ms, int64_t *count, int n);
  * (default on); off forces the staged kernels. No reference counterpart. */
 void k3g_ctx_set_fused(K3gCtx *ctx, int on);
 
-/* Instrumentation: with a device buffer of 2 * tickets + 2 uint64, the fused kernel writes
- * each ticket's start and end wall-clock stamps (100 MHz counter), then the top-k ticket's
- * stamps after its wait and after its selection. NULL turns it off. No reference
- * counterpart. */
+/* Instrumentation: with a device buffer of 3 * tickets + 5 uint64, the fused kernel writes
+ * for each ticket its start, the end of its waits and its end as wall-clock stamps
+ * (100 MHz counter), then the top-k ticket's stamps after its wait, after its selection
+ * and inside the selection. NULL turns it off. No reference counterpart. */
 void k3g_ctx_set_trace(K3gCtx *ctx, void *dev_buf);
 
 /* Force the router's exact re-routing path: 0 normal, 1 every token re-routes its

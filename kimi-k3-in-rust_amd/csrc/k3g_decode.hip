@@ -84,9 +84,11 @@ struct K3Geo {
     int KSS, KSG, KSD, KSR, KSDN; /* K slices of SG, G, SD, R, D tickets */
     int nRc;                     /* router 1024-column chunks */
     int nSGt, nGt, nSDt, nDt;    /* row tiles */
-    int nX, nR, nSG, nG, nSD, nD, nC, total;
+    int nX, nR, nSG, nG, nSD, nD, total;
+    int oSG, oG, oSD, oD;        /* first ticket of each class after S */
     /* counter lines */
-    int lR, lSD, lD, lTSG, lTG, lRE, cX, cSGF, cGF, eX, eSEL, eSGF, eGF, nlines;
+    int lR, lSD, lD, lTSG, lTG, lRE, lDT, cX, cX16, cR, cSGF, cGF, eX, eX16, eR, eSEL, eSGF,
+        eGF, nlines;
 };
 
 __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int SI)
@@ -114,8 +116,11 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.nG = g.P * g.nGt * g.KSG;
     g.nSD = g.nSDt * g.KSD;
     g.nD = g.P * g.nDt * g.KSDN;
-    g.nC = (d + C_ROWS - 1) / C_ROWS;
-    g.total = g.nX + g.nR + 1 + g.nSG + g.nG + g.nSD + g.nD + g.nC;
+    g.total = g.nX + g.nR + 1 + g.nSG + g.nG + g.nSD + g.nD;
+    g.oSG = g.nX + g.nR + 1;
+    g.oG = g.oSG + g.nSG;
+    g.oSD = g.oG + g.nG;
+    g.oD = g.oSD + g.nSD;
     /* counters: one 128-byte line each; events: a counter plus NREP replicated flags */
     g.lR = 0;
     g.lSD = g.lR + NSUB;
@@ -123,11 +128,16 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.lTSG = g.lD + g.P;
     g.lTG = g.lTSG + g.nSGt;
     g.lRE = g.lTG + g.P * g.nGt;
-    g.cX = g.lRE + E;
-    g.cSGF = g.cX + 1;
+    g.lDT = g.lRE + E;
+    g.cX = g.lDT + g.nDt;
+    g.cX16 = g.cX + 1;
+    g.cR = g.cX16 + 1;
+    g.cSGF = g.cR + 1;
     g.cGF = g.cSGF + 1;
     g.eX = g.cGF + g.P;
-    g.eSEL = g.eX + K3_EVLINES;
+    g.eX16 = g.eX + K3_EVLINES;
+    g.eR = g.eX16 + K3_EVLINES;
+    g.eSEL = g.eR + K3_EVLINES;
     g.eSGF = g.eSEL + K3_EVLINES;
     g.eGF = g.eSGF + K3_EVLINES;
     g.nlines = g.eGF + g.P * K3_EVLINES;
@@ -219,6 +229,12 @@ __device__ __forceinline__ void k3d_set_event(int *sync, int ev, int lane)
 __device__ __forceinline__ void k3d_arrive_event(int *sync, int ctr, int count, int ev, int lane)
 {
     if (k3d_arrive(k3d_line(sync, ctr), count - 1, lane)) k3d_set_event(sync, ev, lane);
+}
+
+/* Instrumentation: the moment a ticket's waits are over (its second trace stamp). */
+__device__ __forceinline__ void k3d_trace_go(unsigned long long *trace, int tkg, int lane)
+{
+    if (trace && lane == 0) trace[3 * tkg + 1] = wall_clock64();
 }
 
 /* ----------------------------------------------------------- buffer access ---- */
@@ -435,6 +451,16 @@ struct K3Dec {
         const bool on = col < a.d;
         const float v = on ? a.x[(size_t)t * a.d + col] : 0.0f;
         const int Q = b >> 4;
+        /* the bf16 pieces first: the shared expert's tickets wait only for these */
+        float r2 = v;
+#pragma unroll
+        for (int pc = 0; pc < NPC16; ++pc) {
+            float back;
+            const uint32_t h = k3d_bf16_rn(r2, back);
+            r2 -= back;
+            if (on) k3d_st16_sc1(r16, k3d_b16_off(col, NPC16 * t + pc), h);
+        }
+        k3d_arrive_event(a.sync, G.cX16, G.nX, G.eX16, lane);
         float r = v;
 #pragma unroll
         for (int pc = 0; pc < NPC8; ++pc) {
@@ -444,14 +470,6 @@ struct K3Dec {
                 k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_data(b, e, pc), q);
                 if (e == 0) k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_scale(b, pc), sx + 127);
             }
-        }
-        float r2 = v;
-#pragma unroll
-        for (int pc = 0; pc < NPC16; ++pc) {
-            float back;
-            const uint32_t h = k3d_bf16_rn(r2, back);
-            r2 -= back;
-            if (on) k3d_st16_sc1(r16, k3d_b16_off(col, NPC16 * t + pc), h);
         }
         k3d_arrive_event(a.sync, G.cX, G.nX, G.eX, lane);
     }
@@ -534,7 +552,7 @@ struct K3Dec {
             const float4 v = k3d_route_score(sv, bv, a.bias ? a.bias[e] : 0.0f, a.d);
             k3d_st4_sc1(rr, (lane * a.E + e) * 16, k3v4f{v.x, v.y, v.z, v.w});
         }
-        k3d_signal(k3d_line(a.sync, G.lR + e % NSUB), lane);
+        k3d_arrive_event(a.sync, G.cR, a.E, G.eR, lane);
     }
 
     /* ----------------------------------------------------------------- S ---- */
@@ -542,18 +560,16 @@ struct K3Dec {
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
-        if (!k3d_wait_sum(a.sync, G.lR, NSUB, a.E, a.spin_limit, a.err,
-                          lane))
-            return;
+        if (!k3d_wait_event(a.sync, G.eR, 0, a.spin_limit, a.err, lane)) return;
         /* instrumentation: after the trace's [ticket][2] stamps, the select's own phases */
-        if (a.trace && lane == 0) a.trace[2 * G.total] = wall_clock64();
+        if (a.trace && lane == 0) a.trace[3 * G.total] = wall_clock64();
         /* everything routed waits for this wave: let it issue ahead of its SIMD's others */
         __builtin_amdgcn_s_setprio(3);
         for (int t = 0; t < a.T; ++t)
             k3d_select_token(lds, t, (const float4 *)a.rs, a.bias, a.gate, a.x, a.d, a.E, a.k,
                              a.renorm, a.routed_scale, a.idx, a.wt, a.force, a.stats, lane,
-                             a.trace && t == 0 ? a.trace + 2 * G.total + 2 : nullptr);
-        if (a.trace && lane == 0) a.trace[2 * G.total + 1] = wall_clock64();
+                             a.trace && t == 0 ? a.trace + 3 * G.total + 2 : nullptr);
+        if (a.trace && lane == 0) a.trace[3 * G.total + 1] = wall_clock64();
         /* the routed tickets also need x's pieces: publish the routing once both exist */
         if (!k3d_wait_event(a.sync, G.eX, 0, a.spin_limit, a.err, lane)) return;
         k3d_set_event(a.sync, G.eSEL, lane);
@@ -568,13 +584,13 @@ struct K3Dec {
         const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
         const int st = tk / G.KSS, ks = tk - st * G.KSS;
         const int c0 = ks * G.nCd / G.KSS, c1 = (ks + 1) * G.nCd / G.KSS;
-        if (!k3d_wait_event(a.sync, G.eX, tk, a.spin_limit, a.err, lane)) return;
         const size_t mb = (size_t)a.SI * a.d * 2;
         const K3Rsrc r1 = k3d_rsrc(a.sh1, mb), r3 = k3d_rsrc(a.sh3, mb);
         const K3Rsrc rb = k3d_rsrc(a.xq16, (size_t)G.nCd * 1024);
         const bool bon = (lane & 15) < NPC16 * a.T;
         k3v4f g = {0, 0, 0, 0}, u = {0, 0, 0, 0};
         const int abase = st * G.nCd * 1024 + lane * 16;
+        bool first = true;
         for (int cb = c0; cb < c1; cb += 8) {
             uint4 A1[8], A3[8], B[8];
 #pragma unroll
@@ -582,6 +598,16 @@ struct K3Dec {
                 const int c = cb + i;
                 A1[i] = k3d_b128(r1, c < c1 ? abase + c * 1024 : K3_OOB);
                 A3[i] = k3d_b128(r3, c < c1 ? abase + c * 1024 : K3_OOB);
+            }
+            if (first) {
+                /* the first weights stream in while x's bf16 pieces are made */
+                if (!k3d_wait_event(a.sync, G.eX16, tk, a.spin_limit, a.err, lane)) return;
+                k3d_trace_go(a.trace, G.oSG + tk, lane);
+                first = false;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = cb + i;
                 B[i] = k3d_b128<K3_BPOL>(rb, bon && c < c1 ? c * 1024 + lane * 16 : K3_OOB);
             }
 #pragma unroll
@@ -632,6 +658,7 @@ struct K3Dec {
         const int gt = rem / G.KSG, ks = rem - gt * G.KSG;
         const int q0 = ks * G.nQd / G.KSG, q1 = (ks + 1) * G.nQd / G.KSG;
         if (!k3d_wait_event(a.sync, G.eSEL, tk, a.spin_limit, a.err, lane)) return;
+        k3d_trace_go(a.trace, G.oG + tk, lane);
         const int e = k3d_uniform(__hip_atomic_load(&a.idx[p], __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT));
         const int t = p / a.k;
@@ -729,12 +756,12 @@ struct K3Dec {
         const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
         const int rt = tk / G.KSD, ks = tk - rt * G.KSD;
         const int c0 = ks * G.nCsi / G.KSD, c1 = (ks + 1) * G.nCsi / G.KSD;
-        if (!k3d_wait_event(a.sync, G.eSGF, tk, a.spin_limit, a.err, lane)) return;
         const K3Rsrc r2 = k3d_rsrc(a.sh2, (size_t)a.d * a.SI * 2);
         const K3Rsrc rb = k3d_rsrc(a.hq16, (size_t)G.nCsi * 1024);
         const bool bon = (lane & 15) < NPC16 * a.T;
         k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
         const int o0 = 2 * rt * G.nCsi * 1024 + lane * 16, o1 = o0 + G.nCsi * 1024;
+        bool first = true;
         for (int cb = c0; cb < c1; cb += 8) {
             uint4 A0[8], A1[8], B[8];
 #pragma unroll
@@ -742,6 +769,15 @@ struct K3Dec {
                 const int c = cb + i;
                 A0[i] = k3d_b128(r2, c < c1 ? o0 + c * 1024 : K3_OOB);
                 A1[i] = k3d_b128(r2, c < c1 ? o1 + c * 1024 : K3_OOB);
+            }
+            if (first) {   /* the first weights stream in while the shared h is finished */
+                if (!k3d_wait_event(a.sync, G.eSGF, tk, a.spin_limit, a.err, lane)) return;
+                k3d_trace_go(a.trace, G.oSD + tk, lane);
+                first = false;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = cb + i;
                 B[i] = k3d_b128<K3_BPOL>(rb, bon && c < c1 ? c * 1024 + lane * 16 : K3_OOB);
             }
 #pragma unroll
@@ -759,7 +795,8 @@ struct K3Dec {
             k3d_st4_sc1(rp, ((ks * a.T + t) * a.d + row) * 4, y0);
             k3d_st4_sc1(rp, ((ks * a.T + t) * a.d + row + 16) * 4, y1);
         }
-        k3d_signal(k3d_line(a.sync, G.lSD + tk % NSUB), lane);
+        if (k3d_arrive(k3d_line(a.sync, G.lDT + rt), G.P * G.KSDN + G.KSD - 1, lane))
+            combine_rows(a, G, rt, lane);
     }
 
     /* ----------------------------------------------------------------- D ---- */
@@ -772,8 +809,7 @@ struct K3Dec {
         const int p = tk / per, rem = tk - p * per;
         const int dt = rem / G.KSDN, ks = rem - dt * G.KSDN;
         const int q0 = ks * G.nQi / G.KSDN, q1 = (ks + 1) * G.nQi / G.KSDN;
-        if (!k3d_wait_event(a.sync, G.eGF + p * K3_EVLINES, tk, a.spin_limit, a.err, lane))
-            return;
+        if (!k3d_wait_event(a.sync, G.eSEL, tk, a.spin_limit, a.err, lane)) return;
         const int e = k3d_uniform(__hip_atomic_load(&a.idx[p], __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT));
         k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
@@ -784,6 +820,7 @@ struct K3Dec {
             const bool bon = (lane & 15) < NPC8;
             const int rs = G.nQi * K3G_QT;
             const int o0 = 2 * dt * rs + lane * 16, o1 = o0 + rs;
+            bool first = true;
             for (int Q = q0; Q < q1; ++Q) {
                 const int qo = Q * K3G_QT;
                 uint4 A[2][4];
@@ -794,6 +831,13 @@ struct K3Dec {
                 }
                 const int so = qo + 4096 + lane * 4 - lane * 16;
                 const uint32_t s0 = k3d_b32(r2, o0 + so), s1 = k3d_b32(r2, o1 + so);
+                if (first) {   /* the first weights stream in while this pair's h finishes */
+                    if (!k3d_wait_event(a.sync, G.eGF + p * K3_EVLINES, tk, a.spin_limit,
+                                        a.err, lane))
+                        return;
+                    k3d_trace_go(a.trace, G.oD + tk, lane);
+                    first = false;
+                }
                 uint4 B[4][2];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -821,28 +865,22 @@ struct K3Dec {
             k3d_st4_sc1(rc, ((p * G.KSDN + ks) * a.d + row) * 4, y0);
             k3d_st4_sc1(rc, ((p * G.KSDN + ks) * a.d + row + 16) * 4, y1);
         }
-        k3d_signal(k3d_line(a.sync, G.lD + p), lane);
+        if (k3d_arrive(k3d_line(a.sync, G.lDT + dt), G.P * G.KSDN + G.KSD - 1, lane))
+            combine_rows(a, G, dt, lane);
     }
 
-    /* ----------------------------------------------------------------- C ---- */
-    static __device__ __noinline__ void combine(K3ArgPtr ap, int tk_, int lane)
+    /* ------------------------------------------------------------ combine ---- */
+    /* Rows 32 dt .. 32 dt + 31 of the output, once every routed slot's down-projection
+     * slices and the shared expert's slices for them are in: slots in the engine's order
+     * (float multiply, then add), then + the shared output (slices summed in order).
+     * Lane r < 32 owns row 32 dt + r. */
+    static __device__ void combine_rows(const K3kDecode &a, const K3Geo &G, int dt, int lane)
     {
-        const K3kDecode a = *k3d_uniform_cptr(ap);
-        const int tk = k3d_uniform(tk_);
-        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
-        for (int p0 = 0; p0 < G.P; p0 += 64)
-            if (!k3d_wait_sum(a.sync, G.lD + p0, min(64, G.P - p0),
-                              (long long)G.nDt * G.KSDN * min(64, G.P - p0), a.spin_limit,
-                              a.err, lane))
-                return;
-        if (a.SI > 0 && !k3d_wait_sum(a.sync, G.lSD, NSUB, G.nSD,
-                                      a.spin_limit, a.err, lane))
-            return;
-        const int row = tk * C_ROWS + lane * 4;
+        const int row = 32 * dt + (lane & 31);
         const K3Rsrc rc = k3d_rsrc(a.contrib, (size_t)G.P * G.KSDN * a.d * 4);
         const K3Rsrc rs = k3d_rsrc(a.shpart, (size_t)(G.KSD > 0 ? G.KSD : 1) * a.T * a.d * 4);
         for (int t = 0; t < a.T; ++t) {
-            float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
+            float c = 0.0f;
             for (int j = 0; j < a.k; ++j) {
                 const int p = t * a.k + j;
                 const int e = k3d_uniform(__hip_atomic_load(&a.idx[p], __ATOMIC_RELAXED,
@@ -850,31 +888,18 @@ struct K3Dec {
                 if (e < 0 || e >= a.E) continue;
                 const float w = __hip_atomic_load(&a.wt[p], __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT);
-                float y0 = 0.0f, y1 = 0.0f, y2 = 0.0f, y3 = 0.0f;
-                for (int q = 0; q < G.KSDN; ++q) {
-                    const uint4 y = k3d_b128<K3_BPOL>(
-                        rc, row < a.d ? ((p * G.KSDN + q) * a.d + row) * 4 : K3_OOB);
-                    y0 += __uint_as_float(y.x); y1 += __uint_as_float(y.y);
-                    y2 += __uint_as_float(y.z); y3 += __uint_as_float(y.w);
-                }
-                c0 = __fadd_rn(c0, __fmul_rn(w, y0));
-                c1 = __fadd_rn(c1, __fmul_rn(w, y1));
-                c2 = __fadd_rn(c2, __fmul_rn(w, y2));
-                c3 = __fadd_rn(c3, __fmul_rn(w, y3));
+                float y = 0.0f;
+                for (int q = 0; q < G.KSDN; ++q)
+                    y += __uint_as_float(k3d_b32<K3_BPOL>(rc, ((p * G.KSDN + q) * a.d + row) * 4));
+                c = __fadd_rn(c, __fmul_rn(w, y));
             }
             if (a.SI > 0) {
-                float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
-                for (int q = 0; q < G.KSD; ++q) {
-                    const uint4 v = k3d_b128<K3_BPOL>(rs, row < a.d ? ((q * a.T + t) * a.d + row) * 4
-                                                                   : K3_OOB);
-                    s0 += __uint_as_float(v.x); s1 += __uint_as_float(v.y);
-                    s2 += __uint_as_float(v.z); s3 += __uint_as_float(v.w);
-                }
-                c0 = __fadd_rn(c0, s0); c1 = __fadd_rn(c1, s1);
-                c2 = __fadd_rn(c2, s2); c3 = __fadd_rn(c3, s3);
+                float sh = 0.0f;
+                for (int q = 0; q < G.KSD; ++q)
+                    sh += __uint_as_float(k3d_b32<K3_BPOL>(rs, ((q * a.T + t) * a.d + row) * 4));
+                c = __fadd_rn(c, sh);
             }
-            if (row < a.d)
-                *(float4 *)(a.out + (size_t)t * a.d + row) = make_float4(c0, c1, c2, c3);
+            if (lane < 32) a.out[(size_t)t * a.d + row] = c;
         }
     }
 };
@@ -896,7 +921,11 @@ k_decode_fused(K3kDecode a)
         for (int i = lo + lane; i < hi; i += 64) a.sync_clear[i] = 0;
     }
     for (int tk = w; tk < G.total; tk += W) {
-        if (a.trace && lane == 0) a.trace[2 * tk] = wall_clock64();
+        if (a.trace && lane == 0) {
+            const unsigned long long now = wall_clock64();
+            a.trace[3 * tk] = now;
+            a.trace[3 * tk + 1] = now;
+        }
         int t = tk;
         if (t < G.nX) K3Dec<NT>::prep(ap, t, lane);
         else if ((t -= G.nX) < G.nR) K3Dec<NT>::router(ap, t, lane);
@@ -904,9 +933,8 @@ k_decode_fused(K3kDecode a)
         else if ((t -= 1) < G.nSG) K3Dec<NT>::shared_gateup(ap, t, lane);
         else if ((t -= G.nSG) < G.nG) K3Dec<NT>::routed_gateup(ap, t, lane);
         else if ((t -= G.nG) < G.nSD) K3Dec<NT>::shared_down(ap, t, lane);
-        else if ((t -= G.nSD) < G.nD) K3Dec<NT>::routed_down(ap, t, lane);
-        else K3Dec<NT>::combine(ap, t - G.nD, lane);
-        if (a.trace && lane == 0) a.trace[2 * tk + 1] = wall_clock64();
+        else K3Dec<NT>::routed_down(ap, t - G.nSD, lane);
+        if (a.trace && lane == 0) a.trace[3 * tk + 2] = wall_clock64();
     }
 }
 

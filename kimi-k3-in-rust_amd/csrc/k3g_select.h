@@ -69,19 +69,24 @@ __device__ __forceinline__ uint32_t k3d_dpp(uint32_t v)
     return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWS, 0xf, false);
 }
 
-__device__ __forceinline__ uint64_t k3d_wave_max_u64(uint64_t key)
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint64_t k3d_dpp_max_step(uint64_t k)
 {
-    uint32_t lo = (uint32_t)key, hi = (uint32_t)(key >> 32);
-#define K3_MAX_STEP(C, R)                                                                    \
-    {                                                                                        \
-        const uint32_t ol = k3d_dpp<C, R>(lo), oh = k3d_dpp<C, R>(hi);                       \
-        if (oh > hi || (oh == hi && ol > lo)) { hi = oh; lo = ol; }                          \
-    }
-    K3_MAX_STEP(0x111, 0xf) K3_MAX_STEP(0x112, 0xf) K3_MAX_STEP(0x114, 0xf)
-    K3_MAX_STEP(0x118, 0xf) K3_MAX_STEP(0x142, 0xa) K3_MAX_STEP(0x143, 0xc)
-#undef K3_MAX_STEP
-    hi = __builtin_amdgcn_readlane(hi, 63);
-    lo = __builtin_amdgcn_readlane(lo, 63);
+    const uint64_t o = ((uint64_t)k3d_dpp<CTRL, ROWS>((uint32_t)(k >> 32)) << 32) |
+                       k3d_dpp<CTRL, ROWS>((uint32_t)k);
+    return o > k ? o : k;
+}
+
+__device__ __forceinline__ uint64_t k3d_wave_max_u64(uint64_t k)
+{
+    k = k3d_dpp_max_step<0x111, 0xf>(k);   /* row_shr:1 */
+    k = k3d_dpp_max_step<0x112, 0xf>(k);   /* row_shr:2 */
+    k = k3d_dpp_max_step<0x114, 0xf>(k);   /* row_shr:4 */
+    k = k3d_dpp_max_step<0x118, 0xf>(k);   /* row_shr:8 */
+    k = k3d_dpp_max_step<0x142, 0xa>(k);   /* row_bcast:15 */
+    k = k3d_dpp_max_step<0x143, 0xc>(k);   /* row_bcast:31 */
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(k >> 32), 63);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)k, 63);
     return ((uint64_t)hi << 32) | lo;
 }
 
@@ -131,6 +136,15 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
     }
     if (stamp && lane == 0) stamp[0] = wall_clock64();
 
+    /* the engine's order as one unsigned key per expert: (ordered choice, ~index); 0 for
+     * experts that cannot win (past E, NaN or -inf choice) or are taken */
+    uint64_t key[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int e = lane + 64 * i;
+        key[i] = e < E && v[i].x > -INFINITY
+                     ? ((uint64_t)k3d_ordered(v[i].x) << 32) | (uint32_t)~e : 0;
+    }
     uint32_t taken = 0;
     bool ok = !force;
     float minlo = INFINITY;
@@ -138,24 +152,26 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
     int my_sel = -1;          /* lane j: the j-th selected expert */
     float my_score = 0.0f;
     for (int j = 0; j < k; ++j) {
-        float bv = -INFINITY;
-        int bi = -1;
+        /* this lane's best untaken key: a tree over the slots */
+        uint64_t m[NPL];
 #pragma unroll
-        for (int i = 0; i < NPL; ++i)
-            if (lane + 64 * i < E && !((taken >> i) & 1u) && v[i].x > bv) {
-                bv = v[i].x;
-                bi = lane + 64 * i;
-            }
-        const uint64_t key = bi >= 0 ? ((uint64_t)k3d_ordered(bv) << 32) | (uint32_t)~bi : 0;
-        const uint64_t win = k3d_wave_max_u64(key);
+        for (int i = 0; i < NPL; ++i) m[i] = key[i];
+#pragma unroll
+        for (int h = NPL / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int i = 0; i < h; ++i) m[i] = m[i + h] > m[i] ? m[i + h] : m[i];
+        const uint64_t win = k3d_wave_max_u64(m[0]);
         const int w = win ? (int)~(uint32_t)win : -1;       /* uniform */
         float wlo = 0.0f, whi = 0.0f, wsc = 0.0f;
         if (w >= 0) {
-            const int slot = w >> 6, wl = w & 63;
+            const int slot = w >> 6, wl = w & 63;           /* uniform */
             float lo = 0.0f, hi = 0.0f, sc = 0.0f;
 #pragma unroll
             for (int i = 0; i < NPL; ++i)
-                if (i == slot) { lo = v[i].y; hi = v[i].z; sc = v[i].w; }
+                if (i == slot) {
+                    lo = v[i].y; hi = v[i].z; sc = v[i].w;
+                    if (lane == wl) key[i] = 0;
+                }
             wlo = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(lo), wl));
             whi = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(hi), wl));
             wsc = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sc), wl));
