@@ -116,6 +116,14 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t o_shpart = carve(&at, (size_t)K3G_KS_SD * T4 * d * 4);
     const size_t o_rpart = carve(&at, (size_t)T4 * E * K3G_KS_R * 16);
     const size_t o_dcontrib = carve(&at, P4 * K3G_KS_D * d * 4);
+    /* the grouped GEMMs' activation pieces and column tiles */
+    const size_t d128 = (d + 127) / 128 * 128, I128 = (I + 127) / 128 * 128;
+    const size_t SI128 = (SI + 127) / 128 * 128;
+    const size_t maxt = (P + 127) / 128 + E;
+    const size_t o_xb = carve(&at, 2 * T * d128 * 2), o_hb = carve(&at, 2 * P * I128 * 2);
+    const size_t o_hsb = carve(&at, 2 * T * (SI128 ? SI128 : 128) * 2);
+    const size_t o_tiles = carve(&at, maxt * 16), o_ntiles = carve(&at, 4);
+    const size_t o_xflag = carve(&at, 4);
     /* two banks of counters, one per call in turn; each a multiple of 256 bytes */
     c->sync_bytes = (k3k_decode_sync_bytes(T4, (int)d, (int)E, (int)k, (int)I, (int)SI) + 255) &
                     ~(size_t)255;
@@ -155,6 +163,13 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->rpart = (double *)(b + o_rpart);
     c->dcontrib = (float *)(b + o_dcontrib);
     c->sync = (int *)(b + o_sync);
+    c->xb = (uint16_t *)(b + o_xb);
+    c->hb = (uint16_t *)(b + o_hb);
+    c->hsb = (uint16_t *)(b + o_hsb);
+    c->tiles = (int32_t *)(b + o_tiles);
+    c->ntiles = (int32_t *)(b + o_ntiles);
+    c->xflag = (int32_t *)(b + o_xflag);
+    c->max_tiles = (int)maxt;
     c->fused = 1;
     if (hipMemset(c->ws, 0, at) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         hipFree(c->ws);
@@ -266,6 +281,124 @@ static int fusable(const K3gCtx *c, const K3gLayer *L, int T)
                                      L->shared_inter % 32 == 0));
 }
 
+/* The grouped GEMMs cover the same layer shape at any token count. */
+static int gemmable(const K3gCtx *c, const K3gLayer *L)
+{
+    const int lat = L->latent > 0 ? L->latent : L->hidden;
+    return c->fused && L->expert_fmt == K3G_EXPERT_MXFP4_TILED && !L->down && !L->up &&
+           !L->latent_norm && lat == L->hidden && L->hidden % 32 == 0 && L->inter % 32 == 0 &&
+           (L->shared_inter == 0 || (L->wdt == K3_WBF16 && L->shared_fmt == 1 &&
+                                     L->shared_inter % 32 == 0));
+}
+
+static int r128(int v) { return (v + 127) / 128 * 128; }
+
+/* Routed and shared experts as grouped GEMMs on the bf16 matrix cores (k3g_gemm.hip):
+ * dispatch -> column tiles -> x pieces -> gate/up (+act) -> down -> combine. */
+static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
+                        const int32_t *idx, const float *wt, float *out, hipStream_t st)
+{
+    const int d = L->hidden, E = L->n_experts, k = L->topk, I = L->inter;
+    const int SI = L->shared_inter, P = T * k;
+    const int d128 = r128(d), I128 = r128(c->inter), SI128 = r128(c->shared_inter);
+    int rc = 0;
+    k3g_stage_begin(c, K3G_ST_DISPATCH, st);
+    rc |= k3k_dispatch(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm, c->err,
+                       st);
+    rc |= k3k_gemm_tiles(c->off, E, c->tiles, c->ntiles, c->xflag, st);
+    k3g_stage_end(c, K3G_ST_DISPATCH, st);
+    k3g_stage_begin(c, K3G_ST_PIECES, st);
+    rc |= k3k_xpieces(x, T, d, d128, c->xb, (long long)T * d128, c->xflag, st);
+    k3g_stage_end(c, K3G_ST_PIECES, st);
+
+    K3kGemm g;
+    memset(&g, 0, sizeof g);
+    g.mode = 0;
+    g.afmt = 0;
+    g.rows = I;
+    g.K = d;
+    g.ldb = d128;
+    g.eq = L->experts;
+    g.b = c->xb;
+    g.bpiece = (long long)T * d128;
+    g.perm = c->perm;
+    g.topk = k;
+    g.tiles = c->tiles;
+    g.ntiles = c->ntiles;
+    g.max_tiles = (P + 127) / 128 + (E < P ? E : P);
+    g.npieces = 2;
+    g.lo_flag = c->xflag;
+    g.h = c->hb;
+    g.hpiece = (long long)P * I128;
+    g.ldh = I128;
+    g.b1 = L->act_b1;
+    g.b2 = L->act_b2;
+    g.nft = (I + 255) / 256;
+    k3g_stage_begin(c, K3G_ST_GATEUP, st);
+    rc |= k3k_gemm(&g, st);
+    k3g_stage_end(c, K3G_ST_GATEUP, st);
+
+    K3kGemm s = g;
+    if (SI > 0) {
+        s.afmt = 1;
+        s.rows = SI;
+        s.eq = NULL;
+        s.wa = (const uint16_t *)L->sh1;
+        s.wb = (const uint16_t *)L->sh3;
+        s.perm = NULL;
+        s.tiles = NULL;
+        s.ntiles = NULL;
+        s.dense_rows = T;
+        s.h = c->hsb;
+        s.hpiece = (long long)T * SI128;
+        s.ldh = SI128;
+        s.nft = (SI + 255) / 256;
+        k3g_stage_begin(c, K3G_ST_SH_GATEUP, st);
+        rc |= k3k_gemm(&s, st);
+        k3g_stage_end(c, K3G_ST_SH_GATEUP, st);
+    }
+
+    g.mode = 1;
+    g.rows = d;
+    g.K = I;
+    g.ldb = I128;
+    g.b = c->hb;
+    g.bpiece = (long long)P * I128;
+    g.lo_flag = NULL;
+    g.h = NULL;
+    g.out = c->contrib;
+    g.ldo = d;
+    g.scatter = 1;
+    g.nft = (d + 511) / 512;
+    k3g_stage_begin(c, K3G_ST_DOWN, st);
+    rc |= k3k_gemm(&g, st);
+    k3g_stage_end(c, K3G_ST_DOWN, st);
+
+    if (SI > 0) {
+        s.mode = 1;
+        s.rows = d;
+        s.K = SI;
+        s.ldb = SI128;
+        s.wa = (const uint16_t *)L->sh2;
+        s.wb = NULL;
+        s.b = c->hsb;
+        s.bpiece = (long long)T * SI128;
+        s.lo_flag = NULL;
+        s.h = NULL;
+        s.out = c->sh_out;
+        s.ldo = d;
+        s.scatter = 0;
+        s.nft = (d + 511) / 512;
+        k3g_stage_begin(c, K3G_ST_SH_DOWN, st);
+        rc |= k3k_gemm(&s, st);
+        k3g_stage_end(c, K3G_ST_SH_DOWN, st);
+    }
+    k3g_stage_begin(c, K3G_ST_COMBINE, st);
+    rc |= k3k_combine(c->contrib, idx, wt, T, k, d, SI > 0 ? c->sh_out : NULL, out, st);
+    k3g_stage_end(c, K3G_ST_COMBINE, st);
+    return rc ? -1 : 0;
+}
+
 void k3g_ctx_stats(K3gCtx *c, int64_t *out, int n)
 {
     int s[16] = {0};
@@ -323,9 +456,10 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     const int P = T * k;
     const int projected = L->down != NULL;
     int rc = 0;
+    if (gemmable(c, L)) return experts_gemm(c, L, x, T, idx, wt, out, st);
     if (L->expert_fmt == K3G_EXPERT_MXFP4_TILED || L->shared_fmt != 0) {
-        fprintf(stderr, "k3moe: tiled experts run on the fused decode kernel only (up to 4 "
-                        "tokens, no latent projection)\n");
+        fprintf(stderr, "k3moe: tiled experts need the Kimi-K2 layer shape (no latent "
+                        "projection, bf16 shared expert, widths multiple of 32)\n");
         return -1;
     }
 

@@ -18,7 +18,7 @@ void k3g_fatal(const char *what);
 /* stages of a layer call, for the optional per-stage timing */
 enum {
     K3G_ST_ROUTER = 0, K3G_ST_DISPATCH, K3G_ST_GATEUP, K3G_ST_DOWN, K3G_ST_SH_GATEUP,
-    K3G_ST_SH_DOWN, K3G_ST_COMBINE, K3G_ST_LATENT, K3G_ST_FUSED, K3G_NSTAGE
+    K3G_ST_SH_DOWN, K3G_ST_COMBINE, K3G_ST_LATENT, K3G_ST_FUSED, K3G_ST_PIECES, K3G_NSTAGE
 };
 
 #define K3G_RING 256
@@ -55,6 +55,10 @@ struct K3gCtx {
     size_t sync_bytes;
     int epoch;                   /* fused-kernel calls; its parity picks the counter bank */
     int fused;                   /* use the fused decode kernel when the layer allows */
+    /* grouped GEMMs on the matrix cores (more than 4 tokens, tiled layouts) */
+    uint16_t *xb, *hb, *hsb;     /* bf16 pieces of x [2][T][d128], h [2][T*k][I128], shared h */
+    int32_t *tiles, *ntiles, *xflag;
+    int max_tiles;
     unsigned long long *trace;   /* optional per-ticket timestamps of the fused kernel */
     /* optional per-stage timing: a ring of event pairs around each stage of a call,
      * harvested only when the ring wraps or the totals are read */

@@ -72,6 +72,44 @@ typedef struct {
     unsigned long long *trace;    /* optional: [ticket][2] start/end wall-clock stamps */
 } K3kDecode;
 
+/* One grouped GEMM on the bf16 matrix cores (k3g_gemm.hip). Columns are (token, slot)
+ * pairs grouped by expert (tiles) or all tokens (dense, the shared expert). */
+typedef struct {
+    int mode;                 /* 0: gate/up + activation -> h pieces; 1: down -> fp32 rows */
+    int afmt;                 /* 0: tiled MXFP4 per expert (eq); 1: tiled bf16 (wa, wb) */
+    int rows;                 /* output rows of one weight matrix: inter (mode 0), hidden (1) */
+    int K;                    /* reduction length */
+    int ldb;                  /* row stride of the B pieces (elements), K rounded up to 128 */
+    const K3ExpertQ *eq;      /* mode 0: p1, p3; mode 1: p2 (tiled MXFP4) */
+    const uint16_t *wa, *wb;  /* tiled bf16: mode 0 gate, up; mode 1 down */
+    const uint16_t *b;        /* B pieces, piece p at b + p * bpiece */
+    long long bpiece;
+    const int32_t *perm;      /* sorted position -> pair id (t * topk + j) */
+    int topk;
+    const int32_t *tiles;     /* {expert, first sorted position, count, 0}; NULL: dense */
+    const int32_t *ntiles;
+    int max_tiles;            /* bound on *ntiles (grid size) */
+    int dense_rows;           /* dense: the column count (tokens) */
+    int npieces;              /* B pieces, 1 or 2 */
+    const int32_t *lo_flag;   /* piece 1 only when *lo_flag != 0 (NULL: always) */
+    uint16_t *h;              /* mode 0 out: [2][columns][ldh] bf16 pieces */
+    long long hpiece;
+    int ldh;
+    float b1, b2;             /* activation caps */
+    float *out;               /* mode 1 out: row per column, stride ldo */
+    int ldo;
+    int scatter;              /* mode 1: out row = perm[column] (else the column) */
+    int nft;                  /* feature tiles: ceil(rows / 256) (mode 0), / 512 (mode 1) */
+} K3kGemm;
+
+int k3k_gemm(const K3kGemm *g, hipStream_t st);
+/* column tiles from the dispatch's per-expert ranges; clears *flag */
+int k3k_gemm_tiles(const int32_t *off, int E, int32_t *tiles, int32_t *ntiles,
+                   int32_t *flag, hipStream_t st);
+/* x -> bf16 pieces [2][T][ldb]; *flag = 1 when some piece 1 is not zero */
+int k3k_xpieces(const float *x, int T, int d, int ldb, uint16_t *xb, long long piece,
+                int32_t *flag, hipStream_t st);
+
 /* K slices of the fused kernel's ticket classes (fewer when K is short) */
 #define K3G_KS_G 7                /* routed gate/up: over 512-column quads of d */
 #define K3G_KS_SG 7               /* shared gate/up: over 32-column chunks of d */

@@ -28,11 +28,14 @@ def say(msg):
     print(msg, flush=True)
 
 
-def run_layer(layer, x, ctx=None, force=0, fused=True):
-    """fused: the fused decode kernel on the tiled copy of the layer (up to 4 tokens);
-    otherwise the staged kernels on the checkpoint layout."""
+def run_layer(layer, x, ctx=None, force=0, fused=True, tiled=None):
+    """tiled (default: fused and T <= 4): the tiled copy of the layer, which runs the
+    fused decode kernel up to 4 tokens and the grouped GEMMs beyond; otherwise the staged
+    kernels on the checkpoint layout."""
     T, d, k = x.shape[0], layer.shape.hidden, layer.shape.topk
-    L = layer.dev_tiled if fused and T <= 4 else layer.dev
+    if tiled is None:
+        tiled = fused and T <= 4
+    L = layer.dev_tiled if tiled else layer.dev
     own = ctx is None
     ctx = ctx or k3moe.Ctx(L, max_tokens=T)
     ctx.force_exact(force)
@@ -307,6 +310,38 @@ def test_layer_k2_fused_consecutive_tokens(k2_layer):
         say(f"  launch {i} ({T} tokens): rel-L2 {r:.3e}")
         assert r <= 1e-4, i
     ctx.destroy()
+
+
+@pytest.mark.parametrize("T", [5, 16, 37, 200])
+def test_layer_tiny_grouped_gemm(gpu, T):
+    say(f"case: k3g_moe tiny layer on the grouped bf16 MFMA GEMMs, {T} tokens (fp32 x: "
+        "two activation pieces)")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=4321, layout="both")
+    x = layer.tokens(T)
+    out, idx, wt = run_layer(layer, x, tiled=True)
+    ro, ri, rw = oracle_tokens(layer, x)
+    assert np.array_equal(idx, ri)
+    np.testing.assert_allclose(wt, rw, rtol=1e-6)
+    r = rel_l2(out, ro)
+    say(f"  rel-L2 {r:.3e}")
+    assert r <= 1e-5
+
+
+@pytest.mark.parametrize("T,xkind", [(40, "bf16"), (24, "fp32")])
+def test_layer_k2_grouped_gemm(k2_layer, T, xkind):
+    say(f"case: k3g_moe K2 layer on the grouped bf16 MFMA GEMMs, {T} tokens, x {xkind}")
+    layer = k2_layer
+    x = layer.tokens(T, stream_base=140)
+    if xkind == "fp32":
+        # values that are not bf16: the gate/up products need both activation pieces
+        x = (x * np.float32(1.0 + 2.0 ** -12)).astype(np.float32)
+        assert np.any(x.view(np.uint32) & 0xFFFF)
+    out, idx, _ = run_layer(layer, x, tiled=True)
+    ro, ri, _ = oracle_tokens(layer, x)
+    assert np.array_equal(idx, ri)
+    r = rel_l2(out, ro)
+    say(f"  rel-L2 {r:.3e}")
+    assert r <= 1e-5
 
 
 def test_layer_k2_batch(k2_layer):
