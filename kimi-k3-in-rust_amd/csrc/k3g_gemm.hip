@@ -33,10 +33,11 @@
  * conflicts. K advances 128 per step: one barrier per step, the next step's weights and
  * activations in flight during the current step's matrix work.
  *
- * Workgroup order: the tiles of one expert are consecutive and every XCD gets one
- * contiguous run of them (blockIdx % 8 is the XCD a workgroup lands on), so the column
- * tiles that share a feature tile's weights, and the feature tiles that share a column
- * tile's activations, meet in one XCD's L2.
+ * Workgroup order: column tiles are sorted largest first and dealt to the 8 XCDs in a
+ * snake, so every XCD gets the same amount of work and runs its largest tiles first (the
+ * contiguous alternative left the busiest XCD ~10% behind on the Zipf-skewed prefill);
+ * the feature tiles of one column tile run back to back on one XCD and share the tile's
+ * activations in its L2.
  */
 #include "k3g_dev.h"
 #include "k3g_kernels.h"
@@ -54,6 +55,12 @@ typedef __attribute__((address_space(3))) void *k3lds;
 #define GM_QT 4352                        /* tiled MXFP4 quad tile */
 
 __device__ __forceinline__ int gm_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+/* E8M0 byte -> 2^(b-127) as fp32 without branches (the tiled layout holds no 255) */
+__device__ __forceinline__ float gm_scale(uint32_t b)
+{
+    return __uint_as_float(b ? b << 23 : 0x00400000u);
+}
 
 /* 8 E2M1 values (one 32-bit word, low nibble first) times 2^(s-127) as bf16, exact */
 __device__ __forceinline__ k3v8bf gm_deq8(uint32_t w, float scale)
@@ -80,10 +87,24 @@ __device__ __forceinline__ uint16_t gm_bf16_rn(float f)
 
 __device__ __forceinline__ float gm_bf16_f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
+/* Loads through pointers the compiler cannot prove global (they come from the expert
+ * table) would be flat loads, which also count against the LDS counter and make every
+ * ds_read wait for outstanding HBM loads: address them as global memory explicitly. */
+typedef unsigned int gm_v4u __attribute__((ext_vector_type(4)));
+#ifdef __HIP_DEVICE_COMPILE__
+typedef const __attribute__((address_space(1))) gm_v4u *gm_g4;
+typedef const __attribute__((address_space(1))) uint32_t *gm_g1;
+#else
+typedef const gm_v4u *gm_g4;       /* the host pass only parses device code */
+typedef const uint32_t *gm_g1;
+#endif
+
 __device__ __forceinline__ uint4 gm_ld16(const void *p)
 {
-    return *(const uint4 *)p;
+    const gm_v4u v = *(gm_g4)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint32_t gm_ld4(const void *p) { return *(gm_g1)p; }
 
 /* h = act(gate, up) for 4 consecutive features of one column, stored as two bf16 pieces
  * (piece 1 at o + piece) */
@@ -104,11 +125,20 @@ __device__ __noinline__ void gm_act_store(k3v4f gt, k3v4f up, float b1, float b2
     *(uint2 *)(o + piece) = vl;
 }
 
-/* one DMA instruction: 64 lanes x 16 bytes from their own global addresses to 1 KB of
- * LDS at `dst` (lane l at dst + 16 l) */
-__device__ __forceinline__ void gm_dma16(const void *src, void *dst)
+/* One DMA instruction: 64 lanes x 16 bytes from their own global addresses to 1 KB of LDS
+ * at byte address `lds` (lane l at lds + 16 l). Issued as inline assembly so the
+ * compiler does not treat every later LDS read as waiting on it (it would drain all
+ * outstanding loads before each ds_read); completion is awaited explicitly with
+ * s_waitcnt vmcnt before the barrier that publishes the stage. M0 is saved and restored
+ * around the instruction. */
+__device__ __forceinline__ void gm_dma16(const void *src, uint32_t lds)
 {
-    __builtin_amdgcn_global_load_lds(src, (k3lds)dst, 16, 0, 0);
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %2\n\t"
+                 "global_load_lds_dwordx4 %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(src), "s"(lds) : "memory");
 }
 
 /* s_waitcnt vmcnt(N) (expcnt, lgkmcnt not waited on) */
@@ -119,6 +149,187 @@ __device__ __forceinline__ void gm_wait_vm()
     __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
+/* Everything one workgroup's tile needs, uniform across the workgroup except the
+ * per-lane DMA row offsets. */
+struct GmTile {
+    int p0, np, lane, w, g4, nK, ndma;
+    int orow0;                 /* mode 0: first feature; mode 1: first output row */
+    const uint8_t *abase[4];   /* row group r: its 16-row block of the weight matrix */
+    bool rv[4];                /* row group inside the matrix */
+    uint32_t boff[4];          /* element offsets of this lane's DMA rows (+ swizzled slot) */
+    uint32_t lds;              /* LDS byte address of the staging buffers */
+    uint8_t *ldsp;
+};
+
+/* The tile's GEMM with NB 16-column blocks and NP activation pieces, then its epilogue. */
+template <int AF, int NP, int NB>
+__device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
+{
+    k3v4f acc[4][NB];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) acc[r][cb] = k3v4f{0.f, 0.f, 0.f, 0.f};
+    const int lane = t.lane;
+
+    auto dma = [&](int c) {
+        const uint32_t st = t.lds + (c & 1) * GM_STAGE + t.w * 1024;
+        const uint16_t *b0 = g.b + (size_t)c * GM_KC;
+#pragma unroll
+        for (int pc = 0; pc < NP; ++pc) {
+            const uint16_t *b = b0 + (size_t)pc * g.bpiece;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (i < t.ndma) gm_dma16(b + t.boff[i], st + pc * GM_PIECE + i * 8 * 1024);
+        }
+    };
+    /* B operand: column block cb, logical 16-byte slot q of the step's row */
+    const uint8_t *brow = t.ldsp + (lane & 15) * 256;
+    auto bread = [&](int c, int pc, int cb, int q) -> uint4 {
+        return *(const uint4 *)(brow + (c & 1) * GM_STAGE + pc * GM_PIECE + cb * 16 * 256 +
+                                16 * (q ^ (lane & 15)));
+    };
+    auto mma_step = [&](int c, int q, const k3v8bf *a) {
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) {
+#pragma unroll
+            for (int pc = 0; pc < NP; ++pc) {
+                const uint4 bv = bread(c, pc, cb, q);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[r][cb] = gm_mma(a[r], bv, acc[r][cb]);
+            }
+        }
+    };
+    const uint4 z4 = make_uint4(0, 0, 0, 0);
+
+    if (AF == 0) {
+        /* ------------------------------------------------ MXFP4 weights ---------- */
+        /* step c's weights are loaded two steps ahead (8 loads per step: 4 row groups'
+         * 16 data bytes and their scale dwords); the activations one step ahead. Issue
+         * order per step: DMA(c + 1), then weights(c + 2), so "all but the last 8 loads
+         * done" means step c + 1's stage and weights have landed. */
+        uint4 ab[3][4];
+        uint32_t sb[3][4];
+        auto aload = [&](int c, uint4 (&dst)[4], uint32_t (&sdst)[4]) {
+            const size_t qo = (size_t)(c >> 2) * GM_QT;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint8_t *p = t.abase[r] + qo;
+                dst[r] = gm_ld16(p + 1024 * (c & 3) + 16 * lane);
+                sdst[r] = gm_ld4(p + 4096 + 4 * lane);
+            }
+        };
+        /* One step: weights of step c in cur, weights of step c + 2 loaded into nxt. The
+         * buffers rotate by unrolling (never by register moves, which would wait for the
+         * loads in flight), and every step issues the same loads (clamped to the last step;
+         * the padding steps past nK only skip their matrix work), so the compiler's load
+         * counters agree on every path and its waits stay on the step that is due. */
+        auto step = [&](int c, const uint4 (&cur)[4], const uint32_t (&scl)[4], uint4 (&nxt)[4],
+                        uint32_t (&nsc)[4]) {
+            gm_wait_vm<8>();
+            __syncthreads();
+            dma(min(c + 1, t.nK - 1));
+            aload(min(c + 2, t.nK - 1), nxt, nsc);
+            __builtin_amdgcn_sched_barrier(0);
+            if (c < t.nK) {
+                const int j = c & 3;
+                float sc[4];
+                uint4 wv[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sc[r] = gm_scale((scl[r] >> (8 * j)) & 0xffu);
+                    /* rows outside the matrix multiply as zeros (their loads read block 0) */
+                    wv[r] = t.rv[r] ? cur[r] : z4;
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    k3v8bf a[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t wd = s == 0 ? wv[r].x : s == 1 ? wv[r].y
+                                          : s == 2 ? wv[r].z : wv[r].w;
+                        a[r] = gm_deq8(wd, sc[r]);
+                    }
+                    mma_step(c, 4 * s + t.g4, a);
+                }
+            }
+        };
+        aload(0, ab[0], sb[0]);
+        dma(0);
+        aload(min(1, t.nK - 1), ab[1], sb[1]);
+        for (int c = 0; c < t.nK; c += 3) {
+            step(c, ab[0], sb[0], ab[2], sb[2]);
+            step(c + 1, ab[1], sb[1], ab[0], sb[0]);
+            step(c + 2, ab[2], sb[2], ab[1], sb[1]);
+        }
+        gm_wait_vm<0>();
+    } else {
+        /* ------------------------------------------------ bf16 weights ----------- */
+        /* A operands per (step, sub-step): 4 row groups x 16 bytes; a ring of the 4
+         * sub-steps of a step, each loaded two sub-steps ahead */
+        const int nC32 = g.K / 32;
+        uint4 ring[4][4];
+        auto aload = [&](int c, int s, uint4 *dst) {
+            const int c32 = 4 * c + s;
+            const int cc = c32 < nC32 ? c32 : nC32 - 1;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dst[r] = gm_ld16(t.abase[r] + (size_t)cc * 1024 + 16 * lane);
+        };
+        dma(0);
+        aload(0, 0, ring[0]);
+        aload(0, 1, ring[1]);
+        for (int c = 0; c < t.nK; ++c) {
+            /* the stage's DMA was followed by the loads of sub-steps (c, 0) and (c, 1) */
+            gm_wait_vm<8>();
+            __syncthreads();
+            if (c + 1 < t.nK) dma(c + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int s2 = (s + 2) & 3;
+                aload(c + ((s + 2) >> 2), s2, ring[s2]);
+                __builtin_amdgcn_sched_barrier(0);
+                /* rows outside the matrix and columns past K multiply as zeros */
+                const bool kin = 4 * c + s < nC32;
+                k3v8bf a[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    a[r] = __builtin_bit_cast(k3v8bf, (t.rv[r] && kin) ? ring[s][r] : z4);
+                mma_step(c, 4 * s + t.g4, a);
+            }
+        }
+        gm_wait_vm<0>();
+    }
+
+    /* ---- epilogue -------------------------------------------------------------------- */
+    const int col0 = lane & 15;
+    if (g.mode == 0) {
+        if (!t.rv[0]) return;
+        const int n = t.orow0 + 4 * t.g4;
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) {
+            const int col = 16 * cb + col0;
+            if (col < t.np) {
+                uint16_t *o = g.h + (size_t)(t.p0 + col) * g.ldh + n;
+                gm_act_store(acc[0][cb], acc[2][cb], g.b1, g.b2, o, g.hpiece);
+                gm_act_store(acc[1][cb], acc[3][cb], g.b1, g.b2, o + 16, g.hpiece);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) {
+            const int col = 16 * cb + col0;
+            if (col < t.np) {
+                const int p = t.p0 + col;
+                float *o = g.out + (size_t)(g.scatter ? g.perm[p] : p) * g.ldo + t.orow0 + 4 * t.g4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (t.rv[r]) *(k3v4f *)(o + 16 * r) = acc[r][cb];
+            }
+        }
+    }
+}
+
 template <int AF>
 __global__ void __launch_bounds__(GM_WAVES * 64, 1)
 k_gemm(const K3kGemm g)
@@ -126,34 +337,35 @@ k_gemm(const K3kGemm g)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * GM_STAGE];
 
     /* ---- which tile ---------------------------------------------------------------- */
+    /* Workgroup b runs on XCD b % 8 and is dispatched there in the order of b / 8. The
+     * tiles (largest first) are dealt to the XCDs in a snake: round r gives tile 8 r + x
+     * (r even) or 8 r + 7 - x (r odd) to XCD x, so every XCD gets the same mix, largest
+     * first; the feature tiles of one column tile run back to back on one XCD, sharing
+     * its activations in that XCD's L2. */
     const int ntl = g.tiles ? *g.ntiles : (g.dense_rows + GM_COLS - 1) / GM_COLS;
-    const int N = ntl * g.nft;
-    const int per = (N + 7) >> 3;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-    if (slot >= per) return;
-    const int lam = xcd * per + slot;
-    if (lam >= N) return;
-    const int tile = lam / g.nft, f = lam - tile * g.nft;
-    int e = 0, p0, np;
+    const int rnd = slot / g.nft, f = slot - rnd * g.nft;
+    const int tile = 8 * rnd + ((rnd & 1) ? 7 - xcd : xcd);
+    if (tile >= ntl) return;
+    GmTile t;
+    int e = 0;
     if (g.tiles) {
-        const int4 t = ((const int4 *)g.tiles)[tile];
-        e = t.x; p0 = t.y; np = t.z;
+        const int4 tv = ((const int4 *)g.tiles)[tile];
+        e = tv.x; t.p0 = tv.y; t.np = tv.z;
     } else {
-        p0 = tile * GM_COLS;
-        np = min(GM_COLS, g.dense_rows - p0);
+        t.p0 = tile * GM_COLS;
+        t.np = min(GM_COLS, g.dense_rows - t.p0);
     }
-    const int nb = (np + 15) >> 4;                       /* 16-column blocks in use */
+    const int nb = (t.np + 15) >> 4;                     /* 16-column blocks in use */
     const int npr = (g.npieces > 1 && (!g.lo_flag || *g.lo_flag)) ? 2 : 1;
-    const int lane = threadIdx.x & 63;
-    const int w = gm_uniform(threadIdx.x >> 6);
-    const int K = g.K;
-    const int nK = (K + GM_KC - 1) / GM_KC;
+    t.lane = threadIdx.x & 63;
+    t.w = gm_uniform(threadIdx.x >> 6);
+    t.g4 = t.lane >> 4;
+    t.nK = (g.K + GM_KC - 1) / GM_KC;
+    t.ldsp = lds;
+    t.lds = (uint32_t)(uintptr_t)(k3lds)lds;
 
     /* ---- this wave's weight rows --------------------------------------------------- */
-    /* row group r: matrix base and 16-row block index; valid when inside the matrix */
-    const uint8_t *abase[4];
-    bool rv[4];
-    int orow0;                                            /* first output row (mode 1) or feature (mode 0) */
     {
         const uint8_t *m0, *m1;
         if (AF == 0) {
@@ -165,229 +377,99 @@ k_gemm(const K3kGemm g)
             m1 = (const uint8_t *)(g.mode == 0 ? g.wb : g.wa);
         }
         /* bytes per 16-row block */
-        const size_t rbb = AF == 0 ? (size_t)((K + 511) / 512) * GM_QT : (size_t)(K / 32) * 1024;
+        const size_t rbb = AF == 0 ? (size_t)((g.K + 511) / 512) * GM_QT : (size_t)(g.K / 32) * 1024;
         if (g.mode == 0) {
-            orow0 = 256 * f + 32 * w;
+            t.orow0 = 256 * f + 32 * t.w;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = orow0 + 16 * (r & 1);
-                rv[r] = orow0 < g.rows;
-                abase[r] = (r < 2 ? m0 : m1) + (size_t)(rv[r] ? row / 16 : 0) * rbb;
+                const int row = t.orow0 + 16 * (r & 1);
+                t.rv[r] = t.orow0 < g.rows;
+                t.abase[r] = (r < 2 ? m0 : m1) + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
             }
         } else {
-            orow0 = 512 * f + 64 * w;
+            t.orow0 = 512 * f + 64 * t.w;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = orow0 + 16 * r;
-                rv[r] = row < g.rows;
-                abase[r] = m0 + (size_t)(rv[r] ? row / 16 : 0) * rbb;
+                const int row = t.orow0 + 16 * r;
+                t.rv[r] = row < g.rows;
+                t.abase[r] = m0 + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
             }
         }
     }
-    const bool anyv = rv[0] || rv[1] || rv[2] || rv[3];
 
     /* ---- the activation rows this lane's DMA reads --------------------------------- */
     /* instruction i of wave w fills LDS rows 4 (8 i + w) .. + 3; lane l writes row
      * 4 (8 i + w) + l / 16, physical 16-byte slot l % 16, which holds logical slot
      * (l % 16) ^ (row % 16). row % 16 = (4 w + l / 16) % 16 for every i. */
-    const int qoff = 8 * ((lane & 15) ^ ((4 * w + (lane >> 4)) & 15));
-    uint32_t boff[4];
+    /* The B operand of sub-step s in lane group g is read from logical slot 4 s + g (the
+     * conflict-free order); for MXFP4 weights that slot holds the 8 columns at
+     * 32 g + 8 s of the step (the A operand's column order), i.e. logical slot q holds
+     * columns 8 (4 (q % 4) + q / 4). */
+    const int qlog = (t.lane & 15) ^ ((4 * t.w + (t.lane >> 4)) & 15);
+    const int qoff = 8 * (AF == 0 ? 4 * (qlog & 3) + (qlog >> 2) : qlog);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int r = 4 * (8 * i + w) + (lane >> 4);
-        const int p = p0 + (r < np ? r : 0);
+        const int r = 4 * (8 * i + t.w) + (t.lane >> 4);
+        const int p = t.p0 + (r < t.np ? r : 0);
         const int src = (g.mode == 0 && g.perm) ? g.perm[p] / g.topk : p;
-        boff[i] = (uint32_t)src * (uint32_t)g.ldb + (uint32_t)qoff;
+        t.boff[i] = (uint32_t)src * (uint32_t)g.ldb + (uint32_t)qoff;
     }
-    const int ndma = gm_uniform((4 * nb + 7 - w) / 8 < 4 ? (4 * nb + 7 - w) / 8 : 4);
+    t.ndma = min(4, (4 * nb + 7 - t.w) / 8);
 
-    auto dma = [&](int c) {
-        uint8_t *st = lds + (c & 1) * GM_STAGE + w * 1024;
-        const uint16_t *b0 = g.b + (size_t)c * GM_KC;
-        for (int pc = 0; pc < npr; ++pc) {
-            const uint16_t *b = b0 + (size_t)pc * g.bpiece;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (i < ndma) gm_dma16(b + boff[i], st + pc * GM_PIECE + i * 8 * 1024);
-        }
-    };
-
-    k3v4f acc[4][8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int cb = 0; cb < 8; ++cb) acc[r][cb] = k3v4f{0.f, 0.f, 0.f, 0.f};
-
-    /* B operand read: column block cb, logical slot q of the step's 16 */
-    const int brow = (lane & 15) * 256;
-    auto bread = [&](int c, int pc, int cb, int q) -> uint4 {
-        const uint8_t *p = lds + (c & 1) * GM_STAGE + pc * GM_PIECE + cb * 16 * 256 + brow +
-                           16 * (q ^ (lane & 15));
-        return *(const uint4 *)p;
-    };
-    const int g4 = lane >> 4;
-
-    if (AF == 0) {
-        /* ------------------------------------------------ MXFP4 weights ---------- */
-        uint4 ar[4];
-        uint32_t sw[4];
-        auto aload = [&](int c, uint4 *dst, uint32_t *sdst) {
-            const size_t qo = (size_t)(c >> 2) * GM_QT;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint8_t *t = abase[r] + qo;
-                dst[r] = gm_ld16(t + 1024 * (c & 3) + 16 * lane);
-                if ((c & 3) == 0) sdst[r] = *(const uint32_t *)(t + 4096 + 4 * lane);
-            }
-        };
-        aload(0, ar, sw);
-        dma(0);
-        for (int c = 0; c < nK; ++c) {
-            gm_wait_vm<0>();
-            __syncthreads();
-            uint4 cur[4];
-            uint32_t scl[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) { cur[r] = ar[r]; scl[r] = sw[r]; }
-            if (c + 1 < nK) {
-                aload(c + 1, ar, sw);
-                dma(c + 1);
-            }
-            const int j = c & 3;
-            float sc[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sc[r] = k3d_e8m0((scl[r] >> (8 * j)) & 0xffu);
-            if (anyv) {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    k3v8bf a[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const uint32_t wd = s == 0 ? cur[r].x : s == 1 ? cur[r].y
-                                          : s == 2 ? cur[r].z : cur[r].w;
-                        a[r] = gm_deq8(wd, sc[r]);
-                    }
-                    const int q = 4 * g4 + s;
-#pragma unroll
-                    for (int cb = 0; cb < 8; ++cb) {
-                        if (cb < nb) {
-                            for (int pc = 0; pc < npr; ++pc) {
-                                const uint4 bv = bread(c, pc, cb, q);
-#pragma unroll
-                                for (int r = 0; r < 4; ++r)
-                                    if (rv[r]) acc[r][cb] = gm_mma(a[r], bv, acc[r][cb]);
-                            }
-                        }
-                    }
-                }
-            }
-        }
-    } else {
-        /* ------------------------------------------------ bf16 weights ----------- */
-        /* A operands per (step, sub-step): 4 row groups x 16 bytes; a ring of 4
-         * sub-steps, loaded two sub-steps ahead */
-        const int nC32 = K / 32;
-        uint4 ring[4][4];
-        auto aload = [&](int c, int s, uint4 *dst) {
-            const int c32 = 4 * c + s;
-            const int cc = c32 < nC32 ? c32 : nC32 - 1;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) dst[r] = gm_ld16(abase[r] + (size_t)cc * 1024 + 16 * lane);
-        };
-        dma(0);
-        aload(0, 0, ring[0]);
-        aload(0, 1, ring[1]);
-        for (int c = 0; c < nK; ++c) {
-            /* DMA(c) was followed by the loads of sub-steps (c,0) and (c,1): 8 loads */
-            gm_wait_vm<8>();
-            __syncthreads();
-            if (c + 1 < nK) dma(c + 1);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                /* sub-step s + 2 (wrapping into the next step) */
-                const int s2 = (s + 2) & 3;
-                const int c2 = c + ((s + 2) >> 2);
-                aload(c2 < nK ? c2 : nK - 1, s2, ring[s2]);
-                const bool live = 4 * c + s < nC32;
-                if (anyv && live) {
-                    k3v8bf a[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) a[r] = __builtin_bit_cast(k3v8bf, ring[s][r]);
-                    const int q = 4 * s + g4;
-#pragma unroll
-                    for (int cb = 0; cb < 8; ++cb) {
-                        if (cb < nb) {
-                            for (int pc = 0; pc < npr; ++pc) {
-                                const uint4 bv = bread(c, pc, cb, q);
-#pragma unroll
-                                for (int r = 0; r < 4; ++r)
-                                    if (rv[r]) acc[r][cb] = gm_mma(a[r], bv, acc[r][cb]);
-                            }
-                        }
-                    }
-                }
-            }
-        }
-        gm_wait_vm<0>();
+#define GM_CASE(P, B) case (P) * 16 + (B): gm_tile<AF, P, B>(g, t); break;
+    switch (npr * 16 + nb) {
+        GM_CASE(1, 1) GM_CASE(1, 2) GM_CASE(1, 3) GM_CASE(1, 4)
+        GM_CASE(1, 5) GM_CASE(1, 6) GM_CASE(1, 7) GM_CASE(1, 8)
+        GM_CASE(2, 1) GM_CASE(2, 2) GM_CASE(2, 3) GM_CASE(2, 4)
+        GM_CASE(2, 5) GM_CASE(2, 6) GM_CASE(2, 7) GM_CASE(2, 8)
+        default: break;
     }
-
-    /* ---- epilogue -------------------------------------------------------------------- */
-    const int col0 = lane & 15;
-    if (g.mode == 0) {
-        if (!rv[0]) return;
-        const int n = orow0 + 4 * g4;
-#pragma unroll
-        for (int cb = 0; cb < 8; ++cb) {
-            const int col = 16 * cb + col0;
-            if (cb < nb && col < np) {
-                uint16_t *o = g.h + (size_t)(p0 + col) * g.ldh + n;
-                gm_act_store(acc[0][cb], acc[2][cb], g.b1, g.b2, o, g.hpiece);
-                gm_act_store(acc[1][cb], acc[3][cb], g.b1, g.b2, o + 16, g.hpiece);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            if (!rv[r]) continue;
-            const int orow = orow0 + 16 * r + 4 * g4;
-#pragma unroll
-            for (int cb = 0; cb < 8; ++cb) {
-                const int col = 16 * cb + col0;
-                if (cb < nb && col < np) {
-                    const int p = p0 + col;
-                    const int dst = g.scatter ? g.perm[p] : p;
-                    *(k3v4f *)(g.out + (size_t)dst * g.ldo + orow) = acc[r][cb];
-                }
-            }
-        }
-    }
+#undef GM_CASE
 }
 
 /* ------------------------------------------------------------------ helpers ------ */
-/* Column tiles of up to 128 pairs per active expert, in expert order; also clears the
- * flag the activation pieces raise. One block of 1024 threads (n_experts <= 1024). */
+/* Column tiles of up to 128 pairs per active expert, largest first: the tiles of 8
+ * column blocks (every full tile, in expert order), then the last tiles of the experts by
+ * their block count, 7 down to 1 (in expert order within a count). Also clears the flag
+ * the activation pieces raise. One block of 1024 threads (n_experts <= 1024). */
+__device__ __forceinline__ int gm_block_exscan(int v, int *tmp, int *total)
+{
+    const int e = threadIdx.x;
+    tmp[e] = v;
+    __syncthreads();
+    for (int d = 1; d < 1024; d <<= 1) {
+        const int u = e >= d ? tmp[e - d] : 0;
+        __syncthreads();
+        tmp[e] += u;
+        __syncthreads();
+    }
+    const int inc = tmp[e];
+    *total = tmp[1023];
+    __syncthreads();
+    return inc - v;
+}
+
 __global__ void __launch_bounds__(1024)
 k_gemm_tiles(const int32_t *__restrict__ off, int E, int4 *__restrict__ tiles,
              int32_t *__restrict__ ntiles, int32_t *__restrict__ flag)
 {
-    __shared__ int s[1024];
+    __shared__ int tmp[1024];
     const int e = threadIdx.x;
     const int cnt = e < E ? off[e + 1] - off[e] : 0;
-    const int nt = (cnt + GM_COLS - 1) / GM_COLS;
-    s[e] = nt;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {
-        const int v = e >= d ? s[e - d] : 0;
-        __syncthreads();
-        s[e] += v;
-        __syncthreads();
+    const int nfull = cnt / GM_COLS, rem = cnt - nfull * GM_COLS;
+    const int cls = rem ? (rem + 15) / 16 : 0;          /* block count of the last tile */
+    int tot;
+    const int f0 = gm_block_exscan(nfull, tmp, &tot);
+    for (int i = 0; i < nfull; ++i)
+        tiles[f0 + i] = make_int4(e, off[e] + GM_COLS * i, GM_COLS, 0);
+    int base = tot;
+    for (int k = 8; k >= 1; --k) {
+        int n;
+        const int pos = gm_block_exscan(cls == k, tmp, &n);
+        if (cls == k) tiles[base + pos] = make_int4(e, off[e] + GM_COLS * nfull, rem, 0);
+        base += n;
     }
-    const int first = s[e] - nt;
-    for (int i = 0; i < nt; ++i) {
-        const int p0 = off[e] + GM_COLS * i;
-        tiles[first + i] = make_int4(e, p0, min(GM_COLS, off[e + 1] - p0), 0);
-    }
-    if (e == 1023) { *ntiles = s[1023]; *flag = 0; }
+    if (e == 0) { *ntiles = base; *flag = 0; }
 }
 
 /* x (fp32 [T][d]) -> two bf16 pieces [2][T][ldb]; raises *flag when any piece 1 is not
@@ -447,8 +529,7 @@ extern "C" int k3k_gemm(const K3kGemm *g, hipStream_t st)
     if (g->tiles ? (!g->ntiles || g->max_tiles < 1) : g->dense_rows < 1) return -1;
     if ((g->scatter || (g->mode == 0 && g->tiles)) && !g->perm) return -1;
     const long long maxt = g->tiles ? g->max_tiles : (g->dense_rows + GM_COLS - 1) / GM_COLS;
-    const long long nwg = maxt * g->nft;
-    const long long grid = 8 * ((nwg + 7) / 8);
+    const long long grid = 8 * ((maxt + 7) / 8) * g->nft;
     if (grid > 0x7fffffff) return -1;
     if (g->afmt == 0)
         hipLaunchKernelGGL(k_gemm<0>, dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);

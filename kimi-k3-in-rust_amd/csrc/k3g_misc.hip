@@ -104,44 +104,54 @@ k_disp_count(const int32_t *idx, int P, int E, int32_t *cnt, int *err)
     }
 }
 
-__global__ void __launch_bounds__(256)
+/* One block, a thread per expert: per-chunk bases of each expert's pairs, the expert
+ * ranges and the active list. The chunk counts are read 8 at a time so the loads of a
+ * thread overlap instead of forming one long dependent chain. */
+__global__ void __launch_bounds__(1024)
 k_disp_scan(const int32_t *cnt, int nch, int E, int32_t *base, int32_t *off,
             int32_t *act, int32_t *nact)
 {
-    __shared__ int tot[K3G_MAX_EXPERTS];
-    const int tid = threadIdx.x;
-    for (int e = tid; e < E; e += 256) {
-        int s = 0;
-        for (int c = 0; c < nch; ++c) {
-            base[(size_t)c * E + e] = s;
-            s += cnt[(size_t)c * E + e];
+    __shared__ int sc[1024], sa[1024];
+    const int e = threadIdx.x;
+    int tot = 0;
+    if (e < E) {
+        int c = 0;
+        for (; c + 8 <= nch; c += 8) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = cnt[(size_t)(c + u) * E + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) tot += v[u];
         }
-        tot[e] = s;
+        for (; c < nch; ++c) tot += cnt[(size_t)c * E + e];
     }
+    /* block-wide inclusive scans of the totals and of the active flags */
+    sc[e] = tot;
+    sa[e] = tot > 0;
     __syncthreads();
-    const int per = (E + 255) / 256;
-    int s = 0, a = 0;
-    for (int q = 0; q < per; ++q) {
-        const int e = tid * per + q;
-        if (e < E) { s += tot[e]; a += tot[e] > 0; }
+    for (int d = 1; d < 1024; d <<= 1) {
+        const int a = e >= d ? sc[e - d] : 0, b = e >= d ? sa[e - d] : 0;
+        __syncthreads();
+        sc[e] += a;
+        sa[e] += b;
+        __syncthreads();
     }
-    int stot, atot;
-    int sb = k3d_block_exscan(s, &stot);
-    int ab = k3d_block_exscan(a, &atot);
-    __shared__ int offs[K3G_MAX_EXPERTS];
-    for (int q = 0; q < per; ++q) {
-        const int e = tid * per + q;
-        if (e < E) {
-            off[e] = sb;
-            offs[e] = sb;
-            if (tot[e] > 0) act[ab++] = e;
-            sb += tot[e];
+    if (e < E) {
+        const int first = sc[e] - tot;
+        off[e] = first;
+        if (tot > 0) act[sa[e] - 1] = e;
+        int s = first;
+        int c = 0;
+        for (; c + 8 <= nch; c += 8) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = cnt[(size_t)(c + u) * E + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { base[(size_t)(c + u) * E + e] = s; s += v[u]; }
         }
+        for (; c < nch; ++c) { base[(size_t)c * E + e] = s; s += cnt[(size_t)c * E + e]; }
     }
-    if (tid == 0) { off[E] = stot; *nact = atot; }
-    __syncthreads();
-    for (int e = tid; e < E; e += 256)
-        for (int c = 0; c < nch; ++c) base[(size_t)c * E + e] += offs[e];
+    if (e == 1023) { off[E] = sc[1023]; *nact = sa[1023]; }
 }
 
 __global__ void __launch_bounds__(256)
@@ -170,7 +180,7 @@ extern "C" int k3k_dispatch(const int32_t *idx, int P, int E, int32_t *cnt, int3
     } else {
         const int nch = (P + K3G_DCH - 1) / K3G_DCH;
         hipLaunchKernelGGL(k_disp_count, dim3(nch), dim3(256), 0, st, idx, P, E, cnt, err);
-        hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(256), 0, st, cnt, nch, E, base, off,
+        hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, st, cnt, nch, E, base, off,
                            act, nact);
         hipLaunchKernelGGL(k_disp_scatter, dim3(nch), dim3(256), 0, st, idx, P, E, base, perm);
     }

@@ -78,6 +78,99 @@ k_router_logits(const float *__restrict__ x, int T, const float *__restrict__ W,
     }
 }
 
+/* ------------------------------------------------- logits on the matrix cores ---- */
+/* Many tokens: the logits as a GEMM on v_mfma_f64_16x16x4f64 (fp32 x fp32 products are
+ * exact in fp64, the sums are fp64 fused multiply-adds). One wave per 16 experts x 32
+ * tokens. In each 16-column step lane L holds columns 4 (L / 16) .. + 3 of expert row
+ * L % 16 (A operand) and of token L % 16 (+ 16) (B operand); the four MFMAs of a step
+ * take one column each, so both operands come from one 16-byte load per row. The
+ * f64 MFMA result puts expert 4 i + L / 16, token L % 16 in item i of lane L.
+ * sum|w*x| is bounded by ||w|| ||x|| (Cauchy-Schwarz), both norms summed alongside. */
+typedef double k3v4d __attribute__((ext_vector_type(4)));
+
+#define K3R_RING 4
+
+__global__ void __launch_bounds__(64)
+k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict__ W,
+                     const float *__restrict__ bias, int d, int E, float4 *__restrict__ rs)
+{
+    const int nte = E / 16, ntt = (T + 31) / 32, N = nte * ntt;
+    const int per = (N + 7) >> 3;
+    /* block b runs on XCD b % 8: give each XCD a contiguous run, so the expert tiles of
+     * one token tile (consecutive) share its x rows in one L2 */
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    if (slot >= per) return;
+    const int lam = xcd * per + slot;
+    if (lam >= N) return;
+    const int tt = lam / nte, et = lam - tt * nte;
+    const int e0 = 16 * et, t0 = 32 * tt;
+    const int L = threadIdx.x, g = L >> 4, r = L & 15;
+    const float4 *wp = (const float4 *)(W + (size_t)(e0 + r) * d) + g;
+    const float4 *ap = (const float4 *)(x + (size_t)min(t0 + r, T - 1) * d) + g;
+    const float4 *bp = (const float4 *)(x + (size_t)min(t0 + 16 + r, T - 1) * d) + g;
+    const int ns = d / 16;
+    float4 wv[K3R_RING], av[K3R_RING], bv[K3R_RING];
+#pragma unroll
+    for (int u = 0; u < K3R_RING; ++u) {
+        const int s = min(u, ns - 1);
+        wv[u] = wp[4 * s]; av[u] = ap[4 * s]; bv[u] = bp[4 * s];
+    }
+    /* two chains per output (even and odd columns of a step), so consecutive MFMAs do
+     * not wait for each other's results; they are added at the end */
+    k3v4d acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+    k3v4d acc2 = {0.0, 0.0, 0.0, 0.0}, acc3 = {0.0, 0.0, 0.0, 0.0};
+    double ssw = 0.0, ssa = 0.0, ssb = 0.0;
+    for (int s0 = 0; s0 < ns; s0 += K3R_RING) {
+#pragma unroll
+        for (int u = 0; u < K3R_RING; ++u) {
+            const float4 w4 = wv[u], a4 = av[u], b4 = bv[u];
+            const int sn = min(s0 + u + K3R_RING, ns - 1);
+            wv[u] = wp[4 * sn]; av[u] = ap[4 * sn]; bv[u] = bp[4 * sn];
+            if (s0 + u < ns) {
+                const double w[4] = {w4.x, w4.y, w4.z, w4.w};
+                const double a[4] = {a4.x, a4.y, a4.z, a4.w};
+                const double b[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                for (int k = 0; k < 4; k += 2) {
+                    acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(w[k], a[k], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(w[k], b[k], acc1, 0, 0, 0);
+                    acc2 = __builtin_amdgcn_mfma_f64_16x16x4f64(w[k + 1], a[k + 1], acc2, 0, 0, 0);
+                    acc3 = __builtin_amdgcn_mfma_f64_16x16x4f64(w[k + 1], b[k + 1], acc3, 0, 0, 0);
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    ssw = fma(w[k], w[k], ssw);
+                    ssa = fma(a[k], a[k], ssa);
+                    ssb = fma(b[k], b[k], ssb);
+                }
+            }
+        }
+    }
+    acc0 += acc2;
+    acc1 += acc3;
+    /* norms: sum the four column groups; lane L then holds expert e0 + L % 16 and tokens
+     * t0 + L % 16, t0 + 16 + L % 16 */
+#pragma unroll
+    for (int m = 16; m <= 32; m <<= 1) {
+        ssw += __shfl_xor(ssw, m, K3G_WAVE);
+        ssa += __shfl_xor(ssa, m, K3G_WAVE);
+        ssb += __shfl_xor(ssb, m, K3G_WAVE);
+    }
+    const double nw = sqrt(ssw), na = sqrt(ssa), nb = sqrt(ssb);
+    const double nround = 2.0 * d + 16.0;
+    const double margin = 1.0 + 0x1p-40;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int er = 4 * i + g;                         /* expert row of item i */
+        const double nwe = __shfl(nw, er, K3G_WAVE);
+        const int e = e0 + er;
+        const float be = bias ? bias[e] : 0.0f;
+        const int ta = t0 + r, tb = t0 + 16 + r;
+        if (ta < T) rs[(size_t)ta * E + e] = k3d_route_score_n(acc0[i], nwe * na * margin, be, nround);
+        if (tb < T) rs[(size_t)tb * E + e] = k3d_route_score_n(acc1[i], nwe * nb * margin, be, nround);
+    }
+}
+
 /* ------------------------------------------------------------------ select ---- */
 /* One wave per token. */
 __global__ void __launch_bounds__(64)
@@ -99,7 +192,11 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
     /* the score intervals of token t live at [t][E] */
     /* float4 loads need 16-byte aligned rows; anything else takes the scalar loop */
     const int vec = ((((uintptr_t)x | (uintptr_t)W) & 15) == 0) && ((d & 3) == 0);
-    if (T >= 4) {
+    if (T >= 16 && vec && E % 16 == 0 && d % 64 == 0) {
+        const long long N = (long long)(E / 16) * ((T + 31) / 32);
+        hipLaunchKernelGGL(k_router_logits_mfma, dim3((unsigned)(8 * ((N + 7) / 8))), dim3(64),
+                           0, st, x, T, W, bias, d, E, (float4 *)rs);
+    } else if (T >= 4) {
         hipLaunchKernelGGL(k_router_logits<4>, dim3(E, (T + 3) / 4), dim3(64), 0, st,
                            x, T, W, bias, d, vec, (float4 *)rs, E);
     } else {

@@ -28,15 +28,18 @@ struct K3SelectLds {
     double wsum;
 };
 
-/* {choice, lo, hi, score} of one expert from its fp64 logit sum `acc` over d products and
- * sum|w*x| `ab`:
- *   |acc - engine's double sum| <= B = (d (1 + 1/64) + 16) 2^-53 ab 1.01 + |acc| 2^-51,
- * covering the rounding of both summation orders; the bound is pushed through the
- * float rounding and the sigmoid (monotone) and widened by 4 ulp for a libm expf that
- * differs from a correctly rounded one, then the bias is added (monotone again). */
-__device__ __forceinline__ float4 k3d_route_score(double acc, double ab, float bias, int d)
+/* {choice, lo, hi, score} of one expert from its fp64 logit sum `acc` and a bound `ab` on
+ * sum|w*x|:
+ *   |acc - engine's double sum| <= B = nround 2^-53 ab 1.01 + |acc| 2^-51,
+ * where nround counts the roundings of both summation orders (d (1 + 1/64) + 16 for a
+ * lane-strided tree of d products, 2 d + 16 for a chain of fused multiply-adds); the
+ * bound is pushed through the float rounding and the sigmoid (monotone) and widened by
+ * 4 ulp for a libm expf that differs from a correctly rounded one, then the bias is added
+ * (monotone again). */
+__device__ __forceinline__ float4 k3d_route_score_n(double acc, double ab, float bias,
+                                                     double nround)
 {
-    const double kB = ((double)d * (1.0 + 1.0 / 64.0) + 16.0) * 0x1p-53 * 1.01;
+    const double kB = nround * 0x1p-53 * 1.01;
     const double B = kB * ab + fabs(acc) * 0x1p-51 + 0x1p-1000;
     const float sc = k3d_sigmoid((float)acc);
     float slo = k3d_sigmoid((float)(acc - B));
@@ -47,6 +50,11 @@ __device__ __forceinline__ float4 k3d_route_score(double acc, double ab, float b
         shi = nextafterf(shi, INFINITY);
     }
     return make_float4(__fadd_rn(sc, bias), __fadd_rn(slo, bias), __fadd_rn(shi, bias), sc);
+}
+
+__device__ __forceinline__ float4 k3d_route_score(double acc, double ab, float bias, int d)
+{
+    return k3d_route_score_n(acc, ab, bias, (double)d * (1.0 + 1.0 / 64.0) + 16.0);
 }
 
 /* (value, index) argmax with the engine's rule: larger value wins, equal values go to
@@ -105,6 +113,46 @@ __device__ __forceinline__ uint32_t k3d_ordered(float f)
 {
     const uint32_t u = __float_as_uint(f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+/* The engine's logit: sum_i w[i] x[i] in double, strictly in index order (each product
+ * is exact, so a fused multiply-add rounds exactly like the engine's add). The sum is one
+ * dependent chain; the operands stream in 16-byte loads issued two groups ahead so the
+ * chain, not the loads, sets the pace. */
+__device__ __noinline__ double k3d_serial_dot(const float *w, const float *x, int d)
+{
+    double acc = 0.0;
+    int i = 0;
+    if (((((uintptr_t)w | (uintptr_t)x) & 15) == 0) && d >= 32) {
+        const float4 *w4 = (const float4 *)w, *x4 = (const float4 *)x;
+        const int n4 = d / 4;
+        float4 wa[4], xa[4], wb[4], xb[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) { wa[u] = w4[u]; xa[u] = x4[u]; }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) { wb[u] = w4[4 + u]; xb[u] = x4[4 + u]; }
+        int q = 0;
+        for (; q + 8 <= n4; q += 4) {
+            float4 wn[4], xn[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int qq = min(q + 8 + u, n4 - 1);
+                wn[u] = w4[qq]; xn[u] = x4[qq];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                acc = fma((double)wa[u].x, (double)xa[u].x, acc);
+                acc = fma((double)wa[u].y, (double)xa[u].y, acc);
+                acc = fma((double)wa[u].z, (double)xa[u].z, acc);
+                acc = fma((double)wa[u].w, (double)xa[u].w, acc);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) { wa[u] = wb[u]; xa[u] = xb[u]; wb[u] = wn[u]; xb[u] = xn[u]; }
+        }
+        i = 4 * q;
+    }
+    for (; i < d; ++i) acc = fma((double)w[i], (double)x[i], acc);
+    return acc;
 }
 
 /* Selection for token t from rs [T][E] {choice, lo, hi, score} (read at device
@@ -231,9 +279,7 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
             const int c = c0 + lane;
             if (c < nc) {
                 const int e = s->cand[c];
-                const float *w = W + (size_t)e * d;
-                double acc = 0.0;
-                for (int i = 0; i < d; ++i) acc = fma((double)w[i], (double)xt[i], acc);
+                const double acc = k3d_serial_dot(W + (size_t)e * d, xt, d);
                 const float sc = k3d_sigmoid((float)acc);
                 s->score[e] = sc;
                 s->choice[e] = __fadd_rn(sc, bias ? bias[e] : 0.0f);

@@ -340,6 +340,11 @@ class Shape:
 # The workloads: (c0) tiny layer on the CPU-runnable path, (c1) Kimi-K2-scale layer.
 TINY = Shape("tiny d=256 E=16 k=4 I=128", 256, 16, 4, 128, x_bf16=False)
 K2 = Shape("K2 d=7168 E=384 k=8 I=2048", 7168, 384, 8, 2048)
+# (c2) 64-token batched decode with Zipf(1.1) expert popularity: alpha 0.025 puts ~200
+# distinct experts in a 64-token step; (c3) 4096-token prefill with Zipf(0.8): alpha
+# 0.02 gives a 10x spread between the 90th and 10th percentile of tokens per expert.
+K2_BATCH = Shape("K2 T=64 Zipf(1.1)", 7168, 384, 8, 2048, zipf_s=1.1, zipf_alpha=0.025)
+K2_PREFILL = Shape("K2 T=4096 Zipf(0.8)", 7168, 384, 8, 2048, zipf_s=0.8, zipf_alpha=0.02)
 
 
 class SynthLayer:
