@@ -10,9 +10,11 @@ stream different experts and different shared/router weights, as a decode pass o
 stack of layers does, instead of re-reading what the 256 MB last-level cache holds.
 
 Prints one JSON line. value = tokens/s (1 token per step); ms_per_step is the layer
-latency per token. roofline: the dominant kernel (routed gate/up GEMV) timed with HIP
-events on the stream it runs on, against HBM peak. cpu_baseline: the engine's own CPU
-kernels on this host's cores on a bounded sample of the same workload.
+latency per token. roofline: the dominant kernel (the fused decode kernel) timed with HIP
+events on the stream it runs on, against HBM peak. prefill: a 4096-token prefill of the
+same layer with Zipf(0.8) expert popularity (tokens/s, fraction of the bf16 MFMA peak,
+its own roofline entry for the dominant GEMM). cpu_baseline: the engine's own CPU
+kernels on this host's cores on a bounded sample of the decode workload.
 """
 import argparse
 import json
@@ -91,6 +93,140 @@ def cpu_baseline(seconds: float, max_tokens: int, seed: int):
             "GBps": round((K * B_EXPERT + B_SHARED + B_ROUTER + B_TOKEN) / med / 1e9, 2)}
 
 
+# algorithmic flops of a T-token prefill step (routed gate/up + down, shared, router)
+def prefill_flops(T):
+    routed = 2 * T * K * 3 * I * D
+    shared = 6 * T * I * D
+    router = 2 * T * E * D
+    return routed, shared, router
+
+
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def batch_decode(a):
+    """64-token batched decode through the same K2 layer with Zipf(1.1) expert popularity
+    (~200 distinct experts per step): the grouped expert GEMMs with per-expert column
+    lists, the sort-based dispatch and the slot-ordered combine. HBM-bound: bytes per step
+    = U expert runs + shared + router + activations, U measured from the routing."""
+    import numpy as np
+    import k3moe
+    T = a.batch_tokens
+    log(f"bench: batched decode {T} tokens, Zipf(1.1) routing skew")
+    layers = [k3moe.SynthLayer(k3moe.K2_BATCH, seed=a.seed, layer=l, layout="tiled")
+              for l in range(2)]
+    n = a.batch_warmup + a.batch_steps
+    xs = layers[0].tokens(T * n, stream_base=1900)
+    ctx = k3moe.Ctx(layers[0].dev, max_tokens=T)
+    dx = k3moe.DevBuf.from_array(xs)
+    dout = k3moe.DevBuf(T * n * D * 4)
+    didx, dwt = k3moe.DevBuf(T * n * K * 4), k3moe.DevBuf(T * n * K * 4)
+
+    def step(i):
+        ctx.moe(layers[i % 2].dev, dx.ptr + i * T * D * 4, T, dout.ptr + i * T * D * 4,
+                didx.ptr + i * T * K * 4, dwt.ptr + i * T * K * 4)
+
+    for i in range(a.batch_warmup):
+        step(i)
+    ctx.sync()
+    k3moe.sync()
+    t0 = time.perf_counter()
+    for i in range(a.batch_warmup, n):
+        step(i)
+    k3moe.sync()
+    t1 = time.perf_counter()
+    ctx.sync()
+    idx = didx.download(np.int32, T * n * K).reshape(n, T * K)
+    U = [len(np.unique(r[r >= 0])) for r in idx[a.batch_warmup:]]
+    out = dout.download(np.float32, T * n * D)
+    assert np.isfinite(out).all()
+    ctx.destroy()
+    del layers
+    ms = (t1 - t0) * 1e3 / a.batch_steps
+    u = float(np.mean(U))
+    step_bytes = u * B_EXPERT + B_SHARED + B_ROUTER + T * B_TOKEN
+    return {"tokens": T, "ms_per_step": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+            "us_per_token": round(1e3 * ms / T, 2), "experts_per_step": round(u, 1),
+            "bytes_per_step": int(step_bytes),
+            "hbm_GBps": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "steps": a.batch_steps, "warmup": a.batch_warmup,
+            "workload": "64-token batched decode, same K2 layer, Zipf(1.1) selection-bias "
+                        "skew (alpha 0.025), 2 layers round-robin; grouped bf16 MFMA GEMMs"}
+
+
+def prefill(a):
+    """4096-token prefill through the same K2 layer with Zipf(0.8) expert popularity
+    (selection-bias skew), experts in the tiled layout in HBM, x resident: router +
+    dispatch + grouped bf16 MFMA GEMMs + combine. Reported against the bf16 dense peak."""
+    import numpy as np
+    import k3moe
+    T = a.prefill_tokens
+    log(f"bench: prefill {T} tokens, Zipf(0.8) routing skew")
+    layer = k3moe.SynthLayer(k3moe.K2_PREFILL, seed=a.seed, layer=0, layout="tiled")
+    x = layer.tokens(T, stream_base=900)
+    ctx = k3moe.Ctx(layer.dev, max_tokens=T)
+    dx = k3moe.DevBuf.from_array(x)
+    dout, didx, dwt = k3moe.DevBuf(T * D * 4), k3moe.DevBuf(T * K * 4), k3moe.DevBuf(T * K * 4)
+
+    def run():
+        ctx.moe(layer.dev, dx.ptr, T, dout.ptr, didx.ptr, dwt.ptr)
+
+    for _ in range(a.prefill_warmup):
+        run()
+    ctx.sync()
+    idx = didx.download(np.int32, T * K)
+    cnt = np.bincount(idx[idx >= 0], minlength=E)
+    act = cnt[cnt > 0]
+    ctx.profile(True)
+    k3moe.sync()
+    t0 = time.perf_counter()
+    for _ in range(a.prefill_steps):
+        run()
+    k3moe.sync()
+    t1 = time.perf_counter()
+    ctx.sync()
+    ms_stage, n_stage = ctx.stage_ms()
+    ctx.profile(False)
+    out = dout.download(np.float32, T * D)
+    assert np.isfinite(out).all()
+    reroutes = ctx.stats()[0]
+    ctx.destroy()
+    del layer
+    ms = (t1 - t0) * 1e3 / a.prefill_steps
+    routed, shared, router = prefill_flops(T)
+    flops = routed + shared + router
+    names = ["router", "dispatch", "routed_gateup", "routed_down", "shared_gateup",
+             "shared_down", "combine", "latent", "fused_layer", "activation_pieces"]
+    stage_us = {names[s]: round(1e3 * ms_stage[s] / max(n_stage[s], 1), 1)
+                for s in range(len(names)) if n_stage[s]}
+    gu_us = 1e3 * ms_stage[2] / max(n_stage[2], 1)
+    gu_flops = 2 * T * K * 2 * I * D
+    gu_tf = gu_flops / (gu_us * 1e-6) / 1e12
+    return {
+        "tokens": T,
+        "ms_per_step": round(ms, 4),
+        "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "algorithmic_flop": flops,
+        "achieved_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+        "steps": a.prefill_steps, "warmup": a.prefill_warmup,
+        "workload": "4096-token prefill, same K2 layer, Zipf(0.8) selection-bias skew "
+                    "(alpha 0.02), bf16-valued x; bf16 MFMA grouped GEMMs",
+        "routing": {"experts_used": int(len(act)), "max_tokens": int(cnt.max()),
+                    "min_tokens": int(act.min()),
+                    "p90_over_p10": round(float(np.percentile(act, 90) / max(np.percentile(act, 10), 1)), 2),
+                    "certificate_reroutes": int(reroutes)},
+        "stage_us": stage_us,
+        "roofline": {"kernel": "k_gemm<0> routed gate/up (MXFP4 dequantised to bf16 in "
+                               "registers, bf16 MFMA, SwiGLU epilogue)",
+                     "bound": "mfma", "achieved": round(gu_tf, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(gu_tf / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None, "flop_per_launch": gu_flops,
+                     "avg_launch_us": round(gu_us, 1)},
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,6 +237,14 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-tokens", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--batch-tokens", type=int, default=64,
+                    help="tokens of the batched-decode measurement (0: skip it)")
+    ap.add_argument("--batch-steps", type=int, default=20)
+    ap.add_argument("--batch-warmup", type=int, default=4)
+    ap.add_argument("--prefill-tokens", type=int, default=4096,
+                    help="tokens of the prefill measurement (0: skip it)")
+    ap.add_argument("--prefill-steps", type=int, default=5)
+    ap.add_argument("--prefill-warmup", type=int, default=2)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device-to-device copy (a counter calibration "
                          "point for rocprofv3 --pmc runs), outside the timed region")
@@ -142,7 +286,6 @@ def main():
     for i in range(a.warmup):
         step(i)
     ctx.sync()
-    ctx.profile(True)
     log(f"bench: timing {a.steps} steps")
     k3moe.sync()
     t0 = time.perf_counter()
@@ -150,6 +293,12 @@ def main():
         step(i)
     k3moe.sync()
     t1 = time.perf_counter()
+    ctx.sync()
+    # kernel times: HIP events around each launch on the context's stream, in a separate
+    # pass over the same steps so the events do not sit in the timed region
+    ctx.profile(True)
+    for i in range(a.warmup, n_tok):
+        step(i)
     ctx.sync()
     ms_stage, n_stage = ctx.stage_ms()
     ctx.profile(False)
@@ -202,7 +351,11 @@ def main():
                      "avg_launch_us": round(k_us, 2)},
     }
     ctx.destroy()
-    del layers
+    del layers, dx, dout, didx, dwt
+    if a.batch_tokens > 0:
+        res["batch_decode"] = batch_decode(a)
+    if a.prefill_tokens > 0:
+        res["prefill"] = prefill(a)
     if not a.no_cpu:
         log("bench: CPU baseline")
         res["cpu_baseline"] = cpu_baseline(a.cpu_seconds, a.cpu_tokens, a.seed)
