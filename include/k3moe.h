@@ -277,6 +277,80 @@ int  k3g_moe(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
  * (an exhausted bounded wait, a bad expert index). Returns 0 when clean. */
 int  k3g_sync(K3gCtx *ctx, void *stream);
 
+/* ========================================================== 3. HBM expert cache == */
+
+/* The engine's expert cache (src/cache/k3_cache.h, src/cache/k3_cache.c) re-planned for
+ * one GPU: the slot arena is HBM, the backing store is a pinned host bank holding every
+ * (layer, expert) run, and a miss is a hipMemcpyAsync on the cache's own copy stream.
+ * Policy and accounting follow the engine: LRU with pinning over a linear victim scan,
+ * slots that are EMPTY, INFLIGHT (reserved by a batch) or hold a key, batch prefetch in
+ * three phases (reserve, copy, publish), a per-(layer, expert) request histogram and a
+ * (layer, expert) request trace, and the true hit rate (hits - prefetch_reads) /
+ * requests. get() hands back DEVICE pointers that stay valid until the step that got
+ * them ends (k3gc_step_end). */
+typedef struct K3gcBank K3gcBank;
+typedef struct K3gCache K3gCache;
+
+/* A pinned host bank for n_layers x n_experts expert runs of `layout`: K3G_EXPERT_MXFP4
+ * (the checkpoint run, src/io/k3_load.h:3-9) or K3G_EXPERT_MXFP4_TILED (w1, w3, w2 each
+ * in the tiled MXFP4 layout, back to back). No reference counterpart: the engine reads
+ * experts from the checkpoint files. */
+int  k3gc_bank_create(K3gcBank **bank, int n_layers, int n_experts, int hidden, int inter,
+                      int layout);
+/* A bank with the geometry only (no memory), for caches that keep the bookkeeping only
+ * (k3gc_init with device < 0): replays of a request trace at any capacity, as the
+ * engine's offline simulator does. */
+int  k3gc_bank_geometry(K3gcBank **bank, int n_layers, int n_experts, int64_t expert_bytes);
+void k3gc_bank_free(K3gcBank *bank);
+/* host pointer to the run of (layer, expert), expert_bytes long, for the caller to fill */
+void *k3gc_bank_expert(K3gcBank *bank, int layer, int expert);
+int64_t k3gc_bank_expert_bytes(const K3gcBank *bank);
+
+/* Replaces k3_cache_init (src/cache/k3_cache.h:97, src/cache/k3_cache.c:263-353):
+ * budget_bytes of HBM rounded down to whole slots; fails (-1) below topk + 1 slots.
+ * device < 0 keeps the bookkeeping only (no memory is moved; for policy replays). */
+int  k3gc_init(K3gCache **cache, int device, K3gcBank *bank, int topk, int64_t budget_bytes);
+/* Replaces k3_cache_free. */
+void k3gc_free(K3gCache *cache);
+/* The K3ExpertSrc to pass as K3MoeW.src (get/getmany/resident, device pointers). */
+K3ExpertSrc *k3gc_src(K3gCache *cache);
+/* Replaces k3_cache_pin: pin or unpin the slot holding (layer, expert); 0 if not
+ * resident. */
+int  k3gc_pin(K3gCache *cache, int layer, int expert, int pin);
+/* Replaces k3_cache_prefetch: bring (layer, expert) resident without returning it. */
+int  k3gc_prefetch(K3gCache *cache, int layer, int expert);
+/* Replaces k3_cache_reset_stats, k3_cache_report, k3_cache_dump_hist,
+ * k3_cache_dump_trace (same formats). */
+void k3gc_reset_stats(K3gCache *cache);
+void k3gc_report(K3gCache *cache, const char *label);
+int  k3gc_dump_hist(const K3gCache *cache, const char *path);
+int  k3gc_dump_trace(const K3gCache *cache, const char *path);
+
+typedef struct {
+    int64_t requests, hits, misses, evictions, prefetch_reads, bytes_read;
+    double load_seconds;          /* copy-stream time spent on misses */
+    int nslot, resident, pinned;
+    int64_t slot_bytes;
+} K3gcStats;
+void k3gc_stats(K3gCache *cache, K3gcStats *out);
+
+/* A step: experts handed out between begin and end are not evicted until the work
+ * enqueued on `stream` before end() has finished with them. k3gc_wait makes `stream`
+ * wait for every copy issued so far. No reference counterpart (the engine's reads are
+ * synchronous). */
+void k3gc_step_begin(K3gCache *cache);
+void k3gc_step_end(K3gCache *cache, void *stream);
+void k3gc_wait(K3gCache *cache, void *stream);
+
+/* One streamed layer through the cache (experts in the bank's tiled layout): the
+ * router (or, with route_idx/route_wt given, that routing: host arrays [T][topk]),
+ * then the step's unique experts in first-seen order through getmany + get (the
+ * engine's call pattern, src/core/k3_ops.c:604-627), the shared expert while the misses
+ * copy, then the routed experts. L->experts is ignored; idx/wt are device outputs. */
+int  k3gc_moe(K3gCtx *ctx, K3gCache *cache, const K3gLayer *L, int layer, const float *x,
+              int T, float *out, int32_t *idx, float *wt, const int32_t *route_idx,
+              const float *route_wt, void *stream);
+
 /* Seeded synthetic data, generated identically on host and device from a counter
  * hash, so a CPU check can regenerate any slice of what the GPU holds.
  * byte i of stream `stream` under `seed` is k3s_byte(seed, stream, i). */

@@ -360,6 +360,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         }
     }
 
+    K3gCache *hc_end = NULL;
     if (w->src) {
         Fetcher f;
         memset(&f, 0, sizeof f);
@@ -377,6 +378,12 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         f.table = (K3ExpertQ *)calloc((size_t)E, sizeof(K3ExpertQ));
         f.have = (unsigned char *)calloc((size_t)E, 1);
         if (!f.slot_of || !f.table || !f.have) k3g_fatal("k3_moe: out of host memory");
+        K3gCache *hc = device_src ? k3gc_of_src(w->src) : NULL;
+        if (hc && hc->bank->layout != K3G_EXPERT_MXFP4)
+            k3g_fatal("k3_moe: an HBM cache used through the drop-in must hold checkpoint-"
+                      "layout expert runs");
+        /* every slot handed out during this call stays put until its kernels are done */
+        if (hc) k3gc_step_begin(hc);
         const int per_token = mode == 0 || T <= 1 || cache_only;
         if (per_token) {
             /* src/core/k3_ops.c:604-627 */
@@ -445,12 +452,16 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         free(f.slot_of);
         free(f.table);
         free(f.have);
+        /* the misses copy on the cache's stream: the expert kernels wait for them */
+        if (hc) k3gc_wait(hc, st);
+        hc_end = hc;
     }
 
     K3G_CHECK(hipMemcpyAsync(ctx->idx, ridx, (size_t)T * k * 4, hipMemcpyHostToDevice, st));
     K3G_CHECK(hipMemcpyAsync(ctx->wt, rwt, (size_t)T * k * 4, hipMemcpyHostToDevice, st));
     if (k3g_experts(ctx, &G, xd, T, ctx->idx, ctx->wt, od, st) != 0)
         k3g_fatal("k3_moe: launch failed");
+    if (hc_end) k3gc_step_end(hc_end, st);
     K3G_CHECK(hipMemcpyAsync(out, od, (size_t)T * d * 4, hipMemcpyDeviceToHost, st));
     if (k3g_sync(ctx, NULL) != 0) k3g_fatal("k3_moe: device error");
 

@@ -334,9 +334,6 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     g.b1 = L->act_b1;
     g.b2 = L->act_b2;
     g.nft = (I + 255) / 256;
-    k3g_stage_begin(c, K3G_ST_GATEUP, st);
-    rc |= k3k_gemm(&g, st);
-    k3g_stage_end(c, K3G_ST_GATEUP, st);
 
     K3kGemm s = g;
     if (SI > 0) {
@@ -358,21 +355,6 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         k3g_stage_end(c, K3G_ST_SH_GATEUP, st);
     }
 
-    g.mode = 1;
-    g.rows = d;
-    g.K = I;
-    g.ldb = I128;
-    g.b = c->hb;
-    g.bpiece = (long long)P * I128;
-    g.lo_flag = NULL;
-    g.h = NULL;
-    g.out = c->contrib;
-    g.ldo = d;
-    g.scatter = 1;
-    g.nft = (d + 511) / 512;
-    k3g_stage_begin(c, K3G_ST_DOWN, st);
-    rc |= k3k_gemm(&g, st);
-    k3g_stage_end(c, K3G_ST_DOWN, st);
 
     if (SI > 0) {
         s.mode = 1;
@@ -393,11 +375,39 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         rc |= k3k_gemm(&s, st);
         k3g_stage_end(c, K3G_ST_SH_DOWN, st);
     }
+    /* routed experts last, after any copies they wait for (the shared expert above
+     * overlaps those copies) */
+    if (c->routed_wait) {
+        if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) rc = -1;
+        c->routed_wait = NULL;
+    }
+    k3g_stage_begin(c, K3G_ST_GATEUP, st);
+    rc |= k3k_gemm(&g, st);
+    k3g_stage_end(c, K3G_ST_GATEUP, st);
+
+    g.mode = 1;
+    g.rows = d;
+    g.K = I;
+    g.ldb = I128;
+    g.b = c->hb;
+    g.bpiece = (long long)P * I128;
+    g.lo_flag = NULL;
+    g.h = NULL;
+    g.out = c->contrib;
+    g.ldo = d;
+    g.scatter = 1;
+    g.nft = (d + 511) / 512;
+    k3g_stage_begin(c, K3G_ST_DOWN, st);
+    rc |= k3k_gemm(&g, st);
+    k3g_stage_end(c, K3G_ST_DOWN, st);
+
     k3g_stage_begin(c, K3G_ST_COMBINE, st);
     rc |= k3k_combine(c->contrib, idx, wt, T, k, d, SI > 0 ? c->sh_out : NULL, out, st);
     k3g_stage_end(c, K3G_ST_COMBINE, st);
     return rc ? -1 : 0;
 }
+
+void k3g_ctx_routed_wait(K3gCtx *c, hipEvent_t ev) { if (c) c->routed_wait = ev; }
 
 void k3g_ctx_stats(K3gCtx *c, int64_t *out, int n)
 {
@@ -457,6 +467,10 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     const int projected = L->down != NULL;
     int rc = 0;
     if (gemmable(c, L)) return experts_gemm(c, L, x, T, idx, wt, out, st);
+    if (c->routed_wait) {
+        if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) return -1;
+        c->routed_wait = NULL;
+    }
     if (L->expert_fmt == K3G_EXPERT_MXFP4_TILED || L->shared_fmt != 0) {
         fprintf(stderr, "k3moe: tiled experts need the Kimi-K2 layer shape (no latent "
                         "projection, bf16 shared expert, widths multiple of 32)\n");

@@ -59,6 +59,7 @@ struct K3gCtx {
     uint16_t *xb, *hb, *hsb;     /* bf16 pieces of x [2][T][d128], h [2][T*k][I128], shared h */
     int32_t *tiles, *ntiles, *xflag;
     int max_tiles;
+    hipEvent_t routed_wait;      /* the next k3g_experts waits for it before routed work */
     unsigned long long *trace;   /* optional per-ticket timestamps of the fused kernel */
     /* optional per-stage timing: a ring of event pairs around each stage of a call,
      * harvested only when the ring wraps or the totals are read */
@@ -78,5 +79,8 @@ int k3g_route(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx,
               hipStream_t st);
 int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
                 const float *wt, float *out, hipStream_t st);
+/* Make the next k3g_experts wait for `ev` (recorded on another stream) before its routed
+ * expert kernels; the shared expert does not wait. */
+void k3g_ctx_routed_wait(K3gCtx *c, hipEvent_t ev);
 
 #endif /* K3G_CTX_H */

@@ -157,6 +157,16 @@ int k3k_dense(int fmt, const void *Wa, const void *Wb, int rows, int in,
 int k3k_combine(const float *contrib, const int32_t *idx, const float *wt, int T, int k,
                 int n, const float *add, float *out, hipStream_t st);
 
+/* Write table[e[i]] = q[i] for i < n (device expert tables updated from host-side
+ * decisions without a host staging buffer: the entries travel as kernel arguments). */
+#define K3K_EQSET 64
+typedef struct {
+    int n;
+    int e[K3K_EQSET];
+    K3ExpertQ q[K3K_EQSET];
+} K3kEqSet;
+int k3k_set_experts(K3ExpertQ *table, const K3kEqSet *s, hipStream_t st);
+
 /* y = w * x * (float)(1/sqrt(sum x^2 / n + eps)), double sum; one token per block. */
 int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
                 hipStream_t st);

@@ -347,3 +347,19 @@ extern "C" int k3k_fill_scales(uint8_t *dst, size_t n, uint64_t seed, uint64_t s
                        first, lo, hi);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
+
+/* ------------------------------------------------------------ expert tables ---- */
+__global__ void __launch_bounds__(64)
+k_set_experts(K3ExpertQ *table, const K3kEqSet s)
+{
+    const int i = threadIdx.x;
+    if (i < s.n) table[s.e[i]] = s.q[i];
+}
+
+extern "C" int k3k_set_experts(K3ExpertQ *table, const K3kEqSet *s, hipStream_t st)
+{
+    if (!table || s->n < 0 || s->n > K3K_EQSET) return -1;
+    if (s->n == 0) return 0;
+    hipLaunchKernelGGL(k_set_experts, dim3(1), dim3(64), 0, st, table, *s);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

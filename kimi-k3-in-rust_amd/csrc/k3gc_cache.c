@@ -1,8 +1,604 @@
-/* k3gc_cache.c - HBM-resident expert cache. */
+/* k3gc_cache.c - the engine's expert cache (src/cache/k3_cache.c) re-planned for HBM.
+ *
+ * What stays the engine's: the policy and the accounting. Slots hold a key, are EMPTY or
+ * are INFLIGHT (reserved by a batch); the victim is the first EMPTY slot, else the least
+ * recently used slot that is neither pinned nor INFLIGHT (a linear scan, as in
+ * k3_cache.c:49-60); a batch prefetch reserves serially, copies, then publishes
+ * (k3_cache.c:131-218); every get() counts a histogram entry and appends (layer, expert)
+ * to the trace before it is served (k3_cache.c:235-261); prefetched experts are counted
+ * apart so the true hit rate is (hits - prefetch_reads) / requests (k3_cache.c:403-429).
+ *
+ * What is new for a GPU. The slots are HBM; the backing store is a pinned host bank; a
+ * miss is a hipMemcpyAsync on the cache's own copy stream, ordered after the last step
+ * that read the victim slot (an event recorded on the compute stream when that step
+ * ended), and a consumer makes its stream wait for the copies with one event. A slot
+ * handed out in the open step is never a victim, which is the engine's "capacity above
+ * top-k" rule (k3_cache.c:304-313) applied to a whole step's working set. */
 #include "k3gc_cache.h"
+#include "k3g_ctx.h"
 
-int k3gc_is_device_src(const K3ExpertSrc *src)
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static int has_device(const K3gCache *c) { return c->device >= 0; }
+
+static int64_t run_bytes(int hidden, int inter, int layout)
 {
-    (void)src;
+    if (layout == K3G_EXPERT_MXFP4_TILED)
+        return 2 * (int64_t)k3k_tiled_mxfp4_bytes(inter, hidden) +
+               (int64_t)k3k_tiled_mxfp4_bytes(hidden, inter);
+    return k3g_expert_layout(hidden, inter).nbytes;
+}
+
+/* ------------------------------------------------------------------ host bank ---- */
+int k3gc_bank_create(K3gcBank **out, int n_layers, int n_experts, int hidden, int inter,
+                     int layout)
+{
+    *out = NULL;
+    if (n_layers < 1 || n_experts < 1 || hidden < 32 || inter < 32 ||
+        (layout != K3G_EXPERT_MXFP4 && layout != K3G_EXPERT_MXFP4_TILED)) {
+        fprintf(stderr, "k3gc_bank_create: unsupported shape\n");
+        return -1;
+    }
+    const int64_t eb = run_bytes(hidden, inter, layout);
+    if (eb <= 0) {
+        fprintf(stderr, "k3gc_bank_create: no tiled layout for hidden %d inter %d\n", hidden,
+                inter);
+        return -1;
+    }
+    K3gcBank *b = (K3gcBank *)calloc(1, sizeof *b);
+    if (!b) return -1;
+    b->n_layers = n_layers;
+    b->n_experts = n_experts;
+    b->hidden = hidden;
+    b->inter = inter;
+    b->layout = layout;
+    b->expert_bytes = eb;
+    const size_t total = (size_t)n_layers * n_experts * (size_t)eb;
+    void *p = NULL;
+    if (hipHostMalloc(&p, total, hipHostMallocDefault) != hipSuccess || !p) {
+        fprintf(stderr, "k3gc_bank_create: cannot pin %.2f GB of host memory\n", total / 1e9);
+        free(b);
+        return -1;
+    }
+    b->host = (unsigned char *)p;
+    b->pinned_host = 1;
+    *out = b;
     return 0;
+}
+
+int k3gc_bank_geometry(K3gcBank **out, int n_layers, int n_experts, int64_t expert_bytes)
+{
+    *out = NULL;
+    if (n_layers < 1 || n_experts < 1 || expert_bytes < 1) return -1;
+    K3gcBank *b = (K3gcBank *)calloc(1, sizeof *b);
+    if (!b) return -1;
+    b->n_layers = n_layers;
+    b->n_experts = n_experts;
+    b->layout = K3G_EXPERT_MXFP4;
+    b->expert_bytes = expert_bytes;
+    *out = b;
+    return 0;
+}
+
+void k3gc_bank_free(K3gcBank *b)
+{
+    if (!b) return;
+    if (b->host && b->pinned_host) hipHostFree(b->host);
+    free(b);
+}
+
+void *k3gc_bank_expert(K3gcBank *b, int layer, int expert)
+{
+    if (!b || !b->host || layer < 0 || layer >= b->n_layers || expert < 0 ||
+        expert >= b->n_experts)
+        return NULL;
+    return b->host + ((size_t)layer * b->n_experts + expert) * (size_t)b->expert_bytes;
+}
+
+int64_t k3gc_bank_expert_bytes(const K3gcBank *b) { return b ? b->expert_bytes : 0; }
+
+/* ------------------------------------------------------------------- policy ---- */
+/* The first EMPTY slot; else the least recently used one that is not INFLIGHT, not
+ * pinned and not handed out in the open step. -1 when there is none. */
+static int pick_victim(const K3gCache *c)
+{
+    int best = -1;
+    uint64_t oldest = UINT64_MAX;
+    for (int i = 0; i < c->nslot; i++) {
+        if (c->key_of[i] == K3GC_INFLIGHT) continue;
+        if (c->key_of[i] == K3GC_EMPTY) return i;
+        if (c->pinned[i]) continue;
+        if (c->step_open && c->used_at[i] >= c->step_clock) continue;
+        if (c->used_at[i] < oldest) { oldest = c->used_at[i]; best = i; }
+    }
+    return best;
+}
+
+static void fill_q(const K3gCache *c, int slot, K3ExpertQ *q)
+{
+    const uintptr_t base = (uintptr_t)c->arena + (uintptr_t)slot * (uintptr_t)c->slot_bytes;
+    const K3gcBank *b = c->bank;
+    memset(q, 0, sizeof *q);
+    if (b->layout == K3G_EXPERT_MXFP4_TILED) {
+        const uintptr_t t13 = (uintptr_t)k3k_tiled_mxfp4_bytes(b->inter, b->hidden);
+        q->p1 = (const unsigned char *)base;
+        q->p3 = (const unsigned char *)(base + t13);
+        q->p2 = (const unsigned char *)(base + 2 * t13);
+    } else {
+        const K3gExpertLayout g = k3g_expert_layout(b->hidden, b->inter);
+        q->p1 = (const unsigned char *)(base + g.p1_off);
+        q->s1 = (const unsigned char *)(base + g.s1_off);
+        q->p2 = (const unsigned char *)(base + g.p2_off);
+        q->s2 = (const unsigned char *)(base + g.s2_off);
+        q->p3 = (const unsigned char *)(base + g.p3_off);
+        q->s3 = (const unsigned char *)(base + g.s3_off);
+    }
+}
+
+/* ------------------------------------------------------------- data movement ---- */
+static void harvest_timers(K3gCache *c, int all)
+{
+    while (c->t_used > 0 && (all || c->t_used == K3GC_TIMER_RING)) {
+        const int i = (c->t_head - c->t_used + K3GC_TIMER_RING) % K3GC_TIMER_RING;
+        float ms = 0.0f;
+        K3G_CHECK(hipEventSynchronize(c->tev[i][1]));
+        K3G_CHECK(hipEventElapsedTime(&ms, c->tev[i][0], c->tev[i][1]));
+        c->load_seconds += ms * 1e-3;
+        c->t_used--;
+    }
+}
+
+/* Open a timed batch of copies (once per get/getmany/prefetch that copies). */
+static void batch_open(K3gCache *c)
+{
+    if (!has_device(c) || c->t_open) return;
+    harvest_timers(c, 0);
+    K3G_CHECK(hipEventRecord(c->tev[c->t_head][0], c->copy));
+    c->t_open = 1;
+}
+
+static void batch_close(K3gCache *c)
+{
+    if (!has_device(c) || !c->t_open) return;
+    K3G_CHECK(hipEventRecord(c->tev[c->t_head][1], c->copy));
+    c->t_head = (c->t_head + 1) % K3GC_TIMER_RING;
+    c->t_used++;
+    c->t_open = 0;
+    K3G_CHECK(hipEventRecord(c->last_copy, c->copy));
+    c->copies_pending = 1;
+}
+
+/* Copy (layer, expert) from the bank into `slot`, after the last step that read it. */
+static void copy_in(K3gCache *c, int slot, int32_t key)
+{
+    c->bytes_read += (uint64_t)c->bank->expert_bytes;
+    if (!has_device(c)) return;
+    batch_open(c);
+    const int64_t s = c->use_step[slot];
+    if (s >= 0 && c->step - s <= K3GC_STEP_RING)
+        K3G_CHECK(hipStreamWaitEvent(c->copy, c->step_ev[s % K3GC_STEP_RING], 0));
+    K3G_CHECK(hipMemcpyAsync(c->arena + (size_t)slot * c->slot_bytes,
+                             c->bank->host + (size_t)key * (size_t)c->bank->expert_bytes,
+                             (size_t)c->bank->expert_bytes, hipMemcpyHostToDevice, c->copy));
+}
+
+/* Bring (layer, expert) resident; returns its slot or -1. src/cache/k3_cache.c:63-110 */
+static int admit(K3gCache *c, int layer, int expert)
+{
+    const int32_t key = layer * c->n_experts + expert;
+    int slot = c->slot_of[key];
+    if (slot >= 0) {
+        c->hits++;
+        c->used_at[slot] = ++c->clock;
+        return slot;
+    }
+    c->misses++;
+    slot = pick_victim(c);
+    if (slot < 0) {
+        fprintf(stderr, "k3gc: no evictable slot for L%d expert %d (all pinned or in use by "
+                        "this step)\n", layer, expert);
+        return -1;
+    }
+    if (c->key_of[slot] >= 0) { c->slot_of[c->key_of[slot]] = -1; c->evictions++; }
+    copy_in(c, slot, key);
+    c->key_of[slot] = key;
+    c->slot_of[key] = slot;
+    c->used_at[slot] = ++c->clock;
+    return slot;
+}
+
+/* --------------------------------------------------------- K3ExpertSrc vtable ---- */
+static int cache_get(K3ExpertSrc *self, int layer, int expert, K3ExpertQ *out)
+{
+    K3gCache *c = (K3gCache *)self;
+    if (layer < 0 || layer >= c->n_layers || expert < 0 || expert >= c->n_experts) {
+        fprintf(stderr, "k3gc: out of range L%d expert %d\n", layer, expert);
+        return -1;
+    }
+    c->hist[layer * c->n_experts + expert]++;
+    /* the request as the model made it, before it is served (k3_cache.c:244-255) */
+    if (c->ntrace + 2 > c->captrace) {
+        const int64_t nc = c->captrace ? c->captrace * 2 : (1 << 16);
+        int32_t *nt = (int32_t *)realloc(c->trace, (size_t)nc * sizeof(int32_t));
+        if (nt) { c->trace = nt; c->captrace = nc; }
+    }
+    if (c->ntrace + 2 <= c->captrace) {
+        c->trace[c->ntrace++] = layer;
+        c->trace[c->ntrace++] = expert;
+    }
+    const int slot = admit(c, layer, expert);
+    batch_close(c);
+    if (slot < 0) return -1;
+    if (out) fill_q(c, slot, out);
+    return 0;
+}
+
+/* src/cache/k3_cache.c:131-218: reserve serially, copy, publish. The copies are queued
+ * back to back on the copy stream, so the DMA engine sees the whole batch at once. */
+static int cache_getmany(K3ExpertSrc *self, int layer, const int *ids, int n)
+{
+    K3gCache *c = (K3gCache *)self;
+    if (n <= 0 || layer < 0 || layer >= c->n_layers) return 0;
+    int slots[K3_MAX_TOPK], experts[K3_MAX_TOPK];
+    int nw = 0;
+    for (int i = 0; i < n && nw < K3_MAX_TOPK; i++) {
+        const int e = ids[i];
+        if (e < 0 || e >= c->n_experts) continue;
+        const int32_t key = layer * c->n_experts + e;
+        if (c->slot_of[key] >= 0) continue;
+        int dup = 0;
+        for (int j = 0; j < nw; j++) if (experts[j] == e) { dup = 1; break; }
+        if (dup) continue;
+        const int slot = pick_victim(c);
+        if (slot < 0) break;
+        if (c->key_of[slot] >= 0) { c->slot_of[c->key_of[slot]] = -1; c->evictions++; }
+        c->key_of[slot] = K3GC_INFLIGHT;
+        c->used_at[slot] = ++c->clock;
+        slots[nw] = slot;
+        experts[nw] = e;
+        nw++;
+    }
+    for (int i = 0; i < nw; i++) copy_in(c, slots[i], layer * c->n_experts + experts[i]);
+    batch_close(c);
+    for (int i = 0; i < nw; i++) {
+        const int32_t key = layer * c->n_experts + experts[i];
+        c->key_of[slots[i]] = key;
+        c->slot_of[key] = slots[i];
+        c->used_at[slots[i]] = ++c->clock;
+        c->prefetch_reads++;
+    }
+    return nw;
+}
+
+static int cache_resident(K3ExpertSrc *self, int layer, int expert, K3ExpertQ *out)
+{
+    K3gCache *c = (K3gCache *)self;
+    if (layer < 0 || layer >= c->n_layers || expert < 0 || expert >= c->n_experts) return 0;
+    const int slot = c->slot_of[layer * c->n_experts + expert];
+    if (slot < 0) return 0;
+    if (out) fill_q(c, slot, out);
+    return 1;
+}
+
+int k3gc_is_device_src(const K3ExpertSrc *src) { return src && src->get == cache_get; }
+
+K3gCache *k3gc_of_src(K3ExpertSrc *src)
+{
+    return k3gc_is_device_src(src) ? (K3gCache *)src : NULL;
+}
+
+K3ExpertSrc *k3gc_src(K3gCache *c) { return c ? &c->src : NULL; }
+
+/* ------------------------------------------------------------- construction ---- */
+int k3gc_init(K3gCache **out, int device, K3gcBank *bank, int topk, int64_t budget_bytes)
+{
+    *out = NULL;
+    if (!bank || topk < 1) return -1;
+    if (device >= 0 && !bank->host) {
+        fprintf(stderr, "k3gc_init: the bank holds no host memory\n");
+        return -1;
+    }
+    K3gCache *c = (K3gCache *)calloc(1, sizeof *c);
+    if (!c) return -1;
+    c->src.get = cache_get;
+    c->src.getmany = cache_getmany;
+    c->src.resident = cache_resident;
+    c->src.ctx = c;
+    c->bank = bank;
+    c->device = device;
+    c->n_layers = bank->n_layers;
+    c->n_experts = bank->n_experts;
+    c->topk = topk;
+    /* a slot is one run rounded up to 64 KB, so every slot starts on a 64 KB boundary */
+    c->slot_bytes = (bank->expert_bytes + 65535) & ~(int64_t)65535;
+    c->nslot = (int)(budget_bytes / c->slot_bytes);
+    if (c->nslot < topk + 1) {
+        fprintf(stderr,
+                "k3gc_init: budget %.2f GB gives %d slots of %.2f MB, but top-%d needs at "
+                "least %d\n", (double)budget_bytes / 1e9, c->nslot, c->slot_bytes / 1e6, topk,
+                topk + 1);
+        free(c);
+        return -1;
+    }
+    const size_t nkey = (size_t)c->n_layers * c->n_experts;
+    c->slot_of = (int32_t *)malloc(nkey * sizeof(int32_t));
+    c->key_of = (int32_t *)malloc((size_t)c->nslot * sizeof(int32_t));
+    c->used_at = (uint64_t *)calloc((size_t)c->nslot, sizeof(uint64_t));
+    c->pinned = (unsigned char *)calloc((size_t)c->nslot, 1);
+    c->use_step = (int64_t *)malloc((size_t)c->nslot * sizeof(int64_t));
+    c->hist = (uint32_t *)calloc(nkey, sizeof(uint32_t));
+    if (!c->slot_of || !c->key_of || !c->used_at || !c->pinned || !c->use_step || !c->hist) {
+        k3gc_free(c);
+        return -1;
+    }
+    for (size_t i = 0; i < nkey; i++) c->slot_of[i] = -1;
+    for (int i = 0; i < c->nslot; i++) { c->key_of[i] = K3GC_EMPTY; c->use_step[i] = -1; }
+    if (device >= 0) {
+        if (hipSetDevice(device) != hipSuccess ||
+            hipMalloc((void **)&c->arena, (size_t)c->nslot * c->slot_bytes) != hipSuccess) {
+            fprintf(stderr, "k3gc_init: cannot allocate %.2f GB of HBM slots\n",
+                    (double)c->nslot * c->slot_bytes / 1e9);
+            c->arena = NULL;
+            k3gc_free(c);
+            return -1;
+        }
+        K3G_CHECK(hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking));
+        for (int i = 0; i < K3GC_STEP_RING; i++)
+            K3G_CHECK(hipEventCreateWithFlags(&c->step_ev[i], hipEventDisableTiming));
+        K3G_CHECK(hipEventCreateWithFlags(&c->last_copy, hipEventDisableTiming));
+        for (int i = 0; i < K3GC_TIMER_RING; i++) {
+            K3G_CHECK(hipEventCreate(&c->tev[i][0]));
+            K3G_CHECK(hipEventCreate(&c->tev[i][1]));
+        }
+        const size_t tb = nkey * sizeof(K3ExpertQ);
+        if (hipMalloc((void **)&c->dev_table, tb) != hipSuccess ||
+            hipMemset(c->dev_table, 0, tb) != hipSuccess) {
+            c->dev_table = NULL;
+            k3gc_free(c);
+            return -1;
+        }
+    }
+    *out = c;
+    return 0;
+}
+
+void k3gc_free(K3gCache *c)
+{
+    if (!c) return;
+    if (has_device(c)) {
+        hipSetDevice(c->device);
+        if (c->copy) {
+            hipStreamSynchronize(c->copy);
+            for (int i = 0; i < K3GC_STEP_RING; i++)
+                if (c->step_ev[i]) hipEventDestroy(c->step_ev[i]);
+            if (c->last_copy) hipEventDestroy(c->last_copy);
+            for (int i = 0; i < K3GC_TIMER_RING; i++) {
+                if (c->tev[i][0]) hipEventDestroy(c->tev[i][0]);
+                if (c->tev[i][1]) hipEventDestroy(c->tev[i][1]);
+            }
+            hipStreamDestroy(c->copy);
+        }
+        hipDeviceSynchronize();
+        if (c->arena) hipFree(c->arena);
+        if (c->dev_table) hipFree(c->dev_table);
+        if (c->host_idx) hipHostFree(c->host_idx);
+    }
+    free(c->slot_of);
+    free(c->key_of);
+    free(c->used_at);
+    free(c->pinned);
+    free(c->use_step);
+    free(c->hist);
+    free(c->trace);
+    free(c);
+}
+
+/* ------------------------------------------------------------------- steps ---- */
+void k3gc_step_begin(K3gCache *c)
+{
+    if (!c) return;
+    c->step_open = 1;
+    c->step_clock = c->clock + 1;
+}
+
+void k3gc_step_end(K3gCache *c, void *stream)
+{
+    if (!c) return;
+    if (has_device(c)) {
+        hipEvent_t ev = c->step_ev[c->step % K3GC_STEP_RING];
+        /* the event last marked step - RING: its waits are long satisfied, but make
+         * sure before it is re-recorded */
+        if (c->step >= K3GC_STEP_RING) K3G_CHECK(hipEventSynchronize(ev));
+        K3G_CHECK(hipEventRecord(ev, (hipStream_t)stream));
+    }
+    if (c->step_open)
+        for (int i = 0; i < c->nslot; i++)
+            if (c->key_of[i] != K3GC_EMPTY && c->used_at[i] >= c->step_clock)
+                c->use_step[i] = c->step;
+    c->step++;
+    c->step_open = 0;
+}
+
+void k3gc_wait(K3gCache *c, void *stream)
+{
+    if (!c || !has_device(c) || !c->copies_pending) return;
+    K3G_CHECK(hipStreamWaitEvent((hipStream_t)stream, c->last_copy, 0));
+    c->copies_pending = 0;
+}
+
+/* --------------------------------------------------------------- management ---- */
+int k3gc_pin(K3gCache *c, int layer, int expert, int pin)
+{
+    if (!c || layer < 0 || layer >= c->n_layers || expert < 0 || expert >= c->n_experts)
+        return 0;
+    const int slot = c->slot_of[layer * c->n_experts + expert];
+    if (slot < 0) return 0;
+    c->pinned[slot] = pin ? 1 : 0;
+    return 1;
+}
+
+int k3gc_prefetch(K3gCache *c, int layer, int expert)
+{
+    if (!c || layer < 0 || layer >= c->n_layers || expert < 0 || expert >= c->n_experts)
+        return -1;
+    const int slot = admit(c, layer, expert);
+    batch_close(c);
+    return slot >= 0 ? 0 : -1;
+}
+
+void k3gc_reset_stats(K3gCache *c)
+{
+    if (!c) return;
+    if (has_device(c)) harvest_timers(c, 1);
+    /* prefetch_reads covers the same window as hits (k3_cache.c:384-394) */
+    c->hits = c->misses = c->evictions = c->bytes_read = c->prefetch_reads = 0;
+    c->load_seconds = 0.0;
+}
+
+void k3gc_stats(K3gCache *c, K3gcStats *o)
+{
+    memset(o, 0, sizeof *o);
+    if (!c) return;
+    if (has_device(c)) harvest_timers(c, 1);
+    o->requests = (int64_t)(c->hits + c->misses);
+    o->hits = (int64_t)c->hits;
+    o->misses = (int64_t)c->misses;
+    o->evictions = (int64_t)c->evictions;
+    o->prefetch_reads = (int64_t)c->prefetch_reads;
+    o->bytes_read = (int64_t)c->bytes_read;
+    o->load_seconds = c->load_seconds;
+    o->nslot = c->nslot;
+    o->slot_bytes = c->slot_bytes;
+    for (int i = 0; i < c->nslot; i++) {
+        if (c->key_of[i] >= 0) o->resident++;
+        if (c->pinned[i]) o->pinned++;
+    }
+}
+
+void k3gc_report(K3gCache *c, const char *label)
+{
+    K3gcStats s;
+    k3gc_stats(c, &s);
+    const double n = (double)s.requests;
+    printf("cache [%s]\n", label ? label : "");
+    printf("  slots        : %d of %.2f MB = %.2f GB HBM (%d resident, %d pinned)\n", s.nslot,
+           s.slot_bytes / 1e6, (double)s.nslot * s.slot_bytes / 1e9, s.resident, s.pinned);
+    printf("  requests     : %lld  hits %lld (%.2f%%)  misses %lld  evictions %lld\n",
+           (long long)s.requests, (long long)s.hits, n > 0 ? 100.0 * s.hits / n : 0.0,
+           (long long)s.misses, (long long)s.evictions);
+    if (s.prefetch_reads) {
+        const long long served = s.hits > s.prefetch_reads ? s.hits - s.prefetch_reads : 0;
+        printf("  of those hits : %lld came from the batch prefetch, i.e. copied this step;\n"
+               "                  TRUE resident hit rate %.2f%%\n",
+               (long long)s.prefetch_reads, n > 0 ? 100.0 * served / n : 0.0);
+    }
+    printf("  copied H2D   : %.2f GB in %.3f s of copy-stream time (%.1f GB/s)\n",
+           s.bytes_read / 1e9, s.load_seconds,
+           s.load_seconds > 0 ? s.bytes_read / 1e9 / s.load_seconds : 0.0);
+}
+
+int k3gc_dump_hist(const K3gCache *c, const char *path)
+{
+    FILE *f = fopen(path, "w");
+    if (!f) return -1;
+    fprintf(f, "{\"n_layers\":%d,\"n_experts\":%d,\"counts\":{", c->n_layers, c->n_experts);
+    int first = 1;
+    for (int L = 0; L < c->n_layers; L++)
+        for (int e = 0; e < c->n_experts; e++) {
+            const uint32_t v = c->hist[L * c->n_experts + e];
+            if (!v) continue;
+            fprintf(f, "%s\"%d,%d\":%u", first ? "" : ",", L, e, v);
+            first = 0;
+        }
+    fprintf(f, "}}\n");
+    fclose(f);
+    return 0;
+}
+
+int k3gc_dump_trace(const K3gCache *c, const char *path)
+{
+    if (!c->trace || c->ntrace == 0) return -1;
+    FILE *f = fopen(path, "wb");
+    if (!f) return -1;
+    const size_t n = fwrite(c->trace, sizeof(int32_t), (size_t)c->ntrace, f);
+    fclose(f);
+    return n == (size_t)c->ntrace ? 0 : -1;
+}
+
+/* ------------------------------------------------------------ streamed layer ---- */
+int k3gc_moe(K3gCtx *ctx, K3gCache *c, const K3gLayer *L, int layer, const float *x, int T,
+             float *out, int32_t *idx, float *wt, const int32_t *route_idx,
+             const float *route_wt, void *stream)
+{
+    if (!ctx || !c || !has_device(c) || !L || layer < 0 || layer >= c->n_layers) return -1;
+    if (c->bank->layout != K3G_EXPERT_MXFP4_TILED || L->n_experts != c->n_experts ||
+        L->hidden != c->bank->hidden || L->inter != c->bank->inter) {
+        fprintf(stderr, "k3gc_moe: the layer does not match the cache's tiled bank\n");
+        return -1;
+    }
+    hipStream_t st = stream ? (hipStream_t)stream : (hipStream_t)k3g_ctx_stream(ctx);
+    const int k = L->topk, P = T * k;
+    if (T < 1 || k < 1 || P > 65536) return -1;
+    if (c->host_idx_cap < P) {
+        if (c->host_idx) hipHostFree(c->host_idx);
+        c->host_idx = NULL;
+        if (hipHostMalloc((void **)&c->host_idx, (size_t)P * 4, hipHostMallocDefault) !=
+            hipSuccess) return -1;
+        c->host_idx_cap = P;
+    }
+    if (!route_idx) {
+        if (k3g_route(ctx, L, x, T, idx, wt, st) != 0) return -1;
+        K3G_CHECK(hipMemcpyAsync(c->host_idx, idx, (size_t)P * 4, hipMemcpyDeviceToHost, st));
+        K3G_CHECK(hipStreamSynchronize(st));
+    } else {
+        memcpy(c->host_idx, route_idx, (size_t)P * 4);
+        K3G_CHECK(hipMemcpyAsync(idx, c->host_idx, (size_t)P * 4, hipMemcpyHostToDevice, st));
+        K3G_CHECK(hipMemcpyAsync(wt, route_wt, (size_t)P * 4, hipMemcpyHostToDevice, st));
+        /* the staging buffer is reused by the next call: let the copies finish */
+        K3G_CHECK(hipStreamSynchronize(st));
+    }
+    /* the step's unique experts in first-seen order: getmany, then one get each */
+    int *uniq = (int *)malloc((size_t)P * sizeof(int));
+    unsigned char *seen = (unsigned char *)calloc((size_t)c->n_experts, 1);
+    if (!uniq || !seen) { free(uniq); free(seen); return -1; }
+    int nu = 0;
+    for (int p = 0; p < P; p++) {
+        const int e = c->host_idx[p];
+        if (e >= 0 && e < c->n_experts && !seen[e]) { seen[e] = 1; uniq[nu++] = e; }
+    }
+    k3gc_step_begin(c);
+    for (int i = 0; i < nu; i += K3_MAX_TOPK)
+        cache_getmany(&c->src, layer, uniq + i, nu - i < K3_MAX_TOPK ? nu - i : K3_MAX_TOPK);
+    int rc = 0;
+    K3ExpertQ *table = c->dev_table + (size_t)layer * c->n_experts;
+    K3kEqSet set;
+    memset(&set, 0, sizeof set);
+    for (int i = 0; i < nu; i++) {
+        K3ExpertQ q;
+        if (cache_get(&c->src, layer, uniq[i], &q) != 0) { rc = -1; break; }
+        set.e[set.n] = uniq[i];
+        set.q[set.n] = q;
+        if (++set.n == K3K_EQSET) {
+            rc |= k3k_set_experts(table, &set, st);
+            set.n = 0;
+        }
+    }
+    if (rc == 0 && set.n) rc |= k3k_set_experts(table, &set, st);
+    free(uniq);
+    free(seen);
+    if (rc == 0) {
+        K3gLayer Lc = *L;
+        Lc.experts = table;
+        Lc.expert_fmt = K3G_EXPERT_MXFP4_TILED;
+        /* the shared expert runs while the misses copy; the routed experts wait */
+        if (c->copies_pending) {
+            k3g_ctx_routed_wait(ctx, c->last_copy);
+            c->copies_pending = 0;
+        }
+        rc = k3g_experts(ctx, &Lc, x, T, idx, wt, out, st);
+    }
+    k3gc_step_end(c, st);
+    return rc;
 }

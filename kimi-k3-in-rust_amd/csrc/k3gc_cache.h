@@ -1,10 +1,68 @@
-/* k3gc_cache.h - HBM expert cache (private declarations shared with the drop-in). */
+/* k3gc_cache.h - HBM expert cache (private declarations shared with the drop-in and the
+ * context). The public API is in include/k3moe.h. */
 #ifndef K3GC_CACHE_H
 #define K3GC_CACHE_H
 
 #include "../../include/k3moe.h"
 
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__ 1
+#endif
+#include <hip/hip_runtime_api.h>
+
+/* Slot states in key_of[] (src/cache/k3_cache.h:40-45 keeps the same three): a key,
+ * EMPTY, or INFLIGHT (reserved by a batch whose copies are not yet issued). */
+#define K3GC_EMPTY (-1)
+#define K3GC_INFLIGHT (-2)
+
+#define K3GC_STEP_RING 1024
+#define K3GC_TIMER_RING 256
+
+struct K3gcBank {
+    int n_layers, n_experts, hidden, inter, layout;
+    int64_t expert_bytes;
+    unsigned char *host;          /* pinned, [n_layers][n_experts][expert_bytes] */
+    int pinned_host;              /* 1: hipHostMalloc, 0: malloc (no device) */
+};
+
+struct K3gCache {
+    K3ExpertSrc src;              /* first: callers pass &cache->src as K3MoeW.src */
+    K3gcBank *bank;
+    int device;                   /* < 0: bookkeeping only (no device memory, no copies) */
+    int n_layers, n_experts, topk;
+    int64_t slot_bytes;
+    int nslot;
+    unsigned char *arena;         /* device, nslot * slot_bytes */
+    int32_t *slot_of;             /* [n_layers * n_experts] -> slot or -1 */
+    int32_t *key_of;              /* [nslot] -> key, K3GC_EMPTY or K3GC_INFLIGHT */
+    uint64_t *used_at;            /* [nslot] LRU stamp */
+    unsigned char *pinned;        /* [nslot] */
+    int64_t *use_step;            /* [nslot] last step that handed the slot out, -1 none */
+    uint64_t clock;
+    int step_open;
+    uint64_t step_clock;          /* used_at >= step_clock: handed out in the open step */
+    int64_t step;                 /* steps ended so far */
+    /* device side */
+    hipStream_t copy;             /* the side stream the misses are copied on */
+    hipEvent_t step_ev[K3GC_STEP_RING];   /* compute stream, end of each step */
+    hipEvent_t last_copy;         /* copy stream, after the latest copy */
+    int copies_pending;           /* copies issued since the last k3gc_wait */
+    hipEvent_t tev[K3GC_TIMER_RING][2];   /* copy-stream timing per batch of copies */
+    int t_head, t_used, t_open;
+    K3ExpertQ *dev_table;         /* [n_layers][n_experts] device pointers (k3gc_moe) */
+    int32_t *host_idx;            /* pinned staging of a step's routing */
+    int host_idx_cap;
+    /* stats (src/cache/k3_cache.h:74-83) */
+    uint64_t hits, misses, evictions, bytes_read, prefetch_reads;
+    double load_seconds;
+    uint32_t *hist;               /* [n_layers * n_experts] requests */
+    int32_t *trace;               /* (layer, expert) pairs in request order */
+    int64_t ntrace, captrace;
+};
+
 /* 1 when src is an HBM expert cache, whose get() hands out device pointers. */
 int k3gc_is_device_src(const K3ExpertSrc *src);
+/* The cache behind a device source (NULL otherwise). */
+K3gCache *k3gc_of_src(K3ExpertSrc *src);
 
 #endif

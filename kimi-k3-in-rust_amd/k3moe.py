@@ -51,6 +51,20 @@ class K3ExpertSrc(C.Structure):
                 ("ctx", C.c_void_p)]
 
 
+class K3gcStats(C.Structure):
+    """include/k3moe.h K3gcStats"""
+    _fields_ = [("requests", C.c_int64), ("hits", C.c_int64), ("misses", C.c_int64),
+                ("evictions", C.c_int64), ("prefetch_reads", C.c_int64),
+                ("bytes_read", C.c_int64), ("load_seconds", C.c_double), ("nslot", C.c_int),
+                ("resident", C.c_int), ("pinned", C.c_int), ("slot_bytes", C.c_int64)]
+
+
+# the K3ExpertSrc entry points, called through the vtable as the engine does
+SRC_GET = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p)
+SRC_GETMANY = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int)
+SRC_RESIDENT = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p)
+
+
 class K3MoeW(C.Structure):
     """include/k3/k3.h:357-380."""
     _fields_ = [
@@ -166,6 +180,45 @@ def lib() -> C.CDLL:
         L.k3g_tile_mxfp4.restype = i
         L.k3g_tile_bf16.argtypes = [vp, vp, i, i, vp]
         L.k3g_tile_bf16.restype = i
+        i64 = C.c_int64
+        L.k3gc_bank_create.argtypes = [C.POINTER(vp), i, i, i, i, i]
+        L.k3gc_bank_create.restype = i
+        L.k3gc_bank_geometry.argtypes = [C.POINTER(vp), i, i, i64]
+        L.k3gc_bank_geometry.restype = i
+        L.k3gc_bank_free.argtypes = [vp]
+        L.k3gc_bank_free.restype = None
+        L.k3gc_bank_expert.argtypes = [vp, i, i]
+        L.k3gc_bank_expert.restype = vp
+        L.k3gc_bank_expert_bytes.argtypes = [vp]
+        L.k3gc_bank_expert_bytes.restype = i64
+        L.k3gc_init.argtypes = [C.POINTER(vp), i, vp, i, i64]
+        L.k3gc_init.restype = i
+        L.k3gc_free.argtypes = [vp]
+        L.k3gc_free.restype = None
+        L.k3gc_src.argtypes = [vp]
+        L.k3gc_src.restype = vp
+        L.k3gc_pin.argtypes = [vp, i, i, i]
+        L.k3gc_pin.restype = i
+        L.k3gc_prefetch.argtypes = [vp, i, i]
+        L.k3gc_prefetch.restype = i
+        L.k3gc_reset_stats.argtypes = [vp]
+        L.k3gc_reset_stats.restype = None
+        L.k3gc_report.argtypes = [vp, C.c_char_p]
+        L.k3gc_report.restype = None
+        L.k3gc_dump_hist.argtypes = [vp, C.c_char_p]
+        L.k3gc_dump_hist.restype = i
+        L.k3gc_dump_trace.argtypes = [vp, C.c_char_p]
+        L.k3gc_dump_trace.restype = i
+        L.k3gc_stats.argtypes = [vp, C.POINTER(K3gcStats)]
+        L.k3gc_stats.restype = None
+        L.k3gc_step_begin.argtypes = [vp]
+        L.k3gc_step_begin.restype = None
+        L.k3gc_step_end.argtypes = [vp, vp]
+        L.k3gc_step_end.restype = None
+        L.k3gc_wait.argtypes = [vp, vp]
+        L.k3gc_wait.restype = None
+        L.k3gc_moe.argtypes = [vp, vp, C.POINTER(K3gLayer), i, vp, i, vp, vp, vp, vp, vp, vp]
+        L.k3gc_moe.restype = i
         _lib = L
     return _lib
 
@@ -581,3 +634,120 @@ class Ctx:
         if self.ptr:
             lib().k3g_ctx_destroy(self.ptr)
             self.ptr = C.c_void_p()
+
+
+# ------------------------------------------------------------------ HBM expert cache ----
+
+class Bank:
+    """A pinned host bank of expert runs (k3gc_bank_create), or a geometry-only bank for
+    bookkeeping replays (k3gc_bank_geometry)."""
+
+    def __init__(self, n_layers: int, n_experts: int, hidden: int = 0, inter: int = 0,
+                 layout: int = K3G_EXPERT_MXFP4_TILED, expert_bytes: int = 0):
+        self.ptr = C.c_void_p()
+        if expert_bytes:
+            rc = lib().k3gc_bank_geometry(C.byref(self.ptr), n_layers, n_experts, expert_bytes)
+        else:
+            rc = lib().k3gc_bank_create(C.byref(self.ptr), n_layers, n_experts, hidden, inter,
+                                        layout)
+        if rc != 0:
+            raise RuntimeError("k3gc bank creation failed")
+        self.n_layers, self.n_experts, self.layout = n_layers, n_experts, layout
+        self.expert_bytes = lib().k3gc_bank_expert_bytes(self.ptr)
+
+    def expert(self, layer: int, e: int) -> int:
+        return lib().k3gc_bank_expert(self.ptr, layer, e)
+
+    def fill_from_layer(self, layer_obj: "SynthLayer", layer: int) -> None:
+        """copy every expert run of a device-resident SynthLayer into this bank row"""
+        if self.layout == K3G_EXPERT_MXFP4_TILED:
+            base, step = layer_obj.tbank.ptr, layer_obj.tiled_sizes()[2]
+        else:
+            base, step = layer_obj.bank.ptr, layer_obj.geo.nbytes
+        assert step == self.expert_bytes
+        for e in range(self.n_experts):
+            _check(hip().hipMemcpy(C.c_void_p(self.expert(layer, e)), C.c_void_p(base + e * step),
+                                   step, D2H), "bank fill")
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().k3gc_bank_free(self.ptr)
+            self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Cache:
+    """The HBM expert cache (k3gc_init): slots in device memory (device >= 0) or the
+    bookkeeping alone (device < 0)."""
+
+    def __init__(self, bank: Bank, topk: int, budget_bytes: int, device: int = 0):
+        self.bank = bank
+        self.ptr = C.c_void_p()
+        if lib().k3gc_init(C.byref(self.ptr), device, bank.ptr, topk, int(budget_bytes)) != 0:
+            raise RuntimeError("k3gc_init failed")
+        self.src_ptr = lib().k3gc_src(self.ptr)
+        src = K3ExpertSrc.from_address(self.src_ptr)
+        self._get = SRC_GET(src.get)
+        self._getmany = SRC_GETMANY(src.getmany)
+        self._resident = SRC_RESIDENT(src.resident)
+
+    def get(self, layer: int, e: int):
+        q = K3ExpertQ()
+        rc = self._get(self.src_ptr, layer, e, C.addressof(q))
+        return q if rc == 0 else None
+
+    def getmany(self, layer: int, experts) -> int:
+        a = np.ascontiguousarray(experts, np.int32)
+        return self._getmany(self.src_ptr, layer, a.ctypes.data, a.size)
+
+    def resident(self, layer: int, e: int) -> bool:
+        return bool(self._resident(self.src_ptr, layer, e, None))
+
+    def pin(self, layer, e, on=True) -> int:
+        return lib().k3gc_pin(self.ptr, layer, e, 1 if on else 0)
+
+    def prefetch(self, layer, e) -> int:
+        return lib().k3gc_prefetch(self.ptr, layer, e)
+
+    def stats(self) -> K3gcStats:
+        st = K3gcStats()
+        lib().k3gc_stats(self.ptr, C.byref(st))
+        return st
+
+    def reset_stats(self) -> None:
+        lib().k3gc_reset_stats(self.ptr)
+
+    def report(self, label: str = "") -> None:
+        lib().k3gc_report(self.ptr, label.encode())
+
+    def step_begin(self) -> None:
+        lib().k3gc_step_begin(self.ptr)
+
+    def step_end(self, stream=None) -> None:
+        lib().k3gc_step_end(self.ptr, stream)
+
+    def moe(self, ctx: "Ctx", L: K3gLayer, layer: int, x_ptr: int, T: int, out_ptr: int,
+            idx_ptr: int, wt_ptr: int, route_idx=None, route_wt=None) -> None:
+        ri = None if route_idx is None else np.ascontiguousarray(route_idx, np.int32)
+        rw = None if route_wt is None else np.ascontiguousarray(route_wt, np.float32)
+        rc = lib().k3gc_moe(ctx.ptr, self.ptr, C.byref(L), layer, x_ptr, T, out_ptr, idx_ptr,
+                            wt_ptr, None if ri is None else ri.ctypes.data,
+                            None if rw is None else rw.ctypes.data, None)
+        if rc != 0:
+            raise RuntimeError("k3gc_moe failed")
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().k3gc_free(self.ptr)
+            self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
