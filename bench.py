@@ -155,6 +155,105 @@ def batch_decode(a):
                         "skew (alpha 0.025), 2 layers round-robin; grouped bf16 MFMA GEMMs"}
 
 
+def expert_trace(n_steps, n_layers, T, seed, reuse=0.7, zipf_s=1.0, per_step=40):
+    """Routing of a streamed decode, per (step, layer): the step's `per_step` distinct
+    experts, of which `reuse` are carried over from the previous step's and the rest drawn
+    by Zipf(s) popularity over a seeded per-layer permutation of the experts, dealt to the
+    tokens so every one of them is used (token t takes the K consecutive entries from 8 t,
+    wrapping, of a shuffled list: distinct within a token). Returns idx
+    [steps][layers][T][K] int32 and the routed weights (uniform routed_scale / K)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    pop = []
+    for _ in range(n_layers):
+        perm = rng.permutation(E)
+        p = np.empty(E)
+        p[perm] = np.arange(1, E + 1, dtype=np.float64) ** (-zipf_s)
+        pop.append(p / p.sum())
+    idx = np.empty((n_steps, n_layers, T, K), np.int32)
+    prev = [None] * n_layers
+    for s in range(n_steps):
+        for l in range(n_layers):
+            keep = [] if prev[l] is None else list(rng.choice(prev[l], int(round(reuse * per_step)),
+                                                            replace=False))
+            p = pop[l].copy()
+            p[keep] = 0.0
+            p /= p.sum()
+            fresh = rng.choice(E, per_step - len(keep), replace=False, p=p)
+            cur = np.array(keep + list(fresh), np.int64)
+            prev[l] = cur
+            deal = rng.permutation(cur)
+            for t in range(T):
+                idx[s, l, t] = deal[(K * t + np.arange(K)) % deal.size]
+    wt = np.full(idx.shape, 2.5 / K, np.float32)
+    return idx, wt
+
+
+def streamed_decode(a):
+    """16 stacked K2 layers whose ~144 GB of routed MXFP4 experts live in a pinned host
+    bank, with the HBM expert cache capped at 48 GB: batch-8 decode steps through all
+    layers, per-layer Zipf(1.0) routing with 70% of each step's experts reused from the
+    previous step (trace-driven). Misses are copied on the cache's stream; the shared
+    expert runs while they copy."""
+    import numpy as np
+    import k3moe
+    NL, T = a.cache_layers, a.cache_tokens
+    log(f"bench: streamed decode, {NL} layers in a pinned host bank, {a.cache_gb} GB HBM cache")
+    bank = k3moe.Bank(NL, E, D, I, k3moe.K3G_EXPERT_MXFP4_TILED)
+    layers = []
+    for l in range(NL):
+        lay = k3moe.SynthLayer(k3moe.K2, seed=a.seed, layer=l, layout="tiled")
+        bank.fill_from_layer(lay, l)
+        lay.release_experts()
+        layers.append(lay)
+    cache = k3moe.Cache(bank, topk=K, budget_bytes=int(a.cache_gb * 1e9))
+    n_steps = a.cache_warmup + a.cache_steps
+    idx, wt = expert_trace(n_steps, NL, T, a.seed + 11)
+    ctx = k3moe.Ctx(layers[0].dev_tiled, max_tokens=T)
+    x = layers[0].tokens(T, stream_base=2900)
+    dx = k3moe.DevBuf.from_array(x)
+    dout, didx, dwt = k3moe.DevBuf(T * D * 4), k3moe.DevBuf(T * K * 4), k3moe.DevBuf(T * K * 4)
+
+    def step(s):
+        for l in range(NL):
+            cache.moe(ctx, layers[l].dev_tiled, l, dx.ptr, T, dout.ptr, didx.ptr, dwt.ptr,
+                      idx[s, l], wt[s, l])
+
+    for s in range(a.cache_warmup):
+        step(s)
+    ctx.sync()
+    cache.reset_stats()
+    t0 = time.perf_counter()
+    for s in range(a.cache_warmup, n_steps):
+        step(s)
+    ctx.sync()
+    t1 = time.perf_counter()
+    st = cache.stats()
+    out = dout.download(np.float32, T * D)
+    assert np.isfinite(out).all()
+    ms = (t1 - t0) * 1e3 / a.cache_steps
+    served = max(st.hits - st.prefetch_reads, 0)
+    res = {"layers": NL, "tokens_per_step": T, "steps": a.cache_steps, "warmup": a.cache_warmup,
+           "ms_per_step": round(ms, 3), "ms_per_token_latency": round(ms, 3),
+           "tokens_per_s": round(T / (ms * 1e-3), 2),
+           "hbm_cache_GB": a.cache_gb, "slots": st.nslot, "host_bank_GB": round(NL * E * bank.expert_bytes / 1e9, 1),
+           "bank_layers_pinned": bank.pinned_layers,
+           "requests": st.requests, "true_hit_rate": round(served / max(st.requests, 1), 4),
+           "misses_copied": st.prefetch_reads + st.misses,
+           "pcie_GB": round(st.bytes_read / 1e9, 2),
+           "pcie_GBps_while_copying": round(st.bytes_read / 1e9 / max(st.load_seconds, 1e-9), 1),
+           "pcie_GBps_over_run": round(st.bytes_read / 1e9 / (t1 - t0), 1),
+           "copy_stream_busy_frac": round(st.load_seconds / (t1 - t0), 3),
+           "workload": "16 stacked K2 layers, experts in a pinned host bank, HBM cache 48 GB, "
+                       "batch 8, per-layer Zipf(1.0) routing with 70% step-to-step reuse "
+                       "(trace-driven), LRU"}
+    ctx.destroy()
+    cache.free()
+    bank.free()
+    del layers
+    return res
+
+
 def prefill(a):
     """4096-token prefill through the same K2 layer with Zipf(0.8) expert popularity
     (selection-bias skew), experts in the tiled layout in HBM, x resident: router +
@@ -245,6 +344,12 @@ def main():
                     help="tokens of the prefill measurement (0: skip it)")
     ap.add_argument("--prefill-steps", type=int, default=5)
     ap.add_argument("--prefill-warmup", type=int, default=2)
+    ap.add_argument("--cache-layers", type=int, default=16,
+                    help="layers of the streamed-decode measurement (0: skip it)")
+    ap.add_argument("--cache-gb", type=float, default=48.0)
+    ap.add_argument("--cache-tokens", type=int, default=8)
+    ap.add_argument("--cache-steps", type=int, default=12)
+    ap.add_argument("--cache-warmup", type=int, default=6)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device-to-device copy (a counter calibration "
                          "point for rocprofv3 --pmc runs), outside the timed region")
@@ -356,6 +461,8 @@ def main():
         res["batch_decode"] = batch_decode(a)
     if a.prefill_tokens > 0:
         res["prefill"] = prefill(a)
+    if a.cache_layers > 0:
+        res["streamed_decode"] = streamed_decode(a)
     if not a.no_cpu:
         log("bench: CPU baseline")
         res["cpu_baseline"] = cpu_baseline(a.cpu_seconds, a.cpu_tokens, a.seed)

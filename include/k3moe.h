@@ -291,7 +291,8 @@ int  k3g_sync(K3gCtx *ctx, void *stream);
 typedef struct K3gcBank K3gcBank;
 typedef struct K3gCache K3gCache;
 
-/* A pinned host bank for n_layers x n_experts expert runs of `layout`: K3G_EXPERT_MXFP4
+/* A host bank for n_layers x n_experts expert runs of `layout`, pinned per layer as far
+ * as the driver allows: K3G_EXPERT_MXFP4
  * (the checkpoint run, src/io/k3_load.h:3-9) or K3G_EXPERT_MXFP4_TILED (w1, w3, w2 each
  * in the tiled MXFP4 layout, back to back). No reference counterpart: the engine reads
  * experts from the checkpoint files. */
@@ -305,6 +306,9 @@ void k3gc_bank_free(K3gcBank *bank);
 /* host pointer to the run of (layer, expert), expert_bytes long, for the caller to fill */
 void *k3gc_bank_expert(K3gcBank *bank, int layer, int expert);
 int64_t k3gc_bank_expert_bytes(const K3gcBank *bank);
+/* layers whose runs sit in pinned memory (the rest are pageable when the driver caps
+ * pinned memory below the bank's size) */
+int  k3gc_bank_pinned_layers(const K3gcBank *bank);
 
 /* Replaces k3_cache_init (src/cache/k3_cache.h:97, src/cache/k3_cache.c:263-353):
  * budget_bytes of HBM rounded down to whole slots; fails (-1) below topk + 1 slots.

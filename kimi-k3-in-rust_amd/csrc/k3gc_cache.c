@@ -55,15 +55,35 @@ int k3gc_bank_create(K3gcBank **out, int n_layers, int n_experts, int hidden, in
     b->inter = inter;
     b->layout = layout;
     b->expert_bytes = eb;
-    const size_t total = (size_t)n_layers * n_experts * (size_t)eb;
-    void *p = NULL;
-    if (hipHostMalloc(&p, total, hipHostMallocDefault) != hipSuccess || !p) {
-        fprintf(stderr, "k3gc_bank_create: cannot pin %.2f GB of host memory\n", total / 1e9);
-        free(b);
-        return -1;
+    /* one allocation per layer: pinned while the driver grants it (a box may cap pinned
+     * memory well below the bank's size), pageable beyond that; both are copied with
+     * hipMemcpyAsync, the pageable ones through the runtime's own staging */
+    const size_t per_layer = (size_t)n_experts * (size_t)eb;
+    b->layer_host = (unsigned char **)calloc((size_t)n_layers, sizeof(unsigned char *));
+    b->layer_pinned = (unsigned char *)calloc((size_t)n_layers, 1);
+    if (!b->layer_host || !b->layer_pinned) { k3gc_bank_free(b); return -1; }
+    int pinned_ok = 1;
+    for (int l = 0; l < n_layers; l++) {
+        void *p = NULL;
+        if (pinned_ok && hipHostMalloc(&p, per_layer, hipHostMallocDefault) == hipSuccess && p) {
+            b->layer_pinned[l] = 1;
+            b->pinned_layers++;
+        } else {
+            if (pinned_ok) (void)hipGetLastError();   /* clear the refused allocation */
+            pinned_ok = 0;
+            p = malloc(per_layer);
+            if (!p) {
+                fprintf(stderr, "k3gc_bank_create: cannot allocate %.2f GB of host memory\n",
+                        (double)per_layer * n_layers / 1e9);
+                k3gc_bank_free(b);
+                return -1;
+            }
+        }
+        b->layer_host[l] = (unsigned char *)p;
     }
-    b->host = (unsigned char *)p;
-    b->pinned_host = 1;
+    if (b->pinned_layers < n_layers)
+        fprintf(stderr, "k3gc_bank_create: %d of %d layers pinned, the rest pageable\n",
+                b->pinned_layers, n_layers);
     *out = b;
     return 0;
 }
@@ -85,17 +105,26 @@ int k3gc_bank_geometry(K3gcBank **out, int n_layers, int n_experts, int64_t expe
 void k3gc_bank_free(K3gcBank *b)
 {
     if (!b) return;
-    if (b->host && b->pinned_host) hipHostFree(b->host);
+    if (b->layer_host)
+        for (int l = 0; l < b->n_layers; l++) {
+            if (!b->layer_host[l]) continue;
+            if (b->layer_pinned[l]) hipHostFree(b->layer_host[l]);
+            else free(b->layer_host[l]);
+        }
+    free(b->layer_host);
+    free(b->layer_pinned);
     free(b);
 }
 
 void *k3gc_bank_expert(K3gcBank *b, int layer, int expert)
 {
-    if (!b || !b->host || layer < 0 || layer >= b->n_layers || expert < 0 ||
+    if (!b || !b->layer_host || layer < 0 || layer >= b->n_layers || expert < 0 ||
         expert >= b->n_experts)
         return NULL;
-    return b->host + ((size_t)layer * b->n_experts + expert) * (size_t)b->expert_bytes;
+    return b->layer_host[layer] + (size_t)expert * (size_t)b->expert_bytes;
 }
+
+int k3gc_bank_pinned_layers(const K3gcBank *b) { return b ? b->pinned_layers : 0; }
 
 int64_t k3gc_bank_expert_bytes(const K3gcBank *b) { return b ? b->expert_bytes : 0; }
 
@@ -180,7 +209,7 @@ static void copy_in(K3gCache *c, int slot, int32_t key)
     if (s >= 0 && c->step - s <= K3GC_STEP_RING)
         K3G_CHECK(hipStreamWaitEvent(c->copy, c->step_ev[s % K3GC_STEP_RING], 0));
     K3G_CHECK(hipMemcpyAsync(c->arena + (size_t)slot * c->slot_bytes,
-                             c->bank->host + (size_t)key * (size_t)c->bank->expert_bytes,
+                             k3gc_bank_expert(c->bank, key / c->n_experts, key % c->n_experts),
                              (size_t)c->bank->expert_bytes, hipMemcpyHostToDevice, c->copy));
 }
 
@@ -296,7 +325,7 @@ int k3gc_init(K3gCache **out, int device, K3gcBank *bank, int topk, int64_t budg
 {
     *out = NULL;
     if (!bank || topk < 1) return -1;
-    if (device >= 0 && !bank->host) {
+    if (device >= 0 && !bank->layer_host) {
         fprintf(stderr, "k3gc_init: the bank holds no host memory\n");
         return -1;
     }

@@ -21,8 +21,9 @@
 struct K3gcBank {
     int n_layers, n_experts, hidden, inter, layout;
     int64_t expert_bytes;
-    unsigned char *host;          /* pinned, [n_layers][n_experts][expert_bytes] */
-    int pinned_host;              /* 1: hipHostMalloc, 0: malloc (no device) */
+    unsigned char **layer_host;   /* [n_layers]: [n_experts][expert_bytes] each */
+    unsigned char *layer_pinned;  /* [n_layers]: 1 hipHostMalloc, 0 pageable malloc */
+    int pinned_layers;
 };
 
 struct K3gCache {

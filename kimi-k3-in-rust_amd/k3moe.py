@@ -191,6 +191,8 @@ def lib() -> C.CDLL:
         L.k3gc_bank_expert.restype = vp
         L.k3gc_bank_expert_bytes.argtypes = [vp]
         L.k3gc_bank_expert_bytes.restype = i64
+        L.k3gc_bank_pinned_layers.argtypes = [vp]
+        L.k3gc_bank_pinned_layers.restype = i
         L.k3gc_init.argtypes = [C.POINTER(vp), i, vp, i, i64]
         L.k3gc_init.restype = i
         L.k3gc_free.argtypes = [vp]
@@ -541,6 +543,15 @@ class SynthLayer:
             self.dev_tiled = self.k3g_layer(tiled=True)
         self.dev = self.k3g_layer() if keep_engine else self.dev_tiled
 
+    def release_experts(self) -> None:
+        """free the device copies of the routed experts (the HBM cache serves them from a
+        host bank instead); gate, bias and the shared expert stay resident"""
+        for name in ("bank", "tbank", "d_table", "d_ttable"):
+            b = getattr(self, name, None)
+            if b is not None:
+                b.free()
+                setattr(self, name, None)
+
     def k3g_layer(self, tiled: bool = False) -> K3gLayer:
         s = self.shape
         L = K3gLayer()
@@ -654,6 +665,7 @@ class Bank:
             raise RuntimeError("k3gc bank creation failed")
         self.n_layers, self.n_experts, self.layout = n_layers, n_experts, layout
         self.expert_bytes = lib().k3gc_bank_expert_bytes(self.ptr)
+        self.pinned_layers = lib().k3gc_bank_pinned_layers(self.ptr)
 
     def expert(self, layer: int, e: int) -> int:
         return lib().k3gc_bank_expert(self.ptr, layer, e)
