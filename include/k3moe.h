@@ -252,6 +252,13 @@ int  k3g_ctx_stage_ms(K3gCtx *ctx, double *ms, int64_t *count, int n);
  * (default on); off forces the staged kernels. No reference counterpart. */
 void k3g_ctx_set_fused(K3gCtx *ctx, int on);
 
+/* Routed experts of calls beyond the fused decode kernel on the FP4 x FP8 matrix cores
+ * (v_mfma_scale_f32_16x16x128_f8f6f4): MXFP4 weights as stored, x and the activation h
+ * quantised to MXFP8 (OCP MX: E4M3, an E8M0 scale per 32 values). Off by default (the
+ * bf16 matrix cores, activations exact to 2^-17). The shared expert stays bf16. No
+ * reference counterpart. */
+void k3g_ctx_set_fp8(K3gCtx *ctx, int on);
+
 /* Instrumentation: with a device buffer of 3 * tickets + 5 uint64, the fused kernel writes
  * for each ticket its start, the end of its waits and its end as wall-clock stamps
  * (100 MHz counter), then the top-k ticket's stamps after its wait, after its selection

@@ -124,6 +124,9 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t o_hsb = carve(&at, 2 * T * (SI128 ? SI128 : 128) * 2);
     const size_t o_tiles = carve(&at, maxt * 16), o_ntiles = carve(&at, 4);
     const size_t o_xflag = carve(&at, 4);
+    const size_t d512 = (d + 511) / 512 * 512, I512 = (I + 511) / 512 * 512;
+    const size_t o_xq8b = carve(&at, T * d512 + T * d512 / 32);
+    const size_t o_hq8b = carve(&at, P * I512 + P * I512 / 32);
     /* two banks of counters, one per call in turn; each a multiple of 256 bytes */
     c->sync_bytes = (k3k_decode_sync_bytes(T4, (int)d, (int)E, (int)k, (int)I, (int)SI) + 255) &
                     ~(size_t)255;
@@ -170,6 +173,8 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->ntiles = (int32_t *)(b + o_ntiles);
     c->xflag = (int32_t *)(b + o_xflag);
     c->max_tiles = (int)maxt;
+    c->xq8b = (uint8_t *)(b + o_xq8b);
+    c->hq8b = (uint8_t *)(b + o_hq8b);
     c->fused = 1;
     if (hipMemset(c->ws, 0, at) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         hipFree(c->ws);
@@ -292,6 +297,9 @@ static int gemmable(const K3gCtx *c, const K3gLayer *L)
 }
 
 static int r128(int v) { return (v + 127) / 128 * 128; }
+static int r512(int v) { return (v + 511) / 512 * 512; }
+
+void k3g_ctx_set_fp8(K3gCtx *c, int on) { if (c) c->gemm_fp8 = on; }
 
 /* Routed and shared experts as grouped GEMMs on the bf16 matrix cores (k3g_gemm.hip):
  * dispatch -> column tiles -> x pieces -> gate/up (+act) -> down -> combine. */
@@ -307,8 +315,11 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
                        st);
     rc |= k3k_gemm_tiles(c->off, E, c->tiles, c->ntiles, c->xflag, st);
     k3g_stage_end(c, K3G_ST_DISPATCH, st);
+    const int d512 = r512(d), I512 = r512(c->inter);
     k3g_stage_begin(c, K3G_ST_PIECES, st);
     rc |= k3k_xpieces(x, T, d, d128, c->xb, (long long)T * d128, c->xflag, st);
+    if (c->gemm_fp8)
+        rc |= k3k_xq8(x, T, d, d512, c->xq8b, c->xq8b + (size_t)T * d512, st);
     k3g_stage_end(c, K3G_ST_PIECES, st);
 
     K3kGemm g;
@@ -381,8 +392,16 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) rc = -1;
         c->routed_wait = NULL;
     }
+    if (c->gemm_fp8) {
+        g.bq = c->xq8b;
+        g.bs = c->xq8b + (size_t)T * d512;
+        g.ldb = d512;
+        g.hq = c->hq8b;
+        g.hs = c->hq8b + (size_t)P * I512;
+        g.ldhq = I512;
+    }
     k3g_stage_begin(c, K3G_ST_GATEUP, st);
-    rc |= k3k_gemm(&g, st);
+    rc |= c->gemm_fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
     k3g_stage_end(c, K3G_ST_GATEUP, st);
 
     g.mode = 1;
@@ -397,8 +416,15 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     g.ldo = d;
     g.scatter = 1;
     g.nft = (d + 511) / 512;
+    if (c->gemm_fp8) {
+        g.bq = c->hq8b;
+        g.bs = c->hq8b + (size_t)P * I512;
+        g.ldb = I512;
+        g.hq = NULL;
+        g.hs = NULL;
+    }
     k3g_stage_begin(c, K3G_ST_DOWN, st);
-    rc |= k3k_gemm(&g, st);
+    rc |= c->gemm_fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
     k3g_stage_end(c, K3G_ST_DOWN, st);
 
     k3g_stage_begin(c, K3G_ST_COMBINE, st);

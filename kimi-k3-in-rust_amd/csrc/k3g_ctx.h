@@ -60,6 +60,8 @@ struct K3gCtx {
     int32_t *tiles, *ntiles, *xflag;
     int max_tiles;
     hipEvent_t routed_wait;      /* the next k3g_experts waits for it before routed work */
+    int gemm_fp8;                /* routed experts on the FP4 x FP8 matrix cores */
+    uint8_t *xq8b, *hq8b;        /* MXFP8 x [T][d512] + scales, h [T*k][I512] + scales */
     unsigned long long *trace;   /* optional per-ticket timestamps of the fused kernel */
     /* optional per-stage timing: a ring of event pairs around each stage of a call,
      * harvested only when the ring wraps or the totals are read */

@@ -232,15 +232,12 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
             aload(min(c + 2, t.nK - 1), nxt, nsc);
             __builtin_amdgcn_sched_barrier(0);
             if (c < t.nK) {
+                /* rows outside the matrix read row block 0 and are never stored */
                 const int j = c & 3;
                 float sc[4];
-                uint4 wv[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    sc[r] = gm_scale((scl[r] >> (8 * j)) & 0xffu);
-                    /* rows outside the matrix multiply as zeros (their loads read block 0) */
-                    wv[r] = t.rv[r] ? cur[r] : z4;
-                }
+                for (int r = 0; r < 4; ++r) sc[r] = gm_scale((scl[r] >> (8 * j)) & 0xffu);
+                const uint4 (&wv)[4] = cur;
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     k3v8bf a[4];
@@ -330,24 +327,20 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
     }
 }
 
+/* The workgroup's tile and this wave's weight rows. Workgroup b runs on XCD b % 8 and is
+ * dispatched there in the order of b / 8. The tiles (largest first) are dealt to the XCDs
+ * in a snake: round r gives tile 8 r + x (r even) or 8 r + 7 - x (r odd) to XCD x, so
+ * every XCD gets the same mix, largest first; the feature tiles of one column tile run
+ * back to back on one XCD, sharing its activations in that XCD's L2. Returns false when
+ * the workgroup has no tile. */
 template <int AF>
-__global__ void __launch_bounds__(GM_WAVES * 64, 1)
-k_gemm(const K3kGemm g)
+__device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *lds, int &nb)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * GM_STAGE];
-
-    /* ---- which tile ---------------------------------------------------------------- */
-    /* Workgroup b runs on XCD b % 8 and is dispatched there in the order of b / 8. The
-     * tiles (largest first) are dealt to the XCDs in a snake: round r gives tile 8 r + x
-     * (r even) or 8 r + 7 - x (r odd) to XCD x, so every XCD gets the same mix, largest
-     * first; the feature tiles of one column tile run back to back on one XCD, sharing
-     * its activations in that XCD's L2. */
     const int ntl = g.tiles ? *g.ntiles : (g.dense_rows + GM_COLS - 1) / GM_COLS;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int rnd = slot / g.nft, f = slot - rnd * g.nft;
     const int tile = 8 * rnd + ((rnd & 1) ? 7 - xcd : xcd);
-    if (tile >= ntl) return;
-    GmTile t;
+    if (tile >= ntl) return false;
     int e = 0;
     if (g.tiles) {
         const int4 tv = ((const int4 *)g.tiles)[tile];
@@ -356,52 +349,67 @@ k_gemm(const K3kGemm g)
         t.p0 = tile * GM_COLS;
         t.np = min(GM_COLS, g.dense_rows - t.p0);
     }
-    const int nb = (t.np + 15) >> 4;                     /* 16-column blocks in use */
-    const int npr = (g.npieces > 1 && (!g.lo_flag || *g.lo_flag)) ? 2 : 1;
+    nb = (t.np + 15) >> 4;                               /* 16-column blocks in use */
     t.lane = threadIdx.x & 63;
     t.w = gm_uniform(threadIdx.x >> 6);
     t.g4 = t.lane >> 4;
     t.nK = (g.K + GM_KC - 1) / GM_KC;
     t.ldsp = lds;
     t.lds = (uint32_t)(uintptr_t)(k3lds)lds;
-
-    /* ---- this wave's weight rows --------------------------------------------------- */
-    {
-        const uint8_t *m0, *m1;
-        if (AF == 0) {
-            const K3ExpertQ *q = g.eq + e;
-            m0 = g.mode == 0 ? q->p1 : q->p2;
-            m1 = g.mode == 0 ? q->p3 : q->p2;
-        } else {
-            m0 = (const uint8_t *)g.wa;
-            m1 = (const uint8_t *)(g.mode == 0 ? g.wb : g.wa);
+    const uint8_t *m0, *m1;
+    if (AF == 0) {
+        const K3ExpertQ *q = g.eq + e;
+        m0 = g.mode == 0 ? q->p1 : q->p2;
+        m1 = g.mode == 0 ? q->p3 : q->p2;
+    } else {
+        m0 = (const uint8_t *)g.wa;
+        m1 = (const uint8_t *)(g.mode == 0 ? g.wb : g.wa);
+    }
+    /* bytes per 16-row block */
+    const size_t rbb = AF == 0 ? (size_t)((g.K + 511) / 512) * GM_QT : (size_t)(g.K / 32) * 1024;
+    if (g.mode == 0) {
+        t.orow0 = 256 * f + 32 * t.w;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = t.orow0 + 16 * (r & 1);
+            t.rv[r] = t.orow0 < g.rows;
+            t.abase[r] = (r < 2 ? m0 : m1) + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
         }
-        /* bytes per 16-row block */
-        const size_t rbb = AF == 0 ? (size_t)((g.K + 511) / 512) * GM_QT : (size_t)(g.K / 32) * 1024;
-        if (g.mode == 0) {
-            t.orow0 = 256 * f + 32 * t.w;
+    } else {
+        t.orow0 = 512 * f + 64 * t.w;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = t.orow0 + 16 * (r & 1);
-                t.rv[r] = t.orow0 < g.rows;
-                t.abase[r] = (r < 2 ? m0 : m1) + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
-            }
-        } else {
-            t.orow0 = 512 * f + 64 * t.w;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = t.orow0 + 16 * r;
-                t.rv[r] = row < g.rows;
-                t.abase[r] = m0 + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
-            }
+        for (int r = 0; r < 4; ++r) {
+            const int row = t.orow0 + 16 * r;
+            t.rv[r] = row < g.rows;
+            t.abase[r] = m0 + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
         }
     }
+    return true;
+}
+
+/* the activation row a tile column reads: the token (gate/up of routed pairs) or the
+ * column itself */
+__device__ __forceinline__ int gm_src_row(const K3kGemm &g, const GmTile &t, int r)
+{
+    const int p = t.p0 + (r < t.np ? r : 0);
+    return (g.mode == 0 && g.perm) ? g.perm[p] / g.topk : p;
+}
+
+template <int AF>
+__global__ void __launch_bounds__(GM_WAVES * 64, 1)
+k_gemm(const K3kGemm g)
+{
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * GM_STAGE];
+    GmTile t;
+    int nb;
+    if (!gm_setup<AF>(g, t, lds, nb)) return;
+    const int npr = (g.npieces > 1 && (!g.lo_flag || *g.lo_flag)) ? 2 : 1;
 
     /* ---- the activation rows this lane's DMA reads --------------------------------- */
     /* instruction i of wave w fills LDS rows 4 (8 i + w) .. + 3; lane l writes row
      * 4 (8 i + w) + l / 16, physical 16-byte slot l % 16, which holds logical slot
-     * (l % 16) ^ (row % 16). row % 16 = (4 w + l / 16) % 16 for every i. */
-    /* The B operand of sub-step s in lane group g is read from logical slot 4 s + g (the
+     * (l % 16) ^ (row % 16). row % 16 = (4 w + l / 16) % 16 for every i.
+     * The B operand of sub-step s in lane group g is read from logical slot 4 s + g (the
      * conflict-free order); for MXFP4 weights that slot holds the 8 columns at
      * 32 g + 8 s of the step (the A operand's column order), i.e. logical slot q holds
      * columns 8 (4 (q % 4) + q / 4). */
@@ -410,9 +418,7 @@ k_gemm(const K3kGemm g)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int r = 4 * (8 * i + t.w) + (t.lane >> 4);
-        const int p = t.p0 + (r < t.np ? r : 0);
-        const int src = (g.mode == 0 && g.perm) ? g.perm[p] / g.topk : p;
-        t.boff[i] = (uint32_t)src * (uint32_t)g.ldb + (uint32_t)qoff;
+        t.boff[i] = (uint32_t)gm_src_row(g, t, r) * (uint32_t)g.ldb + (uint32_t)qoff;
     }
     t.ndma = min(4, (4 * nb + 7 - t.w) / 8);
 
@@ -425,6 +431,233 @@ k_gemm(const K3kGemm g)
         default: break;
     }
 #undef GM_CASE
+}
+
+/* ============================================================ FP4 x FP8 variant ==== */
+/* v_mfma_scale_f32_16x16x128_f8f6f4 with cbsz 4 (A: FP4) and blgp 0 (B: FP8 E4M3), each
+ * 32-column block carrying its E8M0 scale. One instruction covers a whole 128-column
+ * step: the tiled MXFP4 chunk is its A operand unchanged (lane L: row L % 16, block
+ * L / 16), and lane 16 q + c of B holds column c's bytes 16 q .. + 15 and 64 + 16 q .. + 15
+ * of the step, with lane 16 g + c giving column c's scale of block g.
+ * LDS per stage: 128 columns x 128 bytes, the 16-byte units stored so each lane's two
+ * units are one logical pair (logical slot 2 q: unit q, 2 q + 1: unit 4 + q), physical
+ * slot = logical ^ ((row / 2) % 8) (conflict-free: 16 lanes of one unit index cover 16
+ * distinct bank groups); then 128 x 4 scale bytes. */
+#define GM_F8_DATA (GM_COLS * GM_KC)
+#define GM_F8_STAGE (GM_F8_DATA + GM_COLS * 4)
+
+__device__ __forceinline__ void gm_dma4(const void *src, uint32_t lds)
+{
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %2\n\t"
+                 "global_load_lds_dword %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(src), "s"(lds) : "memory");
+}
+
+typedef int gm_v8i __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ k3v4f gm_mma_f8(uint4 a, uint32_t sa, const gm_v8i &b, uint32_t sb,
+                                           k3v4f acc)
+{
+    const gm_v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, acc, 4, 0, 0, (int)sa, 0,
+                                                            (int)sb);
+}
+
+/* E8M0 exponent (2^sx) and E4M3 bytes of four values x 2^-sx, nearest-even, clamped to
+ * +-448 first (the OCP MX conversion) */
+__device__ __forceinline__ int gm_mx_exp(float amax)
+{
+    if (!(amax > 0.0f)) return -127;
+    int e;
+    frexpf(amax, &e);
+    const int sx = e - 1 - 8;
+    return sx < -127 ? -127 : (sx > 127 ? 127 : sx);
+}
+
+__device__ __forceinline__ uint32_t gm_e4m3x4(float a, float b, float c, float d, int sx)
+{
+    const float k = ldexpf(1.0f, -sx);
+    a = fminf(fmaxf(a * k, -448.0f), 448.0f);
+    b = fminf(fmaxf(b * k, -448.0f), 448.0f);
+    c = fminf(fmaxf(c * k, -448.0f), 448.0f);
+    d = fminf(fmaxf(d * k, -448.0f), 448.0f);
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+}
+
+/* h = act(gate, up) for the wave's 32 features of one column, quantised as one MX block:
+ * this lane's 4 + 4 values (features 4 g + i and 16 + 4 g + i) */
+__device__ __noinline__ void gm_act_store_f8(k3v4f g0, k3v4f g1, k3v4f u0, k3v4f u1, float b1,
+                                             float b2, uint8_t *o, uint8_t *os, int g4)
+{
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        y[i] = k3d_act(g0[i], u0[i], b1, b2);
+        y[4 + i] = k3d_act(g1[i], u1[i], b1, b2);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(y[i]));
+    m = fmaxf(m, __shfl_xor(m, 16, K3G_WAVE));
+    m = fmaxf(m, __shfl_xor(m, 32, K3G_WAVE));
+    const int sx = gm_mx_exp(m);
+    *(uint32_t *)(o + 4 * g4) = gm_e4m3x4(y[0], y[1], y[2], y[3], sx);
+    *(uint32_t *)(o + 16 + 4 * g4) = gm_e4m3x4(y[4], y[5], y[6], y[7], sx);
+    if (g4 == 0) *os = (uint8_t)(sx + 127);
+}
+
+template <int NB>
+__device__ __forceinline__ void gm_tile_f8(const K3kGemm &g, const GmTile &t,
+                                           const uint32_t (&doff)[2], uint32_t soff, int nd,
+                                           int ns)
+{
+    k3v4f acc[4][NB];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) acc[r][cb] = k3v4f{0.f, 0.f, 0.f, 0.f};
+    const int lane = t.lane;
+    auto dma = [&](int c) {
+        const uint32_t st = t.lds + (c & 1) * GM_F8_STAGE;
+        const uint8_t *b = g.bq + (size_t)c * GM_KC;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            if (i < nd) gm_dma16(b + doff[i], st + (8 * i + t.w) * 1024);
+        if (t.w < ns) gm_dma4(g.bs + soff + 4 * c, st + GM_F8_DATA + t.w * 256);
+    };
+    /* B operand of column block cb: the lane's unit pair and its block scale */
+    const int q = lane >> 4, c0 = lane & 15;
+    auto bread = [&](int c, int cb, gm_v8i &bv, uint32_t &sb) {
+        const int row = 16 * cb + c0;
+        const int hsw = (row >> 1) & 7;
+        const uint8_t *base = t.ldsp + (c & 1) * GM_F8_STAGE + row * 128;
+        const uint4 lo = *(const uint4 *)(base + 16 * ((2 * q) ^ hsw));
+        const uint4 hi = *(const uint4 *)(base + 16 * ((2 * q + 1) ^ hsw));
+        bv = gm_v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                    (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        sb = t.ldsp[(c & 1) * GM_F8_STAGE + GM_F8_DATA + row * 4 + q];
+    };
+    uint4 ab[3][4];
+    uint32_t sbuf[3][4];
+    auto aload = [&](int c, uint4 (&dst)[4], uint32_t (&sdst)[4]) {
+        const size_t qo = (size_t)(c >> 2) * GM_QT;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint8_t *p = t.abase[r] + qo;
+            dst[r] = gm_ld16(p + 1024 * (c & 3) + 16 * lane);
+            sdst[r] = gm_ld4(p + 4096 + 4 * lane);
+        }
+    };
+    const uint4 z4 = make_uint4(0, 0, 0, 0);
+    /* the same pipeline as the bf16 kernel: weights two steps ahead (8 loads per step,
+     * rotating by unrolling), activations one step ahead, every step issuing the same
+     * loads */
+    auto step = [&](int c, const uint4 (&cur)[4], const uint32_t (&scl)[4], uint4 (&nxt)[4],
+                    uint32_t (&nsc)[4]) {
+        gm_wait_vm<8>();
+        __syncthreads();
+        dma(min(c + 1, t.nK - 1));
+        aload(min(c + 2, t.nK - 1), nxt, nsc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (c < t.nK) {
+            /* rows outside the matrix read row block 0 and are never stored */
+            const int j = c & 3;
+            /* B operands two column blocks at a time: reading all of them ahead would not
+             * fit beside the accumulators */
+#pragma unroll
+            for (int cb = 0; cb < NB; ++cb) {
+                gm_v8i bv;
+                uint32_t sb;
+                bread(c, cb, bv, sb);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[r][cb] = gm_mma_f8(cur[r], (scl[r] >> (8 * j)) & 0xffu, bv, sb, acc[r][cb]);
+                if (cb & 1) __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    aload(0, ab[0], sbuf[0]);
+    dma(0);
+    aload(min(1, t.nK - 1), ab[1], sbuf[1]);
+    for (int c = 0; c < t.nK; c += 3) {
+        step(c, ab[0], sbuf[0], ab[2], sbuf[2]);
+        step(c + 1, ab[1], sbuf[1], ab[0], sbuf[0]);
+        step(c + 2, ab[2], sbuf[2], ab[1], sbuf[1]);
+    }
+    gm_wait_vm<0>();
+
+    /* ---- epilogue -------------------------------------------------------------------- */
+    if (g.mode == 0) {
+        if (!t.rv[0]) return;
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) {
+            const int col = 16 * cb + c0;
+            /* all four lane groups of the column take part in the block maximum */
+            const size_t row = (size_t)(t.p0 + min(col, t.np - 1));
+            uint8_t *o = g.hq + row * g.ldhq + t.orow0;
+            uint8_t *os = g.hs + row * (g.ldhq / 32) + t.orow0 / 32;
+            if (col < t.np)
+                gm_act_store_f8(acc[0][cb], acc[1][cb], acc[2][cb], acc[3][cb], g.b1, g.b2, o,
+                                os, t.g4);
+        }
+    } else {
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) {
+            const int col = 16 * cb + c0;
+            if (col < t.np) {
+                const int p = t.p0 + col;
+                float *o = g.out + (size_t)(g.scatter ? g.perm[p] : p) * g.ldo + t.orow0 + 4 * t.g4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (t.rv[r]) *(k3v4f *)(o + 16 * r) = acc[r][cb];
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(GM_WAVES * 64, 1)
+k_gemm_f8(const K3kGemm g)
+{
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * GM_F8_STAGE];
+    GmTile tt;
+    int nbt;
+    if (!gm_setup<0>(g, tt, lds, nbt)) return;
+    /* a 128-column tile runs as two halves of up to 64 columns (4 x 4 accumulators fit
+     * beside the weight pipeline; the second half finds the weights in L2) */
+    for (int half = 0; 64 * half < tt.np; ++half) {
+        GmTile t = tt;
+        t.p0 = tt.p0 + 64 * half;
+        t.np = min(64, tt.np - 64 * half);
+        const int nb = (t.np + 15) >> 4;
+        if (half) __syncthreads();                      /* the first half's stages are free */
+        /* data DMA: instruction i of wave w fills rows 8 (8 i + w) .. + 7 (only i = 0 is
+         * needed for 64 rows); lane l writes row 8 (8 i + w) + l / 8, physical unit l % 8 =
+         * logical unit (l % 8) ^ ((row / 2) % 8); logical unit 2 q holds column unit q,
+         * 2 q + 1 holds unit 4 + q */
+        uint32_t doff[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = 8 * (8 * i + t.w) + (t.lane >> 3);
+            const int ls = (t.lane & 7) ^ ((r >> 1) & 7);
+            const int u = (ls & 1) ? 4 + (ls >> 1) : (ls >> 1);
+            doff[i] = (uint32_t)gm_src_row(g, t, r) * (uint32_t)g.ldb + 16 * u;
+        }
+        const int nd = min(2, (2 * nb + 7 - t.w) / 8);
+        /* scales: wave 0 fills rows 0 .. 63, 4 bytes each */
+        const uint32_t soff = (uint32_t)gm_src_row(g, t, t.lane) * (uint32_t)(g.ldb / 32);
+        switch (nb) {
+            case 1: gm_tile_f8<1>(g, t, doff, soff, nd, 1); break;
+            case 2: gm_tile_f8<2>(g, t, doff, soff, nd, 1); break;
+            case 3: gm_tile_f8<3>(g, t, doff, soff, nd, 1); break;
+            case 4: gm_tile_f8<4>(g, t, doff, soff, nd, 1); break;
+            default: break;
+        }
+    }
 }
 
 /* ------------------------------------------------------------------ helpers ------ */
@@ -509,6 +742,60 @@ extern "C" int k3k_xpieces(const float *x, int T, int d, int ldb, uint16_t *xb,
     const size_t n = (size_t)T * d;
     const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
     hipLaunchKernelGGL(k_xpieces, dim3(blocks), dim3(256), 0, st, x, T, d, ldb, xb, piece, flag);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+/* x -> MXFP8, one thread per 32-column block */
+__global__ void __launch_bounds__(256)
+k_xq8(const float *__restrict__ x, int T, int d, int ldq, uint8_t *__restrict__ xq,
+      uint8_t *__restrict__ xs)
+{
+    const int nbk = d / 32;
+    const long long b = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (b >= (long long)T * nbk) return;
+    const int t = (int)(b / nbk), k = (int)(b - (long long)t * nbk);
+    const float4 *p = (const float4 *)(x + (size_t)t * d + 32 * k);
+    float4 v[8];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        v[i] = p[i];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    const int sx = gm_mx_exp(m);
+    uint32_t *o = (uint32_t *)(xq + (size_t)t * ldq + 32 * k);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = gm_e4m3x4(v[i].x, v[i].y, v[i].z, v[i].w, sx);
+    xs[(size_t)t * (ldq / 32) + k] = (uint8_t)(sx + 127);
+}
+
+extern "C" int k3k_xq8(const float *x, int T, int d, int ldq, uint8_t *xq, uint8_t *xs,
+                       hipStream_t st)
+{
+    if (T < 1 || d < 32 || d % 32 || ldq < d || ldq % 32 || ((uintptr_t)x & 15)) return -1;
+    const long long n = (long long)T * (d / 32);
+    hipLaunchKernelGGL(k_xq8, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, T, d, ldq,
+                       xq, xs);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int k3k_gemm_f8(const K3kGemm *g, hipStream_t st)
+{
+    if (g->mode < 0 || g->mode > 1 || g->afmt != 0 || !g->eq || !g->bq || !g->bs) return -1;
+    if (g->K < 32 || g->K % 32 || g->rows < 16 || g->ldb < g->K || g->ldb % 512 || g->nft < 1)
+        return -1;
+    if (g->mode == 0 && (g->rows % 32 || g->nft * 256 < g->rows || !g->hq || !g->hs ||
+                         g->ldhq < g->rows || g->ldhq % 512))
+        return -1;
+    if (g->mode == 1 && (g->rows % 16 || g->nft * 512 < g->rows || !g->out || g->ldo < g->rows ||
+                         g->ldo % 4))
+        return -1;
+    if (g->tiles ? (!g->ntiles || g->max_tiles < 1) : g->dense_rows < 1) return -1;
+    if ((g->scatter || (g->mode == 0 && g->tiles)) && !g->perm) return -1;
+    const long long maxt = g->tiles ? g->max_tiles : (g->dense_rows + GM_COLS - 1) / GM_COLS;
+    const long long grid = 8 * ((maxt + 7) / 8) * g->nft;
+    if (grid > 0x7fffffff) return -1;
+    hipLaunchKernelGGL(k_gemm_f8, dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

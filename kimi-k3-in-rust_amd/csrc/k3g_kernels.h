@@ -100,9 +100,20 @@ typedef struct {
     int ldo;
     int scatter;              /* mode 1: out row = perm[column] (else the column) */
     int nft;                  /* feature tiles: ceil(rows / 256) (mode 0), / 512 (mode 1) */
+    /* MXFP8 activations (k3k_gemm_f8, MXFP4 weights only): E4M3 bytes [rows][ldb] and
+     * E8M0 block scales [rows][ldb / 32]; mode 0 writes h the same way to hq/hs */
+    const uint8_t *bq, *bs;
+    uint8_t *hq, *hs;
+    int ldhq;                 /* bytes per h row (scales: ldhq / 32) */
 } K3kGemm;
 
 int k3k_gemm(const K3kGemm *g, hipStream_t st);
+/* The same grouped GEMM on v_mfma_scale_f32_16x16x128_f8f6f4: MXFP4 weights as they are,
+ * activations in MXFP8 (bq/bs; mode 0 quantises h to hq/hs). */
+int k3k_gemm_f8(const K3kGemm *g, hipStream_t st);
+/* x -> MXFP8 (OCP MX: block scale 2^(floor(log2 amax) - 8), E4M3 nearest-even, clamped
+ * to +-448): bytes [T][ldq], scales [T][ldq / 32]; the padding columns stay zero. */
+int k3k_xq8(const float *x, int T, int d, int ldq, uint8_t *xq, uint8_t *xs, hipStream_t st);
 /* column tiles from the dispatch's per-expert ranges; clears *flag */
 int k3k_gemm_tiles(const int32_t *off, int E, int32_t *tiles, int32_t *ntiles,
                    int32_t *flag, hipStream_t st);

@@ -150,6 +150,8 @@ def lib() -> C.CDLL:
         L.k3g_ctx_force_exact.restype = None
         L.k3g_ctx_set_fused.argtypes = [vp, i]
         L.k3g_ctx_set_fused.restype = None
+        L.k3g_ctx_set_fp8.argtypes = [vp, i]
+        L.k3g_ctx_set_fp8.restype = None
         L.k3g_ctx_profile.argtypes = [vp, i]
         L.k3g_ctx_profile.restype = None
         L.k3g_ctx_stage_ms.argtypes = [vp, vp, vp, i]
@@ -635,6 +637,9 @@ class Ctx:
         n = np.zeros(16, np.int64)
         ns = lib().k3g_ctx_stage_ms(self.ptr, ms.ctypes.data, n.ctypes.data, 16)
         return ms[:ns], n[:ns]
+
+    def set_fp8(self, on: bool) -> None:
+        lib().k3g_ctx_set_fp8(self.ptr, 1 if on else 0)
 
     def stats(self) -> list:
         out = (C.c_int64 * 4)()

@@ -290,3 +290,42 @@ def k2_forward(layer: "k3moe.SynthLayer", x: np.ndarray, k: Kernels | None = Non
     out, idx, wt = k.moe(w, cfg, x, prefill=prefill)
     del keep
     return out, idx, wt
+
+
+def k2_forward_mxfp8(layer: "k3moe.SynthLayer", x: np.ndarray):
+    """Quantisation-aware oracle of the FP4 x FP8 variant: the engine's layer with the
+    routed experts' inputs quantised to MXFP8 (OCP MX, 32-element blocks) -- x before
+    gate/up, the activation h before down -- and everything else the engine's own
+    arithmetic (router, exact MXFP4 GEMVs in double, SwiGLU, slot-ordered combine, the
+    bf16 shared expert unquantised)."""
+    k = oracle()
+    s = layer.shape
+    d, I, E = s.hidden, s.inter, s.n_experts
+    g = layer.geo
+    cap = float(2.0 ** 100)
+    runs = {}
+    out = np.zeros((x.shape[0], d), np.float32)
+    for t in range(x.shape[0]):
+        xt = np.ascontiguousarray(x[t], np.float32)
+        idx, w = k.router(xt, layer.gate, layer.bias, E, s.topk, s.renorm, s.routed_scale)
+        xq = quant_mxfp8(xt)
+        acc = np.zeros(d, np.float32)
+        for j in range(s.topk):
+            e = int(idx[j])
+            if e not in runs:
+                runs[e] = layer.expert_host(e)
+            r = runs[e]
+            p1 = r[g.p1_off:g.s1_off]; s1 = r[g.s1_off:g.p2_off]
+            p2 = r[g.p2_off:g.s2_off]; s2 = r[g.s2_off:g.p3_off]
+            p3 = r[g.p3_off:g.s3_off]; s3 = r[g.s3_off:g.nbytes]
+            gu = np.concatenate([k.matmul_mxfp4(xq, p1, s1, I), k.matmul_mxfp4(xq, p3, s3, I)])
+            h = quant_mxfp8(k.situ(gu.astype(np.float32), cap, cap))
+            y = k.matmul_mxfp4(h, p2, s2, d)
+            acc = (acc + np.float32(w[j]) * y.astype(np.float32)).astype(np.float32)
+        if layer.SI:
+            SI = layer.SI
+            gu = np.concatenate([k.matmul_bf16(xt, layer.sh1, SI), k.matmul_bf16(xt, layer.sh3, SI)])
+            hs = k.situ(gu.astype(np.float32), cap, cap)
+            acc = (acc + k.matmul_bf16(hs, layer.sh2, d).astype(np.float32)).astype(np.float32)
+        out[t] = acc
+    return out

@@ -442,3 +442,74 @@ def test_dropin_expert_drop(gpu):
     oo, _, _ = O_.moe(w2, cfg2, x)
     assert drops == O_.drops.value - od0 and drops > 0
     assert rel_l2(out, oo) <= REL_L2
+
+
+# ------------------------------------------------------- FP4 x FP8 matrix cores ----
+
+def _e4m3_decode(b):
+    b = b.astype(np.int64)
+    s = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0xF
+    m = b & 7
+    v = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7))
+    return s * v
+
+
+def test_mxfp8_quantiser_matches_the_oracle(gpu):
+    say("case: k3k_xq8 (hardware E4M3 conversion) vs the oracle's OCP MX quantiser, "
+        "incl. zero blocks, 448 clamps, E4M3 subnormals and ties")
+    T, d = 6, 256
+    x = k3moe.host_normal(T * d, 31, 5, 0.0, 1.0).reshape(T, d)
+    x[0, :32] = 0.0                                         # zero block
+    x[1, :32] = 1.0 / 256
+    x[1, 0] = 1.99                                          # 1.99 * 2^8 > 448: clamped
+    x[2, :32] = np.float32(1.0)
+    x[2, 1:8] = np.float32(1e-5)                            # E4M3 subnormals of the block
+    x[3, :32] = np.float32(1.0625) * 2.0 ** -3              # ties between 1.0 and 1.125
+    x[3, 0] = 1.0
+    x = np.ascontiguousarray(x, np.float32)
+    L = k3moe.lib()
+    L.k3k_xq8.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_void_p]
+    dx, dq, ds = k3moe.DevBuf.from_array(x), k3moe.DevBuf(T * d), k3moe.DevBuf(T * d // 32)
+    assert L.k3k_xq8(dx.ptr, T, d, d, dq.ptr, ds.ptr, None) == 0
+    k3moe.sync()
+    q = dq.download(np.uint8, T * d).reshape(T, d // 32, 32)
+    sc = ds.download(np.uint8, T * d // 32).reshape(T, d // 32, 1).astype(np.int64)
+    got = (_e4m3_decode(q) * 2.0 ** (sc - 127)).astype(np.float32).reshape(T, d)
+    exp = O.quant_mxfp8(x.ravel()).reshape(T, d)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+    assert got[1, 0] == np.float32(448.0 * 2.0 ** -8)
+
+
+@pytest.mark.parametrize("T", [16])
+def test_layer_k2_fp4xfp8_variant(k2_layer, T):
+    say(f"case: k3g_moe K2 layer, {T} tokens, routed experts on the FP4 x FP8 matrix cores "
+        "(MXFP8 activations) vs the quantisation-aware oracle")
+    layer = k2_layer
+    x = layer.tokens(T, stream_base=170)
+    ctx = k3moe.Ctx(layer.dev_tiled, max_tokens=T)
+    ctx.set_fp8(True)
+    out, idx, _ = run_layer(layer, x, ctx=ctx, tiled=True)
+    ctx.destroy()
+    q = O.k2_forward_mxfp8(layer, x)
+    ro, ri, _ = oracle_tokens(layer, x)
+    assert np.array_equal(idx, ri)
+    r_q, r_u = rel_l2(out, q), rel_l2(out, ro)
+    say(f"  rel-L2 vs quantisation-aware oracle {r_q:.3e}, vs the unquantised engine {r_u:.3e}")
+    assert r_q <= 5e-3
+    assert r_u <= 0.1
+
+
+def test_layer_tiny_fp4xfp8_variant(gpu):
+    T = 37
+    say(f"case: k3g_moe tiny layer, {T} tokens, FP4 x FP8 variant vs the quantisation-aware oracle")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=4321, layout="tiled")
+    x = layer.tokens(T)
+    ctx = k3moe.Ctx(layer.dev_tiled, max_tokens=T)
+    ctx.set_fp8(True)
+    out, idx, _ = run_layer(layer, x, ctx=ctx, tiled=True)
+    ctx.destroy()
+    q = O.k2_forward_mxfp8(layer, x)
+    r = rel_l2(out, q)
+    say(f"  rel-L2 {r:.3e}")
+    assert r <= 5e-3
