@@ -313,3 +313,49 @@ def test_lru_small_cases():
     # capacity 3: hits at the 2nd 0 and 1, then 0 again, 1 evicted by 4? 3 evicts 2
     assert O.lru_hits(keys, 5, 3) == 3
     assert O.lru_hits(keys, 5, 5) == keys.size - 5
+
+
+# ------------------------------------------------------------------------ MXFP8 ----
+
+def _e4m3_table():
+    """every finite E4M3 value (OCP FP8: bias 7, 3 mantissa bits, subnormals at 2^-6 * m/8,
+    S.1111.111 is NaN), by code"""
+    vals = {}
+    for code in range(256):
+        e, m = (code >> 3) & 15, code & 7
+        if e == 15 and m == 7:
+            continue
+        v = (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+        vals[code] = -v if code & 0x80 else v
+    return vals
+
+
+def test_mxfp8_quantiser_is_the_brute_force_nearest_e4m3():
+    """OCP MX v1.0: block scale 2^(floor(log2 amax) - 8); each element the nearest E4M3
+    value of x / scale (ties to the even code), magnitudes above 448 clamped. Checked by
+    brute force over the 253 finite E4M3 values rather than by re-deriving the rounding."""
+    tab = _e4m3_table()
+    pos = sorted({abs(v) for v in tab.values()})
+    even = {abs(v): c for c, v in tab.items() if c < 0x80}
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(64 * 32) * np.exp(rng.uniform(-12, 12, 64 * 32))).astype(np.float32)
+    x[:32] = 0.0
+    x[64:96] = np.float32(1.0625 * 2.0 ** -3)               # ties
+    x[64] = 1.0
+    q = O.quant_mxfp8(x)
+    for b in range(0, x.size, 32):
+        blk, qb = x[b:b + 32].astype(np.float64), q[b:b + 32].astype(np.float64)
+        amax = np.max(np.abs(blk))
+        if amax == 0:
+            assert np.all(qb == 0)
+            continue
+        sx = int(np.floor(np.log2(amax))) - 8
+        for v, r in zip(blk, qb):
+            a = min(abs(v) * 2.0 ** -sx, 448.0)
+            d = [abs(a - p) for p in pos]
+            best = min(d)
+            cands = [p for p, dd in zip(pos, d) if dd == best]
+            want = cands[0] if len(cands) == 1 else min(cands, key=lambda p: even[p] & 1)
+            assert abs(r) * 2.0 ** -sx == want and (r == 0 or np.sign(r) == np.sign(v)), (b, v, r)
+    # idempotent: a quantised block is its own quantisation
+    assert np.array_equal(O.quant_mxfp8(q).view(np.uint32), q.view(np.uint32))
