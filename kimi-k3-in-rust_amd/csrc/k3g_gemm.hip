@@ -149,6 +149,22 @@ __device__ __forceinline__ void gm_wait_vm()
     __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
+/* s_waitcnt vmcnt(n) for a wave-uniform n in 8..16 */
+__device__ __forceinline__ void gm_wait_vm_n(int n)
+{
+    switch (n) {
+        case 8: gm_wait_vm<8>(); break;
+        case 9: gm_wait_vm<9>(); break;
+        case 10: gm_wait_vm<10>(); break;
+        case 11: gm_wait_vm<11>(); break;
+        case 12: gm_wait_vm<12>(); break;
+        case 13: gm_wait_vm<13>(); break;
+        case 14: gm_wait_vm<14>(); break;
+        case 15: gm_wait_vm<15>(); break;
+        default: gm_wait_vm<8>(); break;
+    }
+}
+
 /* Everything one workgroup's tile needs, uniform across the workgroup except the
  * per-lane DMA row offsets. */
 struct GmTile {
@@ -172,8 +188,11 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
         for (int cb = 0; cb < NB; ++cb) acc[r][cb] = k3v4f{0.f, 0.f, 0.f, 0.f};
     const int lane = t.lane;
 
+    /* stages: three of one piece (activations two steps ahead) or two of two pieces */
+    constexpr int SN = NP == 1 ? 3 : 2;
+    auto stage = [](int c) { return (uint32_t)((c % SN) * (NP * GM_PIECE)); };
     auto dma = [&](int c) {
-        const uint32_t st = t.lds + (c & 1) * GM_STAGE + t.w * 1024;
+        const uint32_t st = t.lds + stage(c) + t.w * 1024;
         const uint16_t *b0 = g.b + (size_t)c * GM_KC;
 #pragma unroll
         for (int pc = 0; pc < NP; ++pc) {
@@ -186,7 +205,7 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
     /* B operand: column block cb, logical 16-byte slot q of the step's row */
     const uint8_t *brow = t.ldsp + (lane & 15) * 256;
     auto bread = [&](int c, int pc, int cb, int q) -> uint4 {
-        return *(const uint4 *)(brow + (c & 1) * GM_STAGE + pc * GM_PIECE + cb * 16 * 256 +
+        return *(const uint4 *)(brow + stage(c) + pc * GM_PIECE + cb * 16 * 256 +
                                 16 * (q ^ (lane & 15)));
     };
     auto mma_step = [&](int c, int q, const k3v8bf *a) {
@@ -224,11 +243,14 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
          * loads in flight), and every step issues the same loads (clamped to the last step;
          * the padding steps past nK only skip their matrix work), so the compiler's load
          * counters agree on every path and its waits stay on the step that is due. */
+        /* loads after the ones step c needs: SN == 3: DMA(c + 1) then weights(c + 1);
+         * SN == 2: weights(c + 1) only (DMA(c) came after them) */
+        const int after = SN == 3 ? 8 + NP * t.ndma : 8;
         auto step = [&](int c, const uint4 (&cur)[4], const uint32_t (&scl)[4], uint4 (&nxt)[4],
                         uint32_t (&nsc)[4]) {
-            gm_wait_vm<8>();
+            gm_wait_vm_n(after);
             __syncthreads();
-            dma(min(c + 1, t.nK - 1));
+            dma(min(c + SN - 1, t.nK - 1));
             aload(min(c + 2, t.nK - 1), nxt, nsc);
             __builtin_amdgcn_sched_barrier(0);
             if (c < t.nK) {
@@ -254,6 +276,7 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
         aload(0, ab[0], sb[0]);
         dma(0);
         aload(min(1, t.nK - 1), ab[1], sb[1]);
+        if (SN == 3) dma(min(1, t.nK - 1));
         for (int c = 0; c < t.nK; c += 3) {
             step(c, ab[0], sb[0], ab[2], sb[2]);
             step(c + 1, ab[1], sb[1], ab[0], sb[0]);
