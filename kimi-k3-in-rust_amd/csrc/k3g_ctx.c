@@ -401,8 +401,11 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         g.ldhq = I512;
     }
     k3g_stage_begin(c, K3G_ST_GATEUP, st);
+    g.trace = c->gemm_fp8 ? NULL : c->trace;
     rc |= c->gemm_fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
     k3g_stage_end(c, K3G_ST_GATEUP, st);
+    /* the down launch's stamps follow the widest gate/up launch's (4-wave workgroups) */
+    if (g.trace) g.trace += 4 * 8 * (size_t)((g.max_tiles + 7) / 8) * (size_t)((I + 127) / 128);
 
     g.mode = 1;
     g.rows = d;

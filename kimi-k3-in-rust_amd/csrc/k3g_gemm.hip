@@ -11,10 +11,14 @@
  *
  * The shared expert is the same GEMM over all tokens with a dense column list.
  *
- * Work unit: one workgroup of 8 waves = one (column tile of up to 128 pairs, feature
- * tile) of one expert. Wave w owns 4 row groups of 16 weight rows (mode 0: 32 gate rows
- * and the 32 up rows of the same features, so the activation is lane-local; mode 1: 64
- * output rows) and all the tile's columns: 4 x 8 accumulators of 16x16.
+ * Work unit: one workgroup = one (column tile of up to 128 pairs, feature tile) of one
+ * expert. Wave w owns 4 row groups of 16 weight rows (mode 0: 32 gate rows and the 32 up
+ * rows of the same features, so the activation is lane-local; mode 1: 64 output rows)
+ * and all the tile's columns: 4 x 8 accumulators of 16x16. Gate/up with one-piece
+ * activations runs 4-wave workgroups (128 features), two per CU, so that one
+ * workgroup's matrix work covers the other's barrier and load waits; two-piece
+ * activations and the down GEMM run 8-wave workgroups (256 features / 512 rows), one per
+ * CU (their stages need 128 KB of LDS).
  *
  * Weights (A operand) go from HBM straight to registers in the tiled layouts of
  * k3g_tile.hip: one 16-byte load per lane and row group gives a 16-row x 128-column block
@@ -172,13 +176,14 @@ struct GmTile {
     int orow0;                 /* mode 0: first feature; mode 1: first output row */
     const uint8_t *abase[4];   /* row group r: its 16-row block of the weight matrix */
     bool rv[4];                /* row group inside the matrix */
-    uint32_t boff[4];          /* element offsets of this lane's DMA rows (+ swizzled slot) */
+    uint32_t boff[8];          /* element offsets of this lane's DMA rows (+ swizzled slot) */
     uint32_t lds;              /* LDS byte address of the staging buffers */
     uint8_t *ldsp;
 };
 
-/* The tile's GEMM with NB 16-column blocks and NP activation pieces, then its epilogue. */
-template <int AF, int NP, int NB>
+/* The tile's GEMM with NB 16-column blocks and NP activation pieces in a workgroup of WV
+ * waves, then its epilogue. */
+template <int AF, int NP, int NB, int WV>
 __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
 {
     k3v4f acc[4][NB];
@@ -188,8 +193,10 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
         for (int cb = 0; cb < NB; ++cb) acc[r][cb] = k3v4f{0.f, 0.f, 0.f, 0.f};
     const int lane = t.lane;
 
-    /* stages: three of one piece (activations two steps ahead) or two of two pieces */
-    constexpr int SN = NP == 1 ? 3 : 2;
+    /* stages: 8 waves: three of one piece (activations two steps ahead) or two of two
+     * pieces; 4 waves (two workgroups per CU): two of one piece */
+    constexpr int SN = (NP == 1 && WV == 8) ? 3 : 2;
+    constexpr int NI = 32 / WV;                  /* DMA instructions per wave and piece */
     auto stage = [](int c) { return (uint32_t)((c % SN) * (NP * GM_PIECE)); };
     auto dma = [&](int c) {
         const uint32_t st = t.lds + stage(c) + t.w * 1024;
@@ -198,8 +205,8 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
         for (int pc = 0; pc < NP; ++pc) {
             const uint16_t *b = b0 + (size_t)pc * g.bpiece;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (i < t.ndma) gm_dma16(b + t.boff[i], st + pc * GM_PIECE + i * 8 * 1024);
+            for (int i = 0; i < NI; ++i)
+                if (i < t.ndma) gm_dma16(b + t.boff[i], st + pc * GM_PIECE + i * WV * 1024);
         }
     };
     /* B operand: column block cb, logical 16-byte slot q of the step's row */
@@ -356,7 +363,7 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
  * every XCD gets the same mix, largest first; the feature tiles of one column tile run
  * back to back on one XCD, sharing its activations in that XCD's L2. Returns false when
  * the workgroup has no tile. */
-template <int AF>
+template <int AF, int WV>
 __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *lds, int &nb)
 {
     const int ntl = g.tiles ? *g.ntiles : (g.dense_rows + GM_COLS - 1) / GM_COLS;
@@ -391,7 +398,7 @@ __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *l
     /* bytes per 16-row block */
     const size_t rbb = AF == 0 ? (size_t)((g.K + 511) / 512) * GM_QT : (size_t)(g.K / 32) * 1024;
     if (g.mode == 0) {
-        t.orow0 = 256 * f + 32 * t.w;
+        t.orow0 = 32 * WV * f + 32 * t.w;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = t.orow0 + 16 * (r & 1);
@@ -399,7 +406,7 @@ __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *l
             t.abase[r] = (r < 2 ? m0 : m1) + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
         }
     } else {
-        t.orow0 = 512 * f + 64 * t.w;
+        t.orow0 = 64 * WV * f + 64 * t.w;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = t.orow0 + 16 * r;
@@ -418,42 +425,68 @@ __device__ __forceinline__ int gm_src_row(const K3kGemm &g, const GmTile &t, int
     return (g.mode == 0 && g.perm) ? g.perm[p] / g.topk : p;
 }
 
-template <int AF>
-__global__ void __launch_bounds__(GM_WAVES * 64, 1)
+/* WV = 8: one workgroup per CU, any piece count. WV = 4 (one-piece B only): two
+ * workgroups of 4 waves per CU, each with 64 KB of stages, so one workgroup's matrix work
+ * fills the other's barrier and load waits. */
+template <int AF, int WV>
+__global__ void __launch_bounds__(WV * 64, 8 / WV)
 k_gemm(const K3kGemm g)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * GM_STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[WV == 8 ? 2 * GM_STAGE : 2 * GM_PIECE];
+    const int npr = (g.npieces > 1 && (!g.lo_flag || *g.lo_flag)) ? 2 : 1;
+    if (WV == 4 ? npr != 1 : (g.np_only == 2 && npr != 2)) return;
     GmTile t;
     int nb;
-    if (!gm_setup<AF>(g, t, lds, nb)) return;
-    const int npr = (g.npieces > 1 && (!g.lo_flag || *g.lo_flag)) ? 2 : 1;
+    if (!gm_setup<AF, WV>(g, t, lds, nb)) return;
+    const unsigned long long t_start = g.trace ? wall_clock64() : 0;
 
     /* ---- the activation rows this lane's DMA reads --------------------------------- */
-    /* instruction i of wave w fills LDS rows 4 (8 i + w) .. + 3; lane l writes row
-     * 4 (8 i + w) + l / 16, physical 16-byte slot l % 16, which holds logical slot
-     * (l % 16) ^ (row % 16). row % 16 = (4 w + l / 16) % 16 for every i.
+    /* instruction i of wave w fills LDS rows 4 (WV i + w) .. + 3; lane l writes row
+     * 4 (WV i + w) + l / 16, physical 16-byte slot l % 16, which holds logical slot
+     * (l % 16) ^ (row % 16). row % 16 = (4 w + l / 16) % 16 for every i (WV = 4 or 8).
      * The B operand of sub-step s in lane group g is read from logical slot 4 s + g (the
      * conflict-free order); for MXFP4 weights that slot holds the 8 columns at
      * 32 g + 8 s of the step (the A operand's column order), i.e. logical slot q holds
      * columns 8 (4 (q % 4) + q / 4). */
     const int qlog = (t.lane & 15) ^ ((4 * t.w + (t.lane >> 4)) & 15);
     const int qoff = 8 * (AF == 0 ? 4 * (qlog & 3) + (qlog >> 2) : qlog);
+    constexpr int NI = 32 / WV;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 4 * (8 * i + t.w) + (t.lane >> 4);
+    for (int i = 0; i < NI; ++i) {
+        const int r = 4 * (WV * i + t.w) + (t.lane >> 4);
         t.boff[i] = (uint32_t)gm_src_row(g, t, r) * (uint32_t)g.ldb + (uint32_t)qoff;
     }
-    t.ndma = min(4, (4 * nb + 7 - t.w) / 8);
+    /* instructions whose first row is inside the tile's 16 nb rows */
+    t.ndma = min(NI, (4 * nb + WV - 1 - t.w) / WV);
 
-#define GM_CASE(P, B) case (P) * 16 + (B): gm_tile<AF, P, B>(g, t); break;
-    switch (npr * 16 + nb) {
-        GM_CASE(1, 1) GM_CASE(1, 2) GM_CASE(1, 3) GM_CASE(1, 4)
-        GM_CASE(1, 5) GM_CASE(1, 6) GM_CASE(1, 7) GM_CASE(1, 8)
-        GM_CASE(2, 1) GM_CASE(2, 2) GM_CASE(2, 3) GM_CASE(2, 4)
-        GM_CASE(2, 5) GM_CASE(2, 6) GM_CASE(2, 7) GM_CASE(2, 8)
-        default: break;
+#define GM_CASE(P, B) case (P) * 16 + (B): gm_tile<AF, P, B, WV>(g, t); break;
+    if constexpr (WV == 8) {
+        switch (npr * 16 + nb) {
+            GM_CASE(1, 1) GM_CASE(1, 2) GM_CASE(1, 3) GM_CASE(1, 4)
+            GM_CASE(1, 5) GM_CASE(1, 6) GM_CASE(1, 7) GM_CASE(1, 8)
+            GM_CASE(2, 1) GM_CASE(2, 2) GM_CASE(2, 3) GM_CASE(2, 4)
+            GM_CASE(2, 5) GM_CASE(2, 6) GM_CASE(2, 7) GM_CASE(2, 8)
+            default: break;
+        }
+    } else {
+        switch (16 + nb) {
+            GM_CASE(1, 1) GM_CASE(1, 2) GM_CASE(1, 3) GM_CASE(1, 4)
+            GM_CASE(1, 5) GM_CASE(1, 6) GM_CASE(1, 7) GM_CASE(1, 8)
+            default: break;
+        }
     }
 #undef GM_CASE
+    if (g.trace && threadIdx.x == 0) {
+        const int slot = blockIdx.x >> 3;
+        const int rnd = slot / g.nft, xcd = blockIdx.x & 7;
+        unsigned long long *o = g.trace + 4 * (size_t)blockIdx.x;
+        o[0] = t_start;
+        o[1] = wall_clock64();
+        o[2] = (unsigned long long)(8 * rnd + ((rnd & 1) ? 7 - xcd : xcd)) << 32 |
+               (unsigned)(slot - rnd * g.nft);
+        o[3] = (unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15) << 32 |
+               (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);
+    }
 }
 
 /* ============================================================ FP4 x FP8 variant ==== */
@@ -576,7 +609,6 @@ __device__ __forceinline__ void gm_tile_f8(const K3kGemm &g, const GmTile &t,
             sdst[r] = gm_ld4(p + 4096 + 4 * lane);
         }
     };
-    const uint4 z4 = make_uint4(0, 0, 0, 0);
     /* the same pipeline as the bf16 kernel: weights two steps ahead (8 loads per step,
      * rotating by unrolling), activations one step ahead, every step issuing the same
      * loads */
@@ -649,7 +681,7 @@ k_gemm_f8(const K3kGemm g)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * GM_F8_STAGE];
     GmTile tt;
     int nbt;
-    if (!gm_setup<0>(g, tt, lds, nbt)) return;
+    if (!gm_setup<0, GM_WAVES>(g, tt, lds, nbt)) return;
     /* a 128-column tile runs as two halves of up to 64 columns (4 x 4 accumulators fit
      * beside the weight pipeline; the second half finds the weights in L2) */
     for (int half = 0; 64 * half < tt.np; ++half) {
@@ -841,9 +873,22 @@ extern "C" int k3k_gemm(const K3kGemm *g, hipStream_t st)
     const long long maxt = g->tiles ? g->max_tiles : (g->dense_rows + GM_COLS - 1) / GM_COLS;
     const long long grid = 8 * ((maxt + 7) / 8) * g->nft;
     if (grid > 0x7fffffff) return -1;
-    if (g->afmt == 0)
-        hipLaunchKernelGGL(k_gemm<0>, dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
-    else
-        hipLaunchKernelGGL(k_gemm<1>, dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
+    if (g->afmt == 0 && g->mode == 0) {
+        /* gate/up of MXFP4 experts: 4-wave workgroups when x is one piece (the usual case:
+         * decided on the device from the flag), 8-wave ones for two pieces; each launch
+         * leaves at once when the other one's case holds */
+        K3kGemm g4 = *g, g8 = *g;
+        g4.nft = (g->rows + 127) / 128;
+        g8.np_only = 2;
+        const long long grid4 = 8 * ((maxt + 7) / 8) * g4.nft;
+        if (grid4 > 0x7fffffff) return -1;
+        hipLaunchKernelGGL((k_gemm<0, 4>), dim3((unsigned)grid4), dim3(4 * 64), 0, st, g4);
+        if (g->npieces > 1)
+            hipLaunchKernelGGL((k_gemm<0, 8>), dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, g8);
+    } else if (g->afmt == 0) {
+        hipLaunchKernelGGL((k_gemm<0, 8>), dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
+    } else {
+        hipLaunchKernelGGL((k_gemm<1, 8>), dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -105,6 +105,10 @@ typedef struct {
     const uint8_t *bq, *bs;
     uint8_t *hq, *hs;
     int ldhq;                 /* bytes per h row (scales: ldhq / 32) */
+    int np_only;              /* set by k3k_gemm: 2 = a launch that runs only two-piece B */
+    /* instrumentation (NULL: off): per workgroup of the launch that does the work, wave
+     * 0's start and end (wall clock), tile << 32 | feature tile, XCC << 32 | HW_ID */
+    unsigned long long *trace;
 } K3kGemm;
 
 int k3k_gemm(const K3kGemm *g, hipStream_t st);

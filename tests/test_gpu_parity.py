@@ -312,12 +312,17 @@ def test_layer_k2_fused_consecutive_tokens(k2_layer):
     ctx.destroy()
 
 
-@pytest.mark.parametrize("T", [5, 16, 37, 200])
-def test_layer_tiny_grouped_gemm(gpu, T):
-    say(f"case: k3g_moe tiny layer on the grouped bf16 MFMA GEMMs, {T} tokens (fp32 x: "
-        "two activation pieces)")
+@pytest.mark.parametrize("T,xkind", [(5, "fp32"), (16, "fp32"), (37, "fp32"), (200, "fp32"),
+                                     (37, "bf16"), (200, "bf16")])
+def test_layer_tiny_grouped_gemm(gpu, T, xkind):
+    say(f"case: k3g_moe tiny layer on the grouped bf16 MFMA GEMMs, {T} tokens, x {xkind} "
+        "(fp32: two activation pieces on 8-wave workgroups; bf16: one piece, 4-wave)")
     layer = k3moe.SynthLayer(k3moe.TINY, seed=4321, layout="both")
     x = layer.tokens(T)
+    if xkind == "bf16":
+        u = x.view(np.uint32).astype(np.uint64)
+        x = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+        assert not np.any(x.view(np.uint32) & 0xFFFF)
     out, idx, wt = run_layer(layer, x, tiled=True)
     ro, ri, rw = oracle_tokens(layer, x)
     assert np.array_equal(idx, ri)
