@@ -237,6 +237,13 @@ __device__ __forceinline__ void k3d_trace_go(unsigned long long *trace, int tkg,
     if (trace && lane == 0) trace[3 * tkg + 1] = wall_clock64();
 }
 
+/* A workgroup's reduction of one router row's slices (4 waves = 4 slices, up to 4 tokens):
+ * {sum, sum|w x|} per slice and token, and the arrival count. */
+struct K3RouterLds {
+    double part[4][4][2];
+    int count;
+};
+
 /* ----------------------------------------------------------- buffer access ---- */
 /* Weights and pieces are read through raw buffer descriptors: the base lives in scalar
  * registers and each lane adds its own byte offset. An offset at or past the
@@ -475,7 +482,8 @@ struct K3Dec {
     }
 
     /* ----------------------------------------------------------------- R ---- */
-    static __device__ __noinline__ void router(K3ArgPtr ap, int tk_, int lane)
+    static __device__ __noinline__ void router(K3ArgPtr ap, int tk_, int lane, K3RouterLds *rl,
+                                               bool wg_slices)
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const int tk = k3d_uniform(tk_);
@@ -525,26 +533,49 @@ struct K3Dec {
                 }
             }
         }
-        /* the slice's partial sums, [t][e][slice] {sum, sum|w x|} */
+        /* the slice's partial sums {sum, sum|w x|}: in LDS when the row's slices are the
+         * four waves of this workgroup, else in memory, [t][e][slice] */
         const K3Rsrc rp = k3d_rsrc(a.rpart, (size_t)a.T * a.E * G.KSR * 16);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const double sv = k3d_wave_sumd(acc[t]);
             const double bv = k3d_wave_sumd(ab[t]);
-            if (lane == 0 && t < a.T)
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(k3v4u, make_double2(sv, bv)), rp,
-                    ((t * a.E + e) * G.KSR + r) * 16, 0, K3_SC1);
+            if (lane == 0 && t < a.T) {
+                if (wg_slices) {
+                    rl->part[r][t][0] = sv;
+                    rl->part[r][t][1] = bv;
+                } else {
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(k3v4u, make_double2(sv, bv)), rp,
+                        ((t * a.E + e) * G.KSR + r) * 16, 0, K3_SC1);
+                }
+            }
         }
-        if (!k3d_arrive(k3d_line(a.sync, G.lRE + e), G.KSR - 1, lane)) return;
+        if (wg_slices) {
+            /* the workgroup's arrival count, in LDS: the wave that completes it has every
+             * slice's partial sums (each wave's LDS writes are done before its count) */
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            int old = 0;
+            if (lane == 0)
+                old = __hip_atomic_fetch_add(&rl->count, 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (k3d_uniform(old) != G.KSR - 1) return;
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        } else if (!k3d_arrive(k3d_line(a.sync, G.lRE + e), G.KSR - 1, lane)) {
+            return;
+        }
         /* the last slice of the row: the slices summed in slice order, then the score
          * interval (any summation order is inside the interval's bound) */
         if (lane < a.T) {
             double sv = 0.0, bv = 0.0;
             for (int q = 0; q < G.KSR; ++q) {
-                const double2 v = __builtin_bit_cast(
-                    double2, __builtin_amdgcn_raw_buffer_load_b128(rp, ((lane * a.E + e) * G.KSR + q) * 16,
-                                                                   0, K3_SC1));
+                double2 v;
+                if (wg_slices)
+                    v = make_double2(rl->part[q][lane][0], rl->part[q][lane][1]);
+                else
+                    v = __builtin_bit_cast(
+                        double2, __builtin_amdgcn_raw_buffer_load_b128(
+                                     rp, ((lane * a.E + e) * G.KSR + q) * 16, 0, K3_SC1));
                 sv += v.x;
                 bv += v.y;
             }
@@ -909,6 +940,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(K3G_DE
 k_decode_fused(K3kDecode a)
 {
     __shared__ K3SelectLds lds;
+    __shared__ K3RouterLds rl;
     const int lane = threadIdx.x & 63;
     const K3ArgPtr ap = (K3ArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
     const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
@@ -920,6 +952,13 @@ k_decode_fused(K3kDecode a)
         const int lo = w * per, hi = min(a.sync_words, lo + per);
         for (int i = lo + lane; i < hi; i += 64) a.sync_clear[i] = 0;
     }
+    /* A router row's K3G_KS_R slices are tickets nX + KSR e .. + KSR - 1: when they are
+     * the four waves of one workgroup, all taking them in the first round, the slices are
+     * reduced in the workgroup's LDS instead of through memory. */
+    const bool wg_slices = G.KSR == (int)(blockDim.x >> 6) && G.nX % G.KSR == 0 &&
+                           G.nX + G.nR <= W;
+    if (threadIdx.x == 0) rl.count = 0;
+    __syncthreads();
     for (int tk = w; tk < G.total; tk += W) {
         if (a.trace && lane == 0) {
             const unsigned long long now = wall_clock64();
@@ -928,7 +967,7 @@ k_decode_fused(K3kDecode a)
         }
         int t = tk;
         if (t < G.nX) K3Dec<NT>::prep(ap, t, lane);
-        else if ((t -= G.nX) < G.nR) K3Dec<NT>::router(ap, t, lane);
+        else if ((t -= G.nX) < G.nR) K3Dec<NT>::router(ap, t, lane, &rl, wg_slices);
         else if ((t -= G.nR) < 1) K3Dec<NT>::select(ap, lane, &lds);
         else if ((t -= 1) < G.nSG) K3Dec<NT>::shared_gateup(ap, t, lane);
         else if ((t -= G.nSG) < G.nG) K3Dec<NT>::routed_gateup(ap, t, lane);
