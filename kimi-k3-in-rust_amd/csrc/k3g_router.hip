@@ -172,7 +172,8 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
 }
 
 /* ------------------------------------------------------------------ select ---- */
-/* One wave per token. */
+/* One wave per token; a token whose certificate fails computes its candidates' exact
+ * logits from rows staged through LDS. */
 __global__ void __launch_bounds__(64)
 k_router_select(const float4 *__restrict__ rs, const float *__restrict__ bias,
                 const float *__restrict__ W, const float *__restrict__ x, int d, int E, int k,
@@ -180,8 +181,9 @@ k_router_select(const float4 *__restrict__ rs, const float *__restrict__ bias,
                 float *__restrict__ wt, int force, int *__restrict__ stats)
 {
     __shared__ K3SelectLds lds;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[K3G_XD_BYTES];
     k3d_select_token(&lds, blockIdx.x, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                     force, stats, threadIdx.x);
+                     force, stats, threadIdx.x, nullptr, stage);
 }
 
 extern "C" int k3k_router(const float *x, int T, const float *W, const float *bias, int d,

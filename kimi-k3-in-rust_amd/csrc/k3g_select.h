@@ -155,6 +155,126 @@ __device__ __noinline__ double k3d_serial_dot(const float *w, const float *x, in
     return acc;
 }
 
+/* LDS staging for the exact logits (k3d_exact_dots_staged): two stages of up to
+ * K3G_XD_ROWS candidate rows + the token's x, 256 fp32 columns each, then the rows' exact
+ * fp64 products of one stage. Rows are skewed by 16 bytes so that the lanes' row reads
+ * fall on different banks. */
+#define K3G_XD_ROWS 12
+#define K3G_XD_ROWB 1040                                  /* 256 fp32 + 16 */
+#define K3G_XD_STAGE ((K3G_XD_ROWS + 1) * K3G_XD_ROWB)
+#define K3G_XD_PROWB 2064                                 /* 256 fp64 + 16 */
+#define K3G_XD_BYTES (2 * K3G_XD_STAGE + K3G_XD_ROWS * K3G_XD_PROWB)
+
+/* One DMA instruction: 64 lanes x 16 bytes from their own global addresses to 1 KB of LDS
+ * at byte address `lds` (lane l at lds + 16 l), M0 saved and restored around it. */
+__device__ __forceinline__ void k3d_dma16(const void *src, uint32_t lds)
+{
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %2\n\t"
+                 "global_load_lds_dwordx4 %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+
+/* s_waitcnt vmcnt(n) for a wave-uniform n in 0..15 */
+__device__ __forceinline__ void k3d_wait_vm(int n)
+{
+    switch (n) {
+#define K3_WVM(N) case N: __builtin_amdgcn_s_waitcnt(0x0F70 | N); break;
+        K3_WVM(1) K3_WVM(2) K3_WVM(3) K3_WVM(4) K3_WVM(5) K3_WVM(6) K3_WVM(7) K3_WVM(8)
+        K3_WVM(9) K3_WVM(10) K3_WVM(11) K3_WVM(12) K3_WVM(13) K3_WVM(14) K3_WVM(15)
+#undef K3_WVM
+        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
+}
+
+/* The engine's logits of nb <= K3G_XD_ROWS candidate rows (uniform row pointers) against
+ * x: lane j < nb returns row j's sum in the engine's serial order, exactly as
+ * k3d_serial_dot (fma(w, x, acc) rounds once, and so does acc + the fp64 product, which is
+ * exact for fp32 factors). The rows and x stream through LDS by DMA, 256 columns per
+ * stage, the next stage in flight; all 64 lanes form a stage's products in fp64, then
+ * lane j runs the dependent chain of additions over row j. d must be a multiple of 4 and
+ * the rows and x 16-byte aligned. */
+__device__ __forceinline__ double k3d_exact_dots_staged(uint8_t *stage,
+                                                       const float *const (&rows)[K3G_XD_ROWS],
+                                                       int nb, const float *x, int d, int lane)
+{
+    const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)stage;
+    uint8_t *prod = stage + 2 * K3G_XD_STAGE;
+    const int nch = (d + 255) / 256;
+    auto issue = [&](int k) {
+        /* columns past d re-read the row's last 16 bytes: never summed */
+        const int col = min(256 * k + 4 * lane, d - 4);
+        const uint32_t st = base + (uint32_t)(k & 1) * K3G_XD_STAGE;
+#pragma unroll
+        for (int j = 0; j < K3G_XD_ROWS; ++j)
+            if (j < nb) k3d_dma16(rows[j] + col, st + j * K3G_XD_ROWB);
+        k3d_dma16(x + col, st + nb * K3G_XD_ROWB);
+    };
+    double acc = 0.0;
+    issue(0);
+    for (int k = 0; k < nch; ++k) {
+        if (k + 1 < nch) {
+            issue(k + 1);
+            k3d_wait_vm(nb + 1);          /* stage k landed; stage k + 1 in flight */
+        } else {
+            k3d_wait_vm(0);
+        }
+        __builtin_amdgcn_wave_barrier();
+        /* the stage's exact products: lane l takes columns 4 l .. 4 l + 3 of every row */
+        const uint8_t *st = stage + (k & 1) * K3G_XD_STAGE;
+        const float4 xv = *(const float4 *)(st + nb * K3G_XD_ROWB + 16 * lane);
+        const double x0 = xv.x, x1 = xv.y, x2 = xv.z, x3 = xv.w;
+#pragma unroll
+        for (int j = 0; j < K3G_XD_ROWS; ++j) {
+            if (j < nb) {
+                const float4 wv = *(const float4 *)(st + j * K3G_XD_ROWB + 16 * lane);
+                double2 *pr = (double2 *)(prod + j * K3G_XD_PROWB + 32 * lane);
+                pr[0] = make_double2((double)wv.x * x0, (double)wv.y * x1);
+                pr[1] = make_double2((double)wv.z * x2, (double)wv.w * x3);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (lane < nb) {
+            const double2 *pr = (const double2 *)(prod + lane * K3G_XD_PROWB);
+            const int n2 = min(128, (d - 256 * k) / 2);
+            if (n2 == 128) {
+                /* a full stage: groups of 8 double2 with no bounds tests, the next group
+                 * read before this group's additions */
+                double2 a[8], b[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) a[u] = pr[u];
+#pragma unroll
+                for (int i0 = 0; i0 < 128; i0 += 16) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) b[u] = pr[i0 + 8 + u];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) { acc += a[u].x; acc += a[u].y; }
+                    if (i0 + 16 < 128) {
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) a[u] = pr[i0 + 16 + u];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) { acc += b[u].x; acc += b[u].y; }
+                }
+            } else {
+                for (int i = 0; i < n2; ++i) {
+                    const double2 v = pr[i];
+                    acc += v.x;
+                    acc += v.y;
+                }
+            }
+        }
+        /* every lane is done with this stage and the products before they are rewritten */
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+    }
+    return acc;
+}
+
 /* Selection for token t from rs [T][E] {choice, lo, hi, score} (read at device
  * coherence: the fused kernel's router tickets write them in the same launch). Each lane
  * owns experts lane, lane + 64, ... (NPL of them); all loads are issued before any is
@@ -169,7 +289,7 @@ __device__ __noinline__ void
 k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
                    const float *W, const float *x, int d, int E, int k, int renorm,
                    float routed_scale, int32_t *idx, float *wt, int force, int *stats,
-                   int lane, unsigned long long *stamp)
+                   int lane, unsigned long long *stamp, uint8_t *stage)
 {
     const int nb = (t + 1) * E * 16;
     const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
@@ -275,11 +395,24 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
         __builtin_amdgcn_wave_barrier();
         const int nc = s->ncand;
         const float *xt = x + (size_t)t * d;
-        for (int c0 = 0; c0 < nc; c0 += 64) {
+        const bool staged = stage && d % 4 == 0 && d >= 4 &&
+                            ((((uintptr_t)W | (uintptr_t)x) & 15) == 0);
+        const int per = staged ? K3G_XD_ROWS : 64;
+        for (int c0 = 0; c0 < nc; c0 += per) {
             const int c = c0 + lane;
-            if (c < nc) {
+            double acc = 0.0;
+            if (staged) {
+                const float *rows[K3G_XD_ROWS];
+                const int nb = min(K3G_XD_ROWS, nc - c0);
+#pragma unroll
+                for (int j = 0; j < K3G_XD_ROWS; ++j)
+                    rows[j] = W + (size_t)__builtin_amdgcn_readfirstlane(
+                                      s->cand[c0 + (j < nb ? j : 0)]) * d;
+                acc = k3d_exact_dots_staged(stage, rows, nb, xt, d, lane);
+            }
+            if (lane < per && c < nc) {
                 const int e = s->cand[c];
-                const double acc = k3d_serial_dot(W + (size_t)e * d, xt, d);
+                if (!staged) acc = k3d_serial_dot(W + (size_t)e * d, xt, d);
                 const float sc = k3d_sigmoid((float)acc);
                 s->score[e] = sc;
                 s->choice[e] = __fadd_rn(sc, bias ? bias[e] : 0.0f);
@@ -341,15 +474,15 @@ __device__ __forceinline__ void
 k3d_select_token(K3SelectLds *s, int t, const float4 *rs, const float *bias, const float *W,
                  const float *x, int d, int E, int k, int renorm, float routed_scale,
                  int32_t *idx, float *wt, int force, int *stats, int lane,
-                 unsigned long long *stamp = nullptr)
+                 unsigned long long *stamp = nullptr, uint8_t *stage = nullptr)
 {
     if (E <= 256)
         k3d_select_token_n<4>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                              force, stats, lane, stamp);
+                              force, stats, lane, stamp, stage);
     else if (E <= 512)
         k3d_select_token_n<8>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                              force, stats, lane, stamp);
+                              force, stats, lane, stamp, stage);
     else
         k3d_select_token_n<16>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                               force, stats, lane, stamp);
+                               force, stats, lane, stamp, stage);
 }
