@@ -122,6 +122,14 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t maxt = (P + 127) / 128 + E;
     const size_t o_xb = carve(&at, 2 * T * d128 * 2), o_hb = carve(&at, 2 * P * I128 * 2);
     const size_t o_hsb = carve(&at, 2 * T * (SI128 ? SI128 : 128) * 2);
+    /* the shared expert's K-slice sums when few columns leave the GPU idle */
+    size_t part = 0;
+    if (SI) {
+        const size_t pg = k3k_gemm_part_bytes((int)((SI + 255) / 256), (int)(2 * SI));
+        const size_t pd = k3k_gemm_part_bytes((int)((d + 511) / 512), (int)d);
+        part = pg > pd ? pg : pd;
+    }
+    const size_t o_kpart = carve(&at, part ? part : 16);
     const size_t o_tiles = carve(&at, maxt * 16), o_ntiles = carve(&at, 4);
     const size_t o_xflag = carve(&at, 4);
     const size_t d512 = (d + 511) / 512 * 512, I512 = (I + 511) / 512 * 512;
@@ -169,6 +177,7 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->xb = (uint16_t *)(b + o_xb);
     c->hb = (uint16_t *)(b + o_hb);
     c->hsb = (uint16_t *)(b + o_hsb);
+    c->kpart = (float *)(b + o_kpart);
     c->tiles = (int32_t *)(b + o_tiles);
     c->ntiles = (int32_t *)(b + o_ntiles);
     c->xflag = (int32_t *)(b + o_xflag);
@@ -361,6 +370,8 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         s.hpiece = (long long)T * SI128;
         s.ldh = SI128;
         s.nft = (SI + 255) / 256;
+        s.ksplit = k3k_gemm_ksplit(s.nft, (T + 127) / 128, d);
+        s.part = c->kpart;
         k3g_stage_begin(c, K3G_ST_SH_GATEUP, st);
         rc |= k3k_gemm(&s, st);
         k3g_stage_end(c, K3G_ST_SH_GATEUP, st);
@@ -382,6 +393,7 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         s.ldo = d;
         s.scatter = 0;
         s.nft = (d + 511) / 512;
+        s.ksplit = k3k_gemm_ksplit(s.nft, (T + 127) / 128, SI);
         k3g_stage_begin(c, K3G_ST_SH_DOWN, st);
         rc |= k3k_gemm(&s, st);
         k3g_stage_end(c, K3G_ST_SH_DOWN, st);

@@ -173,6 +173,7 @@ __device__ __forceinline__ void gm_wait_vm_n(int n)
  * per-lane DMA row offsets. */
 struct GmTile {
     int p0, np, lane, w, g4, nK, ndma;
+    int ks, kstep0, nC32;      /* K slice: its index, first 128-column step, 32-chunks */
     int orow0;                 /* mode 0: first feature; mode 1: first output row */
     const uint8_t *abase[4];   /* row group r: its 16-row block of the weight matrix */
     bool rv[4];                /* row group inside the matrix */
@@ -200,7 +201,7 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
     auto stage = [](int c) { return (uint32_t)((c % SN) * (NP * GM_PIECE)); };
     auto dma = [&](int c) {
         const uint32_t st = t.lds + stage(c) + t.w * 1024;
-        const uint16_t *b0 = g.b + (size_t)c * GM_KC;
+        const uint16_t *b0 = g.b + (size_t)(t.kstep0 + c) * GM_KC;
 #pragma unroll
         for (int pc = 0; pc < NP; ++pc) {
             const uint16_t *b = b0 + (size_t)pc * g.bpiece;
@@ -294,11 +295,11 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
         /* ------------------------------------------------ bf16 weights ----------- */
         /* A operands per (step, sub-step): 4 row groups x 16 bytes; a ring of the 4
          * sub-steps of a step, each loaded two sub-steps ahead */
-        const int nC32 = g.K / 32;
+        const int nC32 = t.nC32;
         uint4 ring[4][4];
         auto aload = [&](int c, int s, uint4 *dst) {
             const int c32 = 4 * c + s;
-            const int cc = c32 < nC32 ? c32 : nC32 - 1;
+            const int cc = 4 * t.kstep0 + (c32 < nC32 ? c32 : nC32 - 1);
 #pragma unroll
             for (int r = 0; r < 4; ++r) dst[r] = gm_ld16(t.abase[r] + (size_t)cc * 1024 + 16 * lane);
         };
@@ -330,6 +331,31 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
 
     /* ---- epilogue -------------------------------------------------------------------- */
     const int col0 = lane & 15;
+    if (g.ksplit > 1) {
+        /* a K slice: its fp32 sums, reduced in slice order by k_gemm_reduce */
+        const int R = g.rows, ncol = g.dense_rows;
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) {
+            const int col = 16 * cb + col0;
+            if (col < t.np) {
+                const size_t cix = (size_t)t.ks * ncol + t.p0 + col;
+                if (g.mode == 0) {
+                    if (!t.rv[0]) continue;
+                    float *o = g.part + cix * 2 * R + t.orow0 + 4 * t.g4;
+                    *(k3v4f *)o = acc[0][cb];
+                    *(k3v4f *)(o + 16) = acc[1][cb];
+                    *(k3v4f *)(o + R) = acc[2][cb];
+                    *(k3v4f *)(o + R + 16) = acc[3][cb];
+                } else {
+                    float *o = g.part + cix * R + t.orow0 + 4 * t.g4;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (t.rv[r]) *(k3v4f *)(o + 16 * r) = acc[r][cb];
+                }
+            }
+        }
+        return;
+    }
     if (g.mode == 0) {
         if (!t.rv[0]) return;
         const int n = t.orow0 + 4 * t.g4;
@@ -366,11 +392,15 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
 template <int AF, int WV>
 __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *lds, int &nb)
 {
-    const int ntl = g.tiles ? *g.ntiles : (g.dense_rows + GM_COLS - 1) / GM_COLS;
+    /* dense GEMMs cut into K slices take (column tile, slice) pairs as their tiles */
+    const int ks_n = g.tiles ? 1 : max(1, g.ksplit);
+    const int ntl = (g.tiles ? *g.ntiles : (g.dense_rows + GM_COLS - 1) / GM_COLS) * ks_n;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int rnd = slot / g.nft, f = slot - rnd * g.nft;
-    const int tile = 8 * rnd + ((rnd & 1) ? 7 - xcd : xcd);
-    if (tile >= ntl) return false;
+    const int tks = 8 * rnd + ((rnd & 1) ? 7 - xcd : xcd);
+    if (tks >= ntl) return false;
+    const int tile = tks / ks_n;
+    t.ks = tks - tile * ks_n;
     int e = 0;
     if (g.tiles) {
         const int4 tv = ((const int4 *)g.tiles)[tile];
@@ -383,7 +413,12 @@ __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *l
     t.lane = threadIdx.x & 63;
     t.w = gm_uniform(threadIdx.x >> 6);
     t.g4 = t.lane >> 4;
-    t.nK = (g.K + GM_KC - 1) / GM_KC;
+    {
+        const int steps = (g.K + GM_KC - 1) / GM_KC, per = (steps + ks_n - 1) / ks_n;
+        t.kstep0 = t.ks * per;
+        t.nK = max(0, min(per, steps - t.kstep0));
+        t.nC32 = min(4 * t.nK, g.K / 32 - 4 * t.kstep0);
+    }
     t.ldsp = lds;
     t.lds = (uint32_t)(uintptr_t)(k3lds)lds;
     const uint8_t *m0, *m1;
@@ -780,6 +815,49 @@ k_xpieces(const float *__restrict__ x, int T, int d, int ldb, uint16_t *__restri
     if (__any(nz) && (threadIdx.x & 63) == 0) *flag = 1;
 }
 
+/* The K slices of a dense GEMM summed in slice order: gate/up (mode 0) -> act -> h as two
+ * bf16 pieces; down (mode 1) -> out rows. One thread per 4 consecutive rows of a column. */
+__global__ void __launch_bounds__(256)
+k_gemm_reduce(const float *__restrict__ part, int ks_n, int ncol, int R, int mode, float b1,
+              float b2, uint16_t *__restrict__ h, long long hpiece, int ldh,
+              float *__restrict__ out, int ldo)
+{
+    const int r4 = R / 4;
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long long)ncol * r4) return;
+    const int col = (int)(i / r4), n = 4 * (int)(i - (long long)col * r4);
+    if (mode == 0) {
+        k3v4f gs = {0, 0, 0, 0}, us = {0, 0, 0, 0};
+        for (int k = 0; k < ks_n; ++k) {
+            const float *p = part + ((size_t)k * ncol + col) * 2 * R + n;
+            gs += *(const k3v4f *)p;
+            us += *(const k3v4f *)(p + R);
+        }
+        gm_act_store(gs, us, b1, b2, h + (size_t)col * ldh + n, hpiece);
+    } else {
+        k3v4f y = {0, 0, 0, 0};
+        for (int k = 0; k < ks_n; ++k) y += *(const k3v4f *)(part + ((size_t)k * ncol + col) * R + n);
+        *(k3v4f *)(out + (size_t)col * ldo + n) = y;
+    }
+}
+
+extern "C" int k3k_gemm_ksplit(int nft, int ntl, int K)
+{
+    const int steps = (K + GM_KC - 1) / GM_KC;
+    const int want = nft * ntl >= 256 ? 1 : 256 / (nft * ntl);
+    int ks = want < steps ? want : steps;
+    if (ks < 1) ks = 1;
+    /* whole steps per slice, no empty slice */
+    const int per = (steps + ks - 1) / ks;
+    return (steps + per - 1) / per;
+}
+
+extern "C" size_t k3k_gemm_part_bytes(int nft, int rows2)
+{
+    /* ksplit x column tiles <= 256 / nft + 1 whenever ksplit > 1 */
+    return (size_t)(256 / nft + 1) * GM_COLS * (size_t)rows2 * 4;
+}
+
 /* ------------------------------------------------------------------ launchers ---- */
 extern "C" int k3k_gemm_tiles(const int32_t *off, int E, int32_t *tiles, int32_t *ntiles,
                               int32_t *flag, hipStream_t st)
@@ -870,7 +948,12 @@ extern "C" int k3k_gemm(const K3kGemm *g, hipStream_t st)
     if (g->afmt == 1 && (!g->wa || (g->mode == 0 && !g->wb))) return -1;
     if (g->tiles ? (!g->ntiles || g->max_tiles < 1) : g->dense_rows < 1) return -1;
     if ((g->scatter || (g->mode == 0 && g->tiles)) && !g->perm) return -1;
-    const long long maxt = g->tiles ? g->max_tiles : (g->dense_rows + GM_COLS - 1) / GM_COLS;
+    const int ks_n = g->ksplit > 1 ? g->ksplit : 1;
+    if (ks_n > 1 && (g->tiles || g->afmt != 1 || !g->part || g->K % GM_KC ||
+                     ks_n > g->K / GM_KC || (g->mode == 0 && g->rows % 4)))
+        return -1;
+    const long long maxt = g->tiles ? g->max_tiles
+                                    : (long long)((g->dense_rows + GM_COLS - 1) / GM_COLS) * ks_n;
     const long long grid = 8 * ((maxt + 7) / 8) * g->nft;
     if (grid > 0x7fffffff) return -1;
     if (g->afmt == 0 && g->mode == 0) {
@@ -888,7 +971,15 @@ extern "C" int k3k_gemm(const K3kGemm *g, hipStream_t st)
     } else if (g->afmt == 0) {
         hipLaunchKernelGGL((k_gemm<0, 8>), dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
     } else {
-        hipLaunchKernelGGL((k_gemm<1, 8>), dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
+        K3kGemm g1 = *g;
+        g1.ksplit = ks_n;
+        hipLaunchKernelGGL((k_gemm<1, 8>), dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, g1);
+        if (ks_n > 1) {
+            const long long n = (long long)g->dense_rows * (g->rows / 4);
+            hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                               g->part, ks_n, g->dense_rows, g->rows, g->mode, g->b1, g->b2,
+                               g->h, g->hpiece, g->ldh, g->out, g->ldo);
+        }
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

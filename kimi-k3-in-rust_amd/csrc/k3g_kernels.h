@@ -106,12 +106,22 @@ typedef struct {
     uint8_t *hq, *hs;
     int ldhq;                 /* bytes per h row (scales: ldhq / 32) */
     int np_only;              /* set by k3k_gemm: 2 = a launch that runs only two-piece B */
+    /* dense tiled-bf16 GEMMs only: K cut into ksplit slices of whole 128-column steps
+     * (1: none); the slices' fp32 sums go to part ([ksplit][columns][2][rows] gate/up,
+     * [ksplit][columns][rows] down) and k3k_gemm reduces them in slice order */
+    int ksplit;
+    float *part;
     /* instrumentation (NULL: off): per workgroup of the launch that does the work, wave
      * 0's start and end (wall clock), tile << 32 | feature tile, XCC << 32 | HW_ID */
     unsigned long long *trace;
 } K3kGemm;
 
 int k3k_gemm(const K3kGemm *g, hipStream_t st);
+/* The K slices a dense GEMM of nft feature tiles x ntl column tiles over K columns uses
+ * to give the GPU about 256 workgroups (1 = no split), and the part buffer bytes a
+ * context needs for any column count (rows: the GEMM's output rows; x2 for gate/up). */
+int k3k_gemm_ksplit(int nft, int ntl, int K);
+size_t k3k_gemm_part_bytes(int nft, int rows2);
 /* The same grouped GEMM on v_mfma_scale_f32_16x16x128_f8f6f4: MXFP4 weights as they are,
  * activations in MXFP8 (bq/bs; mode 0 quantises h to hq/hs). */
 int k3k_gemm_f8(const K3kGemm *g, hipStream_t st);

@@ -43,6 +43,10 @@ k_router_logits(const float *__restrict__ x, int T, const float *__restrict__ W,
 #pragma unroll
     for (int t = 0; t < RT; ++t) { acc[t] = 0.0; ab[t] = 0.0; }
     const int d4 = vec ? (d & ~3) : 0;
+#ifndef K3R_VALU_UNROLL
+#define K3R_VALU_UNROLL 4
+#endif
+#pragma unroll K3R_VALU_UNROLL
     for (int i = lane * 4; i < d4; i += 256) {
         const float4 wv = *(const float4 *)(w + i);
 #pragma unroll
@@ -89,6 +93,11 @@ k_router_logits(const float *__restrict__ x, int T, const float *__restrict__ W,
 typedef double k3v4d __attribute__((ext_vector_type(4)));
 
 #define K3R_RING 4
+/* below this many tokens the 16 x 32 tiles are too few to fill the GPU (T = 64: 48
+ * waves) and the one-wave-per-(expert, 4 tokens) kernel is faster */
+#ifndef K3R_MFMA_MIN_T
+#define K3R_MFMA_MIN_T 512
+#endif
 
 __global__ void __launch_bounds__(64)
 k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict__ W,
@@ -194,7 +203,7 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
     /* the score intervals of token t live at [t][E] */
     /* float4 loads need 16-byte aligned rows; anything else takes the scalar loop */
     const int vec = ((((uintptr_t)x | (uintptr_t)W) & 15) == 0) && ((d & 3) == 0);
-    if (T >= 16 && vec && E % 16 == 0 && d % 64 == 0) {
+    if (T >= K3R_MFMA_MIN_T && vec && E % 16 == 0 && d % 64 == 0) {
         const long long N = (long long)(E / 16) * ((T + 31) / 32);
         hipLaunchKernelGGL(k_router_logits_mfma, dim3((unsigned)(8 * ((N + 7) / 8))), dim3(64),
                            0, st, x, T, W, bias, d, E, (float4 *)rs);
