@@ -88,6 +88,57 @@ k_disp_small(const int32_t *idx, int P, int E, int32_t *off, int32_t *act, int32
     if (tid == 0) { off[E] = stot; *nact = atot; }
 }
 
+/* Single block of 1024 threads, P <= K3G_DONE: the pairs' keys in LDS, one thread per
+ * expert counts its pairs, a block scan places the experts, and each expert thread writes
+ * its pairs in pair order (stable). One launch instead of three for mid-size batches. */
+#define K3G_DONE 4096
+__global__ void __launch_bounds__(1024)
+k_disp_one(const int32_t *idx, int P, int E, int32_t *off, int32_t *act, int32_t *nact,
+           int32_t *perm, int *err)
+{
+    __shared__ __attribute__((aligned(16))) int keys[K3G_DONE];
+    __shared__ int sc[1024], sa[1024];
+    const int e = threadIdx.x;
+    const int P4 = (P + 3) / 4;
+    for (int i = e; i < 4 * P4; i += 1024) keys[i] = k3d_key(idx, i, P, E, err);
+    __syncthreads();
+    /* every thread reads the same keys (LDS broadcasts), four at a time */
+    const int4 *k4 = (const int4 *)keys;
+    int tot = 0;
+    if (e < E) {
+#pragma unroll 8
+        for (int i = 0; i < P4; ++i) {
+            const int4 v = k4[i];
+            tot += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
+        }
+    }
+    sc[e] = tot;
+    sa[e] = tot > 0;
+    __syncthreads();
+    for (int dd = 1; dd < 1024; dd <<= 1) {
+        const int a = e >= dd ? sc[e - dd] : 0, b = e >= dd ? sa[e - dd] : 0;
+        __syncthreads();
+        sc[e] += a;
+        sa[e] += b;
+        __syncthreads();
+    }
+    if (e < E) {
+        const int first = sc[e] - tot;
+        off[e] = first;
+        if (tot > 0) act[sa[e] - 1] = e;
+        int pos = first;
+#pragma unroll 4
+        for (int i = 0; i < P4 && pos < first + tot; ++i) {
+            const int4 v = k4[i];
+            if (v.x == e) perm[pos++] = 4 * i;
+            if (v.y == e) perm[pos++] = 4 * i + 1;
+            if (v.z == e) perm[pos++] = 4 * i + 2;
+            if (v.w == e) perm[pos++] = 4 * i + 3;
+        }
+    }
+    if (e == 1023) { off[E] = sc[1023]; *nact = sa[1023]; }
+}
+
 /* Large P, three passes over chunks of 256 pairs. */
 __global__ void __launch_bounds__(256)
 k_disp_count(const int32_t *idx, int P, int E, int32_t *cnt, int *err)
@@ -176,6 +227,9 @@ extern "C" int k3k_dispatch(const int32_t *idx, int P, int E, int32_t *cnt, int3
     if (E < 1 || E > K3G_MAX_EXPERTS || P < 1) return -1;
     if (P <= K3G_DCH) {
         hipLaunchKernelGGL(k_disp_small, dim3(1), dim3(256), 0, st, idx, P, E, off, act, nact,
+                           perm, err);
+    } else if (P <= K3G_DONE) {
+        hipLaunchKernelGGL(k_disp_one, dim3(1), dim3(1024), 0, st, idx, P, E, off, act, nact,
                            perm, err);
     } else {
         const int nch = (P + K3G_DCH - 1) / K3G_DCH;
