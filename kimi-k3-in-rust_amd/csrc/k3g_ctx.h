@@ -58,6 +58,8 @@ struct K3gCtx {
     /* grouped GEMMs on the matrix cores (more than 4 tokens, tiled layouts) */
     uint16_t *xb, *hb, *hsb;     /* bf16 pieces of x [2][T][d128], h [2][T*k][I128], shared h */
     float *kpart;                /* K-slice sums of the shared expert's GEMMs */
+    double *rtpart;              /* K-slice sums of the router's matrix-core logits */
+    int32_t *rtctr;              /* their per-tile arrival counts (zero between calls) */
     int32_t *tiles, *ntiles, *xflag;
     int max_tiles;
     hipEvent_t routed_wait;      /* the next k3g_experts waits for it before routed work */

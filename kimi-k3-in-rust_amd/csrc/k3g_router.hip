@@ -89,7 +89,11 @@ k_router_logits(const float *__restrict__ x, int T, const float *__restrict__ W,
  * L % 16 (A operand) and of token L % 16 (+ 16) (B operand); the four MFMAs of a step
  * take one column each, so both operands come from one 16-byte load per row. The
  * f64 MFMA result puts expert 4 i + L / 16, token L % 16 in item i of lane L.
- * sum|w*x| is bounded by ||w|| ||x|| (Cauchy-Schwarz), both norms summed alongside. */
+ * sum|w*x| is bounded by ||w|| ||x|| (Cauchy-Schwarz), both norms summed alongside.
+ * With few tiles (S > 1) each tile's columns are cut into S slices taken by S waves; a
+ * slice stores its partial sums, and the wave that completes the tile's count (a device
+ * atomic) sums the S partials in slice order and forms the scores (any summation order
+ * stays inside the interval's bound), then resets the count for the next call. */
 typedef double k3v4d __attribute__((ext_vector_type(4)));
 
 #define K3R_RING 4
@@ -99,11 +103,14 @@ typedef double k3v4d __attribute__((ext_vector_type(4)));
 #define K3R_MFMA_MIN_T 512
 #endif
 
+#define K3R_PART 11    /* doubles per lane of a slice's partial sums */
+
 __global__ void __launch_bounds__(64)
 k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict__ W,
-                     const float *__restrict__ bias, int d, int E, float4 *__restrict__ rs)
+                     const float *__restrict__ bias, int d, int E, float4 *__restrict__ rs,
+                     int S, double *__restrict__ part, int32_t *__restrict__ ctr)
 {
-    const int nte = E / 16, ntt = (T + 31) / 32, N = nte * ntt;
+    const int nte = E / 16, ntt = (T + 31) / 32, N = nte * ntt * S;
     const int per = (N + 7) >> 3;
     /* block b runs on XCD b % 8: give each XCD a contiguous run, so the expert tiles of
      * one token tile (consecutive) share its x rows in one L2 */
@@ -111,17 +118,20 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
     if (slot >= per) return;
     const int lam = xcd * per + slot;
     if (lam >= N) return;
-    const int tt = lam / nte, et = lam - tt * nte;
+    const int tl = lam / S, sl = lam - tl * S;
+    const int tt = tl / nte, et = tl - tt * nte;
     const int e0 = 16 * et, t0 = 32 * tt;
     const int L = threadIdx.x, g = L >> 4, r = L & 15;
-    const float4 *wp = (const float4 *)(W + (size_t)(e0 + r) * d) + g;
-    const float4 *ap = (const float4 *)(x + (size_t)min(t0 + r, T - 1) * d) + g;
-    const float4 *bp = (const float4 *)(x + (size_t)min(t0 + 16 + r, T - 1) * d) + g;
-    const int ns = d / 16;
+    const int nsteps = d / 16, spp = (nsteps + S - 1) / S;
+    const int s_begin = min(nsteps, sl * spp);
+    const float4 *wp = (const float4 *)(W + (size_t)(e0 + r) * d) + g + 4 * s_begin;
+    const float4 *ap = (const float4 *)(x + (size_t)min(t0 + r, T - 1) * d) + g + 4 * s_begin;
+    const float4 *bp = (const float4 *)(x + (size_t)min(t0 + 16 + r, T - 1) * d) + g + 4 * s_begin;
+    const int ns = max(0, min(nsteps, s_begin + spp) - s_begin);
     float4 wv[K3R_RING], av[K3R_RING], bv[K3R_RING];
 #pragma unroll
     for (int u = 0; u < K3R_RING; ++u) {
-        const int s = min(u, ns - 1);
+        const int s = max(0, min(u, ns - 1));
         wv[u] = wp[4 * s]; av[u] = ap[4 * s]; bv[u] = bp[4 * s];
     }
     /* two chains per output (even and odd columns of a step), so consecutive MFMAs do
@@ -133,7 +143,7 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
 #pragma unroll
         for (int u = 0; u < K3R_RING; ++u) {
             const float4 w4 = wv[u], a4 = av[u], b4 = bv[u];
-            const int sn = min(s0 + u + K3R_RING, ns - 1);
+            const int sn = max(0, min(s0 + u + K3R_RING, ns - 1));
             wv[u] = wp[4 * sn]; av[u] = ap[4 * sn]; bv[u] = bp[4 * sn];
             if (s0 + u < ns) {
                 const double w[4] = {w4.x, w4.y, w4.z, w4.w};
@@ -157,6 +167,48 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
     }
     acc0 += acc2;
     acc1 += acc3;
+    if (S > 1) {
+        /* device-coherent stores of the slice's sums, complete before the count moves (no
+         * cache writeback or invalidate: the data never sits in a non-coherent cache) */
+        double *pp = part + ((size_t)tl * S + sl) * (64 * K3R_PART) + L * K3R_PART;
+        const double mine[K3R_PART] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1],
+                                       acc1[2], acc1[3], ssw, ssa, ssb};
+#pragma unroll
+        for (int i = 0; i < K3R_PART; ++i)
+            __hip_atomic_store(pp + i, mine[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        asm volatile("" ::: "memory");
+        int old = 0;
+        /* one count per 128-byte line: counts sharing a line would queue at the L2 */
+        if (L == 0) old = __hip_atomic_fetch_add(&ctr[32 * tl], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane(old) != S - 1) return;
+        asm volatile("" ::: "memory");
+        acc0 = k3v4d{0.0, 0.0, 0.0, 0.0};
+        acc1 = k3v4d{0.0, 0.0, 0.0, 0.0};
+        ssw = 0.0; ssa = 0.0; ssb = 0.0;
+        /* every slice's sums (device-coherent loads), four slices in flight at a time,
+         * summed in slice order */
+        for (int q0 = 0; q0 < S; q0 += 4) {
+            double v[4][K3R_PART];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                double *qq =
+                    part + ((size_t)tl * S + min(q0 + u, S - 1)) * (64 * K3R_PART) + L * K3R_PART;
+#pragma unroll
+                for (int i = 0; i < K3R_PART; ++i)
+                    v[u][i] = __hip_atomic_load(qq + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (q0 + u < S) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) { acc0[i] += v[u][i]; acc1[i] += v[u][4 + i]; }
+                    ssw += v[u][8]; ssa += v[u][9]; ssb += v[u][10];
+                }
+            }
+        }
+        if (L == 0) __hip_atomic_store(&ctr[32 * tl], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     /* norms: sum the four column groups; lane L then holds expert e0 + L % 16 and tokens
      * t0 + L % 16, t0 + 16 + L % 16 */
 #pragma unroll
@@ -195,18 +247,43 @@ k_router_select(const float4 *__restrict__ rs, const float *__restrict__ bias,
                      force, stats, threadIdx.x, nullptr, stage);
 }
 
+/* K slices for the matrix-core logits when the tiles are few: about K3R_WAVES waves, at
+ * most K3R_MAXS slices per tile (the last wave's sum of the slices grows with their
+ * count: at 64 tokens 8 slices measured 40 us, 4 53 us, 16 46 us, 32 89 us) */
+#define K3R_WAVES 512
+#define K3R_MAXS 8
+extern "C" size_t k3k_router_part_bytes(void) { return (size_t)2 * K3R_WAVES * 64 * K3R_PART * 8; }
+
+static int router_slices(int N)
+{
+    if (N >= 512) return 1;
+    const int s = K3R_WAVES / N;
+    return s > K3R_MAXS ? K3R_MAXS : (s < 2 ? 2 : s);
+}
+
 extern "C" int k3k_router(const float *x, int T, const float *W, const float *bias, int d,
                           int E, int k, int renorm, float routed_scale, float *rs,
-                          int32_t *idx, float *wt, int force, int *stats, hipStream_t st)
+                          int32_t *idx, float *wt, int force, int *stats, double *part,
+                          int32_t *ctr, hipStream_t st)
 {
     if (E > K3G_MAX_E || k > K3G_MAX_TOPK || k < 1 || T < 1 || d < 1) return -1;
     /* the score intervals of token t live at [t][E] */
     /* float4 loads need 16-byte aligned rows; anything else takes the scalar loop */
     const int vec = ((((uintptr_t)x | (uintptr_t)W) & 15) == 0) && ((d & 3) == 0);
-    if (T >= K3R_MFMA_MIN_T && vec && E % 16 == 0 && d % 64 == 0) {
-        const long long N = (long long)(E / 16) * ((T + 31) / 32);
+    const long long N1 = (long long)(E / 16) * ((T + 31) / 32);
+    const bool mfma_ok = T >= 16 && vec && E >= 16 && E % 16 == 0 && d % 64 == 0;
+    int S = (mfma_ok && part && ctr && N1 < 512) ? router_slices((int)N1) : 1;
+    if (S > 1) {
+        /* whole 16-column steps per slice and no empty slice */
+        const int nsteps = d / 16;
+        if (S > nsteps) S = nsteps;
+        const int spp = (nsteps + S - 1) / S;
+        S = (nsteps + spp - 1) / spp;
+    }
+    if (mfma_ok && (S > 1 || T >= K3R_MFMA_MIN_T)) {
+        const long long N = N1 * S;
         hipLaunchKernelGGL(k_router_logits_mfma, dim3((unsigned)(8 * ((N + 7) / 8))), dim3(64),
-                           0, st, x, T, W, bias, d, E, (float4 *)rs);
+                           0, st, x, T, W, bias, d, E, (float4 *)rs, S, part, ctr);
     } else if (T >= 4) {
         hipLaunchKernelGGL(k_router_logits<4>, dim3(E, (T + 3) / 4), dim3(64), 0, st,
                            x, T, W, bias, d, vec, (float4 *)rs, E);
