@@ -309,6 +309,13 @@ typedef struct K3gCache K3gCache;
  * experts from the checkpoint files. */
 int  k3gc_bank_create(K3gcBank **bank, int n_layers, int n_experts, int hidden, int inter,
                       int layout);
+/* The same with at most max_pinned_layers layers pinned (< 0: as many as the driver
+ * grants). Misses from pageable layers are copied through K3GC_NSTAGE pinned staging
+ * buffers of the bank (taken before the layers): the host copies the run in with all
+ * threads and the DMA engine copies it out at the pinned rate. Caches sharing a bank
+ * must not copy at the same time. No reference counterpart. */
+int  k3gc_bank_create_ex(K3gcBank **bank, int n_layers, int n_experts, int hidden,
+                         int inter, int layout, int max_pinned_layers);
 /* A bank with the geometry only (no memory), for caches that keep the bookkeeping only
  * (k3gc_init with device < 0): replays of a request trace at any capacity, as the
  * engine's offline simulator does. */
@@ -346,6 +353,7 @@ typedef struct {
     double load_seconds;          /* copy-stream time spent on misses */
     int nslot, resident, pinned;
     int64_t slot_bytes;
+    int64_t staged;               /* misses copied through the bank's pinned staging */
 } K3gcStats;
 void k3gc_stats(K3gCache *cache, K3gcStats *out);
 

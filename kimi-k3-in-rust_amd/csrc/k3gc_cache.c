@@ -35,6 +35,12 @@ static int64_t run_bytes(int hidden, int inter, int layout)
 int k3gc_bank_create(K3gcBank **out, int n_layers, int n_experts, int hidden, int inter,
                      int layout)
 {
+    return k3gc_bank_create_ex(out, n_layers, n_experts, hidden, inter, layout, -1);
+}
+
+int k3gc_bank_create_ex(K3gcBank **out, int n_layers, int n_experts, int hidden, int inter,
+                        int layout, int max_pinned_layers)
+{
     *out = NULL;
     if (n_layers < 1 || n_experts < 1 || hidden < 32 || inter < 32 ||
         (layout != K3G_EXPERT_MXFP4 && layout != K3G_EXPERT_MXFP4_TILED)) {
@@ -56,15 +62,25 @@ int k3gc_bank_create(K3gcBank **out, int n_layers, int n_experts, int hidden, in
     b->layout = layout;
     b->expert_bytes = eb;
     /* one allocation per layer: pinned while the driver grants it (a box may cap pinned
-     * memory well below the bank's size), pageable beyond that; both are copied with
-     * hipMemcpyAsync, the pageable ones through the runtime's own staging */
+     * memory well below the bank's size) and max_pinned_layers allows (< 0: no limit),
+     * pageable beyond that. The staging buffers the pageable layers' misses go through
+     * are taken first, so the pinned layers cannot use up what they need. */
     const size_t per_layer = (size_t)n_experts * (size_t)eb;
     b->layer_host = (unsigned char **)calloc((size_t)n_layers, sizeof(unsigned char *));
     b->layer_pinned = (unsigned char *)calloc((size_t)n_layers, 1);
     if (!b->layer_host || !b->layer_pinned) { k3gc_bank_free(b); return -1; }
-    int pinned_ok = 1;
+    for (int i = 0; i < K3GC_NSTAGE; i++) {
+        void *p = NULL;
+        if (hipHostMalloc(&p, (size_t)eb, hipHostMallocDefault) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            break;
+        }
+        b->stage[b->nstage++] = (unsigned char *)p;
+    }
+    int pinned_ok = max_pinned_layers != 0;
     for (int l = 0; l < n_layers; l++) {
         void *p = NULL;
+        if (max_pinned_layers >= 0 && b->pinned_layers >= max_pinned_layers) pinned_ok = 0;
         if (pinned_ok && hipHostMalloc(&p, per_layer, hipHostMallocDefault) == hipSuccess && p) {
             b->layer_pinned[l] = 1;
             b->pinned_layers++;
@@ -111,6 +127,7 @@ void k3gc_bank_free(K3gcBank *b)
             if (b->layer_pinned[l]) hipHostFree(b->layer_host[l]);
             else free(b->layer_host[l]);
         }
+    for (int i = 0; i < b->nstage; i++) hipHostFree(b->stage[i]);
     free(b->layer_host);
     free(b->layer_pinned);
     free(b);
@@ -199,7 +216,23 @@ static void batch_close(K3gCache *c)
     c->copies_pending = 1;
 }
 
-/* Copy (layer, expert) from the bank into `slot`, after the last step that read it. */
+/* dst <- src with every host thread (a run is tens of MB) */
+static void par_copy(unsigned char *dst, const unsigned char *src, size_t n)
+{
+    const int parts = 16;
+    const size_t per = ((n + parts - 1) / parts + 4095) & ~(size_t)4095;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < parts; i++) {
+        const size_t a = (size_t)i * per;
+        if (a < n) memcpy(dst + a, src + a, (a + per < n ? per : n - a));
+    }
+}
+
+/* Copy (layer, expert) from the bank into `slot`, after the last step that read it. A run
+ * in a pageable layer goes through the next pinned staging buffer: once the DMA engine
+ * has copied that buffer's previous run out, the host copies this run in, and the DMA
+ * engine copies it to the slot at the pinned rate (the host copy of the next miss
+ * overlaps this one's DMA). */
 static void copy_in(K3gCache *c, int slot, int32_t key)
 {
     c->bytes_read += (uint64_t)c->bank->expert_bytes;
@@ -208,9 +241,21 @@ static void copy_in(K3gCache *c, int slot, int32_t key)
     const int64_t s = c->use_step[slot];
     if (s >= 0 && c->step - s <= K3GC_STEP_RING)
         K3G_CHECK(hipStreamWaitEvent(c->copy, c->step_ev[s % K3GC_STEP_RING], 0));
-    K3G_CHECK(hipMemcpyAsync(c->arena + (size_t)slot * c->slot_bytes,
-                             k3gc_bank_expert(c->bank, key / c->n_experts, key % c->n_experts),
-                             (size_t)c->bank->expert_bytes, hipMemcpyHostToDevice, c->copy));
+    const int layer = key / c->n_experts;
+    const unsigned char *src =
+        (const unsigned char *)k3gc_bank_expert(c->bank, layer, key % c->n_experts);
+    const size_t n = (size_t)c->bank->expert_bytes;
+    unsigned char *dst = c->arena + (size_t)slot * c->slot_bytes;
+    if (!c->bank->layer_pinned[layer] && c->bank->nstage > 0) {
+        const int j = (int)(c->stage_next++ % (unsigned)c->bank->nstage);
+        K3G_CHECK(hipEventSynchronize(c->stage_ev[j]));
+        par_copy(c->bank->stage[j], src, n);
+        K3G_CHECK(hipMemcpyAsync(dst, c->bank->stage[j], n, hipMemcpyHostToDevice, c->copy));
+        K3G_CHECK(hipEventRecord(c->stage_ev[j], c->copy));
+        c->staged++;
+    } else {
+        K3G_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->copy));
+    }
 }
 
 /* Bring (layer, expert) resident; returns its slot or -1. src/cache/k3_cache.c:63-110 */
@@ -377,6 +422,10 @@ int k3gc_init(K3gCache **out, int device, K3gcBank *bank, int topk, int64_t budg
         for (int i = 0; i < K3GC_STEP_RING; i++)
             K3G_CHECK(hipEventCreateWithFlags(&c->step_ev[i], hipEventDisableTiming));
         K3G_CHECK(hipEventCreateWithFlags(&c->last_copy, hipEventDisableTiming));
+        for (int i = 0; i < K3GC_NSTAGE; i++) {
+            K3G_CHECK(hipEventCreateWithFlags(&c->stage_ev[i], hipEventDisableTiming));
+            K3G_CHECK(hipEventRecord(c->stage_ev[i], c->copy));
+        }
         for (int i = 0; i < K3GC_TIMER_RING; i++) {
             K3G_CHECK(hipEventCreate(&c->tev[i][0]));
             K3G_CHECK(hipEventCreate(&c->tev[i][1]));
@@ -403,6 +452,8 @@ void k3gc_free(K3gCache *c)
             for (int i = 0; i < K3GC_STEP_RING; i++)
                 if (c->step_ev[i]) hipEventDestroy(c->step_ev[i]);
             if (c->last_copy) hipEventDestroy(c->last_copy);
+            for (int i = 0; i < K3GC_NSTAGE; i++)
+                if (c->stage_ev[i]) hipEventDestroy(c->stage_ev[i]);
             for (int i = 0; i < K3GC_TIMER_RING; i++) {
                 if (c->tev[i][0]) hipEventDestroy(c->tev[i][0]);
                 if (c->tev[i][1]) hipEventDestroy(c->tev[i][1]);
@@ -500,6 +551,7 @@ void k3gc_stats(K3gCache *c, K3gcStats *o)
     o->load_seconds = c->load_seconds;
     o->nslot = c->nslot;
     o->slot_bytes = c->slot_bytes;
+    o->staged = (int64_t)c->staged;
     for (int i = 0; i < c->nslot; i++) {
         if (c->key_of[i] >= 0) o->resident++;
         if (c->pinned[i]) o->pinned++;

@@ -17,6 +17,7 @@
 
 #define K3GC_STEP_RING 1024
 #define K3GC_TIMER_RING 256
+#define K3GC_NSTAGE 4          /* pinned staging buffers for misses from pageable layers */
 
 struct K3gcBank {
     int n_layers, n_experts, hidden, inter, layout;
@@ -24,6 +25,10 @@ struct K3gcBank {
     unsigned char **layer_host;   /* [n_layers]: [n_experts][expert_bytes] each */
     unsigned char *layer_pinned;  /* [n_layers]: 1 hipHostMalloc, 0 pageable malloc */
     int pinned_layers;
+    /* pinned staging for the pageable layers' runs: the host copies a run in (all
+     * threads), the DMA engine copies it out at the pinned rate */
+    unsigned char *stage[K3GC_NSTAGE];
+    int nstage;
 };
 
 struct K3gCache {
@@ -49,6 +54,9 @@ struct K3gCache {
     hipEvent_t last_copy;         /* copy stream, after the latest copy */
     int copies_pending;           /* copies issued since the last k3gc_wait */
     hipEvent_t tev[K3GC_TIMER_RING][2];   /* copy-stream timing per batch of copies */
+    hipEvent_t stage_ev[K3GC_NSTAGE];     /* copy stream, after the copy out of a stage */
+    unsigned stage_next;
+    uint64_t staged;              /* misses copied through the staging buffers */
     int t_head, t_used, t_open;
     K3ExpertQ *dev_table;         /* [n_layers][n_experts] device pointers (k3gc_moe) */
     int32_t *host_idx;            /* pinned staging of a step's routing */

@@ -56,7 +56,8 @@ class K3gcStats(C.Structure):
     _fields_ = [("requests", C.c_int64), ("hits", C.c_int64), ("misses", C.c_int64),
                 ("evictions", C.c_int64), ("prefetch_reads", C.c_int64),
                 ("bytes_read", C.c_int64), ("load_seconds", C.c_double), ("nslot", C.c_int),
-                ("resident", C.c_int), ("pinned", C.c_int), ("slot_bytes", C.c_int64)]
+                ("resident", C.c_int), ("pinned", C.c_int), ("slot_bytes", C.c_int64),
+                ("staged", C.c_int64)]
 
 
 # the K3ExpertSrc entry points, called through the vtable as the engine does
@@ -185,6 +186,8 @@ def lib() -> C.CDLL:
         i64 = C.c_int64
         L.k3gc_bank_create.argtypes = [C.POINTER(vp), i, i, i, i, i]
         L.k3gc_bank_create.restype = i
+        L.k3gc_bank_create_ex.argtypes = [C.POINTER(vp), i, i, i, i, i, i]
+        L.k3gc_bank_create_ex.restype = i
         L.k3gc_bank_geometry.argtypes = [C.POINTER(vp), i, i, i64]
         L.k3gc_bank_geometry.restype = i
         L.k3gc_bank_free.argtypes = [vp]
@@ -659,13 +662,14 @@ class Bank:
     bookkeeping replays (k3gc_bank_geometry)."""
 
     def __init__(self, n_layers: int, n_experts: int, hidden: int = 0, inter: int = 0,
-                 layout: int = K3G_EXPERT_MXFP4_TILED, expert_bytes: int = 0):
+                 layout: int = K3G_EXPERT_MXFP4_TILED, expert_bytes: int = 0,
+                 max_pinned_layers: int = -1):
         self.ptr = C.c_void_p()
         if expert_bytes:
             rc = lib().k3gc_bank_geometry(C.byref(self.ptr), n_layers, n_experts, expert_bytes)
         else:
-            rc = lib().k3gc_bank_create(C.byref(self.ptr), n_layers, n_experts, hidden, inter,
-                                        layout)
+            rc = lib().k3gc_bank_create_ex(C.byref(self.ptr), n_layers, n_experts, hidden,
+                                           inter, layout, max_pinned_layers)
         if rc != 0:
             raise RuntimeError("k3gc bank creation failed")
         self.n_layers, self.n_experts, self.layout = n_layers, n_experts, layout

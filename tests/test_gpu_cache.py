@@ -21,12 +21,17 @@ def _layers(n, layout):
     return [k3moe.SynthLayer(k3moe.TINY, seed=77, layer=l, layout=layout) for l in range(n)]
 
 
-def test_streamed_layers_match_resident(gpu):
+@pytest.mark.parametrize("max_pinned", [-1, 1])
+def test_streamed_layers_match_resident(gpu, max_pinned):
     T, NL = 6, 3
     say(f"case: k3gc_moe tiny layer, {NL} layers x 2 passes, {T} tokens, 18 HBM slots for "
-        f"{NL * 16} experts (evictions), router and given routing")
+        f"{NL * 16} experts (evictions), router and given routing, pinned layers "
+        f"{'all' if max_pinned < 0 else max_pinned} (the rest through the staging buffers)")
     layers = _layers(NL, "tiled")
-    bank = k3moe.Bank(NL, 16, 256, 128, k3moe.K3G_EXPERT_MXFP4_TILED)
+    bank = k3moe.Bank(NL, 16, 256, 128, k3moe.K3G_EXPERT_MXFP4_TILED,
+                      max_pinned_layers=max_pinned)
+    if max_pinned >= 0:
+        assert bank.pinned_layers == max_pinned
     for l, lay in enumerate(layers):
         bank.fill_from_layer(lay, l)
     slot = (bank.expert_bytes + 65535) // 65536 * 65536
@@ -67,6 +72,8 @@ def test_streamed_layers_match_resident(gpu):
     assert st.hits + st.misses == st.requests
     assert st.evictions > 0 and st.prefetch_reads > 0
     assert st.bytes_read == (st.misses + st.prefetch_reads) * bank.expert_bytes
+    if max_pinned >= 0:
+        assert st.staged > 0
     # every call brings its experts in with the batch prefetch first: get() then hits
     assert st.misses == 0
     ctx.destroy()
