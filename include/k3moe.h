@@ -284,6 +284,45 @@ int  k3g_router(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
 int  k3g_moe(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
              float *out, int32_t *idx, float *wt, void *stream);
 
+/* The layer's steps one at a time (the expert-major prefill, src/core/k3_ops.c:717-807),
+ * all device pointers, asynchronous on `stream` (NULL = the context's stream), sizes
+ * within what the context was created for. Each returns 0, or -1 on a bad argument or a
+ * launch error; device-side errors surface at k3g_sync. */
+
+/* Token -> expert dispatch (the unique-expert collection of src/core/k3_ops.c:733-749,
+ * made a counting sort): for P = T * topk (token, slot) pairs with expert ids idx [P],
+ * off [n_experts + 1] receives each expert's first position and perm [P] the pair numbers
+ * t * topk + j grouped by expert, ascending within each expert (a stable sort on idx).
+ * Pairs with idx < 0 are left out (off[n_experts] counts the pairs placed); an id >=
+ * n_experts is left out too and raises the device error that k3g_sync reports. */
+int  k3g_dispatch(K3gCtx *ctx, const int32_t *idx, int T, int topk, int n_experts,
+                  int32_t *perm, int32_t *off, void *stream);
+
+/* Routed experts as per-expert GEMVs over each expert's pairs (the expert-major loop of
+ * src/core/k3_ops.c:751-778, k3_matmul_mxfp4 at src/core/k3_ops.c:108): contrib
+ * [T * topk][hidden] receives w2 . act(w1 . x_t, w3 . x_t) for each pair (t, j) with
+ * e = idx[t * topk + j] valid; other rows are left alone. Experts in the checkpoint MXFP4
+ * layout (K3G_EXPERT_MXFP4) or fp32; no latent projection. */
+int  k3g_expert_gemv(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
+                     const int32_t *idx, float *contrib, void *stream);
+
+/* The same contrib rows as grouped GEMMs over 128-pair column tiles: gate/up with the
+ * activation fused, then down, bf16 matrix cores (weights decoded from MXFP4 exactly,
+ * activations split into two bf16 pieces, fp32 accumulation) or, for _f8f6f4, the
+ * scaled FP4 x FP8 ones with x and h quantised to MXFP8. Experts in the tiled layout
+ * (K3G_EXPERT_MXFP4_TILED), hidden and inter multiples of 32. */
+int  k3g_grouped_gemm_bf16(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
+                           const int32_t *idx, float *contrib, void *stream);
+int  k3g_grouped_gemm_f8f6f4(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
+                             const int32_t *idx, float *contrib, void *stream);
+
+/* Deterministic combine (src/core/k3_ops.c:780-792): out [T][n] = sum over j in top-k
+ * order of wt[t][j] * contrib[t * topk + j] in fp32, starting from 0, then + add[t]
+ * when add (the shared expert's output) is given. Slots with idx < 0 are skipped; n is a
+ * multiple of 4. */
+int  k3g_combine(K3gCtx *ctx, const float *contrib, const int32_t *idx, const float *wt,
+                 int T, int topk, int n, const float *add, float *out, void *stream);
+
 /* Synchronise the stream and report any error a kernel raised on the device
  * (an exhausted bounded wait, a bad expert index). Returns 0 when clean. */
 int  k3g_sync(K3gCtx *ctx, void *stream);

@@ -314,13 +314,16 @@ static int r512(int v) { return (v + 511) / 512 * 512; }
 
 void k3g_ctx_set_fp8(K3gCtx *c, int on) { if (c) c->gemm_fp8 = on; }
 
-/* Routed and shared experts as grouped GEMMs on the bf16 matrix cores (k3g_gemm.hip):
- * dispatch -> column tiles -> x pieces -> gate/up (+act) -> down -> combine. */
+/* Routed and shared experts as grouped GEMMs on the bf16 matrix cores (k3g_gemm.hip), or
+ * the routed experts on the FP4 x FP8 ones (fp8): dispatch -> column tiles -> x pieces ->
+ * [shared gate/up, down] -> routed gate/up (+act) -> down -> [combine]. full = 0 stops at
+ * the routed experts' per-pair rows in contrib. */
 static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
-                        const int32_t *idx, const float *wt, float *out, hipStream_t st)
+                        const int32_t *idx, const float *wt, float *out, float *contrib,
+                        int fp8, int full, hipStream_t st)
 {
     const int d = L->hidden, E = L->n_experts, k = L->topk, I = L->inter;
-    const int SI = L->shared_inter, P = T * k;
+    const int SI = full ? L->shared_inter : 0, P = T * k;
     const int d128 = r128(d), I128 = r128(c->inter), SI128 = r128(c->shared_inter);
     int rc = 0;
     k3g_stage_begin(c, K3G_ST_DISPATCH, st);
@@ -331,7 +334,7 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     const int d512 = r512(d), I512 = r512(c->inter);
     k3g_stage_begin(c, K3G_ST_PIECES, st);
     rc |= k3k_xpieces(x, T, d, d128, c->xb, (long long)T * d128, c->xflag, st);
-    if (c->gemm_fp8)
+    if (fp8)
         rc |= k3k_xq8(x, T, d, d512, c->xq8b, c->xq8b + (size_t)T * d512, st);
     k3g_stage_end(c, K3G_ST_PIECES, st);
 
@@ -408,7 +411,7 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) rc = -1;
         c->routed_wait = NULL;
     }
-    if (c->gemm_fp8) {
+    if (fp8) {
         g.bq = c->xq8b;
         g.bs = c->xq8b + (size_t)T * d512;
         g.ldb = d512;
@@ -417,8 +420,8 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         g.ldhq = I512;
     }
     k3g_stage_begin(c, K3G_ST_GATEUP, st);
-    g.trace = c->gemm_fp8 ? NULL : c->trace;
-    rc |= c->gemm_fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
+    g.trace = fp8 ? NULL : c->trace;
+    rc |= fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
     k3g_stage_end(c, K3G_ST_GATEUP, st);
     /* the down launch's stamps follow the widest gate/up launch's (4-wave workgroups) */
     if (g.trace) g.trace += 4 * 8 * (size_t)((g.max_tiles + 7) / 8) * (size_t)((I + 127) / 128);
@@ -431,11 +434,11 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     g.bpiece = (long long)P * I128;
     g.lo_flag = NULL;
     g.h = NULL;
-    g.out = c->contrib;
+    g.out = contrib;
     g.ldo = d;
     g.scatter = 1;
     g.nft = (d + 511) / 512;
-    if (c->gemm_fp8) {
+    if (fp8) {
         g.bq = c->hq8b;
         g.bs = c->hq8b + (size_t)P * I512;
         g.ldb = I512;
@@ -443,12 +446,14 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         g.hs = NULL;
     }
     k3g_stage_begin(c, K3G_ST_DOWN, st);
-    rc |= c->gemm_fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
+    rc |= fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
     k3g_stage_end(c, K3G_ST_DOWN, st);
 
-    k3g_stage_begin(c, K3G_ST_COMBINE, st);
-    rc |= k3k_combine(c->contrib, idx, wt, T, k, d, SI > 0 ? c->sh_out : NULL, out, st);
-    k3g_stage_end(c, K3G_ST_COMBINE, st);
+    if (full) {
+        k3g_stage_begin(c, K3G_ST_COMBINE, st);
+        rc |= k3k_combine(contrib, idx, wt, T, k, d, SI > 0 ? c->sh_out : NULL, out, st);
+        k3g_stage_end(c, K3G_ST_COMBINE, st);
+    }
     return rc ? -1 : 0;
 }
 
@@ -502,37 +507,17 @@ int k3g_router(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx
 
 static int wfmt(int wdt) { return wdt == K3_WBF16 ? K3K_BF16 : K3K_F32; }
 
-int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
-                const float *wt, float *out, hipStream_t st)
+/* The routed experts of checkpoint-layout (or fp32) weights as per-expert GEMVs over each
+ * expert's pairs (k3g_gemv.hip): dispatch -> gate/up (+act) -> down -> contrib rows. */
+static int routed_staged(K3gCtx *c, const K3gLayer *L, const float *z, int lat, int T,
+                         const int32_t *idx, float *contrib, hipStream_t st)
 {
-    if (!fits(c, L, T)) return -1;
-    const int d = L->hidden, E = L->n_experts, k = L->topk, I = L->inter;
-    const int SI = L->shared_inter, lat = L->latent > 0 ? L->latent : d;
-    const int P = T * k;
-    const int projected = L->down != NULL;
+    const int E = L->n_experts, k = L->topk, P = T * k;
     int rc = 0;
-    if (gemmable(c, L)) return experts_gemm(c, L, x, T, idx, wt, out, st);
-    if (c->routed_wait) {
-        if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) return -1;
-        c->routed_wait = NULL;
-    }
-    if (L->expert_fmt == K3G_EXPERT_MXFP4_TILED || L->shared_fmt != 0) {
-        fprintf(stderr, "k3moe: tiled experts need the Kimi-K2 layer shape (no latent "
-                        "projection, bf16 shared expert, widths multiple of 32)\n");
-        return -1;
-    }
-
     k3g_stage_begin(c, K3G_ST_DISPATCH, st);
     rc |= k3k_dispatch(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm, c->err,
                        st);
     k3g_stage_end(c, K3G_ST_DISPATCH, st);
-    const float *z = x;
-    if (projected) {
-        k3g_stage_begin(c, K3G_ST_LATENT, st);
-        rc |= k3k_dense(wfmt(L->wdt), L->down, NULL, lat, d, x, d, T, c->z, lat, 0.f, 0.f, st);
-        k3g_stage_end(c, K3G_ST_LATENT, st);
-        z = c->z;
-    }
     K3kRouted a;
     memset(&a, 0, sizeof a);
     a.fmt = L->expert_fmt == 1 ? K3K_F32 : K3K_MXFP4;
@@ -545,11 +530,11 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     a.off = c->off;
     a.perm = c->perm;
     a.topk = k;
-    a.inter = I;
+    a.inter = L->inter;
     a.latent = lat;
     a.z = z;
     a.h = c->h;
-    a.contrib = c->contrib;
+    a.contrib = contrib;
     a.b1 = L->act_b1;
     a.b2 = L->act_b2;
     a.err = c->err;
@@ -560,6 +545,37 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     k3g_stage_begin(c, K3G_ST_DOWN, st);
     rc |= k3k_routed_down(&a, maxU, T, st);
     k3g_stage_end(c, K3G_ST_DOWN, st);
+    return rc;
+}
+
+int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
+                const float *wt, float *out, hipStream_t st)
+{
+    if (!fits(c, L, T)) return -1;
+    const int d = L->hidden, k = L->topk;
+    const int SI = L->shared_inter, lat = L->latent > 0 ? L->latent : d;
+    const int projected = L->down != NULL;
+    int rc = 0;
+    if (gemmable(c, L))
+        return experts_gemm(c, L, x, T, idx, wt, out, c->contrib, c->gemm_fp8, 1, st);
+    if (c->routed_wait) {
+        if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) return -1;
+        c->routed_wait = NULL;
+    }
+    if (L->expert_fmt == K3G_EXPERT_MXFP4_TILED || L->shared_fmt != 0) {
+        fprintf(stderr, "k3moe: tiled experts need the Kimi-K2 layer shape (no latent "
+                        "projection, bf16 shared expert, widths multiple of 32)\n");
+        return -1;
+    }
+
+    const float *z = x;
+    if (projected) {
+        k3g_stage_begin(c, K3G_ST_LATENT, st);
+        rc |= k3k_dense(wfmt(L->wdt), L->down, NULL, lat, d, x, d, T, c->z, lat, 0.f, 0.f, st);
+        k3g_stage_end(c, K3G_ST_LATENT, st);
+        z = c->z;
+    }
+    rc |= routed_staged(c, L, z, lat, T, idx, c->contrib, st);
     if (SI > 0) {
         k3g_stage_begin(c, K3G_ST_SH_GATEUP, st);
         rc |= k3k_dense(wfmt(L->wdt), L->sh1, L->sh3, SI, d, x, d, T, c->sh_h, SI,
@@ -665,4 +681,70 @@ int k3g_sync(K3gCtx *c, void *stream)
         return e;
     }
     return 0;
+}
+
+/* ------------------------------------------------------ device API, step by step ---- */
+/* The layer's steps one at a time, device pointers on `stream` (NULL: the context's). */
+
+int k3g_dispatch(K3gCtx *c, const int32_t *idx, int T, int topk, int n_experts, int32_t *perm,
+                 int32_t *off, void *stream)
+{
+    if (!c || !idx || !perm || !off || T < 1 || topk < 1 || T > c->max_tokens ||
+        topk > c->topk || n_experts < 1 || n_experts > c->n_experts)
+        return -1;
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    hipSetDevice(c->device);
+    return k3k_dispatch(idx, T * topk, n_experts, c->cnt, c->base, off, c->act, c->nact, perm,
+                        c->err, st);
+}
+
+int k3g_expert_gemv(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
+                    float *contrib, void *stream)
+{
+    if (!c || !L || !x || !idx || !contrib || !fits(c, L, T)) return -1;
+    if (L->expert_fmt == K3G_EXPERT_MXFP4_TILED || L->down ||
+        (L->latent > 0 && L->latent != L->hidden)) {
+        fprintf(stderr, "k3g_expert_gemv: needs checkpoint-layout (or fp32) experts and no "
+                        "latent projection\n");
+        return -1;
+    }
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    hipSetDevice(c->device);
+    return routed_staged(c, L, x, L->hidden, T, idx, contrib, st) ? -1 : 0;
+}
+
+static int grouped(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
+                   float *contrib, int fp8, void *stream)
+{
+    if (!c || !L || !x || !idx || !contrib || !fits(c, L, T)) return -1;
+    if (L->expert_fmt != K3G_EXPERT_MXFP4_TILED || L->down || L->up || L->latent_norm ||
+        (L->latent > 0 && L->latent != L->hidden) || L->hidden % 32 || L->inter % 32) {
+        fprintf(stderr, "k3g_grouped_gemm: needs experts in the tiled MXFP4 layout and no "
+                        "latent projection\n");
+        return -1;
+    }
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    hipSetDevice(c->device);
+    return experts_gemm(c, L, x, T, idx, NULL, NULL, contrib, fp8, 0, st);
+}
+
+int k3g_grouped_gemm_bf16(K3gCtx *c, const K3gLayer *L, const float *x, int T,
+                          const int32_t *idx, float *contrib, void *stream)
+{
+    return grouped(c, L, x, T, idx, contrib, 0, stream);
+}
+
+int k3g_grouped_gemm_f8f6f4(K3gCtx *c, const K3gLayer *L, const float *x, int T,
+                            const int32_t *idx, float *contrib, void *stream)
+{
+    return grouped(c, L, x, T, idx, contrib, 1, stream);
+}
+
+int k3g_combine(K3gCtx *c, const float *contrib, const int32_t *idx, const float *wt, int T,
+                int topk, int n, const float *add, float *out, void *stream)
+{
+    if (!c || !contrib || !idx || !wt || !out || T < 1 || topk < 1 || n < 1) return -1;
+    hipStream_t st = stream ? (hipStream_t)stream : c->stream;
+    hipSetDevice(c->device);
+    return k3k_combine(contrib, idx, wt, T, topk, n, add, out, st);
 }

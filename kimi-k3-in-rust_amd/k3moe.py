@@ -161,6 +161,13 @@ def lib() -> C.CDLL:
         L.k3g_router.restype = i
         L.k3g_moe.argtypes = [vp, C.POINTER(K3gLayer), vp, i, vp, vp, vp, vp]
         L.k3g_moe.restype = i
+        L.k3g_dispatch.argtypes = [vp, vp, i, i, i, vp, vp, vp]
+        L.k3g_dispatch.restype = i
+        for name in ("k3g_expert_gemv", "k3g_grouped_gemm_bf16", "k3g_grouped_gemm_f8f6f4"):
+            getattr(L, name).argtypes = [vp, C.POINTER(K3gLayer), vp, i, vp, vp, vp]
+            getattr(L, name).restype = i
+        L.k3g_combine.argtypes = [vp, vp, vp, vp, i, i, i, vp, vp, vp]
+        L.k3g_combine.restype = i
         L.k3g_sync.argtypes = [vp, vp]
         L.k3g_sync.restype = i
         L.k3s_byte.argtypes = [u64, u64, u64]
@@ -620,6 +627,33 @@ class Ctx:
                               C.c_void_p(idx_ptr), C.c_void_p(wt_ptr), None)
         if rc != 0:
             raise RuntimeError("k3g_router launch failed")
+
+    # the layer's steps one at a time (device pointers, the context's stream)
+    def dispatch(self, idx_ptr: int, T: int, topk: int, n_experts: int, perm_ptr: int,
+                 off_ptr: int) -> None:
+        rc = lib().k3g_dispatch(self.ptr, C.c_void_p(idx_ptr), T, topk, n_experts,
+                                C.c_void_p(perm_ptr), C.c_void_p(off_ptr), None)
+        if rc != 0:
+            raise RuntimeError("k3g_dispatch failed")
+
+    def experts(self, kind: str, layer: K3gLayer, x_ptr: int, T: int, idx_ptr: int,
+                contrib_ptr: int) -> None:
+        """kind: "gemv", "bf16" or "f8f6f4" (k3g_expert_gemv / k3g_grouped_gemm_*)."""
+        fn = {"gemv": lib().k3g_expert_gemv, "bf16": lib().k3g_grouped_gemm_bf16,
+              "f8f6f4": lib().k3g_grouped_gemm_f8f6f4}[kind]
+        rc = fn(self.ptr, C.byref(layer), C.c_void_p(x_ptr), T, C.c_void_p(idx_ptr),
+                C.c_void_p(contrib_ptr), None)
+        if rc != 0:
+            raise RuntimeError(f"expert products ({kind}) failed")
+
+    def combine(self, contrib_ptr: int, idx_ptr: int, wt_ptr: int, T: int, topk: int, n: int,
+                add_ptr, out_ptr: int) -> None:
+        rc = lib().k3g_combine(self.ptr, C.c_void_p(contrib_ptr), C.c_void_p(idx_ptr),
+                               C.c_void_p(wt_ptr), T, topk, n,
+                               C.c_void_p(add_ptr) if add_ptr else None, C.c_void_p(out_ptr),
+                               None)
+        if rc != 0:
+            raise RuntimeError("k3g_combine failed")
 
     def sync(self) -> None:
         rc = lib().k3g_sync(self.ptr, None)

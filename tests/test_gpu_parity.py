@@ -359,6 +359,203 @@ def test_layer_k2_batch(k2_layer):
     assert rel_l2(out, ro) <= REL_L2
 
 
+# ------------------------------------------------------ the layer's steps one at a time ----
+
+SENTINEL = np.uint32(0x7FC0DEAD)   # a NaN the kernels never write
+
+
+def _shape_only_layer(hidden, E, topk, inter):
+    L = k3moe.K3gLayer()
+    L.hidden, L.n_experts, L.topk, L.inter, L.latent = hidden, E, topk, inter, hidden
+    return L
+
+
+def _random_routing(T, E, k, seed, drop=0.05):
+    """k distinct experts per token, skewed towards low ids, a fraction dropped (-1)."""
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, E + 1) ** 0.9
+    p /= p.sum()
+    idx = np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(T)])
+    idx[rng.random((T, k)) < drop] = -1
+    return idx.astype(np.int32)
+
+
+def _dispatch_expected(idx, E):
+    """Stable sort of the pair numbers by expert id, ids < 0 left out."""
+    flat = idx.reshape(-1)
+    keep = np.nonzero(flat >= 0)[0]
+    perm = keep[np.argsort(flat[keep], kind="stable")].astype(np.int32)
+    cnt = np.bincount(flat[keep], minlength=E)
+    off = np.concatenate([[0], np.cumsum(cnt)]).astype(np.int32)
+    return perm, off
+
+
+@pytest.mark.parametrize("T,E,k", [(1, 384, 8), (20, 384, 8), (32, 384, 8), (33, 384, 8),
+                                   (300, 384, 8), (512, 384, 8), (4096, 384, 8), (50, 16, 4)])
+def test_dispatch_is_a_stable_sort(gpu, T, E, k):
+    P = T * k
+    path = "one block" if P <= 256 else "one 1024-thread block" if P <= 4096 else "three passes"
+    say(f"case: k3g_dispatch, {T} tokens x top-{k} over {E} experts ({P} pairs, {path})")
+    ctx = k3moe.Ctx(_shape_only_layer(128, E, k, 128), max_tokens=T)
+    idx = _random_routing(T, E, k, seed=T * 7 + E)
+    perm_e, off_e = _dispatch_expected(idx, E)
+    didx = k3moe.DevBuf.from_array(idx)
+    dperm, doff = k3moe.DevBuf(P * 4), k3moe.DevBuf((E + 1) * 4)
+    ctx.dispatch(didx.ptr, T, k, E, dperm.ptr, doff.ptr)
+    ctx.sync()
+    off = doff.download(np.int32, E + 1)
+    perm = dperm.download(np.int32, P)
+    assert np.array_equal(off, off_e)
+    assert np.array_equal(perm[:off[E]], perm_e)
+    ctx.destroy()
+
+
+def test_dispatch_all_dropped(gpu):
+    say("case: k3g_dispatch, every slot dropped (idx -1)")
+    ctx = k3moe.Ctx(_shape_only_layer(128, 64, 4, 128), max_tokens=8)
+    didx = k3moe.DevBuf.from_array(np.full((8, 4), -1, np.int32))
+    dperm, doff = k3moe.DevBuf(32 * 4), k3moe.DevBuf(65 * 4)
+    ctx.dispatch(didx.ptr, 8, 4, 64, dperm.ptr, doff.ptr)
+    ctx.sync()
+    assert not np.any(doff.download(np.int32, 65))
+    ctx.destroy()
+
+
+@pytest.mark.parametrize("T,k,n,with_add", [(7, 8, 260, True), (3, 4, 7168, False),
+                                            (64, 8, 1024, True)])
+def test_combine_bit_exact(gpu, T, k, n, with_add):
+    say(f"case: k3g_combine, {T} tokens x top-{k}, width {n}, shared add {with_add}")
+    rng = np.random.default_rng(n + T)
+    contrib = rng.standard_normal((T * k, n)).astype(np.float32)
+    idx = _random_routing(T, 64, k, seed=T, drop=0.2)
+    wt = rng.random((T, k)).astype(np.float32)
+    add = rng.standard_normal((T, n)).astype(np.float32) if with_add else None
+    # slot order, multiply and add rounded separately, dropped slots skipped
+    exp = np.zeros((T, n), np.float32)
+    c3 = contrib.reshape(T, k, n)
+    for j in range(k):
+        m = idx[:, j] >= 0
+        exp[m] = exp[m] + wt[m, j:j + 1] * c3[m, j]
+    if with_add:
+        exp = exp + add
+    ctx = k3moe.Ctx(_shape_only_layer(n, 64, k, 128), max_tokens=T)
+    dc, di, dw = (k3moe.DevBuf.from_array(a) for a in (contrib, idx, wt))
+    da = k3moe.DevBuf.from_array(add) if with_add else None
+    dout = k3moe.DevBuf(T * n * 4)
+    ctx.combine(dc.ptr, di.ptr, dw.ptr, T, k, n, da.ptr if da else None, dout.ptr)
+    ctx.sync()
+    out = dout.download(np.float32, T * n).reshape(T, n)
+    assert np.array_equal(out.view(np.uint32), exp.view(np.uint32))
+    ctx.destroy()
+
+
+def _pair_rows(layer, x, idx, pairs, quant=False):
+    """Oracle rows w2 . SwiGLU(w1 . x_t, w3 . x_t) of the given (t, j) pairs; quant: x and
+    h through MXFP8 first (the FP4 x FP8 variant's inputs)."""
+    k, g, s = O.oracle(), layer.geo, layer.shape
+    cap = k3moe.SWIGLU_CAP
+    runs, out = {}, []
+    for t, j in pairs:
+        e = int(idx[t, j])
+        if e not in runs:
+            runs[e] = layer.expert_host(e)
+        r = runs[e]
+        xt = O.quant_mxfp8(x[t]) if quant else np.ascontiguousarray(x[t])
+        gu = np.concatenate([k.matmul_mxfp4(xt, r[g.p1_off:g.s1_off], r[g.s1_off:g.p2_off],
+                                            s.inter),
+                             k.matmul_mxfp4(xt, r[g.p3_off:g.s3_off], r[g.s3_off:g.nbytes],
+                                            s.inter)])
+        h = k.situ(gu.astype(np.float32), cap, cap)
+        if quant:
+            h = O.quant_mxfp8(h)
+        out.append(k.matmul_mxfp4(h, r[g.p2_off:g.s2_off], r[g.s2_off:g.p3_off], s.hidden))
+    return np.stack(out)
+
+
+def _run_experts(layer, kind, x, idx):
+    T, k, d = x.shape[0], layer.shape.topk, layer.shape.hidden
+    L = layer.dev if kind == "gemv" else layer.dev_tiled
+    ctx = k3moe.Ctx(L, max_tokens=T)
+    dx, di = k3moe.DevBuf.from_array(x), k3moe.DevBuf.from_array(idx)
+    dc = k3moe.DevBuf.from_array(np.full((T * k, d), SENTINEL, np.uint32))
+    ctx.experts(kind, L, dx.ptr, T, di.ptr, dc.ptr)
+    ctx.sync()
+    ctx.destroy()
+    return dc.download(np.float32, T * k * d).reshape(T, k, d)
+
+
+@pytest.mark.parametrize("kind,T", [("gemv", 3), ("gemv", 37), ("bf16", 5), ("bf16", 37),
+                                    ("bf16", 200), ("f8f6f4", 37)])
+def test_expert_products_per_pair(gpu, kind, T):
+    say(f"case: routed expert products alone ({kind}), tiny layer, {T} tokens, 10% slots "
+        "dropped: every kept pair's row vs the oracle, dropped rows untouched")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=777, layout="both")
+    x = layer.tokens(T)
+    idx = _random_routing(T, layer.shape.n_experts, layer.shape.topk, seed=T, drop=0.1)
+    rows = _run_experts(layer, kind, x, idx)
+    kept = [(t, j) for t in range(T) for j in range(layer.shape.topk) if idx[t, j] >= 0]
+    dropped = [(t, j) for t in range(T) for j in range(layer.shape.topk) if idx[t, j] < 0]
+    exp = _pair_rows(layer, x, idx, kept, quant=kind == "f8f6f4")
+    got = np.stack([rows[t, j] for t, j in kept])
+    r = rel_l2(got, exp)
+    worst = max(rel_l2(a, b) for a, b in zip(got, exp))
+    say(f"  rel-L2 {r:.3e}, worst row {worst:.3e}")
+    assert r <= (5e-3 if kind == "f8f6f4" else 1e-5)
+    assert worst <= (1e-2 if kind == "f8f6f4" else 1e-4)
+    for t, j in dropped:
+        assert np.all(rows[t, j].view(np.uint32) == SENTINEL)
+
+
+@pytest.mark.parametrize("kind,T", [("gemv", 2), ("bf16", 24)])
+def test_expert_products_k2(k2_layer, kind, T):
+    say(f"case: routed expert products alone ({kind}), K2 layer, {T} tokens, the routing the "
+        "router picks; the first 24 pairs against the oracle")
+    layer = k2_layer
+    x = layer.tokens(T, stream_base=190)
+    _, idx, _ = oracle_tokens(layer, x)
+    idx = idx.astype(np.int32)
+    rows = _run_experts(layer, kind, x, idx)
+    pairs = [(t, j) for t in range(T) for j in range(layer.shape.topk)][:24]
+    exp = _pair_rows(layer, x, idx, pairs)
+    r = rel_l2(np.stack([rows[t, j] for t, j in pairs]), exp)
+    say(f"  rel-L2 {r:.3e}")
+    assert r <= 1e-5
+
+
+def test_steps_compose_to_the_layer(gpu):
+    T = 37
+    say(f"case: router -> grouped bf16 -> combine, plus the shared expert, against k3g_moe "
+        f"and the oracle, tiny layer, {T} tokens")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=4321, layout="tiled")
+    s, k = layer.shape, O.oracle()
+    x = layer.tokens(T)
+    out, idx, wt = run_layer(layer, x, tiled=True)
+    rows = _run_experts(layer, "bf16", x, idx)
+    ctx = k3moe.Ctx(layer.dev_tiled, max_tokens=T)
+    dc, di, dw = (k3moe.DevBuf.from_array(np.ascontiguousarray(a)) for a in
+                  (rows.reshape(T * s.topk, s.hidden), idx, wt))
+    dr = k3moe.DevBuf(T * s.hidden * 4)
+    ctx.combine(dc.ptr, di.ptr, dw.ptr, T, s.topk, s.hidden, None, dr.ptr)
+    ctx.sync()
+    ctx.destroy()
+    routed = dr.download(np.float32, T * s.hidden).reshape(T, s.hidden)
+    pairs = [(t, j) for t in range(T) for j in range(s.topk)]
+    exp = _pair_rows(layer, x, idx, pairs).reshape(T, s.topk, s.hidden)
+    ref = np.zeros((T, s.hidden), np.float32)
+    for j in range(s.topk):
+        ref = ref + wt[:, j:j + 1] * exp[:, j]
+    r_routed = rel_l2(routed, ref)
+    cap = k3moe.SWIGLU_CAP
+    shared = np.stack([
+        k.matmul_bf16(k.situ(np.concatenate([k.matmul_bf16(x[t], layer.sh1, layer.SI),
+                                             k.matmul_bf16(x[t], layer.sh3, layer.SI)]),
+                             cap, cap), layer.sh2, s.hidden) for t in range(T)])
+    r_layer = rel_l2(routed + shared, out)
+    say(f"  routed sum vs oracle {r_routed:.3e}; + shared expert vs k3g_moe {r_layer:.3e}")
+    assert r_routed <= 1e-5
+    assert r_layer <= 1e-5
+
+
 # --------------------------------------------------------------------- drop-in ABI ----
 
 def _moe_json_weights():
