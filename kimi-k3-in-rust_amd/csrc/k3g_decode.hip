@@ -911,24 +911,53 @@ struct K3Dec {
         const K3Rsrc rc = k3d_rsrc(a.contrib, (size_t)G.P * G.KSDN * a.d * 4);
         const K3Rsrc rs = k3d_rsrc(a.shpart, (size_t)(G.KSD > 0 ? G.KSD : 1) * a.T * a.d * 4);
         for (int t = 0; t < a.T; ++t) {
+            /* every load is issued before any is used: lane j < k holds slot j's routing,
+             * then the slices of 8 slots (and the shared expert's) are read at once */
+            int ev = -1;
+            float wv = 0.0f;
+            if (lane < a.k) {
+                ev = __hip_atomic_load(&a.idx[t * a.k + lane], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                wv = __hip_atomic_load(&a.wt[t * a.k + lane], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+            float sh[K3G_KS_SD];
+#pragma unroll
+            for (int q = 0; q < K3G_KS_SD; ++q)
+                sh[q] = __uint_as_float(k3d_b32<K3_BPOL>(
+                    rs, a.SI > 0 && q < G.KSD ? ((q * a.T + t) * a.d + row) * 4 : K3_OOB));
             float c = 0.0f;
-            for (int j = 0; j < a.k; ++j) {
-                const int p = t * a.k + j;
-                const int e = k3d_uniform(__hip_atomic_load(&a.idx[p], __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_AGENT));
-                if (e < 0 || e >= a.E) continue;
-                const float w = __hip_atomic_load(&a.wt[p], __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-                float y = 0.0f;
-                for (int q = 0; q < G.KSDN; ++q)
-                    y += __uint_as_float(k3d_b32<K3_BPOL>(rc, ((p * G.KSDN + q) * a.d + row) * 4));
-                c = __fadd_rn(c, __fmul_rn(w, y));
+            for (int j0 = 0; j0 < a.k; j0 += 8) {
+                float y[8][K3G_KS_D];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+                    for (int q = 0; q < K3G_KS_D; ++q) {
+                        const int p = t * a.k + j0 + jj;
+                        y[jj][q] = __uint_as_float(k3d_b32<K3_BPOL>(
+                            rc, j0 + jj < a.k && q < G.KSDN ? ((p * G.KSDN + q) * a.d + row) * 4
+                                                            : K3_OOB));
+                    }
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int j = j0 + jj;
+                    if (j >= a.k) break;
+                    const int e = __builtin_amdgcn_readlane(ev, j);
+                    if (e < 0 || e >= a.E) continue;
+                    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), j));
+                    float yy = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < K3G_KS_D; ++q)
+                        if (q < G.KSDN) yy += y[jj][q];
+                    c = __fadd_rn(c, __fmul_rn(w, yy));
+                }
             }
             if (a.SI > 0) {
-                float sh = 0.0f;
-                for (int q = 0; q < G.KSD; ++q)
-                    sh += __uint_as_float(k3d_b32<K3_BPOL>(rs, ((q * a.T + t) * a.d + row) * 4));
-                c = __fadd_rn(c, sh);
+                float s2 = 0.0f;
+#pragma unroll
+                for (int q = 0; q < K3G_KS_SD; ++q)
+                    if (q < G.KSD) s2 += sh[q];
+                c = __fadd_rn(c, s2);
             }
             if (lane < 32) a.out[(size_t)t * a.d + row] = c;
         }
