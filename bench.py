@@ -10,8 +10,9 @@ stream different experts and different shared/router weights, as a decode pass o
 stack of layers does, instead of re-reading what the 256 MB last-level cache holds.
 
 Prints one JSON line. value = tokens/s (1 token per step); ms_per_step is the layer
-latency per token. roofline: the dominant kernel (the fused decode kernel) timed with HIP
-events on the stream it runs on, against HBM peak. prefill: a 4096-token prefill of the
+latency per token. roofline: the dominant kernel (the fused decode kernel), timed with HIP
+events bracketing the timed region on the stream it runs on (every step is one launch, so
+the average includes the gap between back-to-back launches), against HBM peak. prefill: a 4096-token prefill of the
 same layer with Zipf(0.8) expert popularity (tokens/s, fraction of the bf16 MFMA peak,
 its own roofline entry for the dominant GEMM). cpu_baseline: the engine's own CPU
 kernels on this host's cores on a bounded sample of the decode workload.
@@ -39,10 +40,10 @@ B_TOKEN = D * 2 + D * 4                    # bf16-valued input, fp32 output
 B_GATEUP_EXPERT = 2 * (I * D // 2 + I * D // 32)   # w1 + w3 of one expert
 
 # HBM bytes per launch of the fused decode kernel on this workload, from two rocprofv3
-# --pmc runs (FETCH_SIZE x 1.9997 + WRITE_SIZE x 1.0, the factors that make a 256 MiB
+# --pmc runs (FETCH_SIZE x 1.9994 + WRITE_SIZE x 1.0, the factors that make a 256 MiB
 # device-to-device copy read 256 MiB); the run and the numbers are in
 # profiles/k_decode_fused_k2_decode.md. Re-measured whenever the kernel changes.
-TRAFFIC_FUSED = 304692579
+TRAFFIC_FUSED = 304551848
 
 
 def log(msg):
@@ -422,15 +423,20 @@ def main():
         step(i)
     ctx.sync()
     log(f"bench: timing {a.steps} steps")
+    # HIP events bracket the timed region on the context's stream (every step is one
+    # launch of the fused layer kernel, back to back)
+    region = k3moe.Timer(ctx.stream)
     k3moe.sync()
     t0 = time.perf_counter()
+    region.start()
     for i in range(a.warmup, n_tok):
         step(i)
+    region_ms = region.stop()
     k3moe.sync()
     t1 = time.perf_counter()
     ctx.sync()
-    # kernel times: HIP events around each launch on the context's stream, in a separate
-    # pass over the same steps so the events do not sit in the timed region
+    # per-stage times: HIP events around each stage on the context's stream, in a separate
+    # pass over the same steps so those events do not sit in the timed region
     ctx.profile(True)
     for i in range(a.warmup, n_tok):
         step(i)
@@ -449,7 +455,7 @@ def main():
                 for s in range(len(names)) if n_stage[s]}
     if n_stage[8]:
         kern = "k_decode_fused (whole layer: router, top-k, shared + routed MXFP4 GEMVs, combine)"
-        k_us = 1e3 * ms_stage[8] / n_stage[8]
+        k_us = 1e3 * region_ms / a.steps
         k_bytes = layer_bytes
         traffic = TRAFFIC_FUSED
     else:
