@@ -31,9 +31,11 @@
  *      G   routed gate/up of one (token, slot) pair: 32 rows x a K slice of 512-column
  *          quads; the last slice of a tile sums, activates and writes h's FP8 pieces
  *      SD  shared down: 32 rows x a K slice, partial sums per slice
- *      D   routed down of one pair: 32 output rows, all of K; waits for that pair's h
- *      C   combine, 256 output rows: slots in the engine's order (float multiply,
- *          then add), then + the shared output (its slices summed in slice order)
+ *      D   routed down of one pair: 32 output rows x a K slice of 512-column quads;
+ *          waits for that pair's h. The last arrival of an output tile (over every
+ *          pair's slices and the shared expert's) combines it: slots in the engine's
+ *          order (float multiply, then add), then + the shared output (its slices
+ *          summed in slice order)
  *
  *    The shared expert needs no routing, so SG streams while the router and top-k run.
  *
@@ -66,7 +68,6 @@ typedef unsigned int k3v4u __attribute__((ext_vector_type(4)));
 #define K3G_BQ 8448       /* FP8 B quad: 4 x 2 KB chunks + 256 B of scales */
 #define NPC8 6            /* FP8 pieces per value */
 #define NPC16 3           /* bf16 pieces per value */
-#define C_ROWS 256        /* combine rows per ticket: 64 lanes x 4 */
 
 #define SY_LINE 32        /* ints per counter line (128 bytes) */
 #define NSUB 16           /* sub-counters per ticket class with many signalers */
