@@ -349,6 +349,44 @@ def test_layer_k2_grouped_gemm(k2_layer, T, xkind):
     assert r <= 1e-5
 
 
+@pytest.mark.parametrize("shape,T,nsample", [("K2_BATCH", 64, 6), ("K2_PREFILL", 4096, 6)])
+def test_layer_k2_skewed_full_size(gpu, shape, T, nsample):
+    """The batched-decode (64 tokens, Zipf(1.1)) and prefill (4096 tokens, Zipf(0.8))
+    workloads at full size: routing bit-exact for a sample of tokens, sampled output rows
+    against the oracle, and the size-independent property that a token's output does not
+    depend on where it sits in the batch (the same tokens reversed give the same bits)."""
+    say(f"case: k3g_moe {shape} ({T} tokens, skewed routing, grouped bf16 GEMMs): sampled "
+        f"rows vs the oracle, reversed batch bit-identical")
+    layer = k3moe.SynthLayer(getattr(k3moe, shape), seed=2024, layout="tiled")
+    s = layer.shape
+    x = layer.tokens(T, stream_base=500)
+    ctx = k3moe.Ctx(layer.dev_tiled, max_tokens=T)
+    out, idx, wt = run_layer(layer, x, ctx=ctx, tiled=True)
+    out_r, idx_r, _ = run_layer(layer, np.ascontiguousarray(x[::-1]), ctx=ctx, tiled=True)
+    ctx.destroy()
+    assert np.array_equal(out_r[::-1].view(np.uint32), out.view(np.uint32))
+    assert np.array_equal(idx_r[::-1], idx)
+    counts = np.bincount(idx.reshape(-1), minlength=s.n_experts)
+    say(f"  experts used {int((counts > 0).sum())}, most popular {int(counts.max())} pairs")
+    rng = np.random.default_rng(T)
+    rt = np.unique(np.concatenate([[0, T - 1], rng.choice(T, size=min(T, 64), replace=False)]))
+    k = O.oracle()
+    for t in rt:
+        oi, ow = k.router(x[t], layer.gate, layer.bias, s.n_experts, s.topk, s.renorm,
+                          s.routed_scale)
+        assert np.array_equal(idx[t], oi), t
+        np.testing.assert_allclose(wt[t], ow, rtol=1e-6, atol=0)
+    # sampled rows: one token of the most popular expert among them
+    hot = int(np.argmax(counts))
+    t_hot = int(np.nonzero((idx == hot).any(axis=1))[0][0])
+    st = np.unique(np.concatenate([[0, T - 1, t_hot], rng.choice(T, size=nsample, replace=False)]))
+    ro, ri, _ = oracle_tokens(layer, x[st])
+    assert np.array_equal(idx[st], ri)
+    r = rel_l2(out[st], ro)
+    say(f"  {len(st)} sampled rows: rel-L2 {r:.3e}")
+    assert r <= 1e-5
+
+
 def test_layer_k2_batch(k2_layer):
     say("case: k3g_moe K2 layer, 12 tokens in one call")
     layer = k2_layer
