@@ -1025,14 +1025,17 @@ extern "C" int k3k_decode_fused(const K3kDecode *a, hipStream_t st)
         !a->sync || !a->sync_clear ||
         (size_t)a->sync_words * 4 < k3k_decode_sync_bytes(a->T, a->d, a->E, a->k, a->I, a->SI))
         return -1;
-    static int grid[5] = {0, 0, 0, 0, 0};
+    /* the co-resident grid, per device and token-count instance, found once */
+    static int grids[16][5];
     const int NT = a->T <= 1 ? 1 : a->T <= 2 ? 2 : 4;
     const void *fn = NT == 1 ? (const void *)k_decode_fused<1>
                    : NT == 2 ? (const void *)k_decode_fused<2> : (const void *)k_decode_fused<4>;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 16) return -1;
+    int *grid = grids[dev];
     if (!grid[NT]) {
-        int dev = 0, cus = 0, per = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        int cus = 0, per = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, fn, 256, 0) != hipSuccess)
             return -1;
         if (per < 1) per = 1;
