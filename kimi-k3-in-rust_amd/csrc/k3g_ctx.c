@@ -327,9 +327,8 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     const int d128 = r128(d), I128 = r128(c->inter), SI128 = r128(c->shared_inter);
     int rc = 0;
     k3g_stage_begin(c, K3G_ST_DISPATCH, st);
-    rc |= k3k_dispatch(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm, c->err,
-                       st);
-    rc |= k3k_gemm_tiles(c->off, E, c->tiles, c->ntiles, c->xflag, st);
+    rc |= k3k_dispatch_tiles(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm,
+                             c->err, c->tiles, c->ntiles, c->xflag, st);
     k3g_stage_end(c, K3G_ST_DISPATCH, st);
     const int d512 = r512(d), I512 = r512(c->inter);
     k3g_stage_begin(c, K3G_ST_PIECES, st);

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #define K3G_WAVE 64
+#define K3G_TILE_COLS 128      /* pairs per column tile of the grouped GEMMs */
 
 typedef float k3v2f __attribute__((ext_vector_type(2)));
 
@@ -61,6 +62,80 @@ __device__ __forceinline__ float k3d_bf16lo(uint32_t w) { return __uint_as_float
 __device__ __forceinline__ float k3d_bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
 /* Wave-wide sum, every lane gets the total. */
+/* Exclusive scans, across a block of NW <= 64 waves, of N ints per thread at once: wave
+ * scans by shuffles, the waves' totals scanned by wave 0 through lds[(NW + 1) * N]; tot
+ * receives the block sums. Every thread of the block takes part. */
+template <int N, int NW>
+__device__ __forceinline__ void k3d_block_exscan_n(int (&v)[N], int (&tot)[N], int *lds)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int inc[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) inc[i] = v[i];
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int o = __shfl_up(inc[i], m, K3G_WAVE);
+            if (lane >= m) inc[i] += o;
+        }
+    }
+    if (lane == 63) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) lds[wave * N + i] = inc[i];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const int t = lane < NW ? lds[lane * N + i] : 0;
+            int s = t;
+#pragma unroll
+            for (int m = 1; m < NW; m <<= 1) {
+                const int o = __shfl_up(s, m, K3G_WAVE);
+                if (lane >= m) s += o;
+            }
+            if (lane < NW) lds[lane * N + i] = s - t;
+            if (lane == NW - 1) lds[NW * N + i] = s;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        v[i] = lds[wave * N + i] + inc[i] - v[i];
+        tot[i] = lds[NW * N + i];
+    }
+    __syncthreads();
+}
+
+/* Column tiles of up to K3G_TILE_COLS pairs per expert, largest first: every full tile
+ * (in expert order), then the experts' last partial tiles by their count of 16-column
+ * blocks, 8 down to 1 (in expert order within a count); clears *flag. Called by every
+ * thread of a block of 1024 (thread e < E for expert e, its pair count and first sorted
+ * position); lds holds (16 + 1) * 9 ints. */
+__device__ __forceinline__ void k3d_build_tiles(int e, int E, int cnt, int off_e, int4 *tiles,
+                                                int32_t *ntiles, int32_t *flag, int *lds)
+{
+    if (e >= E) cnt = 0;
+    const int nfull = cnt / K3G_TILE_COLS, rem = cnt - nfull * K3G_TILE_COLS;
+    const int cls = rem ? (rem + 15) / 16 : 0;          /* block count of the last tile */
+    int v[9], tot[9];
+    v[0] = nfull;
+#pragma unroll
+    for (int j = 1; j < 9; ++j) v[j] = cls == 9 - j;
+    k3d_block_exscan_n<9, 16>(v, tot, lds);
+    for (int i = 0; i < nfull; ++i)
+        tiles[v[0] + i] = make_int4(e, off_e + K3G_TILE_COLS * i, K3G_TILE_COLS, 0);
+    int base = tot[0];
+#pragma unroll
+    for (int j = 1; j < 9; ++j) {
+        if (cls == 9 - j)
+            tiles[base + v[j]] = make_int4(e, off_e + K3G_TILE_COLS * nfull, rem, 0);
+        base += tot[j];
+    }
+    if (e == 0) { *ntiles = base; *flag = 0; }
+}
+
 __device__ __forceinline__ float k3d_wave_sum(float v)
 {
 #pragma unroll

@@ -751,48 +751,17 @@ k_gemm_f8(const K3kGemm g)
 }
 
 /* ------------------------------------------------------------------ helpers ------ */
-/* Column tiles of up to 128 pairs per active expert, largest first: the tiles of 8
- * column blocks (every full tile, in expert order), then the last tiles of the experts by
- * their block count, 7 down to 1 (in expert order within a count). Also clears the flag
- * the activation pieces raise. One block of 1024 threads (n_experts <= 1024). */
-__device__ __forceinline__ int gm_block_exscan(int v, int *tmp, int *total)
-{
-    const int e = threadIdx.x;
-    tmp[e] = v;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {
-        const int u = e >= d ? tmp[e - d] : 0;
-        __syncthreads();
-        tmp[e] += u;
-        __syncthreads();
-    }
-    const int inc = tmp[e];
-    *total = tmp[1023];
-    __syncthreads();
-    return inc - v;
-}
-
+/* Column tiles from the expert ranges (k3d_build_tiles). One block of 1024 threads
+ * (n_experts <= 1024). */
+static_assert(GM_COLS == K3G_TILE_COLS, "column tile width");
 __global__ void __launch_bounds__(1024)
 k_gemm_tiles(const int32_t *__restrict__ off, int E, int4 *__restrict__ tiles,
              int32_t *__restrict__ ntiles, int32_t *__restrict__ flag)
 {
-    __shared__ int tmp[1024];
+    __shared__ int red[17 * 9];
     const int e = threadIdx.x;
     const int cnt = e < E ? off[e + 1] - off[e] : 0;
-    const int nfull = cnt / GM_COLS, rem = cnt - nfull * GM_COLS;
-    const int cls = rem ? (rem + 15) / 16 : 0;          /* block count of the last tile */
-    int tot;
-    const int f0 = gm_block_exscan(nfull, tmp, &tot);
-    for (int i = 0; i < nfull; ++i)
-        tiles[f0 + i] = make_int4(e, off[e] + GM_COLS * i, GM_COLS, 0);
-    int base = tot;
-    for (int k = 8; k >= 1; --k) {
-        int n;
-        const int pos = gm_block_exscan(cls == k, tmp, &n);
-        if (cls == k) tiles[base + pos] = make_int4(e, off[e] + GM_COLS * nfull, rem, 0);
-        base += n;
-    }
-    if (e == 0) { *ntiles = base; *flag = 0; }
+    k3d_build_tiles(e, E, cnt, e < E ? off[e] : 0, tiles, ntiles, flag, red);
 }
 
 /* x (fp32 [T][d]) -> two bf16 pieces [2][T][ldb]; raises *flag when any piece 1 is not

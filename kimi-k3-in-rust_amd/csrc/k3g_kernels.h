@@ -168,6 +168,11 @@ size_t k3k_router_part_bytes(void);
 int k3k_dispatch(const int32_t *idx, int P, int E, int32_t *cnt, int32_t *base,
                  int32_t *off, int32_t *act, int32_t *nact, int32_t *perm, int *err,
                  hipStream_t st);
+/* The same, followed by the grouped GEMMs' column tiles (as k3k_gemm_tiles), in one
+ * launch when P <= 4096. */
+int k3k_dispatch_tiles(const int32_t *idx, int P, int E, int32_t *cnt, int32_t *base,
+                       int32_t *off, int32_t *act, int32_t *nact, int32_t *perm, int *err,
+                       int32_t *tiles, int32_t *ntiles, int32_t *flag, hipStream_t st);
 
 /* h = act(W1 z, W3 z) and contrib = W2 h for every active expert's pairs. maxU bounds
  * the number of active experts (min(E, T*k)); maxtok bounds tokens per expert. */

@@ -22,121 +22,82 @@ __device__ __forceinline__ int k3d_key(const int32_t *idx, int p, int P, int E, 
     return k;   /* negative keys (dropped slots) are skipped */
 }
 
-/* Block-wide exclusive scan of one int per thread (256 threads). */
-__device__ __forceinline__ int k3d_block_exscan(int v, int *total)
-{
-    __shared__ int wsum[4];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int inc = v;
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const int o = __shfl_up(inc, m, K3G_WAVE);
-        if (lane >= m) inc += o;
-    }
-    if (lane == 63) wsum[wave] = inc;
-    __syncthreads();
-    int before = 0, all = 0;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        if (w < wave) before += wsum[w];
-        all += wsum[w];
-    }
-    __syncthreads();
-    *total = all;
-    return before + inc - v;
-}
-
-/* Single block, P <= 256: count, scan and scatter in one pass. */
-__global__ void __launch_bounds__(256)
-k_disp_small(const int32_t *idx, int P, int E, int32_t *off, int32_t *act, int32_t *nact,
-             int32_t *perm, int *err)
-{
-    __shared__ int keys[K3G_DCH];
-    __shared__ int tot[K3G_MAX_EXPERTS];
-    const int tid = threadIdx.x;
-    keys[tid] = k3d_key(idx, tid, P, E, err);
-    __syncthreads();
-    const int n = P < K3G_DCH ? P : K3G_DCH;
-    for (int e = tid; e < E; e += 256) {
-        int m = 0;
-        for (int i = 0; i < n; ++i) m += keys[i] == e;
-        tot[e] = m;
-    }
-    __syncthreads();
-    /* each thread owns experts [tid*per, tid*per + per) */
-    const int per = (E + 255) / 256;
-    int s = 0, a = 0;
-    for (int q = 0; q < per; ++q) {
-        const int e = tid * per + q;
-        if (e < E) { s += tot[e]; a += tot[e] > 0; }
-    }
-    int stot, atot;
-    int sb = k3d_block_exscan(s, &stot);
-    int ab = k3d_block_exscan(a, &atot);
-    for (int q = 0; q < per; ++q) {
-        const int e = tid * per + q;
-        if (e < E) {
-            off[e] = sb;
-            if (tot[e] > 0) act[ab++] = e;
-            const int base = sb;
-            sb += tot[e];
-            int pos = base;
-            for (int i = 0; i < n; ++i)
-                if (keys[i] == e) perm[pos++] = i;
-        }
-    }
-    if (tid == 0) { off[E] = stot; *nact = atot; }
-}
-
-/* Single block of 1024 threads, P <= K3G_DONE: the pairs' keys in LDS, one thread per
- * expert counts its pairs, a block scan places the experts, and each expert thread writes
- * its pairs in pair order (stable). One launch instead of three for mid-size batches. */
-#define K3G_DONE 4096
+/* One block of 1024 threads for P <= K3G_DSORT pairs: the pairs, as key << 12 | pair
+ * (key = expert, or E for a dropped slot and for the padding of the last 64-pair chunk),
+ * are sorted by key in LDS with one stable split per key bit: a pair's place is the
+ * zeros (or ones) before its chunk plus those before its lane in the chunk's ballot.
+ * Per-expert counts come from LDS atomics; block scans give the expert ranges and the
+ * active list. */
+#define K3G_DSORT 4096
 __global__ void __launch_bounds__(1024)
-k_disp_one(const int32_t *idx, int P, int E, int32_t *off, int32_t *act, int32_t *nact,
-           int32_t *perm, int *err)
+k_disp_sort(const int32_t *idx, int P, int E, int32_t *off, int32_t *act, int32_t *nact,
+            int32_t *perm, int *err, int4 *tiles, int32_t *ntiles, int32_t *flag)
 {
-    __shared__ __attribute__((aligned(16))) int keys[K3G_DONE];
-    __shared__ int sc[1024], sa[1024];
-    const int e = threadIdx.x;
-    const int P4 = (P + 3) / 4;
-    for (int i = e; i < 4 * P4; i += 1024) keys[i] = k3d_key(idx, i, P, E, err);
+    __shared__ uint32_t kv[2][K3G_DSORT];
+    __shared__ int cnt[K3G_MAX_EXPERTS];
+    __shared__ int zc[K3G_DSORT / 64];
+    __shared__ int red[17 * 9];
+    __shared__ int ztot;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int nch = (P + 63) / 64;
+    cnt[tid] = 0;
     __syncthreads();
-    /* every thread reads the same keys (LDS broadcasts), four at a time */
-    const int4 *k4 = (const int4 *)keys;
-    int tot = 0;
-    if (e < E) {
-#pragma unroll 8
-        for (int i = 0; i < P4; ++i) {
-            const int4 v = k4[i];
-            tot += (v.x == e) + (v.y == e) + (v.z == e) + (v.w == e);
+    for (int i = tid; i < 64 * nch; i += 1024) {
+        int key = E;
+        if (i < P) {
+            const int k = idx[i];
+            if (k >= E) k3d_raise(err, K3G_ERR_EXPERT_RANGE);
+            else if (k >= 0) { key = k; atomicAdd(&cnt[k], 1); }
         }
+        kv[0][i] = ((uint32_t)key << 12) | (uint32_t)i;
     }
-    sc[e] = tot;
-    sa[e] = tot > 0;
     __syncthreads();
-    for (int dd = 1; dd < 1024; dd <<= 1) {
-        const int a = e >= dd ? sc[e - dd] : 0, b = e >= dd ? sa[e - dd] : 0;
-        __syncthreads();
-        sc[e] += a;
-        sa[e] += b;
-        __syncthreads();
-    }
-    if (e < E) {
-        const int first = sc[e] - tot;
-        off[e] = first;
-        if (tot > 0) act[sa[e] - 1] = e;
-        int pos = first;
-#pragma unroll 4
-        for (int i = 0; i < P4 && pos < first + tot; ++i) {
-            const int4 v = k4[i];
-            if (v.x == e) perm[pos++] = 4 * i;
-            if (v.y == e) perm[pos++] = 4 * i + 1;
-            if (v.z == e) perm[pos++] = 4 * i + 2;
-            if (v.w == e) perm[pos++] = 4 * i + 3;
+    const int nb = 32 - __clz(E);               /* bits of the largest key, E */
+    int cur = 0;
+    for (int b = 0; b < nb; ++b) {
+        const uint32_t bit = 1u << (12 + b);
+        for (int c = w; c < nch; c += 16) {
+            const uint64_t m = __ballot(!(kv[cur][64 * c + lane] & bit));
+            if (lane == 0) zc[c] = __popcll(m);
         }
+        __syncthreads();
+        if (w == 0) {
+            const int z = lane < nch ? zc[lane] : 0;
+            int inc = z;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int o = __shfl_up(inc, d, K3G_WAVE);
+                if (lane >= d) inc += o;
+            }
+            if (lane < nch) zc[lane] = inc - z;
+            if (lane == 63) ztot = inc;
+        }
+        __syncthreads();
+        const int Z = ztot;
+        const uint64_t lt = (1ull << lane) - 1;
+        for (int c = w; c < nch; c += 16) {
+            const uint32_t v = kv[cur][64 * c + lane];
+            const bool zero = !(v & bit);
+            const uint64_t m = __ballot(zero);
+            const int zb = zc[c];
+            const int pos = zero ? zb + __popcll(m & lt) : Z + 64 * c - zb + __popcll(~m & lt);
+            kv[cur ^ 1][pos] = v;
+        }
+        __syncthreads();
+        cur ^= 1;
     }
-    if (e == 1023) { off[E] = sc[1023]; *nact = sa[1023]; }
+    /* expert ranges and the active list */
+    const int ce = tid < E ? cnt[tid] : 0;
+    int v[2] = {ce, ce > 0}, tot[2];
+    k3d_block_exscan_n<2, 16>(v, tot, red);
+    if (tid < E) {
+        off[tid] = v[0];
+        if (ce > 0) act[v[1]] = tid;
+    }
+    if (tid == 0) { off[E] = tot[0]; *nact = tot[1]; }
+    /* the pairs of real experts come first, in expert order, each expert's in pair order */
+    for (int i = tid; i < tot[0]; i += 1024) perm[i] = (int32_t)(kv[cur][i] & 4095u);
+    if (tiles) k3d_build_tiles(tid, E, ce, v[0], tiles, ntiles, flag, red);
 }
 
 /* Large P, three passes over chunks of 256 pairs. */
@@ -220,25 +181,32 @@ k_disp_scatter(const int32_t *idx, int P, int E, const int32_t *base, int32_t *p
     }
 }
 
+extern "C" int k3k_dispatch_tiles(const int32_t *idx, int P, int E, int32_t *cnt,
+                                  int32_t *base, int32_t *off, int32_t *act, int32_t *nact,
+                                  int32_t *perm, int *err, int32_t *tiles, int32_t *ntiles,
+                                  int32_t *flag, hipStream_t st)
+{
+    if (E < 1 || E > K3G_MAX_EXPERTS || P < 1) return -1;
+    if (P <= K3G_DSORT) {
+        hipLaunchKernelGGL(k_disp_sort, dim3(1), dim3(1024), 0, st, idx, P, E, off, act, nact,
+                           perm, err, (int4 *)tiles, ntiles, flag);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    const int nch = (P + K3G_DCH - 1) / K3G_DCH;
+    hipLaunchKernelGGL(k_disp_count, dim3(nch), dim3(256), 0, st, idx, P, E, cnt, err);
+    hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, st, cnt, nch, E, base, off, act,
+                       nact);
+    hipLaunchKernelGGL(k_disp_scatter, dim3(nch), dim3(256), 0, st, idx, P, E, base, perm);
+    if (hipGetLastError() != hipSuccess) return -1;
+    return tiles ? k3k_gemm_tiles(off, E, tiles, ntiles, flag, st) : 0;
+}
+
 extern "C" int k3k_dispatch(const int32_t *idx, int P, int E, int32_t *cnt, int32_t *base,
                             int32_t *off, int32_t *act, int32_t *nact, int32_t *perm,
                             int *err, hipStream_t st)
 {
-    if (E < 1 || E > K3G_MAX_EXPERTS || P < 1) return -1;
-    if (P <= K3G_DCH) {
-        hipLaunchKernelGGL(k_disp_small, dim3(1), dim3(256), 0, st, idx, P, E, off, act, nact,
-                           perm, err);
-    } else if (P <= K3G_DONE) {
-        hipLaunchKernelGGL(k_disp_one, dim3(1), dim3(1024), 0, st, idx, P, E, off, act, nact,
-                           perm, err);
-    } else {
-        const int nch = (P + K3G_DCH - 1) / K3G_DCH;
-        hipLaunchKernelGGL(k_disp_count, dim3(nch), dim3(256), 0, st, idx, P, E, cnt, err);
-        hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, st, cnt, nch, E, base, off,
-                           act, nact);
-        hipLaunchKernelGGL(k_disp_scatter, dim3(nch), dim3(256), 0, st, idx, P, E, base, perm);
-    }
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    return k3k_dispatch_tiles(idx, P, E, cnt, base, off, act, nact, perm, err, nullptr,
+                              nullptr, nullptr, st);
 }
 
 /* ---------------------------------------------------------------- combine ---- */
