@@ -269,8 +269,10 @@ void k3g_ctx_set_fp8(K3gCtx *ctx, int on);
  * No reference counterpart. */
 void k3g_ctx_set_trace(K3gCtx *ctx, void *dev_buf);
 
-/* Force the router's exact re-routing path: 0 normal, 1 every token re-routes its
- * candidate set, 2 every token recomputes every expert serially (testing only). */
+/* Force the router's exact re-routing path (testing only): 0 normal, 1 every token
+ * re-routes its candidate set, 2 every token recomputes the engine's float logit of every
+ * expert (from a bounded sum in any order, the serial chain where the bound leaves the
+ * float open), 3 as 2 with the serial chain for every logit. */
 void k3g_ctx_force_exact(K3gCtx *ctx, int mode);
 
 /* Router on the GPU for T tokens: x [T][hidden] fp32 -> idx [T][topk] int32,

@@ -23,7 +23,8 @@ struct K3SelectLds {
     unsigned char taken[K3G_MAX_E];
     int sel[64];
     int cand[K3G_MAX_E];
-    int ncand;
+    int redo[K3G_MAX_E];
+    int ncand, nredo;
     int cert;
     double wsum;
 };
@@ -35,7 +36,10 @@ struct K3SelectLds {
  * lane-strided tree of d products, 2 d + 16 for a chain of fused multiply-adds); the
  * bound is pushed through the float rounding and the sigmoid (monotone) and widened by
  * 4 ulp for a libm expf that differs from a correctly rounded one, then the bias is added
- * (monotone again). */
+ * (monotone again). When acc -/+ B round to the same float, that float is the engine's
+ * float logit and score/choice are the engine's values (with its expf): the interval's
+ * upper end then carries an even bit pattern, otherwise an odd one (moving it up by at
+ * most one ulp, so it stays an upper bound); k3d_settled reads the mark. */
 __device__ __forceinline__ float4 k3d_route_score_n(double acc, double ab, float bias,
                                                      double nround)
 {
@@ -49,7 +53,17 @@ __device__ __forceinline__ float4 k3d_route_score_n(double acc, double ab, float
         slo = nextafterf(slo, -INFINITY);
         shi = nextafterf(shi, INFINITY);
     }
-    return make_float4(__fadd_rn(sc, bias), __fadd_rn(slo, bias), __fadd_rn(shi, bias), sc);
+    float hi = __fadd_rn(shi, bias);
+    const bool settled = (float)(acc - B) == (float)(acc + B);
+    if ((int)(__float_as_uint(hi) & 1u) != (settled ? 0 : 1)) hi = nextafterf(hi, INFINITY);
+    return make_float4(__fadd_rn(sc, bias), __fadd_rn(slo, bias), hi, sc);
+}
+
+/* The mark k3d_route_score_n leaves on an interval's upper end: true when the score and
+ * choice were formed from the engine's own float logit. */
+__device__ __forceinline__ bool k3d_settled(float hi)
+{
+    return __builtin_isfinite(hi) && !(__float_as_uint(hi) & 1u);
 }
 
 __device__ __forceinline__ float4 k3d_route_score(double acc, double ab, float bias, int d)
@@ -155,15 +169,13 @@ __device__ __noinline__ double k3d_serial_dot(const float *w, const float *x, in
     return acc;
 }
 
-/* LDS staging for the exact logits (k3d_exact_dots_staged): two stages of up to
- * K3G_XD_ROWS candidate rows + the token's x, 256 fp32 columns each, then the rows' exact
- * fp64 products of one stage. Rows are skewed by 16 bytes so that the lanes' row reads
- * fall on different banks. */
-#define K3G_XD_ROWS 12
+/* LDS staging for the candidates' logits (k3d_fast_dots_staged): two stages of up to
+ * K3G_XD_ROWS candidate rows + the token's x, 256 fp32 columns each. Rows are skewed by
+ * 16 bytes so that the lanes' row reads fall on different banks. */
+#define K3G_XD_ROWS 6
 #define K3G_XD_ROWB 1040                                  /* 256 fp32 + 16 */
 #define K3G_XD_STAGE ((K3G_XD_ROWS + 1) * K3G_XD_ROWB)
-#define K3G_XD_PROWB 2064                                 /* 256 fp64 + 16 */
-#define K3G_XD_BYTES (2 * K3G_XD_STAGE + K3G_XD_ROWS * K3G_XD_PROWB)
+#define K3G_XD_BYTES (2 * K3G_XD_STAGE)
 
 /* One DMA instruction: 64 lanes x 16 bytes from their own global addresses to 1 KB of LDS
  * at byte address `lds` (lane l at lds + 16 l), M0 saved and restored around it. */
@@ -189,22 +201,23 @@ __device__ __forceinline__ void k3d_wait_vm(int n)
     }
 }
 
-/* The engine's logits of nb <= K3G_XD_ROWS candidate rows (uniform row pointers) against
- * x: lane j < nb returns row j's sum in the engine's serial order, exactly as
- * k3d_serial_dot (fma(w, x, acc) rounds once, and so does acc + the fp64 product, which is
- * exact for fp32 factors). The rows and x stream through LDS by DMA, 256 columns per
- * stage, the next stage in flight; all 64 lanes form a stage's products in fp64, then
- * lane j runs the dependent chain of additions over row j. d must be a multiple of 4 and
- * the rows and x 16-byte aligned. */
-__device__ __forceinline__ double k3d_exact_dots_staged(uint8_t *stage,
-                                                       const float *const (&rows)[K3G_XD_ROWS],
-                                                       int nb, const float *x, int d, int lane)
+/* Logits of nb <= K3G_XD_ROWS candidate rows against x in any summation order, with what
+ * bounds their distance from the engine's serial sums: lane j < nb returns in s row j's
+ * sum of exact fp64 products w_i x_i and in a the sum of their magnitudes. Any two
+ * summation orders of n terms differ by at most 2 gamma_(n-1) sum |w_i x_i|, so when the
+ * float roundings of s -/+ that bound agree, they are the float the engine casts its
+ * serial sum to. The rows and x stream through LDS by DMA, 256 columns per stage with the
+ * next stage in flight; every lane multiplies its 4 columns of each row and keeps the row
+ * sums in registers, and a wave reduction ends the row. d a multiple of 4, rows and x
+ * 16-byte aligned. */
+__device__ __forceinline__ void k3d_fast_dots_staged(uint8_t *stage,
+                                                    const float *const (&rows)[K3G_XD_ROWS],
+                                                    int nb, const float *x, int d, int lane,
+                                                    double &s, double &a)
 {
     const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)stage;
-    uint8_t *prod = stage + 2 * K3G_XD_STAGE;
     const int nch = (d + 255) / 256;
     auto issue = [&](int k) {
-        /* columns past d re-read the row's last 16 bytes: never summed */
         const int col = min(256 * k + 4 * lane, d - 4);
         const uint32_t st = base + (uint32_t)(k & 1) * K3G_XD_STAGE;
 #pragma unroll
@@ -212,7 +225,9 @@ __device__ __forceinline__ double k3d_exact_dots_staged(uint8_t *stage,
             if (j < nb) k3d_dma16(rows[j] + col, st + j * K3G_XD_ROWB);
         k3d_dma16(x + col, st + nb * K3G_XD_ROWB);
     };
-    double acc = 0.0;
+    double rs[K3G_XD_ROWS], ra[K3G_XD_ROWS];
+#pragma unroll
+    for (int j = 0; j < K3G_XD_ROWS; ++j) { rs[j] = 0.0; ra[j] = 0.0; }
     issue(0);
     for (int k = 0; k < nch; ++k) {
         if (k + 1 < nch) {
@@ -222,57 +237,47 @@ __device__ __forceinline__ double k3d_exact_dots_staged(uint8_t *stage,
             k3d_wait_vm(0);
         }
         __builtin_amdgcn_wave_barrier();
-        /* the stage's exact products: lane l takes columns 4 l .. 4 l + 3 of every row */
         const uint8_t *st = stage + (k & 1) * K3G_XD_STAGE;
-        const float4 xv = *(const float4 *)(st + nb * K3G_XD_ROWB + 16 * lane);
-        const double x0 = xv.x, x1 = xv.y, x2 = xv.z, x3 = xv.w;
+        /* columns past d (a re-read of the row's last 16 bytes) are not summed */
+        if (256 * k + 4 * lane < d) {
+            const float4 xv = *(const float4 *)(st + nb * K3G_XD_ROWB + 16 * lane);
 #pragma unroll
-        for (int j = 0; j < K3G_XD_ROWS; ++j) {
-            if (j < nb) {
-                const float4 wv = *(const float4 *)(st + j * K3G_XD_ROWB + 16 * lane);
-                double2 *pr = (double2 *)(prod + j * K3G_XD_PROWB + 32 * lane);
-                pr[0] = make_double2((double)wv.x * x0, (double)wv.y * x1);
-                pr[1] = make_double2((double)wv.z * x2, (double)wv.w * x3);
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        if (lane < nb) {
-            const double2 *pr = (const double2 *)(prod + lane * K3G_XD_PROWB);
-            const int n2 = min(128, (d - 256 * k) / 2);
-            if (n2 == 128) {
-                /* a full stage: groups of 8 double2 with no bounds tests, the next group
-                 * read before this group's additions */
-                double2 a[8], b[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) a[u] = pr[u];
-#pragma unroll
-                for (int i0 = 0; i0 < 128; i0 += 16) {
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) b[u] = pr[i0 + 8 + u];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) { acc += a[u].x; acc += a[u].y; }
-                    if (i0 + 16 < 128) {
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) a[u] = pr[i0 + 16 + u];
-                    }
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) { acc += b[u].x; acc += b[u].y; }
-                }
-            } else {
-                for (int i = 0; i < n2; ++i) {
-                    const double2 v = pr[i];
-                    acc += v.x;
-                    acc += v.y;
+            for (int j = 0; j < K3G_XD_ROWS; ++j) {
+                if (j < nb) {
+                    const float4 wv = *(const float4 *)(st + j * K3G_XD_ROWB + 16 * lane);
+                    const double p0 = (double)wv.x * xv.x, p1 = (double)wv.y * xv.y;
+                    const double p2 = (double)wv.z * xv.z, p3 = (double)wv.w * xv.w;
+                    rs[j] += (p0 + p1) + (p2 + p3);
+                    ra[j] += (fabs(p0) + fabs(p1)) + (fabs(p2) + fabs(p3));
                 }
             }
         }
-        /* every lane is done with this stage and the products before they are rewritten */
+        /* every lane is done with this stage before the next issue refills it */
         __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
     }
-    return acc;
+    s = 0.0;
+    a = 0.0;
+#pragma unroll
+    for (int j = 0; j < K3G_XD_ROWS; ++j) {
+        if (j < nb) {
+            const double vs = k3d_wave_sumd(rs[j]), va = k3d_wave_sumd(ra[j]);
+            if (lane == j) { s = vs; a = va; }
+        }
+    }
+}
+
+/* The float the engine casts its serial fp64 sum to, from a sum s of the same n exact
+ * products in another order and the sum a of their magnitudes: true when the bound
+ * settles it (*f set), false when s lies too close to a float rounding boundary. */
+__device__ __forceinline__ bool k3d_settled_float(double s, double a, int n, float *f)
+{
+    /* 2 gamma_(n-1) a, with a itself a rounded sum (a factor 1.01 covers both), plus the
+     * rounding of s -/+ B */
+    const double B = 2.02 * (double)n * 0x1p-53 * a + fabs(s) * 0x1p-52 + 0x1p-1060;
+    const float lo = (float)(s - B), hi = (float)(s + B);
+    *f = lo;
+    return lo == hi;
 }
 
 /* Selection for token t from rs [T][E] {choice, lo, hi, score} (read at device
@@ -379,41 +384,58 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
         if (lane < k) s->sel[lane] = my_sel;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
+        /* theta: the weakest selected lo (lane j < k holds the j-th selection) */
+        float nth = -INFINITY;
+        if (lane < k) nth = my_sel < 0 ? INFINITY : -s->lo[my_sel];
+        const float theta = -k3d_wave_fmax(nth);
+        /* candidates in expert order, and among them those whose float logit the bound
+         * left open (all when forced), by ballots over the lanes' slots */
+        int nc = 0, nr = 0;
+        const uint64_t lt = (1ull << lane) - 1;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int e = lane + 64 * i;
+            const bool cf = e < E && (force >= 2 || v[i].z >= theta || ((taken >> i) & 1u));
+            const bool rf = cf && (force >= 2 || !k3d_settled(v[i].z));
+            const uint64_t cm = __ballot(cf), rm = __ballot(rf);
+            if (cf) s->cand[nc + __popcll(cm & lt)] = e;
+            if (rf) s->redo[nr + __popcll(rm & lt)] = e;
+            nc += __popcll(cm);
+            nr += __popcll(rm);
+        }
         if (lane == 0) {
-            float theta = INFINITY;
-            for (int j = 0; j < k; ++j) {
-                const int e = s->sel[j];
-                theta = e < 0 ? -INFINITY : fminf(theta, s->lo[e]);
-            }
-            int n = 0;
-            for (int e = 0; e < E; ++e)
-                if (force == 2 || s->hi[e] >= theta || s->taken[e]) s->cand[n++] = e;
-            s->ncand = n;
+            s->ncand = nc;
+            s->nredo = nr;
             if (stats) atomicAdd(&stats[0], 1);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
-        const int nc = s->ncand;
         const float *xt = x + (size_t)t * d;
         const bool staged = stage && d % 4 == 0 && d >= 4 &&
                             ((((uintptr_t)W | (uintptr_t)x) & 15) == 0);
         const int per = staged ? K3G_XD_ROWS : 64;
-        for (int c0 = 0; c0 < nc; c0 += per) {
+        /* the settled candidates' scores and choices are the engine's already; the rest
+         * get the engine's float logit */
+        for (int c0 = 0; c0 < nr; c0 += per) {
             const int c = c0 + lane;
-            double acc = 0.0;
+            double ps = 0.0, pa = 0.0;
             if (staged) {
                 const float *rows[K3G_XD_ROWS];
-                const int nb = min(K3G_XD_ROWS, nc - c0);
+                const int nb = min(K3G_XD_ROWS, nr - c0);
 #pragma unroll
                 for (int j = 0; j < K3G_XD_ROWS; ++j)
                     rows[j] = W + (size_t)__builtin_amdgcn_readfirstlane(
-                                      s->cand[c0 + (j < nb ? j : 0)]) * d;
-                acc = k3d_exact_dots_staged(stage, rows, nb, xt, d, lane);
+                                      s->redo[c0 + (j < nb ? j : 0)]) * d;
+                k3d_fast_dots_staged(stage, rows, nb, xt, d, lane, ps, pa);
             }
-            if (lane < per && c < nc) {
-                const int e = s->cand[c];
-                if (!staged) acc = k3d_serial_dot(W + (size_t)e * d, xt, d);
-                const float sc = k3d_sigmoid((float)acc);
+            if (lane < per && c < nr) {
+                const int e = s->redo[c];
+                /* the engine's float logit: settled by the bound, else its serial chain
+                 * (always the chain when force > 2) */
+                float logit;
+                if (!staged || force > 2 || !k3d_settled_float(ps, pa, d, &logit))
+                    logit = (float)k3d_serial_dot(W + (size_t)e * d, xt, d);
+                const float sc = k3d_sigmoid(logit);
                 s->score[e] = sc;
                 s->choice[e] = __fadd_rn(sc, bias ? bias[e] : 0.0f);
             }

@@ -159,9 +159,12 @@ def k2_layer(gpu):
     yield layer
 
 
-@pytest.mark.parametrize("force", [0, 1, 2])
+@pytest.mark.parametrize("force", [0, 1, 2, 3])
 def test_router_k2_bitexact(k2_layer, force):
-    T = 24 if force < 2 else 2
+    """force 1: every token's candidates through the exact path; 2: every expert's float
+    logit from the bounded any-order sum (the serial chain where it is unsettled); 3: the
+    serial chain for every logit. The exact path's scores, hence weights, are bit-exact."""
+    T = 24 if force < 2 else 3
     say(f"case: k3g_router d=7168 E=384 k=8, {T} tokens, force_exact={force}")
     layer = k2_layer
     x = layer.tokens(T, stream_base=7)
@@ -177,6 +180,8 @@ def test_router_k2_bitexact(k2_layer, force):
         oi, ow = O.oracle().router(x[t], layer.gate, layer.bias, 384, 8, 1, 2.5)
         assert np.array_equal(idx[t], oi), (t, idx[t], oi)
         np.testing.assert_allclose(wt[t], ow, rtol=1e-6, atol=0)
+        if force:
+            assert np.array_equal(wt[t].view(np.uint32), ow.view(np.uint32)), t
     if force:
         assert ctx.stats()[0] >= T
     ctx.destroy()
@@ -284,15 +289,18 @@ def test_layer_k2_decode_one_token(k2_layer, fused):
 
 
 def test_layer_k2_fused_repeat_and_force(k2_layer):
-    say("case: fused K2 decode: 4 tokens in one call, forced re-routing, 5 repeated launches")
+    say("case: fused K2 decode: 4 tokens in one call, 6 repeated launches, the exact "
+        "re-routing forced in modes 1, 2 and 3 on three of them")
     layer = k2_layer
     x = layer.tokens(4, stream_base=60)
-    ro, ri, _ = oracle_tokens(layer, x)
+    ro, ri, rw = oracle_tokens(layer, x)
     ctx = k3moe.Ctx(layer.dev, max_tokens=4)
-    for rep in range(5):
-        out, idx, _ = run_layer(layer, x, ctx=ctx, force=1 if rep == 2 else 0)
+    for rep, force in enumerate([0, 1, 0, 2, 3, 0]):
+        out, idx, wt = run_layer(layer, x, ctx=ctx, force=force)
         assert np.array_equal(idx, ri), rep
         assert rel_l2(out, ro) <= REL_L2, rep
+        if force:
+            assert np.array_equal(wt.view(np.uint32), rw.astype(np.float32).view(np.uint32)), rep
     ctx.destroy()
 
 
