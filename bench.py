@@ -43,7 +43,7 @@ B_GATEUP_EXPERT = 2 * (I * D // 2 + I * D // 32)   # w1 + w3 of one expert
 # --pmc runs (FETCH_SIZE x 1.9994 + WRITE_SIZE x 1.0, the factors that make a 256 MiB
 # device-to-device copy read 256 MiB); the run and the numbers are in
 # profiles/k_decode_fused_k2_decode.md. Re-measured whenever the kernel changes.
-TRAFFIC_FUSED = 304551848
+TRAFFIC_FUSED = 304563580
 
 
 def log(msg):
