@@ -104,13 +104,20 @@ typedef double k3v4d __attribute__((ext_vector_type(4)));
 #endif
 
 #define K3R_PART 11    /* doubles per lane of a slice's partial sums */
+#define K3R_WPB 4      /* waves per workgroup when K is sliced */
 
-__global__ void __launch_bounds__(64)
+/* A 16-expert x 32-token tile, its K cut into S slices of whole 16-column steps: the
+ * workgroups of a tile (G of them, blockDim / 64 waves each, one slice per wave; a wave
+ * past S only adds zeros) first add their waves' sums in LDS, then, when G > 1, meet
+ * through device-coherent partial sums where the last arrival adds them in group order. */
+__global__ void __launch_bounds__(64 * K3R_WPB)
 k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict__ W,
                      const float *__restrict__ bias, int d, int E, float4 *__restrict__ rs,
-                     int S, double *__restrict__ part, int32_t *__restrict__ ctr)
+                     int S, int G, double *__restrict__ part, int32_t *__restrict__ ctr)
 {
-    const int nte = E / 16, ntt = (T + 31) / 32, N = nte * ntt * S;
+    extern __shared__ double k3r_red[];
+    const int wpb = blockDim.x >> 6;
+    const int nte = E / 16, ntt = (T + 31) / 32, N = nte * ntt * G;
     const int per = (N + 7) >> 3;
     /* block b runs on XCD b % 8: give each XCD a contiguous run, so the expert tiles of
      * one token tile (consecutive) share its x rows in one L2 */
@@ -118,21 +125,23 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
     if (slot >= per) return;
     const int lam = xcd * per + slot;
     if (lam >= N) return;
-    const int tl = lam / S, sl = lam - tl * S;
+    const int tl = lam / G, grp = lam - tl * G;
+    const int wv = threadIdx.x >> 6, sl = grp * wpb + wv;
     const int tt = tl / nte, et = tl - tt * nte;
     const int e0 = 16 * et, t0 = 32 * tt;
-    const int L = threadIdx.x, g = L >> 4, r = L & 15;
+    const int L = threadIdx.x & 63, g = L >> 4, r = L & 15;
     const int nsteps = d / 16, spp = (nsteps + S - 1) / S;
     const int s_begin = min(nsteps, sl * spp);
-    const float4 *wp = (const float4 *)(W + (size_t)(e0 + r) * d) + g + 4 * s_begin;
-    const float4 *ap = (const float4 *)(x + (size_t)min(t0 + r, T - 1) * d) + g + 4 * s_begin;
-    const float4 *bp = (const float4 *)(x + (size_t)min(t0 + 16 + r, T - 1) * d) + g + 4 * s_begin;
+    const int s_addr = min(s_begin, nsteps - 1);         /* in the rows even for no steps */
+    const float4 *wp = (const float4 *)(W + (size_t)(e0 + r) * d) + g + 4 * s_addr;
+    const float4 *ap = (const float4 *)(x + (size_t)min(t0 + r, T - 1) * d) + g + 4 * s_addr;
+    const float4 *bp = (const float4 *)(x + (size_t)min(t0 + 16 + r, T - 1) * d) + g + 4 * s_addr;
     const int ns = max(0, min(nsteps, s_begin + spp) - s_begin);
-    float4 wv[K3R_RING], av[K3R_RING], bv[K3R_RING];
+    float4 wq[K3R_RING], av[K3R_RING], bv[K3R_RING];
 #pragma unroll
     for (int u = 0; u < K3R_RING; ++u) {
         const int s = max(0, min(u, ns - 1));
-        wv[u] = wp[4 * s]; av[u] = ap[4 * s]; bv[u] = bp[4 * s];
+        wq[u] = wp[4 * s]; av[u] = ap[4 * s]; bv[u] = bp[4 * s];
     }
     /* two chains per output (even and odd columns of a step), so consecutive MFMAs do
      * not wait for each other's results; they are added at the end */
@@ -142,9 +151,9 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
     for (int s0 = 0; s0 < ns; s0 += K3R_RING) {
 #pragma unroll
         for (int u = 0; u < K3R_RING; ++u) {
-            const float4 w4 = wv[u], a4 = av[u], b4 = bv[u];
+            const float4 w4 = wq[u], a4 = av[u], b4 = bv[u];
             const int sn = max(0, min(s0 + u + K3R_RING, ns - 1));
-            wv[u] = wp[4 * sn]; av[u] = ap[4 * sn]; bv[u] = bp[4 * sn];
+            wq[u] = wp[4 * sn]; av[u] = ap[4 * sn]; bv[u] = bp[4 * sn];
             if (s0 + u < ns) {
                 const double w[4] = {w4.x, w4.y, w4.z, w4.w};
                 const double a[4] = {a4.x, a4.y, a4.z, a4.w};
@@ -168,46 +177,59 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
     acc0 += acc2;
     acc1 += acc3;
     if (S > 1) {
-        /* device-coherent stores of the slice's sums, complete before the count moves (no
-         * cache writeback or invalidate: the data never sits in a non-coherent cache) */
-        double *pp = part + ((size_t)tl * S + sl) * (64 * K3R_PART) + L * K3R_PART;
-        const double mine[K3R_PART] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1],
-                                       acc1[2], acc1[3], ssw, ssa, ssb};
+        double v[K3R_PART] = {acc0[0], acc0[1], acc0[2], acc0[3], acc1[0], acc1[1],
+                              acc1[2], acc1[3], ssw, ssa, ssb};
+        if (wpb > 1) {
+            /* the workgroup's slices, added in slice order by wave 0 */
+            double *mine = k3r_red + ((size_t)wv * 64 + L) * K3R_PART;
 #pragma unroll
-        for (int i = 0; i < K3R_PART; ++i)
-            __hip_atomic_store(pp + i, mine[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        asm volatile("" ::: "memory");
-        int old = 0;
-        /* one count per 128-byte line: counts sharing a line would queue at the L2 */
-        if (L == 0) old = __hip_atomic_fetch_add(&ctr[32 * tl], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (__builtin_amdgcn_readfirstlane(old) != S - 1) return;
-        asm volatile("" ::: "memory");
-        acc0 = k3v4d{0.0, 0.0, 0.0, 0.0};
-        acc1 = k3v4d{0.0, 0.0, 0.0, 0.0};
-        ssw = 0.0; ssa = 0.0; ssb = 0.0;
-        /* every slice's sums (device-coherent loads), four slices in flight at a time,
-         * summed in slice order */
-        for (int q0 = 0; q0 < S; q0 += 4) {
-            double v[4][K3R_PART];
+            for (int i = 0; i < K3R_PART; ++i) mine[i] = v[i];
+            __syncthreads();
+            if (wv != 0) return;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                double *qq =
-                    part + ((size_t)tl * S + min(q0 + u, S - 1)) * (64 * K3R_PART) + L * K3R_PART;
+            for (int i = 0; i < K3R_PART; ++i) v[i] = 0.0;
+            for (int q = 0; q < wpb; ++q) {
+                const double *o = k3r_red + ((size_t)q * 64 + L) * K3R_PART;
 #pragma unroll
-                for (int i = 0; i < K3R_PART; ++i)
-                    v[u][i] = __hip_atomic_load(qq + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (q0 + u < S) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) { acc0[i] += v[u][i]; acc1[i] += v[u][4 + i]; }
-                    ssw += v[u][8]; ssa += v[u][9]; ssb += v[u][10];
-                }
+                for (int i = 0; i < K3R_PART; ++i) v[i] += o[i];
             }
         }
-        if (L == 0) __hip_atomic_store(&ctr[32 * tl], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (G > 1) {
+            /* device-coherent stores of the group's sums, complete before the count moves
+             * (no cache writeback or invalidate: the data never sits in a non-coherent
+             * cache); the last arrival adds the groups' sums in group order */
+            double *pp = part + ((size_t)tl * G + grp) * (64 * K3R_PART) + L * K3R_PART;
+#pragma unroll
+            for (int i = 0; i < K3R_PART; ++i)
+                __hip_atomic_store(pp + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+            asm volatile("" ::: "memory");
+            int old = 0;
+            /* one count per 128-byte line: counts sharing a line would queue at the L2 */
+            if (L == 0) old = __hip_atomic_fetch_add(&ctr[32 * tl], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (__builtin_amdgcn_readfirstlane(old) != G - 1) return;
+            asm volatile("" ::: "memory");
+            double u[K3R_WPB][K3R_PART];
+#pragma unroll
+            for (int q = 0; q < K3R_WPB; ++q) {
+                const double *qq = part + ((size_t)tl * G + min(q, G - 1)) * (64 * K3R_PART) + L * K3R_PART;
+#pragma unroll
+                for (int i = 0; i < K3R_PART; ++i)
+                    u[q][i] = __hip_atomic_load(qq + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int i = 0; i < K3R_PART; ++i) v[i] = 0.0;
+#pragma unroll
+            for (int q = 0; q < K3R_WPB; ++q)
+                if (q < G) {
+#pragma unroll
+                    for (int i = 0; i < K3R_PART; ++i) v[i] += u[q][i];
+                }
+            if (L == 0) __hip_atomic_store(&ctr[32 * tl], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { acc0[i] = v[i]; acc1[i] = v[4 + i]; }
+        ssw = v[8]; ssa = v[9]; ssb = v[10];
     }
     /* norms: sum the four column groups; lane L then holds expert e0 + L % 16 and tokens
      * t0 + L % 16, t0 + 16 + L % 16 */
@@ -248,11 +270,11 @@ k_router_select(const float4 *__restrict__ rs, const float *__restrict__ bias,
 }
 
 /* K slices for the matrix-core logits when the tiles are few: about K3R_WAVES waves, at
- * most K3R_MAXS slices per tile (the last wave's sum of the slices grows with their
- * count: at 64 tokens 8 slices measured 40 us, 4 53 us, 16 46 us, 32 89 us) */
-#define K3R_WAVES 512
-#define K3R_MAXS 8
-extern "C" size_t k3k_router_part_bytes(void) { return (size_t)2 * K3R_WAVES * 64 * K3R_PART * 8; }
+ * most K3R_MAXS slices per tile; tiles x groups stays below K3R_WAVES (groups' sums in
+ * memory: tiles < 512 and groups <= slices / 4 + 1 <= 1024 / (4 tiles) + 1) */
+#define K3R_WAVES 1024
+#define K3R_MAXS 16
+extern "C" size_t k3k_router_part_bytes(void) { return (size_t)K3R_WAVES * 64 * K3R_PART * 8; }
 
 static int router_slices(int N)
 {
@@ -281,9 +303,15 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
         S = (nsteps + spp - 1) / spp;
     }
     if (mfma_ok && (S > 1 || T >= K3R_MFMA_MIN_T)) {
-        const long long N = N1 * S;
-        hipLaunchKernelGGL(k_router_logits_mfma, dim3((unsigned)(8 * ((N + 7) / 8))), dim3(64),
-                           0, st, x, T, W, bias, d, E, (float4 *)rs, S, part, ctr);
+        /* slices as the waves of a workgroup (summed in LDS), workgroups of a tile summed
+         * through memory */
+        const int wpb = S < K3R_WPB ? S : K3R_WPB, G = (S + wpb - 1) / wpb;
+        const long long N = N1 * G;
+        if (G > 1 && N > K3R_WAVES) return -1;     /* the groups' sums would not fit */
+        const size_t lds = wpb > 1 ? (size_t)wpb * 64 * K3R_PART * sizeof(double) : 0;
+        hipLaunchKernelGGL(k_router_logits_mfma, dim3((unsigned)(8 * ((N + 7) / 8))),
+                           dim3(64 * wpb), lds, st, x, T, W, bias, d, E, (float4 *)rs, S, G,
+                           part, ctr);
     } else if (T >= 4) {
         hipLaunchKernelGGL(k_router_logits<4>, dim3(E, (T + 3) / 4), dim3(64), 0, st,
                            x, T, W, bias, d, vec, (float4 *)rs, E);
