@@ -1,5 +1,6 @@
 /* k3_oracle.c - CPU restatement of the engine's MoE arithmetic. TEST INFRASTRUCTURE:
- * the checker for the GPU path, never part of it. Build with -ffp-contract=off.
+ * the reference the GPU path is tested against, never part of it. Build with
+ * -ffp-contract=off.
  *
  * Pinned by (tests/test_oracle.py):
  *   ork3_mxfp4_dequant  tests/fixtures/mxfp4.json (real checkpoint bytes, exact), the

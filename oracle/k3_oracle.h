@@ -1,6 +1,6 @@
 /* k3_oracle.h - CPU restatement of the engine's routed-expert MoE arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY. This is the checker the GPU path is compared against. Only
+ * TEST INFRASTRUCTURE ONLY. This is what the GPU path is compared against. Only
  * tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg may load it; the
  * product library never links it and never falls back to it.
  *

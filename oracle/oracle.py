@@ -3,7 +3,8 @@ engine's own compiled kernels (_ref/libk3ref.so, built from the reference source
 they are present).
 
 TEST INFRASTRUCTURE: only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg
-use this module, and only as the checker or the CPU baseline, never as the product.
+use this module, and only as the reference of a test or the CPU baseline, never as the
+product.
 """
 from __future__ import annotations
 

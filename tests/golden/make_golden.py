@@ -1,7 +1,7 @@
 """Writes the golden fixtures under tests/golden/ from the reference's own test data.
 
-Run in a container that has the reference checkout (default /root/reference); the GPU box
-and the tests only read the .npz / .json files this writes. Inputs are data files the
+Run where the reference checkout is (default /root/reference); the tests, on any machine,
+only read the .npz / .json files this writes. Inputs are data files the
 reference's tests hold:
 
   tests/fixtures/ops/router.json    k3_router golden (test_ops.c:350-401)
