@@ -386,8 +386,8 @@ def main():
                          "point for rocprofv3 --pmc runs), outside the timed region")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (this build runs "
-              f"the layer on a single MI355X; sharding across GPUs is design-only)",
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the layer runs "
+              f"on a single MI355X; sharding across GPUs is design-only)",
               file=sys.stderr)
         sys.exit(2)
 

@@ -61,7 +61,7 @@ int k3gc_bank_create_ex(K3gcBank **out, int n_layers, int n_experts, int hidden,
     b->inter = inter;
     b->layout = layout;
     b->expert_bytes = eb;
-    /* one allocation per layer: pinned while the driver grants it (a box may cap pinned
+    /* one allocation per layer: pinned while the driver grants it (a machine may cap pinned
      * memory well below the bank's size) and max_pinned_layers allows (< 0: no limit),
      * pageable beyond that. The staging buffers the pageable layers' misses go through
      * are taken first, so the pinned layers cannot use up what they need. */
