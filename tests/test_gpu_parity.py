@@ -203,6 +203,37 @@ def test_router_ties_and_degenerate(gpu):
     np.testing.assert_array_equal(w, ow)
 
 
+@pytest.mark.parametrize("T,force", [(3, 0), (24, 0), (24, 1), (600, 0)])
+def test_router_k3_shape(gpu, T, force):
+    """The real K3 router shape: 896 experts (14 per lane in the selection), top-16,
+    d = 7168, routed scale 1.0; the per-expert kernel (3 tokens), the sliced matrix-core
+    logits (24), the forced exact re-routing and the unsliced matrix-core logits (600)."""
+    E, d, k = 896, 7168, 16
+    say(f"case: k3g_router K3 shape E={E} k={k} d={d}, {T} tokens, force_exact={force}")
+    W = np.ascontiguousarray(k3moe.host_normal(E * d, 11, 501, 0, 0.02).reshape(E, d))
+    bias = k3moe.host_normal(E, 11, 502, 0, 0.01)
+    x = np.ascontiguousarray(k3moe.host_normal(T * d, 11, 503, 0, 1.0).reshape(T, d))
+    L = k3moe.K3gLayer()
+    L.hidden, L.n_experts, L.topk, L.inter, L.latent = d, E, k, 128, d
+    L.renorm, L.routed_scale = 1, 1.0
+    dW, db, dx = (k3moe.DevBuf.from_array(a) for a in (W, bias, x))
+    L.gate, L.bias = dW.ptr, db.ptr
+    ctx = k3moe.Ctx(L, max_tokens=T)
+    ctx.force_exact(force)
+    didx, dwt = k3moe.DevBuf(T * k * 4), k3moe.DevBuf(T * k * 4)
+    ctx.router(L, dx.ptr, T, didx.ptr, dwt.ptr)
+    ctx.sync()
+    idx = didx.download(np.int32, T * k).reshape(T, k)
+    wt = dwt.download(np.float32, T * k).reshape(T, k)
+    for t in (range(T) if T <= 24 else np.random.default_rng(T).choice(T, 24, replace=False)):
+        oi, ow = O.oracle().router(x[t], W, bias, E, k, 1, 1.0)
+        assert np.array_equal(idx[t], oi), (t, idx[t], oi)
+        np.testing.assert_allclose(wt[t], ow, rtol=1e-6, atol=0)
+        if force:
+            assert np.array_equal(wt[t].view(np.uint32), ow.view(np.uint32)), t
+    ctx.destroy()
+
+
 # ------------------------------------------------------------------- tiled layouts ----
 
 def _tile_mxfp4_host(packed, scales, rows, cols):
