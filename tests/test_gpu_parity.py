@@ -700,6 +700,61 @@ def test_dropin_k3_moe_host_source(gpu, prefill, T):
         assert np.all(idx == -7), "batched prefill must leave idx/wt untouched"
 
 
+def test_dropin_k3_shape_latent_moe(gpu):
+    """The real K3 LatentMoE shape through the drop-in k3_moe: d 7168, 896 MXFP4 experts
+    top-16 at latent width 3584 (I 3072), bf16 latent down/up projections, RMSNorm of the
+    aggregate, two shared experts fused (6144), SiTU(4, 25), routed scale 1.0; synthetic
+    seeded weights, experts from a host source; against the oracle's k3_moe."""
+    T = 2
+    d, E, k, Lw, I, SI = 7168, 896, 16, 3584, 3072, 6144
+    say(f"case: k3_moe K3 shape (d={d}, E={E}, top-{k}, latent {Lw}, I={I}, shared {SI}, "
+        f"SiTU 4/25, latent RMSNorm), {T} tokens, host expert source")
+    shape = k3moe.Shape("K3 latent experts", Lw, E, k, I, n_shared=2, routed_scale=1.0,
+                        x_bf16=False)
+    experts = k3moe.SynthLayer(shape, seed=31, device=False)
+    gate = np.ascontiguousarray(k3moe.host_normal(E * d, 31, 601, 0.0, 0.02))
+    bias = k3moe.host_normal(E, 31, 602, 0.0, 0.01)
+    lnorm = k3moe.host_normal(Lw, 31, 603, 1.0, 0.1)
+    bf = lambda n, s: k3moe.bf16_bits(k3moe.host_normal(n, 31, s, 0.0, 0.02, bf16=True))  # noqa: E731
+    down, up = bf(Lw * d, 604), bf(d * Lw, 605)
+    sh1, sh3, sh2 = bf(SI * d, 606), bf(SI * d, 607), bf(d * SI, 608)
+    x = np.ascontiguousarray(k3moe.host_normal(T * d, 31, 609, 0.0, 1.0).reshape(T, d))
+    kk = O.oracle()
+    used = sorted({int(e) for t in range(T)
+                   for e in kk.router(x[t], gate, bias, E, k, 1, 1.0)[0]})
+    runs = {(0, e): experts.expert_host(e) for e in used}
+
+    def weights():
+        src = O.MemSrc(runs, 1, E, experts.geo)
+        w = k3moe.K3MoeW()
+        w.gate, w.bias, w.latent_norm = gate.ctypes.data, bias.ctypes.data, lnorm.ctypes.data
+        w.down, w.up = down.ctypes.data, up.ctypes.data
+        w.sh1, w.sh3, w.sh2 = sh1.ctypes.data, sh3.ctypes.data, sh2.ctypes.data
+        w.wdt = k3moe.K3_WBF16
+        w.src, w.layer = src.ptr, 0
+        return w, src
+
+    cfg = k3moe.K3Cfg()
+    cfg.hidden, cfg.latent, cfg.moe_inter = d, Lw, I
+    cfg.n_experts, cfg.topk, cfg.n_shared = E, k, 2
+    cfg.routed_scale, cfg.moe_renorm, cfg.latent_norm = 1.0, 1, 1
+    cfg.rms_eps, cfg.situ_b1, cfg.situ_b2, cfg.n_layers = 1e-6, 4.0, 25.0, 1
+    w, src = weights()
+    out = np.zeros_like(x)
+    idx = np.zeros(k, np.int32)
+    wt = np.zeros(k, np.float32)
+    k3moe.lib().k3_moe(out.ctypes.data, x.ctypes.data, C.byref(w), C.byref(cfg), T,
+                       idx.ctypes.data, wt.ctypes.data, None)
+    k3moe.lib().k3moe_forget_weights()
+    w2, src2 = weights()
+    oo, oi, ow = kk.moe(w2, cfg, x)
+    r = rel_l2(out, oo)
+    say(f"  rel-L2 {r:.3e}, {len(used)} experts")
+    assert np.array_equal(idx, oi)
+    np.testing.assert_allclose(wt, ow, rtol=1e-6)
+    assert r <= REL_L2
+
+
 def test_dropin_expert_drop(gpu):
     say("case: k3_moe with a source that fails one expert: drop counted, slot skipped")
     layer = k3moe.SynthLayer(k3moe.TINY, seed=5, device=False)
