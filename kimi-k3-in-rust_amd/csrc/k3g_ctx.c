@@ -417,6 +417,12 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         g.hq = c->hq8b;
         g.hs = c->hq8b + (size_t)P * I512;
         g.ldhq = I512;
+    } else {
+        /* h leaves gate/up as bf16 plus its MXFP8 remainder */
+        g.hmix = 1;
+        g.hq = c->hq8b;
+        g.hs = c->hq8b + (size_t)P * I512;
+        g.ldhq = I512;
     }
     k3g_stage_begin(c, K3G_ST_GATEUP, st);
     g.trace = fp8 ? NULL : c->trace;
@@ -443,6 +449,10 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         g.ldb = I512;
         g.hq = NULL;
         g.hs = NULL;
+    } else {
+        g.npieces = 1;
+        g.bq = c->hq8b;
+        g.bs = c->hq8b + (size_t)P * I512;
     }
     k3g_stage_begin(c, K3G_ST_DOWN, st);
     rc |= fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);

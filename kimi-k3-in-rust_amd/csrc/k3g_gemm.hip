@@ -169,6 +169,103 @@ __device__ __forceinline__ void gm_wait_vm_n(int n)
     }
 }
 
+/* ============================================================ scaled FP8 MFMA ====== */
+/* Used by the FP4 x FP8 variant and by the remainder piece of h in the bf16 path.
+ * v_mfma_scale_f32_16x16x128_f8f6f4 with cbsz 4 (A: FP4) and blgp 0 (B: FP8 E4M3), each
+ * 32-column block carrying its E8M0 scale. One instruction covers a whole 128-column
+ * step: the tiled MXFP4 chunk is its A operand unchanged (lane L: row L % 16, block
+ * L / 16), and lane 16 q + c of B holds column c's bytes 16 q .. + 15 and 64 + 16 q .. + 15
+ * of the step, with lane 16 g + c giving column c's scale of block g.
+ * LDS per stage: 128 columns x 128 bytes, the 16-byte units stored so each lane's two
+ * units are one logical pair (logical slot 2 q: unit q, 2 q + 1: unit 4 + q), physical
+ * slot = logical ^ ((row / 2) % 8) (conflict-free: 16 lanes of one unit index cover 16
+ * distinct bank groups); then 128 x 4 scale bytes. */
+#define GM_F8_DATA (GM_COLS * GM_KC)
+#define GM_F8_STAGE (GM_F8_DATA + GM_COLS * 4)
+
+__device__ __forceinline__ void gm_dma4(const void *src, uint32_t lds)
+{
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %2\n\t"
+                 "global_load_lds_dword %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(src), "s"(lds) : "memory");
+}
+
+typedef int gm_v8i __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ k3v4f gm_mma_f8(uint4 a, uint32_t sa, const gm_v8i &b, uint32_t sb,
+                                           k3v4f acc)
+{
+    const gm_v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, acc, 4, 0, 0, (int)sa, 0,
+                                                            (int)sb);
+}
+
+/* E8M0 exponent (2^sx) and E4M3 bytes of four values x 2^-sx, nearest-even, clamped to
+ * +-448 first (the OCP MX conversion) */
+__device__ __forceinline__ int gm_mx_exp(float amax)
+{
+    if (!(amax > 0.0f)) return -127;
+    int e;
+    frexpf(amax, &e);
+    const int sx = e - 1 - 8;
+    return sx < -127 ? -127 : (sx > 127 ? 127 : sx);
+}
+
+__device__ __forceinline__ uint32_t gm_e4m3x4(float a, float b, float c, float d, int sx)
+{
+    const float k = ldexpf(1.0f, -sx);
+    a = fminf(fmaxf(a * k, -448.0f), 448.0f);
+    b = fminf(fmaxf(b * k, -448.0f), 448.0f);
+    c = fminf(fmaxf(c * k, -448.0f), 448.0f);
+    d = fminf(fmaxf(d * k, -448.0f), 448.0f);
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+}
+
+/* h = act(gate, up) for the wave's 32 features of one column (this lane's features
+ * 4 g + i and 16 + 4 g + i, g = g4): bf16(h) at o (piece 0, bf16 row at o) and the
+ * remainder h - bf16(h) as one MX block: E4M3 bytes at oq, E8M0 scale at *os. The block
+ * exponent puts the largest remainder in [128, 256), under E4M3's 448, so nothing clamps;
+ * the remainder keeps 4 significant bits, h about 12. */
+__device__ __noinline__ void gm_act_store_mix(k3v4f g0, k3v4f g1, k3v4f u0, k3v4f u1, float b1,
+                                              float b2, uint16_t *o, uint8_t *oq, uint8_t *os,
+                                              int g4)
+{
+    uint16_t hi[8];
+    float rr[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float y0 = k3d_act(g0[i], u0[i], b1, b2), y1 = k3d_act(g1[i], u1[i], b1, b2);
+        hi[i] = gm_bf16_rn(y0);
+        hi[4 + i] = gm_bf16_rn(y1);
+        rr[i] = y0 - gm_bf16_f(hi[i]);
+        rr[4 + i] = y1 - gm_bf16_f(hi[4 + i]);
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(rr[i]));
+    m = fmaxf(m, __shfl_xor(m, 16, K3G_WAVE));
+    m = fmaxf(m, __shfl_xor(m, 32, K3G_WAVE));
+    int sx = -127;
+    if (m > 0.0f) {
+        int e;
+        frexpf(m, &e);
+        sx = e - 8 < -127 ? -127 : (e - 8 > 127 ? 127 : e - 8);
+    }
+    uint2 v0, v1;
+    v0.x = hi[0] | ((uint32_t)hi[1] << 16); v0.y = hi[2] | ((uint32_t)hi[3] << 16);
+    v1.x = hi[4] | ((uint32_t)hi[5] << 16); v1.y = hi[6] | ((uint32_t)hi[7] << 16);
+    *(uint2 *)(o + 4 * g4) = v0;
+    *(uint2 *)(o + 16 + 4 * g4) = v1;
+    *(uint32_t *)(oq + 4 * g4) = gm_e4m3x4(rr[0], rr[1], rr[2], rr[3], sx);
+    *(uint32_t *)(oq + 16 + 4 * g4) = gm_e4m3x4(rr[4], rr[5], rr[6], rr[7], sx);
+    if (g4 == 0) *os = (uint8_t)(sx + 127);
+}
+
 /* Everything one workgroup's tile needs, uniform across the workgroup except the
  * per-lane DMA row offsets. */
 struct GmTile {
@@ -363,9 +460,16 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
         for (int cb = 0; cb < NB; ++cb) {
             const int col = 16 * cb + col0;
             if (col < t.np) {
-                uint16_t *o = g.h + (size_t)(t.p0 + col) * g.ldh + n;
-                gm_act_store(acc[0][cb], acc[2][cb], g.b1, g.b2, o, g.hpiece);
-                gm_act_store(acc[1][cb], acc[3][cb], g.b1, g.b2, o + 16, g.hpiece);
+                const size_t row = (size_t)(t.p0 + col);
+                if (AF == 0 && g.hmix) {
+                    gm_act_store_mix(acc[0][cb], acc[1][cb], acc[2][cb], acc[3][cb], g.b1, g.b2,
+                                     g.h + row * g.ldh + t.orow0, g.hq + row * g.ldhq + t.orow0,
+                                     g.hs + row * (g.ldhq / 32) + t.orow0 / 32, t.g4);
+                } else {
+                    uint16_t *o = g.h + row * g.ldh + n;
+                    gm_act_store(acc[0][cb], acc[2][cb], g.b1, g.b2, o, g.hpiece);
+                    gm_act_store(acc[1][cb], acc[3][cb], g.b1, g.b2, o + 16, g.hpiece);
+                }
             }
         }
     } else {
@@ -379,6 +483,122 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
                 for (int r = 0; r < 4; ++r)
                     if (t.rv[r]) *(k3v4f *)(o + 16 * r) = acc[r][cb];
             }
+        }
+    }
+}
+
+/* The down GEMM of MXFP4 experts with h as bf16 piece 0 (bf16 matrix cores, as gm_tile)
+ * plus its MX remainder (scaled FP8 matrix cores, one 16x16x128 instruction per step
+ * on the same weight registers, at twice the bf16 rate): three quarters of the matrix
+ * time of two bf16 pieces. Stage c % 2: piece 0 (GM_PIECE, gm_tile's layout), then the
+ * remainder's bytes and scales (GM_F8_STAGE, k_gemm_f8's layout). The weight and DMA
+ * pipeline is gm_tile's with two stages: a step waits for all but the 8 weight loads
+ * issued after its stage's DMA. */
+template <int NB>
+__device__ __forceinline__ void gm_tile_mix(const K3kGemm &g, const GmTile &t,
+                                            const uint32_t (&doff)[2], uint32_t soff, int nd,
+                                            int ns)
+{
+    k3v4f acc[4][NB];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int cb = 0; cb < NB; ++cb) acc[r][cb] = k3v4f{0.f, 0.f, 0.f, 0.f};
+    const int lane = t.lane;
+    constexpr uint32_t ST = GM_PIECE + GM_F8_STAGE;
+    auto dma = [&](int c) {
+        const uint32_t st = t.lds + (c & 1) * ST;
+        const uint16_t *b = g.b + (size_t)c * GM_KC;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < t.ndma) gm_dma16(b + t.boff[i], st + t.w * 1024 + i * 8 * 1024);
+        const uint8_t *q = g.bq + (size_t)c * GM_KC;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            if (i < nd) gm_dma16(q + doff[i], st + GM_PIECE + (8 * i + t.w) * 1024);
+        if (t.w < ns) gm_dma4(g.bs + soff + 4 * c, st + GM_PIECE + GM_F8_DATA + t.w * 256);
+    };
+    const uint8_t *brow = t.ldsp + (lane & 15) * 256;
+    const int q4 = lane >> 4, c0 = lane & 15;
+    uint4 ab[3][4];
+    uint32_t sbuf[3][4];
+    auto aload = [&](int c, uint4 (&dst)[4], uint32_t (&sdst)[4]) {
+        const size_t qo = (size_t)(c >> 2) * GM_QT;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint8_t *p = t.abase[r] + qo;
+            dst[r] = gm_ld16(p + 1024 * (c & 3) + 16 * lane);
+            sdst[r] = gm_ld4(p + 4096 + 4 * lane);
+        }
+    };
+    auto step = [&](int c, const uint4 (&cur)[4], const uint32_t (&scl)[4], uint4 (&nxt)[4],
+                    uint32_t (&nsc)[4]) {
+        gm_wait_vm<8>();
+        __syncthreads();
+        dma(min(c + 1, t.nK - 1));
+        aload(min(c + 2, t.nK - 1), nxt, nsc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (c < t.nK) {
+            /* rows outside the matrix read row block 0 and are never stored */
+            const int j = c & 3;
+            const uint32_t so = (c & 1) * ST;
+            /* the remainder first: the weight words then die sub-step by sub-step */
+#pragma unroll
+            for (int cb = 0; cb < NB; ++cb) {
+                const int row = 16 * cb + c0;
+                const int hsw = (row >> 1) & 7;
+                const uint8_t *base = t.ldsp + so + GM_PIECE + row * 128;
+                const uint4 lo = *(const uint4 *)(base + 16 * ((2 * q4) ^ hsw));
+                const uint4 hi = *(const uint4 *)(base + 16 * ((2 * q4 + 1) ^ hsw));
+                const gm_v8i bv = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                                   (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+                const uint32_t sb = t.ldsp[so + GM_PIECE + GM_F8_DATA + row * 4 + q4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[r][cb] = gm_mma_f8(cur[r], (scl[r] >> (8 * j)) & 0xffu, bv, sb, acc[r][cb]);
+                if (cb & 1) __builtin_amdgcn_sched_barrier(0);
+            }
+            float sc[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[r] = gm_scale((scl[r] >> (8 * j)) & 0xffu);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                k3v8bf a[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t wd = s == 0 ? cur[r].x : s == 1 ? cur[r].y
+                                      : s == 2 ? cur[r].z : cur[r].w;
+                    a[r] = gm_deq8(wd, sc[r]);
+                }
+                const int qs = 4 * s + t.g4;
+#pragma unroll
+                for (int cb = 0; cb < NB; ++cb) {
+                    const uint4 bv = *(const uint4 *)(brow + so + cb * 16 * 256 + 16 * (qs ^ c0));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[r][cb] = gm_mma(a[r], bv, acc[r][cb]);
+                }
+            }
+        }
+    };
+    aload(0, ab[0], sbuf[0]);
+    dma(0);
+    aload(min(1, t.nK - 1), ab[1], sbuf[1]);
+    for (int c = 0; c < t.nK; c += 3) {
+        step(c, ab[0], sbuf[0], ab[2], sbuf[2]);
+        step(c + 1, ab[1], sbuf[1], ab[0], sbuf[0]);
+        step(c + 2, ab[2], sbuf[2], ab[1], sbuf[1]);
+    }
+    gm_wait_vm<0>();
+
+#pragma unroll
+    for (int cb = 0; cb < NB; ++cb) {
+        const int col = 16 * cb + c0;
+        if (col < t.np) {
+            const int p = t.p0 + col;
+            float *o = g.out + (size_t)(g.scatter ? g.perm[p] : p) * g.ldo + t.orow0 + 4 * t.g4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (t.rv[r]) *(k3v4f *)(o + 16 * r) = acc[r][cb];
         }
     }
 }
@@ -494,8 +714,41 @@ k_gemm(const K3kGemm g)
     /* instructions whose first row is inside the tile's 16 nb rows */
     t.ndma = min(NI, (4 * nb + WV - 1 - t.w) / WV);
 
+    bool mixed = false;
+    if constexpr (AF == 0 && WV == 8) {
+        if (g.mode == 1 && g.hmix) {
+            /* the remainder's DMA (k_gemm_f8's layout, 128 rows): instruction i of wave w
+             * fills rows 8 (8 i + w) .. + 7; waves 0 and 1 fill the scales of rows 0 .. 63
+             * and 64 .. 127 */
+            mixed = true;
+            uint32_t doff[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = 8 * (8 * i + t.w) + (t.lane >> 3);
+                const int ls = (t.lane & 7) ^ ((r >> 1) & 7);
+                const int u = (ls & 1) ? 4 + (ls >> 1) : (ls >> 1);
+                doff[i] = (uint32_t)gm_src_row(g, t, r) * (uint32_t)g.ldhq + 16 * u;
+            }
+            const int nd = min(2, (2 * nb + 7 - t.w) / 8);
+            const int ns = nb > 4 ? 2 : 1;
+            const uint32_t soff =
+                (uint32_t)gm_src_row(g, t, 64 * min(t.w, 1) + t.lane) * (uint32_t)(g.ldhq / 32);
+            switch (nb) {
+                case 1: gm_tile_mix<1>(g, t, doff, soff, nd, ns); break;
+                case 2: gm_tile_mix<2>(g, t, doff, soff, nd, ns); break;
+                case 3: gm_tile_mix<3>(g, t, doff, soff, nd, ns); break;
+                case 4: gm_tile_mix<4>(g, t, doff, soff, nd, ns); break;
+                case 5: gm_tile_mix<5>(g, t, doff, soff, nd, ns); break;
+                case 6: gm_tile_mix<6>(g, t, doff, soff, nd, ns); break;
+                case 7: gm_tile_mix<7>(g, t, doff, soff, nd, ns); break;
+                case 8: gm_tile_mix<8>(g, t, doff, soff, nd, ns); break;
+                default: break;
+            }
+        }
+    }
 #define GM_CASE(P, B) case (P) * 16 + (B): gm_tile<AF, P, B, WV>(g, t); break;
-    if constexpr (WV == 8) {
+    if (mixed) {
+    } else if constexpr (WV == 8) {
         switch (npr * 16 + nb) {
             GM_CASE(1, 1) GM_CASE(1, 2) GM_CASE(1, 3) GM_CASE(1, 4)
             GM_CASE(1, 5) GM_CASE(1, 6) GM_CASE(1, 7) GM_CASE(1, 8)
@@ -525,61 +778,6 @@ k_gemm(const K3kGemm g)
 }
 
 /* ============================================================ FP4 x FP8 variant ==== */
-/* v_mfma_scale_f32_16x16x128_f8f6f4 with cbsz 4 (A: FP4) and blgp 0 (B: FP8 E4M3), each
- * 32-column block carrying its E8M0 scale. One instruction covers a whole 128-column
- * step: the tiled MXFP4 chunk is its A operand unchanged (lane L: row L % 16, block
- * L / 16), and lane 16 q + c of B holds column c's bytes 16 q .. + 15 and 64 + 16 q .. + 15
- * of the step, with lane 16 g + c giving column c's scale of block g.
- * LDS per stage: 128 columns x 128 bytes, the 16-byte units stored so each lane's two
- * units are one logical pair (logical slot 2 q: unit q, 2 q + 1: unit 4 + q), physical
- * slot = logical ^ ((row / 2) % 8) (conflict-free: 16 lanes of one unit index cover 16
- * distinct bank groups); then 128 x 4 scale bytes. */
-#define GM_F8_DATA (GM_COLS * GM_KC)
-#define GM_F8_STAGE (GM_F8_DATA + GM_COLS * 4)
-
-__device__ __forceinline__ void gm_dma4(const void *src, uint32_t lds)
-{
-    uint32_t keep;
-    asm volatile("s_mov_b32 %0, m0\n\t"
-                 "s_mov_b32 m0, %2\n\t"
-                 "global_load_lds_dword %1, off\n\t"
-                 "s_mov_b32 m0, %0"
-                 : "=&s"(keep) : "v"(src), "s"(lds) : "memory");
-}
-
-typedef int gm_v8i __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ k3v4f gm_mma_f8(uint4 a, uint32_t sa, const gm_v8i &b, uint32_t sb,
-                                           k3v4f acc)
-{
-    const gm_v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, b, acc, 4, 0, 0, (int)sa, 0,
-                                                            (int)sb);
-}
-
-/* E8M0 exponent (2^sx) and E4M3 bytes of four values x 2^-sx, nearest-even, clamped to
- * +-448 first (the OCP MX conversion) */
-__device__ __forceinline__ int gm_mx_exp(float amax)
-{
-    if (!(amax > 0.0f)) return -127;
-    int e;
-    frexpf(amax, &e);
-    const int sx = e - 1 - 8;
-    return sx < -127 ? -127 : (sx > 127 ? 127 : sx);
-}
-
-__device__ __forceinline__ uint32_t gm_e4m3x4(float a, float b, float c, float d, int sx)
-{
-    const float k = ldexpf(1.0f, -sx);
-    a = fminf(fmaxf(a * k, -448.0f), 448.0f);
-    b = fminf(fmaxf(b * k, -448.0f), 448.0f);
-    c = fminf(fmaxf(c * k, -448.0f), 448.0f);
-    d = fminf(fmaxf(d * k, -448.0f), 448.0f);
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
-    return (uint32_t)w;
-}
-
 /* h = act(gate, up) for the wave's 32 features of one column, quantised as one MX block:
  * this lane's 4 + 4 values (features 4 g + i and 16 + 4 g + i) */
 __device__ __noinline__ void gm_act_store_f8(k3v4f g0, k3v4f g1, k3v4f u0, k3v4f u1, float b1,
@@ -914,6 +1112,10 @@ extern "C" int k3k_gemm(const K3kGemm *g, hipStream_t st)
                          g->ldo % 4))
         return -1;
     if (g->afmt == 0 && !g->eq) return -1;
+    if (g->hmix && (g->afmt != 0 || g->ldhq % 512 ||
+                    (g->mode == 0 ? (!g->hq || !g->hs || g->ldhq < g->rows)
+                                  : (!g->bq || !g->bs || g->ldhq < g->K || g->npieces != 1))))
+        return -1;
     if (g->afmt == 1 && (!g->wa || (g->mode == 0 && !g->wb))) return -1;
     if (g->tiles ? (!g->ntiles || g->max_tiles < 1) : g->dense_rows < 1) return -1;
     if ((g->scatter || (g->mode == 0 && g->tiles)) && !g->perm) return -1;

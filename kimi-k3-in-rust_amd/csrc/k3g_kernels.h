@@ -105,6 +105,10 @@ typedef struct {
     const uint8_t *bq, *bs;
     uint8_t *hq, *hs;
     int ldhq;                 /* bytes per h row (scales: ldhq / 32) */
+    /* k3k_gemm with MXFP4 weights: h as bf16 piece 0 (h, b) plus its remainder
+     * h - bf16(h) as MXFP8 (mode 0 writes hq/hs, mode 1 reads bq/bs; row stride ldhq bytes)
+     * on the scaled FP8 matrix cores; mode 1 then takes npieces = 1 */
+    int hmix;
     int np_only;              /* set by k3k_gemm: 2 = a launch that runs only two-piece B */
     /* dense tiled-bf16 GEMMs only: K cut into ksplit slices of whole 128-column steps
      * (1: none); the slices' fp32 sums go to part ([ksplit][columns][2][rows] gate/up,

@@ -17,6 +17,9 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 REL_L2 = 1e-3
+# the grouped bf16 GEMMs: x and the weights exact in bf16, h as bf16 plus its MXFP8
+# remainder (about 12 significant bits), fp32 accumulation: rel-L2 about 4e-5
+GEMM_REL = 1e-4
 
 
 def rel_l2(a, b):
@@ -368,7 +371,7 @@ def test_layer_tiny_grouped_gemm(gpu, T, xkind):
     np.testing.assert_allclose(wt, rw, rtol=1e-6)
     r = rel_l2(out, ro)
     say(f"  rel-L2 {r:.3e}")
-    assert r <= 1e-5
+    assert r <= GEMM_REL
 
 
 @pytest.mark.parametrize("T,xkind", [(40, "bf16"), (24, "fp32")])
@@ -385,7 +388,7 @@ def test_layer_k2_grouped_gemm(k2_layer, T, xkind):
     assert np.array_equal(idx, ri)
     r = rel_l2(out, ro)
     say(f"  rel-L2 {r:.3e}")
-    assert r <= 1e-5
+    assert r <= GEMM_REL
 
 
 @pytest.mark.parametrize("shape,T,nsample", [("K2_BATCH", 64, 6), ("K2_PREFILL", 4096, 6)])
@@ -423,7 +426,7 @@ def test_layer_k2_skewed_full_size(gpu, shape, T, nsample):
     assert np.array_equal(idx[st], ri)
     r = rel_l2(out[st], ro)
     say(f"  {len(st)} sampled rows: rel-L2 {r:.3e}")
-    assert r <= 1e-5
+    assert r <= GEMM_REL
 
 
 def test_layer_k2_batch(k2_layer):
@@ -577,8 +580,8 @@ def test_expert_products_per_pair(gpu, kind, T):
     r = rel_l2(got, exp)
     worst = max(rel_l2(a, b) for a, b in zip(got, exp))
     say(f"  rel-L2 {r:.3e}, worst row {worst:.3e}")
-    assert r <= (5e-3 if kind == "f8f6f4" else 1e-5)
-    assert worst <= (1e-2 if kind == "f8f6f4" else 1e-4)
+    assert r <= (5e-3 if kind == "f8f6f4" else GEMM_REL if kind == "bf16" else 1e-5)
+    assert worst <= (1e-2 if kind == "f8f6f4" else 4 * GEMM_REL if kind == "bf16" else 1e-4)
     for t, j in dropped:
         assert np.all(rows[t, j].view(np.uint32) == SENTINEL)
 
@@ -596,7 +599,7 @@ def test_expert_products_k2(k2_layer, kind, T):
     exp = _pair_rows(layer, x, idx, pairs)
     r = rel_l2(np.stack([rows[t, j] for t, j in pairs]), exp)
     say(f"  rel-L2 {r:.3e}")
-    assert r <= 1e-5
+    assert r <= GEMM_REL
 
 
 def test_steps_compose_to_the_layer(gpu):
@@ -629,7 +632,7 @@ def test_steps_compose_to_the_layer(gpu):
                              cap, cap), layer.sh2, s.hidden) for t in range(T)])
     r_layer = rel_l2(routed + shared, out)
     say(f"  routed sum vs oracle {r_routed:.3e}; + shared expert vs k3g_moe {r_layer:.3e}")
-    assert r_routed <= 1e-5
+    assert r_routed <= GEMM_REL
     assert r_layer <= 1e-5
 
 
