@@ -154,7 +154,8 @@ def batch_decode(a):
             "hbm_frac": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "steps": a.batch_steps, "warmup": a.batch_warmup,
             "workload": "64-token batched decode, same K2 layer, Zipf(1.1) selection-bias "
-                        "skew (alpha 0.025), 2 layers round-robin; grouped bf16 MFMA GEMMs"}
+                        "skew (alpha 0.025), 2 layers round-robin; grouped bf16 MFMA GEMMs, "
+                        "h's MXFP8 remainder on scaled FP8 MFMA"}
 
 
 def expert_trace(n_steps, n_layers, T, seed, reuse=0.7, zipf_s=1.0, per_step=40):
@@ -331,7 +332,8 @@ def prefill(a):
         "achieved_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
         "steps": a.prefill_steps, "warmup": a.prefill_warmup,
         "workload": "4096-token prefill, same K2 layer, Zipf(0.8) selection-bias skew "
-                    "(alpha 0.02), bf16-valued x; bf16 MFMA grouped GEMMs",
+                    "(alpha 0.02), bf16-valued x; bf16 MFMA grouped GEMMs, h's MXFP8 "
+                    "remainder on scaled FP8 MFMA",
         "routing": {"experts_used": int(len(act)), "max_tokens": int(cnt.max()),
                     "min_tokens": int(act.min()),
                     "p90_over_p10": round(float(np.percentile(act, 90) / max(np.percentile(act, 10), 1)), 2),
