@@ -564,6 +564,31 @@ def _run_experts(layer, kind, x, idx):
     return dc.download(np.float32, T * k * d).reshape(T, k, d)
 
 
+def test_grouped_remainder_extremes(gpu):
+    """h's MXFP8 remainder at its edges: tokens of zeros (every remainder block zero, scale
+    byte 0) give rows of exact zeros; tokens scaled by 2^-20 and 2^12 (remainder blocks far
+    from 1, activation caps reached) stay within the grouped tolerance of the oracle."""
+    T = 24
+    say(f"case: grouped bf16 experts, tiny layer, {T} tokens: zero rows, tiny and large rows")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=4242, layout="both")
+    x = layer.tokens(T).copy()
+    x[0:4] = 0.0
+    x[4:10] *= np.float32(2.0 ** -20)
+    x[10:16] *= np.float32(2.0 ** 12)
+    idx = _random_routing(T, layer.shape.n_experts, layer.shape.topk, seed=5, drop=0.0)
+    rows = _run_experts(layer, "bf16", x, idx)
+    assert np.all(rows[0:4] == 0.0), "zero tokens must give exact zeros"
+    kept = [(t, j) for t in range(4, T) for j in range(layer.shape.topk)]
+    exp = _pair_rows(layer, x, idx, kept)
+    got = np.stack([rows[t, j] for t, j in kept])
+    assert np.all(np.isfinite(got))
+    for lo, hi in ((4, 10), (10, 16), (16, T)):
+        sel = [i for i, (t, _) in enumerate(kept) if lo <= t < hi]
+        r = rel_l2(got[sel], exp[sel])
+        say(f"  tokens {lo}..{hi - 1}: rel-L2 {r:.3e}")
+        assert r <= GEMM_REL
+
+
 @pytest.mark.parametrize("kind,T", [("gemv", 3), ("gemv", 37), ("bf16", 5), ("bf16", 37),
                                     ("bf16", 200), ("f8f6f4", 37)])
 def test_expert_products_per_pair(gpu, kind, T):
