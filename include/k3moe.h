@@ -310,7 +310,8 @@ int  k3g_expert_gemv(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
 
 /* The same contrib rows as grouped GEMMs over 128-pair column tiles: gate/up with the
  * activation fused, then down, bf16 matrix cores (weights decoded from MXFP4 exactly,
- * activations split into two bf16 pieces, fp32 accumulation) or, for _f8f6f4, the
+ * x as two bf16 pieces, h as a bf16 piece plus its MXFP8 remainder on the scaled FP8
+ * matrix cores, fp32 accumulation; rel-L2 about 4e-5) or, for _f8f6f4, the
  * scaled FP4 x FP8 ones with x and h quantised to MXFP8. Experts in the tiled layout
  * (K3G_EXPERT_MXFP4_TILED), hidden and inter multiples of 32. */
 int  k3g_grouped_gemm_bf16(K3gCtx *ctx, const K3gLayer *L, const float *x, int T,
