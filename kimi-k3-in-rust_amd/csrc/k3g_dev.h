@@ -58,6 +58,30 @@ __device__ __forceinline__ void k3d_fp4x8(uint32_t w, float scale, float *o)
     o[4] = c.x; o[5] = c.y; o[6] = d.x; o[7] = d.y;
 }
 
+/* One DMA instruction: 64 lanes x 16 bytes from their own global addresses to 1 KB of LDS
+ * at byte address `lds` (lane l at lds + 16 l), M0 saved and restored around it. */
+__device__ __forceinline__ void k3d_dma16(const void *src, uint32_t lds)
+{
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %2\n\t"
+                 "global_load_lds_dwordx4 %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+
+/* s_waitcnt vmcnt(n) for a wave-uniform n in 0..15 */
+__device__ __forceinline__ void k3d_wait_vm(int n)
+{
+    switch (n) {
+#define K3_WVM(N) case N: __builtin_amdgcn_s_waitcnt(0x0F70 | N); break;
+        K3_WVM(1) K3_WVM(2) K3_WVM(3) K3_WVM(4) K3_WVM(5) K3_WVM(6) K3_WVM(7) K3_WVM(8)
+        K3_WVM(9) K3_WVM(10) K3_WVM(11) K3_WVM(12) K3_WVM(13) K3_WVM(14) K3_WVM(15)
+#undef K3_WVM
+        default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    }
+}
+
 __device__ __forceinline__ float k3d_bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float k3d_bf16hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
