@@ -326,6 +326,22 @@ int  k3g_grouped_gemm_f8f6f4(K3gCtx *ctx, const K3gLayer *L, const float *x, int
 int  k3g_combine(K3gCtx *ctx, const float *contrib, const int32_t *idx, const float *wt,
                  int T, int topk, int n, const float *add, float *out, void *stream);
 
+/* k3g_moe at decode sizes WITHOUT ANY ALLOCATION. No reference counterpart: it is for
+ * callers that cannot allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc). It runs the fused decode kernel (1 <= T <= 4; Kimi-K2 layer shape: experts
+ * in the tiled MXFP4 layout, shared expert in the tiled bf16 layout, no latent
+ * projection) with every buffer beyond x, out, idx and wt in one fixed device array of
+ * 16 MiB per GPU, set up on the first call on a device and held until the process ends.
+ * A layer whose buffers exceed it (e.g. top-k 64 at hidden 7168) is rejected with -1 and
+ * a message, as is any other shape or T. idx/wt (device, [T][topk]) may be NULL (the
+ * routing then stays in the array); err (device int, may be NULL) receives a device
+ * error the kernel raises (an exhausted bounded wait), as k3g_sync reports it for a
+ * context. Asynchronous on `stream` (NULL = the null stream). Every call on a GPU shares
+ * that GPU's array and it keeps the last call's contents: calls that overlap on one GPU
+ * race and must be ordered by the caller. Returns 0, or -1. */
+int  k3g_moe_noalloc(const K3gLayer *L, const float *x, int T, float *out, int32_t *idx,
+                     float *wt, int *err, void *stream);
+
 /* Synchronise the stream and report any error a kernel raised on the device
  * (an exhausted bounded wait, a bad expert index). Returns 0 when clean. */
 int  k3g_sync(K3gCtx *ctx, void *stream);

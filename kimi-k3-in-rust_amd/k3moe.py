@@ -168,6 +168,8 @@ def lib() -> C.CDLL:
             getattr(L, name).restype = i
         L.k3g_combine.argtypes = [vp, vp, vp, vp, i, i, i, vp, vp, vp]
         L.k3g_combine.restype = i
+        L.k3g_moe_noalloc.argtypes = [C.POINTER(K3gLayer), vp, i, vp, vp, vp, vp, vp]
+        L.k3g_moe_noalloc.restype = i
         L.k3g_sync.argtypes = [vp, vp]
         L.k3g_sync.restype = i
         L.k3s_byte.argtypes = [u64, u64, u64]
