@@ -138,10 +138,19 @@ size_t k3_moe_scratch(const K3Cfg *c);
 /* Replaces include/k3/k3.h:418-419 (src/core/k3_ops.c:556-656). x, out are host
  * [T][hidden] fp32. idx/wt receive the LAST token's routing, as in the engine. scratch
  * is accepted for ABI compatibility and not used: the GPU workspace is preallocated
- * per device. Weights are uploaded to HBM on first use and keyed by host address, so
- * they must not change afterwards (call k3moe_forget_weights() if they do). Experts
- * come from w->src (MXFP4) or from the fp32 resident bank w->w1/w3/w2. A source that
- * fails to deliver an expert bumps k3_expert_drops, as the engine does. */
+ * per device. Weights are uploaded to HBM on first use and keyed by host address and
+ * size; a sampled fingerprint of the bytes is checked every call, and a caller that
+ * rewrites a weight buffer in place (a ring of layer buffers) calls
+ * k3moe_invalidate_weights() on it. Experts come from w->src (MXFP4) or from the fp32
+ * resident bank w->w1/w3/w2. A source that fails to deliver an expert bumps
+ * k3_expert_drops, as the engine does.
+ *
+ * With bf16 shared and latent weights (wdt K3_WBF16) and experts from a source, the layer
+ * runs on the matrix cores: the fused decode kernel (no latent, up to 4 tokens) or the
+ * grouped GEMMs; an HBM expert cache (k3gc_*) with a tiled bank serves its experts in
+ * place, any other source's experts are copied and tiled per call. Through an HBM cache
+ * the tokens are run in groups whose experts fit the cache's unpinned slots, one cache
+ * step each, so a cache of top-k + 1 slots serves any T without dropping an expert. */
 void k3_moe(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
             int T, int *idx, float *wt, float *scratch);
 
@@ -163,6 +172,18 @@ void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
 /* Drop every HBM copy of host weights made by k3_moe/k3_router. No reference
  * counterpart: the engine reads host weights in place. */
 void k3moe_forget_weights(void);
+
+/* Which kernels the last k3_moe / k3_moe_prefill call ran, as bits: 1 the staged VALU
+ * kernels, 2 the fused decode kernel, 4 the grouped matrix-core GEMMs. No reference
+ * counterpart (diagnostics). */
+int k3moe_last_kernels(void);
+
+/* Drop the HBM copies of host weights overlapping [host, host + bytes): the next call
+ * uploads them again. For callers that reuse a weight buffer for other weights at the
+ * same address (the engine's trunk ring, src/io/k3_trunk.c). The copies are also kept
+ * within K3MOE_MIRROR_BYTES of device memory (default 64 GiB), least recently used
+ * dropped first. No reference counterpart: the engine reads host weights in place. */
+void k3moe_invalidate_weights(const void *host, size_t bytes);
 
 /* ============================================================== 2. device API == */
 
@@ -192,7 +213,8 @@ K3gExpertLayout k3g_expert_layout(int hidden, int inter);
  *                   granularity into the matrix cores; it serves up to 4 tokens a call.
  *   shared expert, tagged by wdt (K3_WF32 or K3_WBF16): sh1/sh3 [shared_inter][hidden],
  *     sh2 [hidden][shared_inter]; shared_inter == 0 means none. shared_fmt 0: row-major;
- *     1: bf16 in the tiled layout k3g_tile_bf16 writes (goes with expert_fmt 2)
+ *     1: bf16 in the tiled layout k3g_tile_bf16 writes, for the shared expert and the
+ *     latent projections alike (goes with expert_fmt 2)
  *   latent projections, tagged by wdt: down [latent][hidden], up [hidden][latent];
  *     NULL for the Kimi-K2 shape (latent == hidden). latent_norm [latent] or NULL.
  *   act_b1/act_b2: SiTU caps; a value >= 2^64 means uncapped (SwiGLU). */

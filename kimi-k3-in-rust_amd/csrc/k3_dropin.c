@@ -3,14 +3,27 @@
  * with the engine's host-pointer signatures, synchronous semantics and error
  * behaviour (C99).
  *
- * Host weights are mirrored into HBM on first use, keyed by (address, size), and then
- * reused: the engine binds a layer's weights once and passes the same pointers every
- * token. Experts from a K3ExpertSrc are fetched with the engine's own call pattern
- * (getmany then get per slot for k3_moe, per unique expert per 64-token chunk for
- * k3_moe_prefill, src/core/k3_ops.c:604-627 and :756-766), so a cache behind the source
- * sees the same requests. A source returning host pointers has each expert copied to
- * HBM right after get(), before the next get() can evict it; the HBM expert cache
- * (k3gc_*) returns device pointers and is used in place. */
+ * Host weights are mirrored into HBM on first use, keyed by (address, size, layout), and
+ * then reused: the engine binds a layer's weights once and passes the same pointers every
+ * token. A sampled fingerprint of the host bytes is checked on every call and
+ * k3moe_invalidate_weights() drops a mirror explicitly (a buffer reused for other weights
+ * at the same address, as a ring of layer buffers does).
+ *
+ * Experts from a K3ExpertSrc are fetched with the engine's own call pattern (getmany then
+ * get per slot for k3_moe, per unique expert per 64-token chunk for k3_moe_prefill,
+ * src/core/k3_ops.c:604-627 and :756-766), so a cache behind the source sees the same
+ * requests. A layer with bf16 shared/latent weights and MXFP4 experts from a source runs
+ * on the matrix-core kernels: the fused decode kernel (Kimi-K2 shape, up to 4 tokens,
+ * the routing given) or the grouped GEMMs. Their weights are in the tiled layouts: the
+ * mirrors of the bf16 matrices are tiled once at upload; an HBM expert cache (k3gc_*)
+ * with a tiled bank hands out tiled experts as they are; any other expert is copied to
+ * HBM (a host source) and tiled into a staging slot before the next get() can evict it.
+ * Other layers (fp32 weights, the fp32 resident expert bank, int8 draft weights) run on
+ * the staged VALU kernels with experts in the checkpoint layout.
+ *
+ * Through an HBM cache the tokens of a call are cut into groups whose experts fit the
+ * cache's unpinned slots at once; each group is one cache step: its experts stay put
+ * until its kernels are done, then the next group fetches. */
 #include "k3g_ctx.h"
 #include "k3gc_cache.h"
 
@@ -22,13 +35,21 @@
 long k3_expert_drops = 0;
 
 static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
+static int g_last_paths = 0;     /* kernels the last k3_moe / k3_moe_prefill call ran */
+
+int k3moe_last_kernels(void) { return g_last_paths; }
 
 /* ----------------------------------------------------------- per-device state ---- */
+enum { MIR_ROWMAJOR = 0, MIR_TILED_BF16 = 1 };
+
 typedef struct {
     const void *host;
-    size_t bytes;
+    size_t bytes;                /* host bytes mirrored */
+    int kind, rows, cols;
     uint64_t print;              /* sampled fingerprint of the host bytes at upload */
+    uint64_t used;               /* call stamp of the last use */
     void *dev;
+    size_t dev_bytes;
 } Mirror;
 
 typedef struct {
@@ -38,10 +59,20 @@ typedef struct {
     int ctx_tokens;
     Mirror *mir;
     int nmir, capmir;
+    size_t mir_bytes;            /* device bytes the mirrors hold */
+    uint64_t calls;
     void *stage;                 /* scratch device buffer, grow-only */
     size_t stage_bytes;
     K3ExpertQ *eq_dev;           /* [cap_e] device expert table */
     int cap_e;
+    /* host scratch of a call, grow-only */
+    int *ridx;
+    float *rwt;
+    size_t cap_pairs;
+    int *slot_of, *uniq;
+    K3ExpertQ *table;
+    unsigned char *have, *seen;
+    int cap_host_e;
 } DevState;
 
 #define K3_MAX_DEV 16
@@ -56,9 +87,34 @@ static DevState *dev_state(void)
     return &g_dev[d];
 }
 
+static void *xgrow(void *p, size_t bytes)
+{
+    void *q = realloc(p, bytes ? bytes : 1);
+    if (!q) k3g_fatal("out of host memory in the drop-in");
+    return q;
+}
+
+/* host scratch for T * k pairs and E experts */
+static void host_scratch(DevState *s, size_t pairs, int E)
+{
+    if (pairs > s->cap_pairs) {
+        s->ridx = (int *)xgrow(s->ridx, pairs * sizeof(int));
+        s->rwt = (float *)xgrow(s->rwt, pairs * sizeof(float));
+        s->uniq = (int *)xgrow(s->uniq, pairs * sizeof(int));
+        s->cap_pairs = pairs;
+    }
+    if (E > s->cap_host_e) {
+        s->slot_of = (int *)xgrow(s->slot_of, (size_t)E * sizeof(int));
+        s->table = (K3ExpertQ *)xgrow(s->table, (size_t)E * sizeof(K3ExpertQ));
+        s->have = (unsigned char *)xgrow(s->have, (size_t)E);
+        s->seen = (unsigned char *)xgrow(s->seen, (size_t)E);
+        s->cap_host_e = E;
+    }
+}
+
 /* FNV-1a over 64 eight-byte samples spread across the buffer (all of it when short):
- * cheap enough to check on every call, and it catches a buffer that was freed and
- * reused for other weights at the same address. */
+ * cheap enough to check on every call, and it catches a buffer that was rewritten with
+ * other weights at the same address. */
 static uint64_t fingerprint(const void *host, size_t bytes)
 {
     const unsigned char *b = (const unsigned char *)host;
@@ -74,42 +130,119 @@ static uint64_t fingerprint(const void *host, size_t bytes)
     return h;
 }
 
-/* Device copy of `bytes` of host memory at `host`, uploaded on first use and again
- * whenever the sampled fingerprint shows the host bytes changed. */
-static const void *mirror(DevState *s, const void *host, size_t bytes)
+static void *stage(DevState *s, size_t bytes);
+
+/* Bytes the mirrors may hold on one device (K3MOE_MIRROR_BYTES; default 64 GB): beyond
+ * it the least recently used mirrors not used by the current call are dropped. */
+static size_t mirror_budget(void)
+{
+    static size_t budget = 0;
+    if (!budget) {
+        const char *e = getenv("K3MOE_MIRROR_BYTES");
+        const double v = e ? atof(e) : 0.0;
+        budget = v > 0.0 ? (size_t)v : (size_t)64 << 30;
+    }
+    return budget;
+}
+
+static void mirror_drop(DevState *s, int i)
+{
+    K3G_CHECK(hipDeviceSynchronize());
+    K3G_CHECK(hipFree(s->mir[i].dev));
+    s->mir_bytes -= s->mir[i].dev_bytes;
+    s->mir[i] = s->mir[--s->nmir];
+}
+
+static void mirror_make_room(DevState *s, size_t need)
+{
+    while (s->nmir > 0 && s->mir_bytes + need > mirror_budget()) {
+        int victim = -1;
+        for (int i = 0; i < s->nmir; i++)
+            if (s->mir[i].used < s->calls && (victim < 0 || s->mir[i].used < s->mir[victim].used))
+                victim = i;
+        if (victim < 0) break;          /* everything is this call's: go over the budget */
+        mirror_drop(s, victim);
+    }
+}
+
+/* (Re)fill a mirror's device copy from the host bytes. */
+static void mirror_upload(DevState *s, Mirror *m, hipStream_t st)
+{
+    if (m->kind == MIR_ROWMAJOR) {
+        K3G_CHECK(hipMemcpy(m->dev, m->host, m->bytes, hipMemcpyHostToDevice));
+        return;
+    }
+    /* row-major bf16 to the staging buffer, then tiled into the mirror */
+    void *tmp = stage(s, m->bytes);
+    K3G_CHECK(hipMemcpy(tmp, m->host, m->bytes, hipMemcpyHostToDevice));
+    if (k3k_tile_bf16((uint16_t *)m->dev, (const uint16_t *)tmp, m->rows, m->cols, st) != 0)
+        k3g_fatal("tiling a bf16 weight matrix failed");
+    K3G_CHECK(hipStreamSynchronize(st));
+}
+
+/* Device copy of host weights: row-major (`bytes` of them), or for MIR_TILED_BF16 a bf16
+ * [rows][cols] matrix in the tiled layout. Uploaded on first use and again whenever the
+ * sampled fingerprint shows the host bytes changed. */
+static const void *mirror_kind(DevState *s, const void *host, size_t bytes, int kind, int rows,
+                               int cols, hipStream_t st)
 {
     if (!host || !bytes) return NULL;
     const uint64_t fp = fingerprint(host, bytes);
-    for (int i = 0; i < s->nmir; i++)
-        if (s->mir[i].host == host && s->mir[i].bytes == bytes) {
-            if (s->mir[i].print != fp) {
-                K3G_CHECK(hipMemcpy(s->mir[i].dev, host, bytes, hipMemcpyHostToDevice));
-                s->mir[i].print = fp;
+    for (int i = 0; i < s->nmir; i++) {
+        Mirror *m = &s->mir[i];
+        if (m->host == host && m->bytes == bytes && m->kind == kind && m->rows == rows &&
+            m->cols == cols) {
+            m->used = s->calls;
+            if (m->print != fp) {
+                m->print = fp;
+                mirror_upload(s, m, st);
             }
-            return s->mir[i].dev;
+            return m->dev;
         }
+    }
+    const size_t db = kind == MIR_ROWMAJOR ? bytes : k3k_tiled_bf16_bytes(rows, cols);
+    if (!db) k3g_fatal("a bf16 weight matrix has no tiled layout (rows % 16, cols % 32)");
+    mirror_make_room(s, db);
     if (s->nmir == s->capmir) {
         const int nc = s->capmir ? 2 * s->capmir : 32;
-        Mirror *m = (Mirror *)realloc(s->mir, (size_t)nc * sizeof *m);
-        if (!m) k3g_fatal("out of host memory for the weight mirror table");
-        s->mir = m;
+        s->mir = (Mirror *)xgrow(s->mir, (size_t)nc * sizeof(Mirror));
         s->capmir = nc;
     }
-    void *dev = NULL;
-    K3G_CHECK(hipMalloc(&dev, bytes));
-    K3G_CHECK(hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice));
-    s->mir[s->nmir].host = host;
-    s->mir[s->nmir].bytes = bytes;
-    s->mir[s->nmir].print = fp;
-    s->mir[s->nmir].dev = dev;
+    Mirror *m = &s->mir[s->nmir];
+    memset(m, 0, sizeof *m);
+    m->host = host;
+    m->bytes = bytes;
+    m->kind = kind;
+    m->rows = rows;
+    m->cols = cols;
+    m->print = fp;
+    m->used = s->calls;
+    m->dev_bytes = db;
+    K3G_CHECK(hipMalloc(&m->dev, db));
     s->nmir++;
-    return dev;
+    s->mir_bytes += db;
+    mirror_upload(s, m, st);
+    return m->dev;
+}
+
+static const void *mirror(DevState *s, const void *host, size_t bytes)
+{
+    return mirror_kind(s, host, bytes, MIR_ROWMAJOR, 0, 0, NULL);
+}
+
+static const void *mirror_tiled(DevState *s, const void *host, int rows, int cols,
+                                hipStream_t st)
+{
+    return mirror_kind(s, host, (size_t)rows * cols * 2, MIR_TILED_BF16, rows, cols, st);
 }
 
 static void *stage(DevState *s, size_t bytes)
 {
     if (bytes > s->stage_bytes) {
-        if (s->stage) K3G_CHECK(hipFree(s->stage));
+        if (s->stage) {
+            K3G_CHECK(hipDeviceSynchronize());
+            K3G_CHECK(hipFree(s->stage));
+        }
         s->stage = NULL;
         const size_t nb = bytes + bytes / 4;
         K3G_CHECK(hipMalloc(&s->stage, nb));
@@ -130,6 +263,28 @@ void k3moe_forget_weights(void)
         hipDeviceSynchronize();
         for (int i = 0; i < s->nmir; i++) hipFree(s->mir[i].dev);
         s->nmir = 0;
+        s->mir_bytes = 0;
+    }
+    hipSetDevice(cur);
+    pthread_mutex_unlock(&g_lock);
+}
+
+void k3moe_invalidate_weights(const void *host, size_t bytes)
+{
+    if (!host || !bytes) return;
+    const uintptr_t a = (uintptr_t)host, b = a + bytes;
+    pthread_mutex_lock(&g_lock);
+    int cur = 0;
+    hipGetDevice(&cur);
+    for (int d = 0; d < K3_MAX_DEV; d++) {
+        DevState *s = &g_dev[d];
+        if (!s->used) continue;
+        hipSetDevice(d);
+        for (int i = 0; i < s->nmir;) {
+            const uintptr_t ma = (uintptr_t)s->mir[i].host, mb = ma + s->mir[i].bytes;
+            if (ma < b && a < mb) mirror_drop(s, i);
+            else i++;
+        }
     }
     hipSetDevice(cur);
     pthread_mutex_unlock(&g_lock);
@@ -172,6 +327,7 @@ void k3_router(int *idx, float *w, const float *x, const float *W, const float *
         k3g_fatal("k3_router: top-k or expert count outside what the GPU router supports");
     pthread_mutex_lock(&g_lock);
     DevState *s = dev_state();
+    s->calls++;
     K3gLayer L;
     memset(&L, 0, sizeof L);
     L.hidden = hidden;
@@ -205,14 +361,53 @@ size_t k3_moe_scratch(const K3Cfg *c)
 /* ---------------------------------------------------------------- MoE layer ---- */
 static size_t wsz(int wdt) { return wdt == K3_WBF16 ? 2 : 4; }
 
-/* Copy one host-resident expert into staging slot `slot` and record its device
- * pointers. */
-static K3ExpertQ stage_expert(const K3ExpertQ *q, unsigned char *base, const K3gExpertLayout *g,
-                              int I, int L, hipStream_t st)
+/* How a fetched expert reaches the kernels. */
+enum {
+    F_DIRECT = 0,      /* device pointers in the layout the kernels read */
+    F_DEV_TILE,        /* device pointers in the checkpoint layout, tiled into a slot */
+    F_HOST_STAGE,      /* host pointers, copied into a checkpoint-layout slot */
+    F_HOST_TILE        /* host pointers, copied to a ring buffer and tiled into a slot */
+};
+
+typedef struct {
+    const K3MoeW *w;
+    int I, L, how;
+    K3gExpertLayout geo;
+    size_t t13, t2, slot_bytes;  /* tiled matrix sizes; bytes per staging slot */
+    unsigned char *slots;        /* staging slots */
+    unsigned char *ring[2];      /* checkpoint-layout buffers for F_HOST_TILE */
+    int nring;
+    int nslot, maxslot;
+    int *slot_of;                /* [E] */
+    K3ExpertQ *table;            /* [E] the pointers the kernels read */
+    unsigned char *have;         /* [E] expert resolved in this call */
+    K3gCache *hc;
+    hipStream_t st;
+} Fetcher;
+
+/* Tile one checkpoint-layout expert (device pointers) into tiled slot memory. */
+static K3ExpertQ tile_expert(Fetcher *f, const K3ExpertQ *q, unsigned char *dst)
 {
     K3ExpertQ d;
+    memset(&d, 0, sizeof d);
+    if (k3k_tile_mxfp4(dst, q->p1, q->s1, f->I, f->L, f->st) != 0 ||
+        k3k_tile_mxfp4(dst + f->t13, q->p3, q->s3, f->I, f->L, f->st) != 0 ||
+        k3k_tile_mxfp4(dst + 2 * f->t13, q->p2, q->s2, f->L, f->I, f->st) != 0)
+        k3g_fatal("k3_moe: tiling an expert failed");
+    d.p1 = dst;
+    d.p3 = dst + f->t13;
+    d.p2 = dst + 2 * f->t13;
+    return d;
+}
+
+/* Copy one host-resident expert to the device in the checkpoint layout at `base`. */
+static K3ExpertQ upload_expert(Fetcher *f, const K3ExpertQ *q, unsigned char *base)
+{
+    const K3gExpertLayout *g = &f->geo;
+    const int I = f->I, L = f->L;
     const size_t p13 = (size_t)I * (L / 2), s13 = (size_t)I * ((L + 31) / 32);
     const size_t p2 = (size_t)L * (I / 2), s2 = (size_t)L * ((I + 31) / 32);
+    hipStream_t st = f->st;
     K3G_CHECK(hipMemcpyAsync(base + g->p1_off, q->p1, p13, hipMemcpyHostToDevice, st));
     K3G_CHECK(hipMemcpyAsync(base + g->s1_off, q->s1, s13, hipMemcpyHostToDevice, st));
     K3G_CHECK(hipMemcpyAsync(base + g->p2_off, q->p2, p2, hipMemcpyHostToDevice, st));
@@ -221,24 +416,12 @@ static K3ExpertQ stage_expert(const K3ExpertQ *q, unsigned char *base, const K3g
     K3G_CHECK(hipMemcpyAsync(base + g->s3_off, q->s3, s13, hipMemcpyHostToDevice, st));
     /* the source may evict these bytes at its next get(); finish the copy first */
     K3G_CHECK(hipStreamSynchronize(st));
+    K3ExpertQ d;
     d.p1 = base + g->p1_off; d.s1 = base + g->s1_off;
     d.p2 = base + g->p2_off; d.s2 = base + g->s2_off;
     d.p3 = base + g->p3_off; d.s3 = base + g->s3_off;
     return d;
 }
-
-typedef struct {
-    DevState *s;
-    const K3MoeW *w;
-    int E, I, L, device_src;
-    K3gExpertLayout geo;
-    unsigned char *slots;        /* staging slots for host-resident experts */
-    int nslot, maxslot;
-    int *slot_of;                /* [E] */
-    K3ExpertQ *table;            /* host copy of the device table [E] */
-    unsigned char *have;         /* [E] expert resolved in this call */
-    hipStream_t st;
-} Fetcher;
 
 /* get() one expert and resolve it to device pointers. Returns 0, or -1 on a miss. */
 static int fetch_one(Fetcher *f, int e, int resident_only)
@@ -248,14 +431,25 @@ static int fetch_one(Fetcher *f, int e, int resident_only)
     const int miss = resident_only ? !w->src->resident(w->src, w->layer, e, &q)
                                    : (w->src->get(w->src, w->layer, e, &q) != 0);
     if (miss) return -1;
-    if (f->device_src) {
+    if (f->how == F_DIRECT) {
         f->table[e] = q;
     } else if (!f->have[e]) {
         if (f->nslot >= f->maxslot) k3g_fatal("expert staging overflow");
         const int sl = f->nslot++;
         f->slot_of[e] = sl;
-        f->table[e] = stage_expert(&q, f->slots + (size_t)sl * f->geo.nbytes, &f->geo, f->I,
-                                   f->L, f->st);
+        unsigned char *slot = f->slots + (size_t)sl * f->slot_bytes;
+        if (f->how == F_HOST_STAGE) {
+            f->table[e] = upload_expert(f, &q, slot);
+        } else if (f->how == F_HOST_TILE) {
+            /* two ring buffers alternate: the copy into one waits (stream order) for the
+             * tiling that read it two experts ago */
+            const K3ExpertQ d = upload_expert(f, &q, f->ring[f->nring++ & 1]);
+            f->table[e] = tile_expert(f, &d, slot);
+        } else {
+            /* the cache's copy of this expert may still be in flight */
+            k3gc_wait(f->hc, f->st);
+            f->table[e] = tile_expert(f, &q, slot);
+        }
     }
     f->have[e] = 1;
     return 0;
@@ -266,6 +460,121 @@ static void drop_msg(int layer, int e, const char *what)
     k3_expert_drops++;
     fprintf(stderr, "EXPERT DROP: layer %d expert %d failed to load; this %s is CORRUPT\n",
             layer, e, what);
+}
+
+/* The engine's fetch calls for tokens [t0, t1) (per-token pattern) or for whole 64-token
+ * prefill chunks starting at t0 (mode 1). Routing entries of dropped experts become -1. */
+static void fetch_tokens(Fetcher *f, DevState *s, int *ridx, int k, int E, int t0, int t1,
+                         int batched, int cache_only)
+{
+    const K3MoeW *w = f->w;
+    if (!batched) {
+        /* src/core/k3_ops.c:604-627 */
+        for (int t = t0; t < t1; t++) {
+            int *it = ridx + (size_t)t * k;
+            int ids[K3_MAX_TOPK], nk = 0;
+            for (int j = 0; j < k; j++) if (it[j] >= 0) ids[nk++] = it[j];
+            if (!cache_only && w->src->getmany) w->src->getmany(w->src, w->layer, ids, nk);
+            for (int j = 0; j < k; j++) {
+                if (it[j] < 0) continue;
+                if (fetch_one(f, it[j], cache_only) != 0) {
+                    if (!cache_only) drop_msg(w->layer, it[j], "token");
+                    it[j] = -1;
+                }
+            }
+        }
+        return;
+    }
+    /* src/core/k3_ops.c:707-766: 64-token chunks, unique experts in first-seen order,
+     * one get() each */
+    for (int c0 = t0; c0 < t1; c0 += 64) {
+        const int n = t1 - c0 < 64 ? t1 - c0 : 64;
+        if (n == 1) {
+            /* a one-token chunk takes k3_moe's per-slot path (:709-710) */
+            fetch_tokens(f, s, ridx, k, E, c0, c0 + 1, 0, 0);
+            continue;
+        }
+        memset(s->seen, 0, (size_t)E);
+        int nu = 0;
+        for (int t = c0; t < c0 + n; t++)
+            for (int j = 0; j < k; j++) {
+                const int e = ridx[(size_t)t * k + j];
+                if (e >= 0 && e < E && !s->seen[e]) { s->seen[e] = 1; s->uniq[nu++] = e; }
+            }
+        if (w->src->getmany) w->src->getmany(w->src, w->layer, s->uniq, nu);
+        for (int u = 0; u < nu; u++) {
+            if (fetch_one(f, s->uniq[u], 0) == 0) continue;
+            drop_msg(w->layer, s->uniq[u], "chunk");
+            for (int t = c0; t < c0 + n; t++)
+                for (int j = 0; j < k; j++)
+                    if (ridx[(size_t)t * k + j] == s->uniq[u]) ridx[(size_t)t * k + j] = -1;
+        }
+    }
+}
+
+/* Tentatively add the experts of tokens [t0, t1) to the set in seen[] (1: in the group,
+ * 2: tentative); returns how many are new. */
+static int add_tokens(unsigned char *seen, const int *ridx, int k, int E, int t0, int t1)
+{
+    int n = 0;
+    for (size_t p = (size_t)t0 * k; p < (size_t)t1 * k; p++) {
+        const int e = ridx[p];
+        if (e >= 0 && e < E && !seen[e]) { seen[e] = 2; n++; }
+    }
+    return n;
+}
+
+static void settle_tokens(unsigned char *seen, const int *ridx, int k, int E, int t0, int t1,
+                          int keep)
+{
+    for (size_t p = (size_t)t0 * k; p < (size_t)t1 * k; p++) {
+        const int e = ridx[p];
+        if (e >= 0 && e < E && seen[e] == 2) seen[e] = keep ? 1 : 0;
+    }
+}
+
+/* The end of the next token group from t0: whole units (one token, or a 64-token prefill
+ * chunk) while the group's distinct experts fit in cap slots; a unit that alone exceeds
+ * cap is split into tokens (at least one: the cache holds top-k + 1 slots). */
+static int next_group(DevState *s, const int *ridx, int k, int E, int T, int t0, int unit,
+                      int cap)
+{
+    unsigned char *seen = s->seen;
+    memset(seen, 0, (size_t)E);
+    int n = 0, t1 = t0;
+    while (t1 < T) {
+        const int u1 = t1 + unit < T ? t1 + unit : T;
+        const int add = add_tokens(seen, ridx, k, E, t1, u1);
+        const int fits = n + add <= cap;
+        settle_tokens(seen, ridx, k, E, t1, u1, fits);
+        if (fits) { n += add; t1 = u1; continue; }
+        if (t1 > t0) break;
+        /* the first unit alone is too wide: as many of its tokens as fit */
+        int t = t0;
+        while (t < u1) {
+            const int a = add_tokens(seen, ridx, k, E, t, t + 1);
+            const int ok = n + a <= cap || t == t0;
+            settle_tokens(seen, ridx, k, E, t, t + 1, ok);
+            if (!ok) break;
+            n += a;
+            t++;
+        }
+        return t;
+    }
+    return t1 > t0 ? t1 : t0 + 1;
+}
+
+/* The fast path: bf16 shared/latent weights (tiled mirrors) and MXFP4 experts from a
+ * source in the tiled layout, on the matrix-core kernels. */
+static int fast_layer(const K3MoeW *w, const K3Cfg *c, int L, int SI)
+{
+    static int staged = -1;
+    if (staged < 0) staged = getenv("K3MOE_DROPIN_STAGED") ? 1 : 0;
+    const int d = c->hidden, I = c->moe_inter;
+    if (staged || !w->src || d % 32 || I % 32 || L % 32) return 0;
+    if ((SI > 0 || w->down || w->up) && w->wdt != K3_WBF16) return 0;
+    if (SI % 32) return 0;
+    return k3k_tiled_mxfp4_bytes(I, L) > 0 && k3k_tiled_mxfp4_bytes(L, I) > 0;
 }
 
 /* mode 0: k3_moe semantics; mode 1: k3_moe_prefill semantics. */
@@ -280,9 +589,16 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     const int SI = c->moe_inter * c->n_shared;
     if (!w->down && c->latent != d && c->latent != 0)
         k3g_fatal("k3_moe: down == NULL (no latent) needs latent == hidden");
+    if (mode == 1) {
+        /* src/core/k3_ops.c:692-695: one binary gives both token streams for an A/B */
+        static int no_batch = -1;
+        if (no_batch < 0) no_batch = getenv("K3_NO_BATCH_PREFILL") ? 1 : 0;
+        if (no_batch) mode = 0;
+    }
 
     pthread_mutex_lock(&g_lock);
     DevState *s = dev_state();
+    s->calls++;
     K3gLayer G;
     memset(&G, 0, sizeof G);
     G.hidden = d;
@@ -297,41 +613,82 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     G.act_b2 = c->situ_b2;
     G.rms_eps = c->rms_eps;
     G.wdt = w->wdt;
-    G.gate = (const float *)mirror(s, w->gate, (size_t)E * d * 4);
-    G.bias = (const float *)mirror(s, w->bias, w->bias ? (size_t)E * 4 : 0);
-    G.down = mirror(s, w->down, w->down ? (size_t)L * d * wsz(w->wdt) : 0);
-    G.up = mirror(s, w->up, w->up ? (size_t)d * L * wsz(w->wdt) : 0);
-    G.latent_norm = c->latent_norm ? (const float *)mirror(s, w->latent_norm, (size_t)L * 4)
-                                   : NULL;
-    if (SI > 0) {
-        G.sh1 = mirror(s, w->sh1, (size_t)SI * d * wsz(w->wdt));
-        G.sh3 = mirror(s, w->sh3, (size_t)SI * d * wsz(w->wdt));
-        G.sh2 = mirror(s, w->sh2, (size_t)d * SI * wsz(w->wdt));
-    }
-    if (!w->src) {
-        G.expert_fmt = 1;
-        G.w1 = (const float *)mirror(s, w->w1, (size_t)E * I * L * 4);
-        G.w3 = (const float *)mirror(s, w->w3, (size_t)E * I * L * 4);
-        G.w2 = (const float *)mirror(s, w->w2, (size_t)E * L * I * 4);
-    }
+    const int device_src = w->src ? k3gc_is_device_src(w->src) : 0;
+    K3gCache *hc = device_src ? k3gc_of_src(w->src) : NULL;
+    const int fast = fast_layer(w, c, L, SI);
+    if (hc && (hc->bank->hidden != L || hc->bank->inter != I || hc->n_experts < E))
+        k3g_fatal("k3_moe: the HBM cache's bank does not hold this layer's expert shape");
+    if (hc && hc->bank->layout == K3G_EXPERT_MXFP4_TILED && !fast)
+        k3g_fatal("k3_moe: experts in the tiled layout need bf16 shared and latent weights "
+                  "(widths multiples of 32)");
+    /* sizes first (the context may be recreated), then the mirrors on its stream */
     K3gCtx *ctx = ctx_for(s, &G, T);
     hipStream_t st = ctx->stream;
+    G.gate = (const float *)mirror(s, w->gate, (size_t)E * d * 4);
+    G.bias = (const float *)mirror(s, w->bias, w->bias ? (size_t)E * 4 : 0);
+    G.latent_norm = c->latent_norm ? (const float *)mirror(s, w->latent_norm, (size_t)L * 4)
+                                   : NULL;
+    if (fast) {
+        G.shared_fmt = 1;
+        G.expert_fmt = K3G_EXPERT_MXFP4_TILED;
+        if (w->down) G.down = mirror_tiled(s, w->down, L, d, st);
+        if (w->up) G.up = mirror_tiled(s, w->up, d, L, st);
+        if (SI > 0) {
+            G.sh1 = mirror_tiled(s, w->sh1, SI, d, st);
+            G.sh3 = mirror_tiled(s, w->sh3, SI, d, st);
+            G.sh2 = mirror_tiled(s, w->sh2, d, SI, st);
+        }
+    } else {
+        G.down = mirror(s, w->down, w->down ? (size_t)L * d * wsz(w->wdt) : 0);
+        G.up = mirror(s, w->up, w->up ? (size_t)d * L * wsz(w->wdt) : 0);
+        if (SI > 0) {
+            G.sh1 = mirror(s, w->sh1, (size_t)SI * d * wsz(w->wdt));
+            G.sh3 = mirror(s, w->sh3, (size_t)SI * d * wsz(w->wdt));
+            G.sh2 = mirror(s, w->sh2, (size_t)d * SI * wsz(w->wdt));
+        }
+        if (!w->src) {
+            G.expert_fmt = 1;
+            G.w1 = (const float *)mirror(s, w->w1, (size_t)E * I * L * 4);
+            G.w3 = (const float *)mirror(s, w->w3, (size_t)E * I * L * 4);
+            G.w2 = (const float *)mirror(s, w->w2, (size_t)E * L * I * 4);
+        }
+    }
 
-    /* one staging buffer: x [T][d], out [T][d], then the host-resident experts' slots */
-    const int device_src = w->src ? k3gc_is_device_src(w->src) : 0;
-    const K3gExpertLayout geo = k3g_expert_layout(L, I);
-    const int maxslot = (w->src && !device_src) ? (T * k < E ? T * k : E) : 0;
+    /* how fetched experts reach the kernels, and the staging this call needs */
+    Fetcher f;
+    memset(&f, 0, sizeof f);
+    f.w = w;
+    f.I = I;
+    f.L = L;
+    f.st = st;
+    f.hc = hc;
+    f.geo = k3g_expert_layout(L, I);
+    f.t13 = fast ? k3k_tiled_mxfp4_bytes(I, L) : 0;
+    f.t2 = fast ? k3k_tiled_mxfp4_bytes(L, I) : 0;
+    if (!w->src) f.how = F_DIRECT;
+    else if (hc) f.how = (fast && hc->bank->layout != K3G_EXPERT_MXFP4_TILED) ? F_DEV_TILE : F_DIRECT;
+    else f.how = fast ? F_HOST_TILE : F_HOST_STAGE;
+    const size_t geo_b = ((size_t)f.geo.nbytes + 255) & ~(size_t)255;
+    f.slot_bytes = fast ? ((2 * f.t13 + f.t2 + 255) & ~(size_t)255) : geo_b;
+    const int pairs = T * k < E ? T * k : E;
+    f.maxslot = f.how == F_DIRECT ? 0 : pairs;
     const size_t xb = ((size_t)T * d * 4 + 255) & ~(size_t)255;
-    unsigned char *sb = (unsigned char *)stage(s, 2 * xb + (size_t)maxslot * geo.nbytes);
+    const size_t nring = f.how == F_HOST_TILE ? 2 : 0;
+    unsigned char *sb = (unsigned char *)stage(
+        s, 2 * xb + nring * geo_b + (size_t)f.maxslot * f.slot_bytes);
     float *xd = (float *)sb, *od = (float *)(sb + xb);
+    f.ring[0] = sb + 2 * xb;
+    f.ring[1] = sb + 2 * xb + geo_b;
+    f.slots = sb + 2 * xb + nring * geo_b;
+
     K3G_CHECK(hipMemcpyAsync(xd, x, (size_t)T * d * 4, hipMemcpyHostToDevice, st));
     if (k3g_route(ctx, &G, xd, T, ctx->idx, ctx->wt, st) != 0) k3g_fatal("k3_moe: router launch");
-
-    int *ridx = (int *)malloc((size_t)T * k * sizeof(int));
-    float *rwt = (float *)malloc((size_t)T * k * sizeof(float));
-    int *last = (int *)malloc((size_t)k * sizeof(int));
-    float *lastw = (float *)malloc((size_t)k * sizeof(float));
-    if (!ridx || !rwt || !last || !lastw) k3g_fatal("k3_moe: out of host memory");
+    ctx->paths = 0;
+    host_scratch(s, (size_t)T * k, E);
+    int *ridx = s->ridx;
+    float *rwt = s->rwt;
+    int last[K3_MAX_TOPK];
+    float lastw[K3_MAX_TOPK];
     K3G_CHECK(hipMemcpyAsync(ridx, ctx->idx, (size_t)T * k * 4, hipMemcpyDeviceToHost, st));
     K3G_CHECK(hipMemcpyAsync(rwt, ctx->wt, (size_t)T * k * 4, hipMemcpyDeviceToHost, st));
     if (k3g_sync(ctx, NULL) != 0) k3g_fatal("k3_moe: device error in the router");
@@ -360,110 +717,78 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         }
     }
 
-    K3gCache *hc_end = NULL;
-    if (w->src) {
-        Fetcher f;
-        memset(&f, 0, sizeof f);
-        f.s = s;
-        f.w = w;
-        f.E = E;
-        f.I = I;
-        f.L = L;
-        f.st = st;
-        f.device_src = device_src;
-        f.geo = geo;
-        f.slots = sb + 2 * xb;
-        f.maxslot = maxslot;
-        f.slot_of = (int *)malloc((size_t)E * sizeof(int));
-        f.table = (K3ExpertQ *)calloc((size_t)E, sizeof(K3ExpertQ));
-        f.have = (unsigned char *)calloc((size_t)E, 1);
-        if (!f.slot_of || !f.table || !f.have) k3g_fatal("k3_moe: out of host memory");
-        K3gCache *hc = device_src ? k3gc_of_src(w->src) : NULL;
-        if (hc && hc->bank->layout != K3G_EXPERT_MXFP4)
-            k3g_fatal("k3_moe: an HBM cache used through the drop-in must hold checkpoint-"
-                      "layout expert runs");
-        /* every slot handed out during this call stays put until its kernels are done */
-        if (hc) k3gc_step_begin(hc);
-        const int per_token = mode == 0 || T <= 1 || cache_only;
-        if (per_token) {
-            /* src/core/k3_ops.c:604-627 */
-            for (int t = 0; t < T; t++) {
-                int *it = ridx + (size_t)t * k;
-                int ids[K3_MAX_TOPK], nk = 0;
-                for (int j = 0; j < k; j++) if (it[j] >= 0) ids[nk++] = it[j];
-                if (!cache_only && w->src->getmany) w->src->getmany(w->src, w->layer, ids, nk);
-                for (int j = 0; j < k; j++) {
-                    if (it[j] < 0) continue;
-                    if (fetch_one(&f, it[j], cache_only) != 0) {
-                        if (!cache_only) drop_msg(w->layer, it[j], "token");
-                        it[j] = -1;
-                    }
-                }
-            }
-        } else {
-            /* src/core/k3_ops.c:707-766: 64-token chunks, unique experts in first-seen
-             * order, one get() each */
-            int *uniq = (int *)malloc((size_t)64 * k * sizeof(int));
-            unsigned char *seen = (unsigned char *)malloc((size_t)E);
-            if (!uniq || !seen) k3g_fatal("k3_moe_prefill: out of host memory");
-            for (int t0 = 0; t0 < T; t0 += 64) {
-                const int n = T - t0 < 64 ? T - t0 : 64;
-                memset(seen, 0, (size_t)E);
-                int nu = 0;
-                for (int t = t0; t < t0 + n; t++)
-                    for (int j = 0; j < k; j++) {
-                        const int e = ridx[(size_t)t * k + j];
-                        if (e >= 0 && e < E && !seen[e]) { seen[e] = 1; uniq[nu++] = e; }
-                    }
-                if (n > 1 && w->src->getmany) w->src->getmany(w->src, w->layer, uniq, nu);
-                if (n == 1 && w->src->getmany) w->src->getmany(w->src, w->layer, ridx + (size_t)t0 * k, k);
-                if (n == 1) {
-                    /* a one-token chunk takes k3_moe's per-slot path (:709-710) */
-                    for (int j = 0; j < k; j++) {
-                        int *e = ridx + (size_t)t0 * k + j;
-                        if (*e >= 0 && fetch_one(&f, *e, 0) != 0) {
-                            drop_msg(w->layer, *e, "token");
-                            *e = -1;
-                        }
-                    }
-                    continue;
-                }
-                for (int u = 0; u < nu; u++) {
-                    if (fetch_one(&f, uniq[u], 0) == 0) continue;
-                    drop_msg(w->layer, uniq[u], "chunk");
-                    for (int t = t0; t < t0 + n; t++)
-                        for (int j = 0; j < k; j++)
-                            if (ridx[(size_t)t * k + j] == uniq[u]) ridx[(size_t)t * k + j] = -1;
-                }
-            }
-            free(uniq);
-            free(seen);
-        }
+    if (!w->src) {
+        K3G_CHECK(hipMemcpyAsync(ctx->idx, ridx, (size_t)T * k * 4, hipMemcpyHostToDevice, st));
+        K3G_CHECK(hipMemcpyAsync(ctx->wt, rwt, (size_t)T * k * 4, hipMemcpyHostToDevice, st));
+        if (k3g_experts(ctx, &G, xd, T, ctx->idx, ctx->wt, od, st) != 0)
+            k3g_fatal("k3_moe: launch failed");
+    } else {
+        f.slot_of = s->slot_of;
+        f.table = s->table;
+        f.have = s->have;
+        memset(f.have, 0, (size_t)E);
         if (s->cap_e < E) {
-            if (s->eq_dev) K3G_CHECK(hipFree(s->eq_dev));
+            if (s->eq_dev) {
+                K3G_CHECK(hipDeviceSynchronize());
+                K3G_CHECK(hipFree(s->eq_dev));
+            }
             K3G_CHECK(hipMalloc((void **)&s->eq_dev, (size_t)E * sizeof(K3ExpertQ)));
             s->cap_e = E;
         }
-        K3G_CHECK(hipMemcpyAsync(s->eq_dev, f.table, (size_t)E * sizeof(K3ExpertQ),
-                                 hipMemcpyHostToDevice, st));
-        G.expert_fmt = 0;
         G.experts = s->eq_dev;
-        K3G_CHECK(hipStreamSynchronize(st));
-        free(f.slot_of);
-        free(f.table);
-        free(f.have);
-        /* the misses copy on the cache's stream: the expert kernels wait for them */
-        if (hc) k3gc_wait(hc, st);
-        hc_end = hc;
+        const int batched = mode == 1 && T > 1 && !cache_only;
+        /* every slot a group fetches stays put until the group's kernels are done: a
+         * group's experts must fit the cache's unpinned slots together */
+        int cap = E;
+        if (hc) {
+            int pinned = 0;
+            for (int i = 0; i < hc->nslot; i++) pinned += hc->pinned[i] != 0;
+            cap = hc->nslot - pinned;
+            if (cap < 1) k3g_fatal("k3_moe: every slot of the HBM cache is pinned");
+        }
+        for (int t0 = 0; t0 < T;) {
+            const int t1 = hc ? next_group(s, ridx, k, E, T, t0, batched ? 64 : 1, cap) : T;
+            if (hc) k3gc_step_begin(hc);
+            fetch_tokens(&f, s, ridx, k, E, t0, t1, batched, cache_only);
+            /* the group's experts into the device table, as kernel arguments */
+            K3kEqSet set;
+            memset(&set, 0, sizeof set);
+            memset(s->seen, 0, (size_t)E);
+            for (size_t p = (size_t)t0 * k; p < (size_t)t1 * k; p++) {
+                const int e = ridx[p];
+                if (e < 0 || e >= E || s->seen[e]) continue;
+                s->seen[e] = 1;
+                set.e[set.n] = e;
+                set.q[set.n] = f.table[e];
+                if (++set.n == K3K_EQSET) {
+                    if (k3k_set_experts(s->eq_dev, &set, st) != 0)
+                        k3g_fatal("k3_moe: expert table update failed");
+                    set.n = 0;
+                }
+            }
+            if (set.n && k3k_set_experts(s->eq_dev, &set, st) != 0)
+                k3g_fatal("k3_moe: expert table update failed");
+            const size_t pk = (size_t)t0 * k, np = (size_t)(t1 - t0) * k;
+            K3G_CHECK(hipMemcpyAsync(ctx->idx + pk, ridx + pk, np * 4, hipMemcpyHostToDevice, st));
+            K3G_CHECK(hipMemcpyAsync(ctx->wt + pk, rwt + pk, np * 4, hipMemcpyHostToDevice, st));
+            /* the misses copy on the cache's stream: the routed experts wait for them
+             * (the shared expert does not) */
+            if (hc && hc->copies_pending) {
+                k3g_ctx_routed_wait(ctx, hc->last_copy);
+                hc->copies_pending = 0;
+            }
+            if (k3g_experts(ctx, &G, xd + (size_t)t0 * d, t1 - t0, ctx->idx + pk, ctx->wt + pk,
+                            od + (size_t)t0 * d, st) != 0)
+                k3g_fatal("k3_moe: launch failed");
+            if (hc) k3gc_step_end(hc, st);
+            /* the host routing of this group travels before the next group edits it */
+            K3G_CHECK(hipStreamSynchronize(st));
+            t0 = t1;
+        }
     }
-
-    K3G_CHECK(hipMemcpyAsync(ctx->idx, ridx, (size_t)T * k * 4, hipMemcpyHostToDevice, st));
-    K3G_CHECK(hipMemcpyAsync(ctx->wt, rwt, (size_t)T * k * 4, hipMemcpyHostToDevice, st));
-    if (k3g_experts(ctx, &G, xd, T, ctx->idx, ctx->wt, od, st) != 0)
-        k3g_fatal("k3_moe: launch failed");
-    if (hc_end) k3gc_step_end(hc_end, st);
     K3G_CHECK(hipMemcpyAsync(out, od, (size_t)T * d * 4, hipMemcpyDeviceToHost, st));
     if (k3g_sync(ctx, NULL) != 0) k3g_fatal("k3_moe: device error");
+    g_last_paths = ctx->paths;
 
     /* idx/wt hold the last token's routing when the engine's per-token path produced
      * it; the batched prefill path leaves them untouched (src/core/k3_ops.c:699-714).
@@ -474,10 +799,6 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         memcpy(idx_out, last, (size_t)k * sizeof(int));
         memcpy(wt_out, lastw, (size_t)k * sizeof(float));
     }
-    free(ridx);
-    free(rwt);
-    free(last);
-    free(lastw);
     pthread_mutex_unlock(&g_lock);
 }
 

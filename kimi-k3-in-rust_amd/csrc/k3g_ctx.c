@@ -122,20 +122,31 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t maxt = (P + 127) / 128 + E;
     const size_t o_xb = carve(&at, 2 * T * d128 * 2), o_hb = carve(&at, 2 * P * I128 * 2);
     const size_t o_hsb = carve(&at, 2 * T * (SI128 ? SI128 : 128) * 2);
-    /* the shared expert's K-slice sums when few columns leave the GPU idle */
+    /* the dense GEMMs' K-slice sums when few columns leave the GPU idle: the shared
+     * expert's gate/up and down, the latent down and up projections */
     size_t part = 0;
     if (SI) {
         const size_t pg = k3k_gemm_part_bytes((int)((SI + 255) / 256), (int)(2 * SI));
         const size_t pd = k3k_gemm_part_bytes((int)((d + 511) / 512), (int)d);
         part = pg > pd ? pg : pd;
     }
+    if (L != d) {
+        const size_t pz = k3k_gemm_part_bytes((int)((L + 511) / 512), (int)L);
+        const size_t pu = k3k_gemm_part_bytes((int)((d + 511) / 512), (int)d);
+        if (pz > part) part = pz;
+        if (pu > part) part = pu;
+    }
     const size_t o_kpart = carve(&at, part ? part : 16);
+    const size_t L128 = (L + 127) / 128 * 128;
+    const size_t o_zb = carve(&at, L != d ? 2 * T * L128 * 2 : 16);
+    const size_t o_zflag = carve(&at, 4);
     const size_t o_rtpart = carve(&at, k3k_router_part_bytes());
     const size_t o_rtctr = carve(&at, 512 * 128);
     const size_t o_tiles = carve(&at, maxt * 16), o_ntiles = carve(&at, 4);
     const size_t o_xflag = carve(&at, 4);
     const size_t d512 = (d + 511) / 512 * 512, I512 = (I + 511) / 512 * 512;
-    const size_t o_xq8b = carve(&at, T * d512 + T * d512 / 32);
+    const size_t L512 = (L + 511) / 512 * 512, q512 = d512 > L512 ? d512 : L512;
+    const size_t o_xq8b = carve(&at, T * q512 + T * q512 / 32);
     const size_t o_hq8b = carve(&at, P * I512 + P * I512 / 32);
     /* two banks of counters, one per call in turn; each a multiple of 256 bytes */
     c->sync_bytes = (k3k_decode_sync_bytes(T4, (int)d, (int)E, (int)k, (int)I, (int)SI) + 255) &
@@ -179,6 +190,8 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->xb = (uint16_t *)(b + o_xb);
     c->hb = (uint16_t *)(b + o_hb);
     c->hsb = (uint16_t *)(b + o_hsb);
+    c->zb = (uint16_t *)(b + o_zb);
+    c->zflag = (int32_t *)(b + o_zflag);
     c->kpart = (float *)(b + o_kpart);
     c->rtpart = (double *)(b + o_rtpart);
     c->rtctr = (int32_t *)(b + o_rtctr);
@@ -299,20 +312,59 @@ static int fusable(const K3gCtx *c, const K3gLayer *L, int T)
                                      L->shared_inter % 32 == 0));
 }
 
-/* The grouped GEMMs cover the same layer shape at any token count. */
+/* The grouped GEMMs cover any token count on tiled experts, with the shared expert and
+ * the latent projections (when present) in the tiled bf16 layout. */
 static int gemmable(const K3gCtx *c, const K3gLayer *L)
 {
     const int lat = L->latent > 0 ? L->latent : L->hidden;
-    return c->fused && L->expert_fmt == K3G_EXPERT_MXFP4_TILED && !L->down && !L->up &&
-           !L->latent_norm && lat == L->hidden && L->hidden % 32 == 0 && L->inter % 32 == 0 &&
-           (L->shared_inter == 0 || (L->wdt == K3_WBF16 && L->shared_fmt == 1 &&
-                                     L->shared_inter % 32 == 0));
+    if (!c->fused || L->expert_fmt != K3G_EXPERT_MXFP4_TILED || L->hidden % 32 ||
+        L->inter % 32 || lat % 32)
+        return 0;
+    const int bf16_tiled = L->wdt == K3_WBF16 && L->shared_fmt == 1;
+    if (L->shared_inter && (!bf16_tiled || L->shared_inter % 32)) return 0;
+    if ((L->down || L->up) && !bf16_tiled) return 0;
+    return 1;
 }
+
+static int run_fused(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out,
+                     int32_t *idx, float *wt, int given, hipStream_t st);
 
 static int r128(int v) { return (v + 127) / 128 * 128; }
 static int r512(int v) { return (v + 511) / 512 * 512; }
 
 void k3g_ctx_set_fp8(K3gCtx *c, int on) { if (c) c->gemm_fp8 = on; }
+
+/* K slices of a dense GEMM (whole 128-column steps only) */
+static int dense_ksplit(int nft, int T, int K)
+{
+    return K % 128 ? 1 : k3k_gemm_ksplit(nft, (T + 127) / 128, K);
+}
+
+/* out [T][rows] = W B for a dense tiled-bf16 matrix W [rows][K] and two-piece B [2][T][ldb]
+ * (piece 1 skipped when *lo_flag == 0), fp32 rows at stride ldo. */
+static int dense_gemm(K3gCtx *c, const void *W, int rows, int K, const uint16_t *b, int ldb,
+                      const int32_t *lo_flag, int T, float *out, int ldo, hipStream_t st)
+{
+    K3kGemm s;
+    memset(&s, 0, sizeof s);
+    s.mode = 1;
+    s.afmt = 1;
+    s.rows = rows;
+    s.K = K;
+    s.ldb = ldb;
+    s.wa = (const uint16_t *)W;
+    s.b = b;
+    s.bpiece = (long long)T * ldb;
+    s.dense_rows = T;
+    s.npieces = 2;
+    s.lo_flag = lo_flag;
+    s.out = out;
+    s.ldo = ldo;
+    s.nft = (rows + 511) / 512;
+    s.ksplit = dense_ksplit(s.nft, T, K);
+    s.part = c->kpart;
+    return k3k_gemm(&s, st);
+}
 
 /* Routed and shared experts as grouped GEMMs on the bf16 matrix cores (k3g_gemm.hip), or
  * the routed experts on the FP4 x FP8 ones (fp8): dispatch -> column tiles -> x pieces ->
@@ -325,6 +377,8 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     const int d = L->hidden, E = L->n_experts, k = L->topk, I = L->inter;
     const int SI = full ? L->shared_inter : 0, P = T * k;
     const int d128 = r128(d), I128 = r128(c->inter), SI128 = r128(c->shared_inter);
+    const int lat = L->latent > 0 ? L->latent : d, lat128 = r128(lat);
+    const int projected = L->down != NULL;
     int rc = 0;
     k3g_stage_begin(c, K3G_ST_DISPATCH, st);
     rc |= k3k_dispatch_tiles(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm,
@@ -333,27 +387,45 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     const int d512 = r512(d), I512 = r512(c->inter);
     k3g_stage_begin(c, K3G_ST_PIECES, st);
     rc |= k3k_xpieces(x, T, d, d128, c->xb, (long long)T * d128, c->xflag, st);
-    if (fp8)
+    if (fp8 && !projected)
         rc |= k3k_xq8(x, T, d, d512, c->xq8b, c->xq8b + (size_t)T * d512, st);
     k3g_stage_end(c, K3G_ST_PIECES, st);
+    /* the routed experts' input: x, or its latent projection z = down x as two bf16
+     * pieces (piece 1 always taken) */
+    const uint16_t *rb = c->xb;
+    int ldr = d128;
+    const int32_t *rflag = c->xflag;
+    if (projected) {
+        k3g_stage_begin(c, K3G_ST_LATENT, st);
+        rc |= dense_gemm(c, L->down, lat, d, c->xb, d128, c->xflag, T, c->z, lat, st);
+        rc |= k3k_xpieces(c->z, T, lat, lat128, c->zb, (long long)T * lat128, c->zflag, st);
+        if (fp8) {
+            const int l512 = r512(lat);
+            rc |= k3k_xq8(c->z, T, lat, l512, c->xq8b, c->xq8b + (size_t)T * l512, st);
+        }
+        k3g_stage_end(c, K3G_ST_LATENT, st);
+        rb = c->zb;
+        ldr = lat128;
+        rflag = NULL;
+    }
 
     K3kGemm g;
     memset(&g, 0, sizeof g);
     g.mode = 0;
     g.afmt = 0;
     g.rows = I;
-    g.K = d;
-    g.ldb = d128;
+    g.K = lat;
+    g.ldb = ldr;
     g.eq = L->experts;
-    g.b = c->xb;
-    g.bpiece = (long long)T * d128;
+    g.b = rb;
+    g.bpiece = (long long)T * ldr;
     g.perm = c->perm;
     g.topk = k;
     g.tiles = c->tiles;
     g.ntiles = c->ntiles;
     g.max_tiles = (P + 127) / 128 + (E < P ? E : P);
     g.npieces = 2;
-    g.lo_flag = c->xflag;
+    g.lo_flag = rflag;
     g.h = c->hb;
     g.hpiece = (long long)P * I128;
     g.ldh = I128;
@@ -365,6 +437,11 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     if (SI > 0) {
         s.afmt = 1;
         s.rows = SI;
+        s.K = d;
+        s.ldb = d128;
+        s.b = c->xb;
+        s.bpiece = (long long)T * d128;
+        s.lo_flag = c->xflag;
         s.eq = NULL;
         s.wa = (const uint16_t *)L->sh1;
         s.wb = (const uint16_t *)L->sh3;
@@ -376,7 +453,7 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         s.hpiece = (long long)T * SI128;
         s.ldh = SI128;
         s.nft = (SI + 255) / 256;
-        s.ksplit = k3k_gemm_ksplit(s.nft, (T + 127) / 128, d);
+        s.ksplit = dense_ksplit(s.nft, T, d);
         s.part = c->kpart;
         k3g_stage_begin(c, K3G_ST_SH_GATEUP, st);
         rc |= k3k_gemm(&s, st);
@@ -399,7 +476,7 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         s.ldo = d;
         s.scatter = 0;
         s.nft = (d + 511) / 512;
-        s.ksplit = k3k_gemm_ksplit(s.nft, (T + 127) / 128, SI);
+        s.ksplit = dense_ksplit(s.nft, T, SI);
         k3g_stage_begin(c, K3G_ST_SH_DOWN, st);
         rc |= k3k_gemm(&s, st);
         k3g_stage_end(c, K3G_ST_SH_DOWN, st);
@@ -411,9 +488,10 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         c->routed_wait = NULL;
     }
     if (fp8) {
+        const int l512 = r512(lat);
         g.bq = c->xq8b;
-        g.bs = c->xq8b + (size_t)T * d512;
-        g.ldb = d512;
+        g.bs = c->xq8b + (size_t)T * l512;
+        g.ldb = l512;
         g.hq = c->hq8b;
         g.hs = c->hq8b + (size_t)P * I512;
         g.ldhq = I512;
@@ -432,7 +510,7 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     if (g.trace) g.trace += 4 * 8 * (size_t)((g.max_tiles + 7) / 8) * (size_t)((I + 127) / 128);
 
     g.mode = 1;
-    g.rows = d;
+    g.rows = lat;
     g.K = I;
     g.ldb = I128;
     g.b = c->hb;
@@ -440,9 +518,9 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     g.lo_flag = NULL;
     g.h = NULL;
     g.out = contrib;
-    g.ldo = d;
+    g.ldo = lat;
     g.scatter = 1;
-    g.nft = (d + 511) / 512;
+    g.nft = (lat + 511) / 512;
     if (fp8) {
         g.bq = c->hq8b;
         g.bs = c->hq8b + (size_t)P * I512;
@@ -458,10 +536,29 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     rc |= fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
     k3g_stage_end(c, K3G_ST_DOWN, st);
 
-    if (full) {
+    if (full && !projected && !L->up && !L->latent_norm) {
         k3g_stage_begin(c, K3G_ST_COMBINE, st);
         rc |= k3k_combine(contrib, idx, wt, T, k, d, SI > 0 ? c->sh_out : NULL, out, st);
         k3g_stage_end(c, K3G_ST_COMBINE, st);
+    } else if (full) {
+        /* the routed aggregate at latent width, its RMSNorm, up = the up projection as a
+         * dense GEMM on its two bf16 pieces, then + the shared expert */
+        k3g_stage_begin(c, K3G_ST_COMBINE, st);
+        rc |= k3k_combine(contrib, idx, wt, T, k, lat, NULL, c->accl, st);
+        if (L->latent_norm)
+            rc |= k3k_rmsnorm(c->accl, c->accl, L->latent_norm, lat, T, L->rms_eps, st);
+        k3g_stage_end(c, K3G_ST_COMBINE, st);
+        if (L->up) {
+            k3g_stage_begin(c, K3G_ST_LATENT, st);
+            rc |= k3k_xpieces(c->accl, T, lat, lat128, c->zb, (long long)T * lat128, c->zflag,
+                              st);
+            rc |= dense_gemm(c, L->up, d, lat, c->zb, lat128, NULL, T, out, d, st);
+            k3g_stage_end(c, K3G_ST_LATENT, st);
+        } else if (hipMemcpyAsync(out, c->accl, (size_t)T * d * 4, hipMemcpyDeviceToDevice, st) !=
+                   hipSuccess) {
+            rc = -1;
+        }
+        if (SI > 0) rc |= k3k_add(out, c->sh_out, (size_t)T * d, st);
     }
     return rc ? -1 : 0;
 }
@@ -565,8 +662,20 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     const int SI = L->shared_inter, lat = L->latent > 0 ? L->latent : d;
     const int projected = L->down != NULL;
     int rc = 0;
-    if (gemmable(c, L))
+    if (fusable(c, L, T)) {
+        /* one launch: the copies it needs must be in before it starts */
+        if (c->routed_wait) {
+            if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) return -1;
+            c->routed_wait = NULL;
+        }
+        c->paths |= 2;
+        return run_fused(c, L, x, T, out, (int32_t *)idx, (float *)wt, 1, st);
+    }
+    if (gemmable(c, L)) {
+        c->paths |= 4;
         return experts_gemm(c, L, x, T, idx, wt, out, c->contrib, c->gemm_fp8, 1, st);
+    }
+    c->paths |= 1;
     if (c->routed_wait) {
         if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) return -1;
         c->routed_wait = NULL;
@@ -614,6 +723,60 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
     return rc ? -1 : 0;
 }
 
+/* The fused decode kernel for T <= 4 tokens: with given = 0 it routes inside (idx/wt
+ * receive the routing), with given = 1 it takes the routing in idx/wt. */
+static int run_fused(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out,
+                     int32_t *idx, float *wt, int given, hipStream_t st)
+{
+    K3kDecode a;
+    memset(&a, 0, sizeof a);
+    a.T = T;
+    a.d = L->hidden;
+    a.E = L->n_experts;
+    a.k = L->topk;
+    a.I = L->inter;
+    a.SI = L->shared_inter;
+    a.renorm = L->renorm;
+    a.routed_scale = L->routed_scale;
+    a.b1 = L->act_b1;
+    a.b2 = L->act_b2;
+    a.gate = L->gate;
+    a.bias = L->bias;
+    a.eq = L->experts;
+    a.sh1 = (const uint16_t *)L->sh1;
+    a.sh3 = (const uint16_t *)L->sh3;
+    a.sh2 = (const uint16_t *)L->sh2;
+    a.x = x;
+    a.out = out;
+    a.idx = idx;
+    a.wt = wt;
+    a.rs = c->rs;
+    a.xq8 = c->xq8;
+    a.xq16 = c->xq16;
+    a.gpart = c->gpart;
+    a.hq8 = c->hq8;
+    a.sgpart = c->sgpart;
+    a.hq16 = c->hq16;
+    a.contrib = c->dcontrib;
+    a.shpart = c->shpart;
+    a.rpart = c->rpart;
+    const int words = (int)(c->sync_bytes / 4);
+    a.sync = c->sync + (size_t)(c->epoch & 1) * words;
+    a.sync_clear = c->sync + (size_t)((c->epoch & 1) ^ 1) * words;
+    a.sync_words = words;
+    a.err = c->err;
+    a.stats = c->stats;
+    a.force = c->force_exact;
+    a.given = given;
+    a.spin_limit = 1ll << 21;
+    a.trace = c->trace;
+    k3g_stage_begin(c, K3G_ST_FUSED, st);
+    const int rc = k3k_decode_fused(&a, st);
+    k3g_stage_end(c, K3G_ST_FUSED, st);
+    if (rc == 0) c->epoch = (c->epoch + 1) & 0x3fffffff;   /* the next call's bank */
+    return rc;
+}
+
 int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int32_t *idx,
             float *wt, void *stream)
 {
@@ -622,52 +785,8 @@ int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int
     if (!wt) wt = c->wt;
     if (!fits(c, L, T)) return -1;
     if (fusable(c, L, T)) {
-        K3kDecode a;
-        memset(&a, 0, sizeof a);
-        a.T = T;
-        a.d = L->hidden;
-        a.E = L->n_experts;
-        a.k = L->topk;
-        a.I = L->inter;
-        a.SI = L->shared_inter;
-        a.renorm = L->renorm;
-        a.routed_scale = L->routed_scale;
-        a.b1 = L->act_b1;
-        a.b2 = L->act_b2;
-        a.gate = L->gate;
-        a.bias = L->bias;
-        a.eq = L->experts;
-        a.sh1 = (const uint16_t *)L->sh1;
-        a.sh3 = (const uint16_t *)L->sh3;
-        a.sh2 = (const uint16_t *)L->sh2;
-        a.x = x;
-        a.out = out;
-        a.idx = idx;
-        a.wt = wt;
-        a.rs = c->rs;
-        a.xq8 = c->xq8;
-        a.xq16 = c->xq16;
-        a.gpart = c->gpart;
-        a.hq8 = c->hq8;
-        a.sgpart = c->sgpart;
-        a.hq16 = c->hq16;
-        a.contrib = c->dcontrib;
-        a.shpart = c->shpart;
-        a.rpart = c->rpart;
-        const int words = (int)(c->sync_bytes / 4);
-        a.sync = c->sync + (size_t)(c->epoch & 1) * words;
-        a.sync_clear = c->sync + (size_t)((c->epoch & 1) ^ 1) * words;
-        a.sync_words = words;
-        a.err = c->err;
-        a.stats = c->stats;
-        a.force = c->force_exact;
-        a.spin_limit = 1ll << 21;
-        a.trace = c->trace;
-        k3g_stage_begin(c, K3G_ST_FUSED, st);
-        const int rc = k3k_decode_fused(&a, st);
-        k3g_stage_end(c, K3G_ST_FUSED, st);
-        if (rc == 0) c->epoch = (c->epoch + 1) & 0x3fffffff;   /* the next call's bank */
-        return rc;
+        c->paths |= 2;
+        return run_fused(c, L, x, T, out, idx, wt, 0, st);
     }
     if (k3g_route(c, L, x, T, idx, wt, st) != 0) return -1;
     return k3g_experts(c, L, x, T, idx, wt, out, st);

@@ -55,8 +55,13 @@ struct K3gCtx {
     size_t sync_bytes;
     int epoch;                   /* fused-kernel calls; its parity picks the counter bank */
     int fused;                   /* use the fused decode kernel when the layer allows */
+    int paths;                   /* kernels the calls ran since it was cleared: bit 0 the
+                                  * staged kernels, 1 the fused decode kernel, 2 the
+                                  * grouped GEMMs */
     /* grouped GEMMs on the matrix cores (more than 4 tokens, tiled layouts) */
     uint16_t *xb, *hb, *hsb;     /* bf16 pieces of x [2][T][d128], h [2][T*k][I128], shared h */
+    uint16_t *zb;                /* bf16 pieces of the latent input / aggregate [2][T][L128] */
+    int32_t *zflag;              /* their piece-1 flag (written, not read) */
     float *kpart;                /* K-slice sums of the shared expert's GEMMs */
     double *rtpart;              /* K-slice sums of the router's matrix-core logits */
     int32_t *rtctr;              /* their per-tile arrival counts (zero between calls) */

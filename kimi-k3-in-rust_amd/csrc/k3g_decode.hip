@@ -487,6 +487,7 @@ struct K3Dec {
                                                bool wg_slices)
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
+        if (a.given) return;
         const int tk = k3d_uniform(tk_);
         const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
         const int e = tk / G.KSR, r = tk - e * G.KSR;
@@ -592,6 +593,12 @@ struct K3Dec {
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        if (a.given) {
+            /* the routing came with the call: publish it once x's pieces exist */
+            if (!k3d_wait_event(a.sync, G.eX, 0, a.spin_limit, a.err, lane)) return;
+            k3d_set_event(a.sync, G.eSEL, lane);
+            return;
+        }
         if (!k3d_wait_event(a.sync, G.eR, 0, a.spin_limit, a.err, lane)) return;
         /* instrumentation: after the trace's [ticket][2] stamps, the select's own phases */
         if (a.trace && lane == 0) a.trace[3 * G.total] = wall_clock64();

@@ -68,6 +68,8 @@ typedef struct {
     int sync_words;               /* ints per bank */
     int *err, *stats;
     int force;
+    int given;                    /* 1: idx/wt hold the routing already (entries < 0 are
+                                   * left out); the router tickets do nothing */
     long long spin_limit;
     unsigned long long *trace;    /* optional: [ticket][2] start/end wall-clock stamps */
 } K3kDecode;

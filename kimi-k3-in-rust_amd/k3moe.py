@@ -137,6 +137,10 @@ def lib() -> C.CDLL:
         L.k3_mxfp4_dequant.restype = None
         L.k3moe_forget_weights.argtypes = []
         L.k3moe_forget_weights.restype = None
+        L.k3moe_invalidate_weights.argtypes = [vp, sz]
+        L.k3moe_invalidate_weights.restype = None
+        L.k3moe_last_kernels.argtypes = []
+        L.k3moe_last_kernels.restype = i
         L.k3g_expert_layout.argtypes = [i, i]
         L.k3g_expert_layout.restype = K3gExpertLayout
         L.k3g_ctx_create.argtypes = [C.POINTER(vp), i, C.POINTER(K3gLayer), i]

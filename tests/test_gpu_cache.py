@@ -97,8 +97,8 @@ def test_dropin_through_the_hbm_cache(gpu, prefill, T):
     bank = k3moe.Bank(1, 16, 256, 128, k3moe.K3G_EXPERT_MXFP4)
     bank.fill_from_layer(layer, 0)
     slot = (bank.expert_bytes + 65535) // 65536 * 65536
-    # the drop-in stages a whole call's experts before its kernels run, so the cache must
-    # hold their union (here up to all 16)
+    # a cache that holds the call's whole union runs it as one group, as the host source
+    # does, so the two give the same bits
     cache = k3moe.Cache(bank, topk=4, budget_bytes=17 * slot)
     w.src = cache.src_ptr
     w.layer = 0

@@ -1,0 +1,227 @@
+"""GPU parity of the drop-in entry points (k3_moe, k3_moe_prefill) on the matrix-core
+kernels: bf16 shared weights and MXFP4 experts from a source run the fused decode kernel
+(routing given, up to 4 tokens) or the grouped GEMMs; experts come from a host source
+(copied and tiled per call) or from the HBM expert cache (a tiled bank served in place, a
+checkpoint-layout bank tiled per call). Checked against the oracle's k3_moe /
+k3_moe_prefill on the same seeded inputs: routing bit-exact, outputs within rel-L2 1e-4
+(the kernels measure about 1e-5 fused and 4e-5 grouped), no expert dropped, and the
+source sees the engine's request pattern. Each test prints its case first."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import k3moe
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+REL = 1e-4
+STAGED, FUSED, GROUPED = 1, 2, 4
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - np.asarray(b, np.float64)) /
+                 max(np.linalg.norm(np.asarray(b, np.float64)), 1e-30))
+
+
+def drops():
+    return C.c_long.in_dll(k3moe.lib(), "k3_expert_drops").value
+
+
+def dropin(w, cfg, x, prefill=False):
+    """One drop-in call: (out, idx, wt, kernels it ran)."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros_like(x)
+    idx = np.full(cfg.topk, -7, np.int32)
+    wt = np.zeros(cfg.topk, np.float32)
+    f = k3moe.lib().k3_moe_prefill if prefill else k3moe.lib().k3_moe
+    f(out.ctypes.data, x.ctypes.data, C.byref(w), C.byref(cfg), x.shape[0], idx.ctypes.data,
+      wt.ctypes.data, None)
+    return out, idx, wt, k3moe.lib().k3moe_last_kernels()
+
+
+def cache_weights(layer, cache):
+    """K3MoeW of a synthetic K2-shaped layer whose experts the HBM cache serves."""
+    w = k3moe.K3MoeW()
+    w.gate, w.bias = layer.gate.ctypes.data, layer.bias.ctypes.data
+    w.sh1, w.sh3, w.sh2 = layer.sh1.ctypes.data, layer.sh3.ctypes.data, layer.sh2.ctypes.data
+    w.wdt = k3moe.K3_WBF16
+    w.src = cache.src_ptr
+    w.layer = layer.layer
+    return w
+
+
+def tiled_bank(layer, layout=k3moe.K3G_EXPERT_MXFP4_TILED):
+    bank = k3moe.Bank(layer.layer + 1, layer.shape.n_experts, layer.shape.hidden,
+                      layer.shape.inter, layout)
+    bank.fill_from_layer(layer, layer.layer)
+    return bank
+
+
+# ----------------------------------------------------------------- host source ----
+
+@pytest.mark.parametrize("prefill,T,want", [(False, 1, FUSED), (False, 2, FUSED),
+                                            (False, 4, FUSED), (False, 7, GROUPED),
+                                            (True, 70, GROUPED)])
+def test_host_source_fast_path(gpu, prefill, T, want):
+    say(f"case: {'k3_moe_prefill' if prefill else 'k3_moe'} tiny K2 layer T={T}, host source, "
+        f"bf16 shared -> matrix-core kernels")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=41, device=False)
+    x = layer.tokens(T)
+    experts = list(range(layer.shape.n_experts))
+    w, cfg, keep = O.k2_weights(layer, experts)
+    d0 = drops()
+    out, idx, wt, paths = dropin(w, cfg, x, prefill)
+    gets = keep[1].s.gets
+    w2, cfg2, keep2 = O.k2_weights(layer, experts)
+    oo, oi, ow = O.oracle().moe(w2, cfg2, x, prefill=prefill)
+    r = rel_l2(out, oo)
+    say(f"  kernels {paths}, rel-L2 {r:.3e}")
+    assert paths == want
+    assert drops() == d0
+    assert r <= REL
+    assert gets == keep2[1].s.gets, "the source saw a different request pattern"
+    if not prefill:
+        assert np.array_equal(idx, oi)
+        np.testing.assert_allclose(wt, ow, rtol=1e-6)
+
+
+def test_cache_only_draft_routing(gpu):
+    """cache_only: each token keeps the routed experts the source holds resident, in slot
+    order, with weights divided by their float sum (src/core/k3_ops.c:585-594); resident()
+    serves them and the rest are skipped without a drop."""
+    say("case: k3_moe tiny layer T=5, cache_only with 4 routed experts not resident")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=43, device=False)
+    x = layer.tokens(5)
+    union = O.routed_union(layer, x)
+    absent = set(union[:4])
+    experts = [e for e in range(layer.shape.n_experts) if e not in absent]
+    w, cfg, keep = O.k2_weights(layer, experts)
+    w.cache_only = 1
+    d0 = drops()
+    out, idx, wt, paths = dropin(w, cfg, x)
+    w2, cfg2, keep2 = O.k2_weights(layer, experts)
+    w2.cache_only = 1
+    od0 = O.oracle().drops.value
+    oo, oi, ow = O.oracle().moe(w2, cfg2, x)
+    r = rel_l2(out, oo)
+    say(f"  kernels {paths}, rel-L2 {r:.3e}")
+    assert drops() == d0 and O.oracle().drops.value == od0
+    assert np.array_equal(idx, oi)
+    np.testing.assert_allclose(wt, ow, rtol=1e-6)
+    assert r <= REL
+    assert keep[1].s.gets == 0 and keep2[1].s.gets == 0
+    assert keep[1].s.residents == keep2[1].s.residents
+
+
+def test_weights_rewritten_in_place(gpu):
+    """A weight buffer rewritten with other weights at the same address (a ring of layer
+    buffers): the fingerprint catches a rewrite of the whole buffer, and
+    k3moe_invalidate_weights catches any change."""
+    say("case: k3_moe tiny layer T=3, gate and shared weights rewritten in place")
+    a = k3moe.SynthLayer(k3moe.TINY, seed=51, device=False)
+    b = k3moe.SynthLayer(k3moe.TINY, seed=52, device=False)
+    x = a.tokens(3)
+    experts = list(range(a.shape.n_experts))
+    w, cfg, keep = O.k2_weights(a, experts)
+    out_a, _, _, _ = dropin(w, cfg, x)
+    # rewrite every weight buffer the drop-in mirrors with layer b's values
+    for name in ("gate", "bias", "sh1", "sh3", "sh2"):
+        np.copyto(getattr(a, name), getattr(b, name))
+    out_b, _, _, _ = dropin(w, cfg, x)
+    wb, cfgb, keepb = O.k2_weights(a, experts)
+    ob, _, _ = O.oracle().moe(wb, cfgb, x)
+    say(f"  whole rewrite: rel-L2 {rel_l2(out_b, ob):.3e} (before: {rel_l2(out_a, ob):.3e})")
+    assert rel_l2(out_a, ob) > 1e-2
+    assert rel_l2(out_b, ob) <= REL
+    # one value the sampled fingerprint does not read
+    n = a.gate.nbytes
+    at = ((n - 8) // 63) // 2 // 4
+    a.gate[at] += np.float32(0.5)
+    k3moe.lib().k3moe_invalidate_weights(a.gate.ctypes.data, 4)
+    out_c, idx_c, _, _ = dropin(w, cfg, x)
+    wc, cfgc, keepc = O.k2_weights(a, experts)
+    oc, oic, _ = O.oracle().moe(wc, cfgc, x)
+    say(f"  invalidated one value: rel-L2 {rel_l2(out_c, oc):.3e}")
+    assert np.array_equal(idx_c, oic)
+    assert rel_l2(out_c, oc) <= REL
+
+
+# ------------------------------------------------------------- HBM expert cache ----
+
+@pytest.mark.parametrize("layout", ["tiled", "checkpoint"])
+def test_small_cache_never_drops(gpu, layout):
+    """A cache of top-k + 1 slots (the engine's minimum) through the drop-in: the tokens
+    run in groups whose experts fit, so nothing is dropped (the engine, token by token,
+    needs no more either)."""
+    lay = k3moe.K3G_EXPERT_MXFP4_TILED if layout == "tiled" else k3moe.K3G_EXPERT_MXFP4
+    say(f"case: tiny layer through a {layout} HBM cache of top-k + 1 slots, k3_moe T=6 and "
+        f"k3_moe_prefill T=70")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=61, layout="both")
+    bank = tiled_bank(layer, lay)
+    cache = k3moe.Cache(bank, topk=layer.shape.topk,
+                        budget_bytes=(layer.shape.topk + 1) * ((bank.expert_bytes + 65535) // 65536) * 65536)
+    assert cache.stats().nslot == layer.shape.topk + 1
+    w = cache_weights(layer, cache)
+    cfg = layer.cfg()
+    experts = list(range(layer.shape.n_experts))
+    for prefill, T in ((False, 6), (True, 70)):
+        x = layer.tokens(T, stream_base=7 * T)
+        d0 = drops()
+        out, idx, wt, paths = dropin(w, cfg, x, prefill)
+        wo, cfgo, keepo = O.k2_weights(layer, experts)
+        oo, oi, ow = O.oracle().moe(wo, cfgo, x, prefill=prefill)
+        r = rel_l2(out, oo)
+        say(f"  T={T}: kernels {paths}, rel-L2 {r:.3e}, evictions {cache.stats().evictions}")
+        assert drops() == d0
+        assert r <= REL
+        assert paths & (FUSED | GROUPED) and not paths & STAGED
+        if not prefill:
+            assert np.array_equal(idx, oi)
+    assert cache.stats().evictions > 0
+    cache.free()
+    bank.free()
+
+
+def test_k2_through_tiled_cache(gpu):
+    """The K2 layer through the drop-in with its experts in a tiled HBM cache: one token on
+    the fused decode kernel, 8 tokens on the grouped GEMMs, and a 64-token prefill through
+    a cache of 100 slots (fewer than the call's experts: several groups, evictions)."""
+    say("case: K2 layer, tiled HBM cache, k3_moe T=1 and T=8, k3_moe_prefill T=64 (100 slots)")
+    layer = k3moe.SynthLayer(k3moe.K2, seed=71, layout="tiled")
+    bank = tiled_bank(layer)
+    layer.release_experts()
+    slot = (bank.expert_bytes + 65535) // 65536 * 65536
+    cache = k3moe.Cache(bank, topk=8, budget_bytes=384 * slot)
+    w = cache_weights(layer, cache)
+    cfg = layer.cfg()
+    for T, want in ((1, FUSED), (8, GROUPED)):
+        x = layer.tokens(T, stream_base=300 + T)
+        d0 = drops()
+        out, idx, wt, paths = dropin(w, cfg, x)
+        oo, oi, ow = O.k2_forward(layer, x)
+        r = rel_l2(out, oo)
+        say(f"  T={T}: kernels {paths}, rel-L2 {r:.3e}")
+        assert paths == want and drops() == d0
+        assert np.array_equal(idx, oi)
+        assert r <= REL
+    cache.free()
+    small = k3moe.Cache(bank, topk=8, budget_bytes=100 * slot)
+    w = cache_weights(layer, small)
+    x = layer.tokens(64, stream_base=400)
+    d0 = drops()
+    out, _, _, paths = dropin(w, cfg, x, prefill=True)
+    st = small.stats()
+    say(f"  T=64 prefill: kernels {paths}, requests {st.requests}, evictions {st.evictions}")
+    assert drops() == d0 and st.evictions > 0 and paths == GROUPED
+    for t in (0, 17, 40, 63):
+        oo, _, _ = O.k2_forward(layer, x[t:t + 1])
+        r = rel_l2(out[t:t + 1], oo)
+        say(f"  token {t}: rel-L2 {r:.3e}")
+        assert r <= REL
+    small.free()
+    bank.free()
