@@ -50,12 +50,36 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(seconds: float, max_tokens: int, seed: int):
+def host_cpu():
+    """CPU model, sockets and physical cores of this host (lscpu)."""
+    info = {"model": platform.processor() or "cpu", "sockets": None, "physical_cores": None,
+            "logical_cpus": os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        f = {}
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                f[k.strip()] = v.strip()
+        info["model"] = f.get("Model name", info["model"])
+        if f.get("Socket(s)", "").isdigit():
+            info["sockets"] = int(f["Socket(s)"])
+        if f.get("Core(s) per socket", "").isdigit() and info["sockets"]:
+            info["physical_cores"] = int(f["Core(s) per socket"]) * info["sockets"]
+    except OSError:
+        pass
+    return info
+
+
+def cpu_baseline(seconds: float, max_tokens: int, seed: int, legs=("decode", "batch", "prefill")):
     """The engine's CPU kernels (k3_router, k3_matmul_mxfp4, k3_situ_glu, k3_matmul_bf16,
-    compiled from src/core/k3_ops.c with the engine's flags) composed as k3_moe for the
-    same K2 layer without identity latent projections; falls back to the C restatement
-    when the compiled engine kernels are not present. Median over a bounded sample of
-    decode tokens; expert regeneration on the host is outside the timed region."""
+    compiled from the engine's src/core/k3_ops.c with its flags: kind "reference"; the C
+    restatement when that library is absent: kind "port") composed as k3_moe /
+    k3_moe_prefill for the same K2 layers without identity latent projections. Expert
+    regeneration on the host is outside the timed regions.
+      decode: median over a bounded sample of 1-token calls (the c1 workload);
+      batch: one 64-token k3_moe_prefill call (64-token chunk) on the Zipf(1.1) layer;
+      prefill: 128 tokens (two 64-token chunks) of the Zipf(0.8) 4096-token prefill."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import k3moe
@@ -64,34 +88,51 @@ def cpu_baseline(seconds: float, max_tokens: int, seed: int):
     kind = "reference" if ref else "port"
     if ref:
         O.set_kernels(ref)
-    layer = k3moe.SynthLayer(k3moe.K2, seed=seed, layer=0, device=False)
-    times = []
-    for i in range(max_tokens):
-        x = layer.tokens(1, stream_base=5000 + i)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    cpu = host_cpu()
+    what = ("the engine's own kernels compiled from src/core/k3_ops.c" if ref else
+            "the C restatement of the engine's kernels")
+    res = {"cores": threads, "kind": kind, "cpu": cpu}
+    if "decode" in legs:
+        layer = k3moe.SynthLayer(k3moe.K2, seed=seed, layer=0, device=False)
+        times = []
+        for i in range(max_tokens):
+            x = layer.tokens(1, stream_base=5000 + i)
+            experts = O.routed_union(layer, x)
+            w, cfg, keep = O.k2_weights(layer, experts)
+            t0 = time.perf_counter()
+            O.oracle().moe(w, cfg, x)
+            times.append(time.perf_counter() - t0)
+            del keep
+            if sum(times) >= seconds and len(times) >= 3:
+                break
+        med = float(np.median(times))
+        res.update({"value": round(1e6 * med, 1), "unit": "us/token",
+                    "sample": f"{len(times)} decode tokens through the same K2 layer (median), "
+                              f"{what} composed as k3_moe without identity latent, OpenMP "
+                              f"{threads} threads on {cpu['model']}",
+                    "tokens_per_s": round(1.0 / med, 2),
+                    "GBps": round((K * B_EXPERT + B_SHARED + B_ROUTER + B_TOKEN) / med / 1e9, 2)})
+        del layer
+    for leg, shape, T, base in (("batch", k3moe.K2_BATCH, 64, 1900),
+                                ("prefill", k3moe.K2_PREFILL, 128, 900)):
+        if leg not in legs:
+            continue
+        layer = k3moe.SynthLayer(shape, seed=seed, layer=0, device=False)
+        x = layer.tokens(T, stream_base=base)
         experts = O.routed_union(layer, x)
         w, cfg, keep = O.k2_weights(layer, experts)
         t0 = time.perf_counter()
-        out, _, _ = O.oracle().moe(w, cfg, x)
-        times.append(time.perf_counter() - t0)
-        del keep
-        if sum(times) >= seconds and len(times) >= 3:
-            break
+        O.oracle().moe(w, cfg, x, prefill=True)
+        dt = time.perf_counter() - t0
+        del keep, layer
+        res[leg] = {"tokens": T, "seconds": round(dt, 3), "tokens_per_s": round(T / dt, 2),
+                    "us_per_token": round(1e6 * dt / T, 1), "experts": len(experts),
+                    "sample": f"{T} tokens of the {shape.name} workload through one "
+                              f"k3_moe_prefill call (64-token chunks, first-seen unique "
+                              f"experts), {what}, OpenMP {threads} threads"}
     O.set_kernels(None)
-    med = float(np.median(times))
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
-    model = platform.processor() or "cpu"
-    try:
-        for line in subprocess.run(["lscpu"], capture_output=True, text=True).stdout.splitlines():
-            if line.startswith("Model name:"):
-                model = line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return {"value": round(1e6 * med, 1), "unit": "us/token", "cores": threads, "kind": kind,
-            "sample": f"{len(times)} decode tokens through the same K2 layer (median), "
-                      f"engine kernels composed as k3_moe without identity latent, "
-                      f"OpenMP {threads} threads on {model}",
-            "tokens_per_s": round(1.0 / med, 2),
-            "GBps": round((K * B_EXPERT + B_SHARED + B_ROUTER + B_TOKEN) / med / 1e9, 2)}
+    return res
 
 
 # algorithmic flops of a T-token prefill step (routed gate/up + down, shared, router)
@@ -359,6 +400,202 @@ def prefill(a):
     }
 
 
+def dropin(a):
+    """The engine's own entry point k3_moe on the c1 workload: host x and out (the PCIe
+    round trip of 28 KB each way is inside the measured time), router/shared weights from
+    host pointers mirrored in HBM once, experts from an HBM expert cache (tiled bank)
+    holding all of the --layers layers' experts: per call the router, the engine's
+    getmany + get per slot, then the fused decode kernel with the routing given. Then
+    64-token calls (the grouped GEMMs) on the Zipf(1.1) batch workload."""
+    import ctypes as C
+    import numpy as np
+    import k3moe
+    NL = a.layers
+    log(f"bench: drop-in k3_moe, {NL} K2 layers with every expert in a tiled HBM cache")
+    L = k3moe.lib()
+
+    def build(shape, nl, base_layer=0):
+        bank = k3moe.Bank(nl, E, D, I, k3moe.K3G_EXPERT_MXFP4_TILED)
+        layers = []
+        for l in range(nl):
+            lay = k3moe.SynthLayer(shape, seed=a.seed, layer=l, layout="tiled")
+            bank.fill_from_layer(lay, l)
+            lay.release_experts()
+            layers.append(lay)
+        slot = (bank.expert_bytes + 65535) // 65536 * 65536
+        cache = k3moe.Cache(bank, topk=K, budget_bytes=nl * E * slot)
+        for l in range(nl):
+            for e in range(E):
+                cache.prefetch(l, e)
+        cache.reset_stats()
+        ws = []
+        for lay in layers:
+            w = k3moe.K3MoeW()
+            w.gate, w.bias = lay.gate.ctypes.data, lay.bias.ctypes.data
+            w.sh1, w.sh3, w.sh2 = lay.sh1.ctypes.data, lay.sh3.ctypes.data, lay.sh2.ctypes.data
+            w.wdt = k3moe.K3_WBF16
+            w.src, w.layer = cache.src_ptr, lay.layer
+            ws.append(w)
+        return bank, cache, layers, ws
+
+    def timed(ws, cfg, xs, T, warm, steps, fn):
+        n = warm + steps
+        out = np.zeros((n * T, D), np.float32)
+        idx = np.zeros(K, np.int32)
+        wt = np.zeros(K, np.float32)
+
+        def call(i):
+            fn(out[i * T:].ctypes.data, xs[i * T:].ctypes.data, C.byref(ws[i % len(ws)]),
+               C.byref(cfg), T, idx.ctypes.data, wt.ctypes.data, None)
+
+        for i in range(warm):
+            call(i)
+        t0 = time.perf_counter()
+        for i in range(warm, n):
+            call(i)
+        dt = time.perf_counter() - t0
+        assert np.isfinite(out).all()
+        return dt / steps, L.k3moe_last_kernels()
+
+    bank, cache, layers, ws = build(k3moe.K2, NL)
+    cfg = layers[0].cfg()
+    xs = np.ascontiguousarray(layers[0].tokens(a.warmup + a.steps, stream_base=900))
+    d0 = C.c_long.in_dll(L, "k3_expert_drops").value
+    sec, kern = timed(ws, cfg, xs, 1, a.warmup, a.steps, L.k3_moe)
+    st = cache.stats()
+    assert C.c_long.in_dll(L, "k3_expert_drops").value == d0
+    res = {"us_per_token": round(1e6 * sec, 2), "tokens_per_s": round(1.0 / sec, 1),
+           "hbm_GBps": round((K * B_EXPERT + B_SHARED + B_ROUTER + B_TOKEN) / sec / 1e9, 1),
+           "kernels": {1: "staged", 2: "fused decode kernel",
+                       4: "grouped GEMMs"}.get(kern, str(kern)),
+           "steps": a.steps, "warmup": a.warmup, "cache_hit_rate": round(st.hits / max(st.requests, 1), 4),
+           "workload": "k3_moe (host x/out, host weight pointers, K3ExpertSrc = HBM expert "
+                       "cache with every expert of %d K2 layers resident), 1 token per call, "
+                       "layers round-robin" % NL}
+    cache.free()
+    bank.free()
+    del layers, ws
+    if a.batch_tokens > 0:
+        T = a.batch_tokens
+        bank, cache, layers, ws = build(k3moe.K2_BATCH, 2)
+        cfg = layers[0].cfg()
+        xs = np.ascontiguousarray(layers[0].tokens(T * (a.batch_warmup + a.batch_steps),
+                                                   stream_base=1900))
+        sec, kern = timed(ws, cfg, xs, T, a.batch_warmup, a.batch_steps, L.k3_moe)
+        res["batch"] = {"tokens": T, "ms_per_step": round(1e3 * sec, 3),
+                        "us_per_token": round(1e6 * sec / T, 2),
+                        "kernels": {4: "grouped GEMMs"}.get(kern, str(kern)),
+                        "workload": f"k3_moe on {T} tokens per call, Zipf(1.1) batch layers, "
+                                    f"experts resident in the HBM cache"}
+        cache.free()
+        bank.free()
+        del layers, ws
+    return res
+
+
+def k3_shape(a):
+    """The real Kimi-K3 LatentMoE layer on the device API: d 7168, 896 MXFP4 experts top-16
+    at latent 3584 x I 3072, bf16 latent down/up projections, RMSNorm of the aggregate, two
+    shared experts fused (6144), SiTU(4, 25), routed scale 1.0; synthetic seeded weights.
+    Decode (1 token, 2 layers round-robin) and a --k3-prefill-tokens prefill, on the
+    grouped matrix-core GEMMs."""
+    import ctypes as C
+    import numpy as np
+    import k3moe
+    d, E3, k3, Lw, I3, SI3 = 7168, 896, 16, 3584, 3072, 6144
+    log(f"bench: K3 LatentMoE layer (E={E3}, top-{k3}, latent {Lw}, I={I3}, shared {SI3})")
+    lib = k3moe.lib()
+    shape = k3moe.Shape("K3 latent experts", Lw, E3, k3, I3, n_shared=2, routed_scale=1.0,
+                        x_bf16=False)
+    keep = []
+
+    def tiled_bf16(v, rows, cols):
+        src = k3moe.DevBuf.from_array(k3moe.bf16_bits(v))
+        t = k3moe.DevBuf(lib.k3g_tiled_bf16_bytes(rows, cols))
+        k3moe._check(lib.k3g_tile_bf16(C.c_void_p(t.ptr), C.c_void_p(src.ptr), rows, cols, None),
+                     "k3g_tile_bf16")
+        k3moe.sync()
+        keep.append(t)
+        return t.ptr
+
+    def layer(l):
+        ex = k3moe.SynthLayer(shape, seed=a.seed, layer=l, layout="tiled")
+        keep.append(ex)
+        n = lambda cnt, s, m, sd, bf=False: k3moe.host_normal(cnt, a.seed, 700 + 20 * l + s, m, sd, bf16=bf)  # noqa: E731
+        g = k3moe.DevBuf.from_array(n(E3 * d, 1, 0.0, 0.02))
+        b = k3moe.DevBuf.from_array(n(E3, 2, 0.0, 0.01))
+        ln = k3moe.DevBuf.from_array(n(Lw, 3, 1.0, 0.1))
+        keep.extend([g, b, ln])
+        Lk = k3moe.K3gLayer()
+        Lk.hidden, Lk.n_experts, Lk.topk, Lk.inter = d, E3, k3, I3
+        Lk.shared_inter, Lk.latent = SI3, Lw
+        Lk.renorm, Lk.routed_scale, Lk.act_b1, Lk.act_b2, Lk.rms_eps = 1, 1.0, 4.0, 25.0, 1e-6
+        Lk.gate, Lk.bias, Lk.latent_norm = g.ptr, b.ptr, ln.ptr
+        Lk.expert_fmt, Lk.experts = k3moe.K3G_EXPERT_MXFP4_TILED, ex.d_ttable.ptr
+        Lk.wdt, Lk.shared_fmt = k3moe.K3_WBF16, 1
+        Lk.down = tiled_bf16(n(Lw * d, 4, 0.0, 0.02, True), Lw, d)
+        Lk.up = tiled_bf16(n(d * Lw, 5, 0.0, 0.02, True), d, Lw)
+        Lk.sh1 = tiled_bf16(n(SI3 * d, 6, 0.0, 0.02, True), SI3, d)
+        Lk.sh3 = tiled_bf16(n(SI3 * d, 7, 0.0, 0.02, True), SI3, d)
+        Lk.sh2 = tiled_bf16(n(d * SI3, 8, 0.0, 0.02, True), d, SI3)
+        return Lk
+
+    Ls = [layer(0), layer(1)]
+    Tp = a.k3_prefill_tokens
+    ctx = k3moe.Ctx(Ls[0], max_tokens=max(Tp, 1))
+    n = a.warmup + a.steps
+    xs = k3moe.host_normal(max(n, Tp) * d, a.seed, 790, 0.0, 1.0).reshape(-1, d)
+    dx = k3moe.DevBuf.from_array(xs)
+    dout = k3moe.DevBuf(max(n, Tp) * d * 4)
+    didx, dwt = k3moe.DevBuf(max(n, Tp) * k3 * 4), k3moe.DevBuf(max(n, Tp) * k3 * 4)
+
+    def step(i):
+        ctx.moe(Ls[i % 2], dx.ptr + i * d * 4, 1, dout.ptr + i * d * 4, didx.ptr + i * k3 * 4,
+                dwt.ptr + i * k3 * 4)
+
+    for i in range(a.warmup):
+        step(i)
+    ctx.sync()
+    tm = k3moe.Timer(ctx.stream)
+    tm.start()
+    for i in range(a.warmup, n):
+        step(i)
+    us = 1e3 * tm.stop() / a.steps
+    ctx.sync()
+    assert np.isfinite(dout.download(np.float32, n * d)).all()
+    B_e3 = 3 * I3 * Lw * 17 // 32
+    dense = 6 * SI3 * d + 4 * E3 * d + 4 * E3 + 2 * 2 * Lw * d + d * 8
+    tok_bytes = k3 * B_e3 + dense
+    res = {"decode": {"us_per_token": round(us, 2), "bytes_per_token": tok_bytes,
+                      "hbm_GBps": round(tok_bytes / (us * 1e-6) / 1e9, 1),
+                      "hbm_frac": round(tok_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                      "steps": a.steps, "kernels": "router + grouped GEMMs (latent)"}}
+    if Tp > 0:
+        def run():
+            ctx.moe(Ls[0], dx.ptr, Tp, dout.ptr, didx.ptr, dwt.ptr)
+        run()
+        ctx.sync()
+        tm.start()
+        for _ in range(a.prefill_steps):
+            run()
+        ms = tm.stop() / a.prefill_steps
+        ctx.sync()
+        assert np.isfinite(dout.download(np.float32, Tp * d)).all()
+        flops = (2 * Tp * k3 * 3 * I3 * Lw + 6 * Tp * SI3 * d + 2 * 2 * Tp * Lw * d +
+                 2 * Tp * E3 * d)
+        res["prefill"] = {"tokens": Tp, "ms_per_step": round(ms, 3),
+                          "tokens_per_s": round(Tp / (ms * 1e-3), 1), "algorithmic_flop": flops,
+                          "achieved_TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+                          "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                          "steps": a.prefill_steps}
+    res["workload"] = ("Kimi-K3 LatentMoE layer: d 7168, 896 MXFP4 experts top-16, latent "
+                       "3584, I 3072, bf16 latent down/up, latent RMSNorm, 2 shared experts "
+                       "(6144), SiTU(4,25); x N(0,1) fp32; decode 2 layers round-robin")
+    ctx.destroy()
+    del Ls, keep
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -383,10 +620,14 @@ def main():
     ap.add_argument("--cache-tokens", type=int, default=8)
     ap.add_argument("--cache-steps", type=int, default=12)
     ap.add_argument("--cache-warmup", type=int, default=6)
+    ap.add_argument("--legs", default="decode,batch,prefill,stream,dropin,k3,cpu",
+                    help="comma list of the measurements to run (decode is the headline)")
+    ap.add_argument("--k3-prefill-tokens", type=int, default=4096)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run one 256 MiB device-to-device copy (a counter calibration "
                          "point for rocprofv3 --pmc runs), outside the timed region")
     a = ap.parse_args()
+    legs = set(a.legs.split(","))
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the layer runs "
               f"on a single MI355X; sharding across GPUs is design-only)",
@@ -495,13 +736,17 @@ def main():
     }
     ctx.destroy()
     del layers, dx, dout, didx, dwt
-    if a.batch_tokens > 0:
+    if a.batch_tokens > 0 and "batch" in legs:
         res["batch_decode"] = batch_decode(a)
-    if a.prefill_tokens > 0:
+    if a.prefill_tokens > 0 and "prefill" in legs:
         res["prefill"] = prefill(a)
-    if a.cache_layers > 0:
+    if "dropin" in legs:
+        res["dropin_decode"] = dropin(a)
+    if "k3" in legs:
+        res["k3_latent_moe"] = k3_shape(a)
+    if a.cache_layers > 0 and "stream" in legs:
         res["streamed_decode"] = streamed_decode(a)
-    if not a.no_cpu:
+    if not a.no_cpu and "cpu" in legs:
         log("bench: CPU baseline")
         res["cpu_baseline"] = cpu_baseline(a.cpu_seconds, a.cpu_tokens, a.seed)
     print(json.dumps(res), flush=True)

@@ -65,7 +65,12 @@ typedef struct {
     size_t stage_bytes;
     K3ExpertQ *eq_dev;           /* [cap_e] device expert table */
     int cap_e;
-    /* host scratch of a call, grow-only */
+    /* host scratch of a call, grow-only; the routing and the activations travel through
+     * pinned memory (asynchronous copies at the DMA rate) */
+    unsigned char *pin;
+    size_t pin_bytes;
+    unsigned char *io;           /* device I/O area of a call, grow-only, starts zeroed */
+    size_t io_bytes;
     int *ridx;
     float *rwt;
     size_t cap_pairs;
@@ -94,12 +99,44 @@ static void *xgrow(void *p, size_t bytes)
     return q;
 }
 
+/* pinned host memory of at least `bytes`, grow-only */
+static unsigned char *pinned(DevState *s, size_t bytes)
+{
+    if (bytes > s->pin_bytes) {
+        if (s->pin) {
+            K3G_CHECK(hipDeviceSynchronize());
+            K3G_CHECK(hipHostFree(s->pin));
+        }
+        s->pin = NULL;
+        const size_t nb = bytes + bytes / 4;
+        K3G_CHECK(hipHostMalloc((void **)&s->pin, nb, hipHostMallocDefault));
+        s->pin_bytes = nb;
+    }
+    return s->pin;
+}
+
+/* The device I/O area of a call, grow-only. Its first word is the device error word of
+ * the drop-in's context: zero, since any error aborts the process. */
+static unsigned char *io_area(DevState *s, size_t bytes)
+{
+    if (bytes > s->io_bytes) {
+        if (s->io) {
+            K3G_CHECK(hipDeviceSynchronize());
+            K3G_CHECK(hipFree(s->io));
+        }
+        s->io = NULL;
+        const size_t nb = bytes + bytes / 4;
+        K3G_CHECK(hipMalloc((void **)&s->io, nb));
+        K3G_CHECK(hipMemset(s->io, 0, nb));
+        s->io_bytes = nb;
+    }
+    return s->io;
+}
+
 /* host scratch for T * k pairs and E experts */
 static void host_scratch(DevState *s, size_t pairs, int E)
 {
     if (pairs > s->cap_pairs) {
-        s->ridx = (int *)xgrow(s->ridx, pairs * sizeof(int));
-        s->rwt = (float *)xgrow(s->rwt, pairs * sizeof(float));
         s->uniq = (int *)xgrow(s->uniq, pairs * sizeof(int));
         s->cap_pairs = pairs;
     }
@@ -675,27 +712,75 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     const size_t xb = ((size_t)T * d * 4 + 255) & ~(size_t)255;
     const size_t nring = f.how == F_HOST_TILE ? 2 : 0;
     unsigned char *sb = (unsigned char *)stage(
-        s, 2 * xb + nring * geo_b + (size_t)f.maxslot * f.slot_bytes);
-    float *xd = (float *)sb, *od = (float *)(sb + xb);
-    f.ring[0] = sb + 2 * xb;
-    f.ring[1] = sb + 2 * xb + geo_b;
-    f.slots = sb + 2 * xb + nring * geo_b;
+        s, xb + nring * geo_b + (size_t)f.maxslot * f.slot_bytes);
+    float *xd = (float *)sb;
+    f.ring[0] = sb + xb;
+    f.ring[1] = sb + xb + geo_b;
+    f.slots = sb + xb + nring * geo_b;
 
-    K3G_CHECK(hipMemcpyAsync(xd, x, (size_t)T * d * 4, hipMemcpyHostToDevice, st));
-    if (k3g_route(ctx, &G, xd, T, ctx->idx, ctx->wt, st) != 0) k3g_fatal("k3_moe: router launch");
+    /* The call's device I/O area and its pinned twin, one transfer each way:
+     * [error word | idx [T][k] | wt [T][k] | out [T][d]], x after it on the host side.
+     * The context reports device errors into the area's first word. */
+    const size_t xbytes = (size_t)T * d * 4, pbytes = (size_t)T * k * 4;
+    const size_t o_idx = 256, o_wt = o_idx + ((pbytes + 255) & ~(size_t)255);
+    const size_t o_out = o_wt + ((pbytes + 255) & ~(size_t)255), io_n = o_out + xbytes;
+    unsigned char *io = io_area(s, io_n);
+    unsigned char *pin = pinned(s, io_n + xbytes);
+    ctx->err = (int *)io;
+    int32_t *didx = (int32_t *)(io + o_idx);
+    float *dwt = (float *)(io + o_wt), *od = (float *)(io + o_out);
+    int *perr = (int *)pin, *ridx = (int *)(pin + o_idx);
+    float *rwt = (float *)(pin + o_wt), *pout = (float *)(pin + o_out);
+    float *px = (float *)(pin + io_n);
+    memcpy(px, x, xbytes);
+    K3G_CHECK(hipMemcpyAsync(xd, px, xbytes, hipMemcpyHostToDevice, st));
     ctx->paths = 0;
     host_scratch(s, (size_t)T * k, E);
-    int *ridx = s->ridx;
-    float *rwt = s->rwt;
     int last[K3_MAX_TOPK];
     float lastw[K3_MAX_TOPK];
-    K3G_CHECK(hipMemcpyAsync(ridx, ctx->idx, (size_t)T * k * 4, hipMemcpyDeviceToHost, st));
-    K3G_CHECK(hipMemcpyAsync(rwt, ctx->wt, (size_t)T * k * 4, hipMemcpyDeviceToHost, st));
-    if (k3g_sync(ctx, NULL) != 0) k3g_fatal("k3_moe: device error in the router");
+    const int cache_only = w->cache_only && w->src && w->src->resident;
+
+    /* Every expert of the layer in the HBM cache: the whole layer runs at once against
+     * the cache's device expert table (the fused decode kernel routes inside), and the
+     * engine's getmany/get calls follow on the host in the engine's order, all hits: the
+     * same results and the same cache state and accounting as fetching first. */
+    const int resident = hc && fast && hc->bank->layout == K3G_EXPERT_MXFP4_TILED &&
+                         !cache_only && k3gc_layer_all_resident(hc, w->layer);
+    if (resident) {
+        k3gc_wait(hc, st);
+        G.experts = k3gc_layer_table(hc, w->layer, st);
+        if (!G.experts) k3g_fatal("k3_moe: expert table update failed");
+        if (k3g_moe(ctx, &G, xd, T, od, didx, dwt, st) != 0) k3g_fatal("k3_moe: launch failed");
+        K3G_CHECK(hipMemcpyAsync(pin, io, io_n, hipMemcpyDeviceToHost, st));
+        K3G_CHECK(hipStreamSynchronize(st));
+        if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error");
+        f.table = s->table;
+        f.have = s->have;
+        const long d0 = k3_expert_drops;
+        k3gc_step_begin(hc);
+        fetch_tokens(&f, s, ridx, k, E, 0, T, mode == 1 && T > 1, 0);
+        k3gc_step_end(hc, st);
+        if (k3_expert_drops != d0) k3g_fatal("k3_moe: a resident expert was not served");
+        memcpy(out, pout, xbytes);
+        g_last_paths = ctx->paths;
+        const int batched = mode == 1 && T > 1;
+        if (!batched || (T - 1) % 64 == 0) {
+            memcpy(idx_out, ridx + (size_t)(T - 1) * k, (size_t)k * sizeof(int));
+            memcpy(wt_out, rwt + (size_t)(T - 1) * k, (size_t)k * sizeof(float));
+        }
+        pthread_mutex_unlock(&g_lock);
+        return;
+    }
+
+    if (k3g_route(ctx, &G, xd, T, didx, dwt, st) != 0) k3g_fatal("k3_moe: router launch");
+    K3G_CHECK(hipMemcpyAsync(pin, io, o_out, hipMemcpyDeviceToHost, st));
+    K3G_CHECK(hipStreamSynchronize(st));
+    if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error in the router");
     memcpy(last, ridx + (size_t)(T - 1) * k, (size_t)k * sizeof(int));
     memcpy(lastw, rwt + (size_t)(T - 1) * k, (size_t)k * sizeof(float));
 
-    const int cache_only = w->cache_only && w->src && w->src->resident;
+    /* the device keeps the router's idx/wt; they travel again only where the host
+     * changed them (drops, the cache-only filter) */
     if (cache_only) {
         /* src/core/k3_ops.c:585-594: keep the resident subset in slot order and divide
          * its weights by their float sum */
@@ -718,9 +803,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     }
 
     if (!w->src) {
-        K3G_CHECK(hipMemcpyAsync(ctx->idx, ridx, (size_t)T * k * 4, hipMemcpyHostToDevice, st));
-        K3G_CHECK(hipMemcpyAsync(ctx->wt, rwt, (size_t)T * k * 4, hipMemcpyHostToDevice, st));
-        if (k3g_experts(ctx, &G, xd, T, ctx->idx, ctx->wt, od, st) != 0)
+        if (k3g_experts(ctx, &G, xd, T, didx, dwt, od, st) != 0)
             k3g_fatal("k3_moe: launch failed");
     } else {
         f.slot_of = s->slot_of;
@@ -736,14 +819,15 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
             s->cap_e = E;
         }
         G.experts = s->eq_dev;
+        const long drops0 = k3_expert_drops;
         const int batched = mode == 1 && T > 1 && !cache_only;
         /* every slot a group fetches stays put until the group's kernels are done: a
          * group's experts must fit the cache's unpinned slots together */
         int cap = E;
         if (hc) {
-            int pinned = 0;
-            for (int i = 0; i < hc->nslot; i++) pinned += hc->pinned[i] != 0;
-            cap = hc->nslot - pinned;
+            int npinned = 0;
+            for (int i = 0; i < hc->nslot; i++) npinned += hc->pinned[i] != 0;
+            cap = hc->nslot - npinned;
             if (cap < 1) k3g_fatal("k3_moe: every slot of the HBM cache is pinned");
         }
         for (int t0 = 0; t0 < T;) {
@@ -769,25 +853,30 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
             if (set.n && k3k_set_experts(s->eq_dev, &set, st) != 0)
                 k3g_fatal("k3_moe: expert table update failed");
             const size_t pk = (size_t)t0 * k, np = (size_t)(t1 - t0) * k;
-            K3G_CHECK(hipMemcpyAsync(ctx->idx + pk, ridx + pk, np * 4, hipMemcpyHostToDevice, st));
-            K3G_CHECK(hipMemcpyAsync(ctx->wt + pk, rwt + pk, np * 4, hipMemcpyHostToDevice, st));
+            if (cache_only || drops0 != k3_expert_drops) {
+                K3G_CHECK(hipMemcpyAsync(didx + pk, ridx + pk, np * 4, hipMemcpyHostToDevice, st));
+                K3G_CHECK(hipMemcpyAsync(dwt + pk, rwt + pk, np * 4, hipMemcpyHostToDevice, st));
+            }
             /* the misses copy on the cache's stream: the routed experts wait for them
              * (the shared expert does not) */
             if (hc && hc->copies_pending) {
                 k3g_ctx_routed_wait(ctx, hc->last_copy);
                 hc->copies_pending = 0;
             }
-            if (k3g_experts(ctx, &G, xd + (size_t)t0 * d, t1 - t0, ctx->idx + pk, ctx->wt + pk,
+            if (k3g_experts(ctx, &G, xd + (size_t)t0 * d, t1 - t0, didx + pk, dwt + pk,
                             od + (size_t)t0 * d, st) != 0)
                 k3g_fatal("k3_moe: launch failed");
             if (hc) k3gc_step_end(hc, st);
-            /* the host routing of this group travels before the next group edits it */
-            K3G_CHECK(hipStreamSynchronize(st));
+            /* the pinned routing of this group travels before the next group edits it */
+            if (t1 < T) K3G_CHECK(hipStreamSynchronize(st));
             t0 = t1;
         }
     }
-    K3G_CHECK(hipMemcpyAsync(out, od, (size_t)T * d * 4, hipMemcpyDeviceToHost, st));
-    if (k3g_sync(ctx, NULL) != 0) k3g_fatal("k3_moe: device error");
+    K3G_CHECK(hipMemcpyAsync(pout, od, xbytes, hipMemcpyDeviceToHost, st));
+    K3G_CHECK(hipMemcpyAsync(perr, io, 4, hipMemcpyDeviceToHost, st));
+    K3G_CHECK(hipStreamSynchronize(st));
+    if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error");
+    memcpy(out, pout, xbytes);
     g_last_paths = ctx->paths;
 
     /* idx/wt hold the last token's routing when the engine's per-token path produced

@@ -798,6 +798,11 @@ int k3g_sync(K3gCtx *c, void *stream)
     if (hipStreamSynchronize(st) != hipSuccess) return -1;
     int e = 0;
     if (hipMemcpy(&e, c->err, sizeof e, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return k3g_err_settle(c, e);
+}
+
+int k3g_err_settle(K3gCtx *c, int e)
+{
     if (e) {
         fprintf(stderr, "k3moe: device reported error %d (%s)\n", e,
                 e == 1 ? "routed expert index out of range" : "bounded wait ran out");

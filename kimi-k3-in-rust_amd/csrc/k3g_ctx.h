@@ -92,5 +92,9 @@ int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32
 /* Make the next k3g_experts wait for `ev` (recorded on another stream) before its routed
  * expert kernels; the shared expert does not wait. */
 void k3g_ctx_routed_wait(K3gCtx *c, hipEvent_t ev);
+/* The device error word `e`, read back by the caller (c->err): 0 when clean; otherwise
+ * reports it, clears it on the device and resets the fused kernel's counters, and
+ * returns it (what k3g_sync does after its own read). */
+int k3g_err_settle(K3gCtx *c, int e);
 
 #endif /* K3G_CTX_H */

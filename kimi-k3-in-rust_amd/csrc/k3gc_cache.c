@@ -183,6 +183,21 @@ static void fill_q(const K3gCache *c, int slot, K3ExpertQ *q)
     }
 }
 
+/* slot bookkeeping: a key enters or leaves a slot */
+static void key_in(K3gCache *c, int32_t key)
+{
+    const int layer = key / c->n_experts;
+    c->layer_resident[layer]++;
+    c->table_dirty[layer] = 1;
+}
+
+static void key_out(K3gCache *c, int32_t key)
+{
+    const int layer = key / c->n_experts;
+    c->layer_resident[layer]--;
+    c->table_dirty[layer] = 1;
+}
+
 /* ------------------------------------------------------------- data movement ---- */
 static void harvest_timers(K3gCache *c, int all)
 {
@@ -275,10 +290,15 @@ static int admit(K3gCache *c, int layer, int expert)
                         "this step)\n", layer, expert);
         return -1;
     }
-    if (c->key_of[slot] >= 0) { c->slot_of[c->key_of[slot]] = -1; c->evictions++; }
+    if (c->key_of[slot] >= 0) {
+        key_out(c, c->key_of[slot]);
+        c->slot_of[c->key_of[slot]] = -1;
+        c->evictions++;
+    }
     copy_in(c, slot, key);
     c->key_of[slot] = key;
     c->slot_of[key] = slot;
+    key_in(c, key);
     c->used_at[slot] = ++c->clock;
     return slot;
 }
@@ -327,7 +347,11 @@ static int cache_getmany(K3ExpertSrc *self, int layer, const int *ids, int n)
         if (dup) continue;
         const int slot = pick_victim(c);
         if (slot < 0) break;
-        if (c->key_of[slot] >= 0) { c->slot_of[c->key_of[slot]] = -1; c->evictions++; }
+        if (c->key_of[slot] >= 0) {
+            key_out(c, c->key_of[slot]);
+            c->slot_of[c->key_of[slot]] = -1;
+            c->evictions++;
+        }
         c->key_of[slot] = K3GC_INFLIGHT;
         c->used_at[slot] = ++c->clock;
         slots[nw] = slot;
@@ -340,6 +364,7 @@ static int cache_getmany(K3ExpertSrc *self, int layer, const int *ids, int n)
         const int32_t key = layer * c->n_experts + experts[i];
         c->key_of[slots[i]] = key;
         c->slot_of[key] = slots[i];
+        key_in(c, key);
         c->used_at[slots[i]] = ++c->clock;
         c->prefetch_reads++;
     }
@@ -357,6 +382,32 @@ static int cache_resident(K3ExpertSrc *self, int layer, int expert, K3ExpertQ *o
 }
 
 int k3gc_is_device_src(const K3ExpertSrc *src) { return src && src->get == cache_get; }
+
+int k3gc_layer_all_resident(const K3gCache *c, int layer)
+{
+    return c && layer >= 0 && layer < c->n_layers && c->layer_resident[layer] == c->n_experts;
+}
+
+const K3ExpertQ *k3gc_layer_table(K3gCache *c, int layer, hipStream_t st)
+{
+    if (!c || !has_device(c) || layer < 0 || layer >= c->n_layers) return NULL;
+    K3ExpertQ *row = c->dev_table + (size_t)layer * c->n_experts;
+    if (!c->table_dirty[layer]) return row;
+    K3kEqSet set;
+    memset(&set, 0, sizeof set);
+    for (int e = 0; e < c->n_experts; e++) {
+        const int slot = c->slot_of[layer * c->n_experts + e];
+        set.e[set.n] = e;
+        if (slot >= 0) fill_q(c, slot, &set.q[set.n]);
+        else memset(&set.q[set.n], 0, sizeof set.q[set.n]);
+        if (++set.n == K3K_EQSET || e == c->n_experts - 1) {
+            if (k3k_set_experts(row, &set, st) != 0) return NULL;
+            set.n = 0;
+        }
+    }
+    c->table_dirty[layer] = 0;
+    return row;
+}
 
 K3gCache *k3gc_of_src(K3ExpertSrc *src)
 {
@@ -403,7 +454,11 @@ int k3gc_init(K3gCache **out, int device, K3gcBank *bank, int topk, int64_t budg
     c->pinned = (unsigned char *)calloc((size_t)c->nslot, 1);
     c->use_step = (int64_t *)malloc((size_t)c->nslot * sizeof(int64_t));
     c->hist = (uint32_t *)calloc(nkey, sizeof(uint32_t));
-    if (!c->slot_of || !c->key_of || !c->used_at || !c->pinned || !c->use_step || !c->hist) {
+    c->layer_resident = (int32_t *)calloc((size_t)c->n_layers, sizeof(int32_t));
+    c->table_dirty = (unsigned char *)malloc((size_t)c->n_layers);
+    if (c->table_dirty) memset(c->table_dirty, 1, (size_t)c->n_layers);
+    if (!c->slot_of || !c->key_of || !c->used_at || !c->pinned || !c->use_step || !c->hist ||
+        !c->layer_resident || !c->table_dirty) {
         k3gc_free(c);
         return -1;
     }
@@ -472,6 +527,8 @@ void k3gc_free(K3gCache *c)
     free(c->use_step);
     free(c->hist);
     free(c->trace);
+    free(c->layer_resident);
+    free(c->table_dirty);
     free(c);
 }
 

@@ -59,6 +59,8 @@ struct K3gCache {
     uint64_t staged;              /* misses copied through the staging buffers */
     int t_head, t_used, t_open;
     K3ExpertQ *dev_table;         /* [n_layers][n_experts] device pointers (k3gc_moe) */
+    int32_t *layer_resident;      /* [n_layers] experts of the layer holding a slot */
+    unsigned char *table_dirty;   /* [n_layers] dev_table row behind the slots */
     int32_t *host_idx;            /* pinned staging of a step's routing */
     int host_idx_cap;
     /* stats (src/cache/k3_cache.h:74-83) */
@@ -73,5 +75,10 @@ struct K3gCache {
 int k3gc_is_device_src(const K3ExpertSrc *src);
 /* The cache behind a device source (NULL otherwise). */
 K3gCache *k3gc_of_src(K3ExpertSrc *src);
+/* 1 when every expert of the layer holds a slot (a get() of any of them is a hit). */
+int k3gc_layer_all_resident(const K3gCache *c, int layer);
+/* The layer's row of the device expert table, brought up to date with the slots on
+ * `stream` when they changed since it was last written. */
+const K3ExpertQ *k3gc_layer_table(K3gCache *c, int layer, hipStream_t stream);
 
 #endif

@@ -225,3 +225,40 @@ def test_k2_through_tiled_cache(gpu):
         assert r <= REL
     small.free()
     bank.free()
+
+
+@pytest.mark.parametrize("prefill,T,want", [(False, 1, FUSED), (False, 3, FUSED),
+                                            (False, 9, GROUPED), (True, 70, GROUPED)])
+def test_resident_layer_runs_at_once(gpu, prefill, T, want):
+    """Every expert of the layer in the HBM cache: the layer runs at once on the cache's
+    device table (the fused kernel routes inside) and the engine's getmany/get calls follow,
+    all hits: the output matches the oracle and the cache sees the engine's requests."""
+    say(f"case: {'k3_moe_prefill' if prefill else 'k3_moe'} tiny layer T={T}, all 16 experts "
+        f"resident in a tiled HBM cache")
+    layer = k3moe.SynthLayer(k3moe.TINY, seed=81, layout="tiled")
+    bank = tiled_bank(layer)
+    slot = (bank.expert_bytes + 65535) // 65536 * 65536
+    cache = k3moe.Cache(bank, topk=layer.shape.topk, budget_bytes=17 * slot)
+    for e in range(layer.shape.n_experts):
+        assert cache.prefetch(0, e) == 0
+    cache.reset_stats()
+    w = cache_weights(layer, cache)
+    cfg = layer.cfg()
+    x = layer.tokens(T, stream_base=11 * T)
+    d0 = drops()
+    out, idx, wt, paths = dropin(w, cfg, x, prefill)
+    st = cache.stats()
+    experts = list(range(layer.shape.n_experts))
+    wo, cfgo, keepo = O.k2_weights(layer, experts)
+    oo, oi, ow = O.oracle().moe(wo, cfgo, x, prefill=prefill)
+    r = rel_l2(out, oo)
+    say(f"  kernels {paths}, rel-L2 {r:.3e}, requests {st.requests} (oracle source "
+        f"{keepo[1].s.gets})")
+    assert paths == want and drops() == d0
+    assert r <= REL
+    assert st.requests == keepo[1].s.gets and st.hits == st.requests and st.misses == 0
+    if not prefill:
+        assert np.array_equal(idx, oi)
+        np.testing.assert_allclose(wt, ow, rtol=1e-6)
+    cache.free()
+    bank.free()
