@@ -44,6 +44,10 @@ B_GATEUP_EXPERT = 2 * (I * D // 2 + I * D // 32)   # w1 + w3 of one expert
 # device-to-device copy read 256 MiB); the run and the numbers are in
 # profiles/k_decode_fused_k2_decode.md. Re-measured whenever the kernel changes.
 TRAFFIC_FUSED = 304563580
+# HBM bytes per launch of the routed gate/up GEMM (k_gemm<0, 4>) of the 4096-token
+# Zipf(0.8) prefill, the same way (FETCH_SIZE x 1.9997 + WRITE_SIZE, mean of 3 launches):
+# 7.804 GB read + 0.204 GB written; profiles/k_gemm_k2_prefill4096.md.
+TRAFFIC_GATEUP_PREFILL = 8008000000
 
 
 def log(msg):
@@ -395,7 +399,7 @@ def prefill(a):
                                "registers, bf16 MFMA, SwiGLU epilogue)",
                      "bound": "mfma", "achieved": round(gu_tf, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gu_tf / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None, "flop_per_launch": gu_flops,
+                     "traffic": TRAFFIC_GATEUP_PREFILL, "flop_per_launch": gu_flops,
                      "avg_launch_us": round(gu_us, 1)},
     }
 
@@ -596,49 +600,11 @@ def k3_shape(a):
     return res
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--layers", type=int, default=4)
-    ap.add_argument("--seed", type=int, default=2024)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--cpu-tokens", type=int, default=64)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--batch-tokens", type=int, default=64,
-                    help="tokens of the batched-decode measurement (0: skip it)")
-    ap.add_argument("--batch-steps", type=int, default=20)
-    ap.add_argument("--batch-warmup", type=int, default=4)
-    ap.add_argument("--prefill-tokens", type=int, default=4096,
-                    help="tokens of the prefill measurement (0: skip it)")
-    ap.add_argument("--prefill-steps", type=int, default=5)
-    ap.add_argument("--prefill-warmup", type=int, default=2)
-    ap.add_argument("--cache-layers", type=int, default=16,
-                    help="layers of the streamed-decode measurement (0: skip it)")
-    ap.add_argument("--cache-gb", type=float, default=48.0)
-    ap.add_argument("--cache-tokens", type=int, default=8)
-    ap.add_argument("--cache-steps", type=int, default=12)
-    ap.add_argument("--cache-warmup", type=int, default=6)
-    ap.add_argument("--legs", default="decode,batch,prefill,stream,dropin,k3,cpu",
-                    help="comma list of the measurements to run (decode is the headline)")
-    ap.add_argument("--k3-prefill-tokens", type=int, default=4096)
-    ap.add_argument("--calib-copy", action="store_true",
-                    help="also run one 256 MiB device-to-device copy (a counter calibration "
-                         "point for rocprofv3 --pmc runs), outside the timed region")
-    a = ap.parse_args()
-    legs = set(a.legs.split(","))
-    if a.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the layer runs "
-              f"on a single MI355X; sharding across GPUs is design-only)",
-              file=sys.stderr)
-        sys.exit(2)
-
+def decode(a):
+    """The headline: 1-token decode through the fused decode kernel, --layers K2 layers
+    round-robin. Returns the JSON line's fields."""
     import numpy as np
-    import __graft_entry__ as g
-    g._ensure_built()
     import k3moe
-
     log(f"bench: building {a.layers} K2 layers (d={D}, E={E}, top-{K}, I={I}) in HBM")
     layers = [k3moe.SynthLayer(k3moe.K2, seed=a.seed, layer=l, layout="tiled")
               for l in range(a.layers)]
@@ -654,13 +620,6 @@ def main():
         ctx.moe(layers[i % a.layers].dev, dx.ptr + i * D * 4, 1, dout.ptr + i * D * 4,
                 didx.ptr + i * K * 4, dwt.ptr + i * K * 4)
 
-    if a.calib_copy:
-        n = 256 << 20
-        src, dst = k3moe.DevBuf(n), k3moe.DevBuf(n)
-        k3moe._check(k3moe.hip().hipMemcpy(k3moe.C.c_void_p(dst.ptr), k3moe.C.c_void_p(src.ptr),
-                                           n, k3moe.D2D), "calibration copy")
-        k3moe.sync()
-        del src, dst
     log(f"bench: warmup {a.warmup} steps")
     for i in range(a.warmup):
         step(i)
@@ -736,6 +695,66 @@ def main():
     }
     ctx.destroy()
     del layers, dx, dout, didx, dwt
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-tokens", type=int, default=64)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--batch-tokens", type=int, default=64,
+                    help="tokens of the batched-decode measurement (0: skip it)")
+    ap.add_argument("--batch-steps", type=int, default=20)
+    ap.add_argument("--batch-warmup", type=int, default=4)
+    ap.add_argument("--prefill-tokens", type=int, default=4096,
+                    help="tokens of the prefill measurement (0: skip it)")
+    ap.add_argument("--prefill-steps", type=int, default=5)
+    ap.add_argument("--prefill-warmup", type=int, default=2)
+    ap.add_argument("--cache-layers", type=int, default=16,
+                    help="layers of the streamed-decode measurement (0: skip it)")
+    ap.add_argument("--cache-gb", type=float, default=48.0)
+    ap.add_argument("--cache-tokens", type=int, default=8)
+    ap.add_argument("--cache-steps", type=int, default=12)
+    ap.add_argument("--cache-warmup", type=int, default=6)
+    ap.add_argument("--legs", default="decode,batch,prefill,stream,dropin,k3,cpu",
+                    help="comma list of the measurements to run (decode is the headline)")
+    ap.add_argument("--k3-prefill-tokens", type=int, default=4096)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one 256 MiB device-to-device copy (a counter calibration "
+                         "point for rocprofv3 --pmc runs), outside the timed region")
+    a = ap.parse_args()
+    legs = set(a.legs.split(","))
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported (the layer runs "
+              f"on a single MI355X; sharding across GPUs is design-only)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import __graft_entry__ as g
+    g._ensure_built()
+    import k3moe
+
+    if a.calib_copy:
+        n = 256 << 20
+        src, dst = k3moe.DevBuf(n), k3moe.DevBuf(n)
+        k3moe._check(k3moe.hip().hipMemcpy(k3moe.C.c_void_p(dst.ptr), k3moe.C.c_void_p(src.ptr),
+                                           n, k3moe.D2D), "calibration copy")
+        k3moe.sync()
+        del src, dst
+    if "decode" in legs:
+        res = decode(a)
+    else:
+        res = {"metric": METRIC, "value": None, "unit": "tokens/s", "n_gpus": 1,
+               "steps": 0, "warmup": 0, "ms_per_step": None, "higher_is_better": True,
+               "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+               "config": {"workload": "decode leg skipped (--legs)"}}
     if a.batch_tokens > 0 and "batch" in legs:
         res["batch_decode"] = batch_decode(a)
     if a.prefill_tokens > 0 and "prefill" in legs:

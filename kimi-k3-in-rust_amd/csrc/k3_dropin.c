@@ -99,6 +99,22 @@ static void *xgrow(void *p, size_t bytes)
     return q;
 }
 
+/* dst <- src, with every host thread for large copies (the activations of a prefill) */
+static void host_copy(void *dst, const void *src, size_t n)
+{
+    if (n < ((size_t)1 << 20)) {
+        memcpy(dst, src, n);
+        return;
+    }
+    const int parts = 16;
+    const size_t per = ((n + parts - 1) / parts + 4095) & ~(size_t)4095;
+#pragma omp parallel for schedule(static)
+    for (int i = 0; i < parts; i++) {
+        const size_t a = (size_t)i * per;
+        if (a < n) memcpy((char *)dst + a, (const char *)src + a, a + per < n ? per : n - a);
+    }
+}
+
 /* pinned host memory of at least `bytes`, grow-only */
 static unsigned char *pinned(DevState *s, size_t bytes)
 {
@@ -732,7 +748,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     int *perr = (int *)pin, *ridx = (int *)(pin + o_idx);
     float *rwt = (float *)(pin + o_wt), *pout = (float *)(pin + o_out);
     float *px = (float *)(pin + io_n);
-    memcpy(px, x, xbytes);
+    host_copy(px, x, xbytes);
     K3G_CHECK(hipMemcpyAsync(xd, px, xbytes, hipMemcpyHostToDevice, st));
     ctx->paths = 0;
     host_scratch(s, (size_t)T * k, E);
@@ -761,7 +777,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         fetch_tokens(&f, s, ridx, k, E, 0, T, mode == 1 && T > 1, 0);
         k3gc_step_end(hc, st);
         if (k3_expert_drops != d0) k3g_fatal("k3_moe: a resident expert was not served");
-        memcpy(out, pout, xbytes);
+        host_copy(out, pout, xbytes);
         g_last_paths = ctx->paths;
         const int batched = mode == 1 && T > 1;
         if (!batched || (T - 1) % 64 == 0) {
@@ -876,7 +892,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     K3G_CHECK(hipMemcpyAsync(perr, io, 4, hipMemcpyDeviceToHost, st));
     K3G_CHECK(hipStreamSynchronize(st));
     if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error");
-    memcpy(out, pout, xbytes);
+    host_copy(out, pout, xbytes);
     g_last_paths = ctx->paths;
 
     /* idx/wt hold the last token's routing when the engine's per-token path produced
