@@ -242,7 +242,11 @@ def streamed_decode(a):
     bank, with the HBM expert cache capped at 48 GB: batch-8 decode steps through all
     layers, per-layer Zipf(1.0) routing with 70% of each step's experts reused from the
     previous step (trace-driven). Misses are copied on the cache's stream; the shared
-    expert runs while they copy."""
+    expert runs while they copy. The trace runs as a previous segment (--cache-steps
+    steps, untimed) and the measured segment (--cache-steps steps): first with LRU, then
+    with the hottest half of the slots pinned from the previous segment's request
+    histogram (k3gc_pin_hottest), warmed on the previous segment's last --cache-warmup
+    steps."""
     import numpy as np
     import k3moe
     NL, T = a.cache_layers, a.cache_tokens
@@ -254,49 +258,85 @@ def streamed_decode(a):
         bank.fill_from_layer(lay, l)
         lay.release_experts()
         layers.append(lay)
-    cache = k3moe.Cache(bank, topk=K, budget_bytes=int(a.cache_gb * 1e9))
-    n_steps = a.cache_warmup + a.cache_steps
-    idx, wt = expert_trace(n_steps, NL, T, a.seed + 11)
+    S = a.cache_steps
+    idx, wt = expert_trace(2 * S, NL, T, a.seed + 11)
     ctx = k3moe.Ctx(layers[0].dev_tiled, max_tokens=T)
     x = layers[0].tokens(T, stream_base=2900)
     dx = k3moe.DevBuf.from_array(x)
     dout, didx, dwt = k3moe.DevBuf(T * D * 4), k3moe.DevBuf(T * K * 4), k3moe.DevBuf(T * K * 4)
 
-    def step(s):
+    def step(cache, s):
         for l in range(NL):
             cache.moe(ctx, layers[l].dev_tiled, l, dx.ptr, T, dout.ptr, didx.ptr, dwt.ptr,
                       idx[s, l], wt[s, l])
 
-    for s in range(a.cache_warmup):
-        step(s)
+    def measured(cache, label, extra):
+        cache.reset_stats()
+        t0 = time.perf_counter()
+        for s in range(S, 2 * S):
+            step(cache, s)
+        ctx.sync()
+        t1 = time.perf_counter()
+        st = cache.stats()
+        assert np.isfinite(dout.download(np.float32, T * D)).all()
+        ms = (t1 - t0) * 1e3 / S
+        served = max(st.hits - st.prefetch_reads, 0)
+        r = {"policy": label, "ms_per_step": round(ms, 3), "ms_per_token_latency": round(ms, 3),
+             "tokens_per_s": round(T / (ms * 1e-3), 2), "requests": st.requests,
+             "true_hit_rate": round(served / max(st.requests, 1), 4),
+             "misses_copied": st.prefetch_reads + st.misses,
+             "pcie_GB": round(st.bytes_read / 1e9, 2),
+             "pcie_GBps_while_copying": round(st.bytes_read / 1e9 / max(st.load_seconds, 1e-9), 1),
+             "pcie_GBps_over_run": round(st.bytes_read / 1e9 / (t1 - t0), 1),
+             "copy_stream_busy_frac": round(st.load_seconds / (t1 - t0), 3)}
+        r.update(extra)
+        return r, st
+
+    lru_cache = k3moe.Cache(bank, topk=K, budget_bytes=int(a.cache_gb * 1e9))
+    for s in range(S):                      # the previous segment
+        step(lru_cache, s)
     ctx.sync()
-    cache.reset_stats()
-    t0 = time.perf_counter()
-    for s in range(a.cache_warmup, n_steps):
-        step(s)
+    hist = lru_cache.hist()
+    lru, st = measured(lru_cache, "LRU", {})
+    nslot = st.nslot
+    lru_cache.free()
+    pin_cache = k3moe.Cache(bank, topk=K, budget_bytes=int(a.cache_gb * 1e9))
+    npin = pin_cache.pin_hottest(hist, nslot // 2)
+    for s in range(S - a.cache_warmup, S):
+        step(pin_cache, s)
     ctx.sync()
-    t1 = time.perf_counter()
-    st = cache.stats()
-    out = dout.download(np.float32, T * D)
-    assert np.isfinite(out).all()
-    ms = (t1 - t0) * 1e3 / a.cache_steps
-    served = max(st.hits - st.prefetch_reads, 0)
-    res = {"layers": NL, "tokens_per_step": T, "steps": a.cache_steps, "warmup": a.cache_warmup,
-           "ms_per_step": round(ms, 3), "ms_per_token_latency": round(ms, 3),
-           "tokens_per_s": round(T / (ms * 1e-3), 2),
-           "hbm_cache_GB": a.cache_gb, "slots": st.nslot, "host_bank_GB": round(NL * E * bank.expert_bytes / 1e9, 1),
-           "bank_layers_pinned": bank.pinned_layers,
-           "requests": st.requests, "true_hit_rate": round(served / max(st.requests, 1), 4),
-           "misses_copied": st.prefetch_reads + st.misses,
-           "pcie_GB": round(st.bytes_read / 1e9, 2),
-           "pcie_GBps_while_copying": round(st.bytes_read / 1e9 / max(st.load_seconds, 1e-9), 1),
-           "pcie_GBps_over_run": round(st.bytes_read / 1e9 / (t1 - t0), 1),
-           "copy_stream_busy_frac": round(st.load_seconds / (t1 - t0), 3),
-           "workload": "16 stacked K2 layers, experts in a pinned host bank, HBM cache 48 GB, "
-                       "batch 8, per-layer Zipf(1.0) routing with 70% step-to-step reuse "
-                       "(trace-driven), LRU"}
+    pinned, _ = measured(pin_cache, "pinned hottest + LRU",
+                         {"pinned_slots": npin,
+                          "pins_from": f"request histogram of the previous {S} steps"})
+    pin_cache.free()
+    # the same request stream (each step's unique experts per layer, in first-seen order,
+    # as k3gc_moe asks for them) replayed offline at the cache's capacity
+    req = []
+    for s_ in range(2 * S):
+        for l in range(NL):
+            seen = []
+            for e in idx[s_, l].reshape(-1):
+                if int(e) not in seen:
+                    seen.append(int(e))
+            req.extend((l, e) for e in seen)
+    req = np.array(req, np.int32)
+    n_req = len(req)
+    replays = {p: round(k3moe.replay(p, req, nslot, nslot // 2) / n_req, 4)
+               for p in ("lru", "belady", "pinned_lru")}
+    res = dict(lru)
+    res.update({"layers": NL, "tokens_per_step": T, "steps": S, "warmup": S,
+                "hbm_cache_GB": a.cache_gb, "slots": nslot,
+                "host_bank_GB": round(NL * E * bank.expert_bytes / 1e9, 1),
+                "bank_layers_pinned": bank.pinned_layers,
+                "histogram_pinning": pinned,
+                "offline_replay_hit_rates": dict(replays, what=f"both segments' {n_req} "
+                                                 f"requests from cold at {nslot} slots; "
+                                                 f"belady and pinned_lru see the future"),
+                "workload": "16 stacked K2 layers, experts in a pinned host bank, HBM cache "
+                            "48 GB, batch 8, per-layer Zipf(1.0) routing with 70% step-to-step "
+                            "reuse (trace-driven); LRU, then the hottest half of the slots "
+                            "pinned from the previous segment's histogram"})
     ctx.destroy()
-    cache.free()
     bank.free()
     del layers
     return res

@@ -428,6 +428,32 @@ void k3gc_report(K3gCache *cache, const char *label);
 int  k3gc_dump_hist(const K3gCache *cache, const char *path);
 int  k3gc_dump_trace(const K3gCache *cache, const char *path);
 
+/* Histogram-driven pinning: make the npin most requested (layer, expert) of a histogram
+ * [n_layers][n_experts] resident and pin them (ties to the lower layer, then expert). The
+ * histogram is a previous workload's (the cache's own, k3gc_hist, or one read back from
+ * k3gc_dump_hist); pinning stops short of leaving fewer than top-k + 1 unpinned slots.
+ * Returns the number pinned. The use the engine's request histogram and k3_cache_pin are
+ * for (src/cache/k3_cache.h:29-31, :100-102); the engine has no such call itself. */
+int  k3gc_pin_hottest(K3gCache *cache, const uint32_t *hist, int npin);
+/* The cache's request histogram, [n_layers][n_experts] counts of get() calls. */
+const uint32_t *k3gc_hist(const K3gCache *cache);
+
+/* Offline replays of a (layer, expert) request trace (int32 pairs, the format
+ * k3gc_dump_trace writes) at `capacity` experts; each returns the hits, first touches
+ * counted as misses. The engine's tools/sim_cache.py:36-110 with the same definitions:
+ *   lru         least recently used;
+ *   belady      the optimal offline policy: evict the expert used furthest in the
+ *               future, and do not cache a request used later than every resident one;
+ *   pinned_lru  the npin most requested experts of the trace (ties to the first seen)
+ *               held once read, LRU in the remaining capacity - npin slots (at least 1);
+ *               npin >= capacity is taken as capacity - 1.
+ * Belady and pinned_lru see the whole trace, so they are ceilings for the policies a
+ * cache can run. */
+int64_t k3gc_replay_lru(const int32_t *trace_pairs, int64_t n, int64_t capacity);
+int64_t k3gc_replay_belady(const int32_t *trace_pairs, int64_t n, int64_t capacity);
+int64_t k3gc_replay_pinned_lru(const int32_t *trace_pairs, int64_t n, int64_t capacity,
+                               int64_t npin);
+
 typedef struct {
     int64_t requests, hits, misses, evictions, prefetch_reads, bytes_read;
     double load_seconds;          /* copy-stream time spent on misses */

@@ -239,6 +239,15 @@ def lib() -> C.CDLL:
         L.k3gc_wait.restype = None
         L.k3gc_moe.argtypes = [vp, vp, C.POINTER(K3gLayer), i, vp, i, vp, vp, vp, vp, vp, vp]
         L.k3gc_moe.restype = i
+        L.k3gc_pin_hottest.argtypes = [vp, vp, i]
+        L.k3gc_pin_hottest.restype = i
+        L.k3gc_hist.argtypes = [vp]
+        L.k3gc_hist.restype = vp
+        for name in ("k3gc_replay_lru", "k3gc_replay_belady"):
+            getattr(L, name).argtypes = [vp, i64, i64]
+            getattr(L, name).restype = i64
+        L.k3gc_replay_pinned_lru.argtypes = [vp, i64, i64, i64]
+        L.k3gc_replay_pinned_lru.restype = i64
         _lib = L
     return _lib
 
@@ -697,6 +706,17 @@ class Ctx:
 
 # ------------------------------------------------------------------ HBM expert cache ----
 
+def replay(policy: str, trace_pairs: np.ndarray, capacity: int, npin: int = 0) -> int:
+    """Hits of an offline replay of a (layer, expert) trace: policy "lru", "belady" or
+    "pinned_lru" (k3gc_replay_*)."""
+    t = np.ascontiguousarray(trace_pairs, np.int32).reshape(-1)
+    n = t.size // 2
+    if policy == "pinned_lru":
+        return lib().k3gc_replay_pinned_lru(t.ctypes.data, n, capacity, npin)
+    return getattr(lib(), "k3gc_replay_" + policy)(t.ctypes.data, n, capacity)
+
+
+
 class Bank:
     """A pinned host bank of expert runs (k3gc_bank_create), or a geometry-only bank for
     bookkeeping replays (k3gc_bank_geometry)."""
@@ -771,6 +791,16 @@ class Cache:
 
     def pin(self, layer, e, on=True) -> int:
         return lib().k3gc_pin(self.ptr, layer, e, 1 if on else 0)
+
+    def hist(self) -> np.ndarray:
+        """A copy of the request histogram [n_layers][n_experts]."""
+        n = self.bank.n_layers * self.bank.n_experts
+        p = lib().k3gc_hist(self.ptr)
+        return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint32)), (n,)).copy()
+
+    def pin_hottest(self, hist: np.ndarray, npin: int) -> int:
+        h = np.ascontiguousarray(hist, np.uint32)
+        return lib().k3gc_pin_hottest(self.ptr, h.ctypes.data, npin)
 
     def prefetch(self, layer, e) -> int:
         return lib().k3gc_prefetch(self.ptr, layer, e)

@@ -330,3 +330,76 @@ def k2_forward_mxfp8(layer: "k3moe.SynthLayer", x: np.ndarray):
             acc = (acc + k.matmul_bf16(hs, layer.sh2, d).astype(np.float32)).astype(np.float32)
         out[t] = acc
     return out
+
+
+# --------------------------------------------------- cache policies (offline replays) ----
+# The engine's tools/sim_cache.py, restated for small traces (pure Python): the product's
+# k3gc_replay_* must give the same hits. keys: any hashable request keys in trace order.
+
+def sim_lru(keys, cap):
+    """tools/sim_cache.py:36-49"""
+    from collections import OrderedDict
+    seen, hits = OrderedDict(), 0
+    for k in keys:
+        if k in seen:
+            seen.move_to_end(k)
+            hits += 1
+        else:
+            if len(seen) >= cap:
+                seen.popitem(last=False)
+            seen[k] = 1
+    return hits
+
+
+def sim_belady(keys, cap):
+    """tools/sim_cache.py:52-76: evict the resident key used furthest in the future; a
+    request used later than every resident key is not cached."""
+    n = len(keys)
+    nxt, last = [n] * n, {}
+    for i in range(n - 1, -1, -1):
+        nxt[i] = last.get(keys[i], n)
+        last[keys[i]] = i
+    resident, hits = {}, 0
+    for i, k in enumerate(keys):
+        if k in resident:
+            hits += 1
+            resident[k] = nxt[i]
+            continue
+        if len(resident) >= cap:
+            victim = max(resident, key=resident.get)
+            if resident[victim] < nxt[i]:
+                continue
+            del resident[victim]
+        resident[k] = nxt[i]
+    return hits
+
+
+def sim_pinned_lru(keys, cap, npin, hot=None, preloaded=False):
+    """tools/sim_cache.py:79-110: the npin most requested keys (ties to the first seen)
+    held once read, LRU in the remaining room. hot: an explicit hot set instead;
+    preloaded: the hot keys are resident before the first request (a cache pinned from a
+    previous workload's histogram), so their first touch is a hit too."""
+    from collections import Counter, OrderedDict
+    if npin >= cap:
+        npin = cap - 1
+    if hot is None:
+        hot = {k for k, _ in Counter(keys).most_common(npin)}
+    loaded = set(hot) if preloaded else set()
+    seen, hits = OrderedDict(), 0
+    room = max(cap - len(hot), 1)
+    for k in keys:
+        if k in hot:
+            if k in loaded:
+                hits += 1
+            else:
+                loaded.add(k)
+            continue
+        if k in seen:
+            seen.move_to_end(k)
+            hits += 1
+        else:
+            if len(seen) >= room:
+                seen.popitem(last=False)
+            seen[k] = 1
+    return hits
+

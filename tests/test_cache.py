@@ -124,3 +124,112 @@ def test_device_src_vtable_is_exposed():
     c = dry_cache(1, 4, 3)
     src = k3moe.K3ExpertSrc.from_address(c.src_ptr)
     assert src.get and src.getmany and src.resident
+
+
+# ------------------------------------------------------------ policy beyond LRU ----
+# docs/data/expert-cache-capacity.txt:20-28 (the engine's tools/sim_cache.py on its
+# recorded trace): capacity in GB, slots of one K3 expert, LRU / BELADY / PIN+LRU hit rates
+CAPACITY_TABLE = [
+    (8, 455, 36.24, 39.42, 37.82), (16, 911, 36.24, 42.61, 39.42),
+    (32, 1823, 36.24, 48.99, 42.57), (64, 3647, 36.24, 61.74, 48.66),
+    (128, 7294, 49.19, 84.59, 62.86), (192, 10941, 90.00, 90.00, 90.00),
+    (256, 14589, 90.00, 90.00, 90.00), (384, 21883, 90.00, 90.00, 90.00),
+    (512, 29178, 90.00, 90.00, 90.00), (768, 43767, 90.00, 90.00, 90.00),
+    (1024, 58356, 90.00, 90.00, 90.00), (1450, 82633, 90.00, 90.00, 90.00)]
+
+
+def test_policy_replays_reproduce_the_engine_table():
+    """k3gc_replay_lru / _belady / _pinned_lru (npin = capacity // 2, sim_cache.py:163) on
+    the engine's 100,096-request trace give every entry of its published table."""
+    pairs = np.load(os.path.join(GOLDEN, "expert_trace.npz"))["pairs"]
+    n = pairs.shape[0]
+    for gb, slots, p_lru, p_bel, p_pin in CAPACITY_TABLE:
+        cap = int(gb * 1e9 // K3_EXPERT)
+        assert cap == slots
+        got = (k3moe.replay("lru", pairs, cap), k3moe.replay("belady", pairs, cap),
+               k3moe.replay("pinned_lru", pairs, cap, cap // 2))
+        pct = tuple(round(100.0 * h / n, 2) for h in got)
+        assert pct == (p_lru, p_bel, p_pin), (gb, got, pct)
+
+
+def _small_traces():
+    rng = np.random.default_rng(5)
+    for n, nkeys, s in ((300, 12, 0.8), (2000, 60, 1.1), (1500, 200, 0.5)):
+        p = np.arange(1, nkeys + 1, dtype=np.float64) ** -s
+        k = rng.choice(nkeys, size=n, p=p / p.sum())
+        yield np.stack([k % 3, k // 3], axis=1).astype(np.int32)
+
+
+def test_policy_replays_agree_with_the_restatement():
+    for pairs in _small_traces():
+        keys = [(int(a), int(b)) for a, b in pairs]
+        for cap in (1, 2, 3, 7, 16, 40, 250):
+            assert k3moe.replay("lru", pairs, cap) == O.sim_lru(keys, cap), cap
+            assert k3moe.replay("belady", pairs, cap) == O.sim_belady(keys, cap), cap
+            for npin in (0, 1, cap // 2, cap, cap + 5):
+                assert k3moe.replay("pinned_lru", pairs, cap, npin) == \
+                    O.sim_pinned_lru(keys, cap, npin), (cap, npin)
+
+
+def _best_possible(keys, cap):
+    """Brute force over every choice at every miss with a full cache (evict any resident
+    key, or do not cache the request): the most hits any policy gets."""
+    from functools import lru_cache
+
+    @lru_cache(maxsize=None)
+    def go(i, res):
+        if i == len(keys):
+            return 0
+        k = keys[i]
+        if k in res:
+            return 1 + go(i + 1, res)
+        if len(res) < cap:
+            return go(i + 1, res | {k})
+        best = go(i + 1, res)
+        for v in res:
+            best = max(best, go(i + 1, (res - {v}) | {k}))
+        return best
+    return go(0, frozenset())
+
+
+def test_belady_is_optimal_on_tiny_traces():
+    rng = np.random.default_rng(9)
+    for _ in range(60):
+        n, nk, cap = int(rng.integers(4, 11)), int(rng.integers(2, 6)), int(rng.integers(1, 4))
+        k = rng.integers(0, nk, size=n)
+        pairs = np.stack([np.zeros(n), k], axis=1).astype(np.int32)
+        keys = tuple(int(v) for v in k)
+        assert k3moe.replay("belady", pairs, cap) == _best_possible(keys, cap), (keys, cap)
+
+
+def test_pin_hottest_from_a_previous_histogram():
+    """The hot set of one workload pinned for the next: the pinned keys are the npin
+    most requested of the histogram (ties to the lower key), they stay resident, and the
+    next workload's hits equal the pinned-LRU replay with that hot set already resident."""
+    pairs = np.load(os.path.join(GOLDEN, "expert_trace.npz"))["pairs"]
+    half = pairs.shape[0] // 2
+    slots = int(32e9 // K3_EXPERT)
+    bank = k3moe.Bank(93, 896, expert_bytes=K3_EXPERT)
+    first = k3moe.Cache(bank, topk=16, budget_bytes=slots * SLOT, device=-1)
+    for layer, e in pairs[:half]:
+        first.get(int(layer), int(e))
+    hist = first.hist()
+    assert hist.sum() == half
+    npin = slots // 2
+    c = k3moe.Cache(bank, topk=16, budget_bytes=slots * SLOT, device=-1)
+    assert c.pin_hottest(hist, npin) == npin
+    order = np.lexsort((np.arange(hist.size), -hist.astype(np.int64)))
+    want = set(int(v) for v in order[:npin])
+    got = {L * 896 + e for L in range(93) for e in range(896)
+           if c.resident(L, e)}
+    assert got == want and c.stats().pinned == npin
+    c.reset_stats()
+    for layer, e in pairs[half:]:
+        c.get(int(layer), int(e))
+    st = c.stats()
+    keys = [int(L) * 896 + int(e) for L, e in pairs[half:]]
+    assert st.hits == O.sim_pinned_lru(keys, slots, npin, hot=want, preloaded=True)
+    assert all(c.resident(k // 896, k % 896) for k in want)
+    lru_only = O.sim_lru(keys, slots)
+    print(f"pinned {npin} of {slots} slots from the first half's histogram: second half "
+          f"hits {st.hits} vs LRU {lru_only}")
