@@ -309,6 +309,38 @@ def streamed_decode(a):
                          {"pinned_slots": npin,
                           "pins_from": f"request histogram of the previous {S} steps"})
     pin_cache.free()
+    # the 16 layers chained with the hidden state in HBM (k3gc_chain: RMSNorm x post-norm,
+    # MoE, residual add per layer), every expert resident: per-token latency of the stack
+    slot = (bank.expert_bytes + 65535) // 65536 * 65536
+    full = k3moe.Cache(bank, topk=K, budget_bytes=NL * E * slot)
+    for l in range(NL):
+        for e in range(E):
+            full.prefetch(l, e)
+    full.reset_stats()
+    norms = [k3moe.DevBuf.from_array(k3moe.host_normal(D, a.seed, 950 + l, 1.0, 0.1))
+             for l in range(NL)]
+    Ls = [lay.dev_tiled for lay in layers]
+    chain = {}
+    for Tc in (1, T):
+        h = k3moe.DevBuf.from_array(layers[0].tokens(Tc, stream_base=2950))
+        for _ in range(2):
+            full.chain(ctx, Ls, [b.ptr for b in norms], 0, h.ptr, Tc)
+        ctx.sync()
+        reps = 10
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            full.chain(ctx, Ls, [b.ptr for b in norms], 0, h.ptr, Tc)
+        ctx.sync()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        assert np.isfinite(h.download(np.float32, Tc * D)).all()
+        chain[f"T{Tc}"] = {"ms_per_step": round(ms, 3), "ms_per_token": round(ms / Tc, 3),
+                           "us_per_layer": round(1e3 * ms / NL, 1)}
+    fst = full.stats()
+    chain.update({"layers": NL, "all_experts_resident": True,
+                  "cache_hit_rate": round(fst.hits / max(fst.requests, 1), 4),
+                  "what": "k3gc_chain over the 16 layers, h [T][7168] kept in HBM, one host "
+                          "synchronisation per chain call"})
+    full.free()
     # the same request stream (each step's unique experts per layer, in first-seen order,
     # as k3gc_moe asks for them) replayed offline at the cache's capacity
     req = []
@@ -329,6 +361,7 @@ def streamed_decode(a):
                 "host_bank_GB": round(NL * E * bank.expert_bytes / 1e9, 1),
                 "bank_layers_pinned": bank.pinned_layers,
                 "histogram_pinning": pinned,
+                "chained_layers": chain,
                 "offline_replay_hit_rates": dict(replays, what=f"both segments' {n_req} "
                                                  f"requests from cold at {nslot} slots; "
                                                  f"belady and pinned_lru see the future"),

@@ -519,6 +519,8 @@ void k3gc_free(K3gCache *c)
         if (c->arena) hipFree(c->arena);
         if (c->dev_table) hipFree(c->dev_table);
         if (c->host_idx) hipHostFree(c->host_idx);
+        if (c->chain_dev) hipFree(c->chain_dev);
+        if (c->chain_host) hipHostFree(c->chain_host);
     }
     free(c->slot_of);
     free(c->key_of);
@@ -697,46 +699,175 @@ int k3gc_moe(K3gCtx *ctx, K3gCache *c, const K3gLayer *L, int layer, const float
         /* the staging buffer is reused by the next call: let the copies finish */
         K3G_CHECK(hipStreamSynchronize(st));
     }
-    /* the step's unique experts in first-seen order: getmany, then one get each */
+    /* tokens in groups whose experts fit the unpinned slots together (every slot a
+     * group gets stays put until the group's kernels are done); per group, its unique
+     * experts in first-seen order: getmany, then one get each */
+    int npinned = 0;
+    for (int i = 0; i < c->nslot; i++) npinned += c->pinned[i] != 0;
+    const int cap = c->nslot - npinned;
     int *uniq = (int *)malloc((size_t)P * sizeof(int));
     unsigned char *seen = (unsigned char *)calloc((size_t)c->n_experts, 1);
-    if (!uniq || !seen) { free(uniq); free(seen); return -1; }
-    int nu = 0;
-    for (int p = 0; p < P; p++) {
-        const int e = c->host_idx[p];
-        if (e >= 0 && e < c->n_experts && !seen[e]) { seen[e] = 1; uniq[nu++] = e; }
+    if (!uniq || !seen || cap < 1) { free(uniq); free(seen); return -1; }
+    K3ExpertQ *table = c->dev_table + (size_t)layer * c->n_experts;
+    const int d = L->hidden;
+    int rc = 0;
+    for (int t0 = 0; t0 < T && rc == 0;) {
+        memset(seen, 0, (size_t)c->n_experts);
+        int nu = 0, t1 = t0;
+        while (t1 < T) {
+            int add = 0;
+            for (int j = 0; j < k; j++) {
+                const int e = c->host_idx[t1 * k + j];
+                if (e >= 0 && e < c->n_experts && !seen[e]) {
+                    int dup = 0;
+                    for (int q = 0; q < j; q++) dup |= c->host_idx[t1 * k + q] == e;
+                    add += !dup;
+                }
+            }
+            if (nu + add > cap && t1 > t0) break;
+            for (int j = 0; j < k; j++) {
+                const int e = c->host_idx[t1 * k + j];
+                if (e >= 0 && e < c->n_experts && !seen[e]) { seen[e] = 1; uniq[nu++] = e; }
+            }
+            t1++;
+        }
+        k3gc_step_begin(c);
+        for (int i = 0; i < nu; i += K3_MAX_TOPK)
+            cache_getmany(&c->src, layer, uniq + i, nu - i < K3_MAX_TOPK ? nu - i : K3_MAX_TOPK);
+        K3kEqSet set;
+        memset(&set, 0, sizeof set);
+        for (int i = 0; i < nu && rc == 0; i++) {
+            K3ExpertQ q;
+            if (cache_get(&c->src, layer, uniq[i], &q) != 0) { rc = -1; break; }
+            set.e[set.n] = uniq[i];
+            set.q[set.n] = q;
+            if (++set.n == K3K_EQSET) {
+                rc |= k3k_set_experts(table, &set, st);
+                set.n = 0;
+            }
+        }
+        if (rc == 0 && set.n) rc |= k3k_set_experts(table, &set, st);
+        if (rc == 0) {
+            K3gLayer Lc = *L;
+            Lc.experts = table;
+            Lc.expert_fmt = K3G_EXPERT_MXFP4_TILED;
+            /* the shared expert runs while the misses copy; the routed experts wait */
+            if (c->copies_pending) {
+                k3g_ctx_routed_wait(ctx, c->last_copy);
+                c->copies_pending = 0;
+            }
+            rc = k3g_experts(ctx, &Lc, x + (size_t)t0 * d, t1 - t0, idx + (size_t)t0 * k,
+                             wt + (size_t)t0 * k, out + (size_t)t0 * d, st);
+        }
+        k3gc_step_end(c, st);
+        t0 = t1;
+    }
+    free(uniq);
+    free(seen);
+    return rc;
+}
+
+/* ------------------------------------------------------------- chained layers ---- */
+/* The step's unique experts of routing idx [T][k] in first-seen order, through getmany
+ * then one get each (the calls k3gc_moe makes); returns 0 or -1 on a failed get. */
+static int account_step(K3gCache *c, int layer, const int32_t *idx, int P, hipStream_t st)
+{
+    int uniq[4 * K3_MAX_TOPK * 4];
+    int nu = 0, rc = 0;
+    for (int p = 0; p < P && nu < (int)(sizeof uniq / sizeof uniq[0]); p++) {
+        const int e = idx[p];
+        if (e < 0 || e >= c->n_experts) continue;
+        int dup = 0;
+        for (int j = 0; j < nu; j++) if (uniq[j] == e) { dup = 1; break; }
+        if (!dup) uniq[nu++] = e;
     }
     k3gc_step_begin(c);
     for (int i = 0; i < nu; i += K3_MAX_TOPK)
         cache_getmany(&c->src, layer, uniq + i, nu - i < K3_MAX_TOPK ? nu - i : K3_MAX_TOPK);
-    int rc = 0;
-    K3ExpertQ *table = c->dev_table + (size_t)layer * c->n_experts;
-    K3kEqSet set;
-    memset(&set, 0, sizeof set);
-    for (int i = 0; i < nu; i++) {
-        K3ExpertQ q;
-        if (cache_get(&c->src, layer, uniq[i], &q) != 0) { rc = -1; break; }
-        set.e[set.n] = uniq[i];
-        set.q[set.n] = q;
-        if (++set.n == K3K_EQSET) {
-            rc |= k3k_set_experts(table, &set, st);
-            set.n = 0;
-        }
-    }
-    if (rc == 0 && set.n) rc |= k3k_set_experts(table, &set, st);
-    free(uniq);
-    free(seen);
-    if (rc == 0) {
-        K3gLayer Lc = *L;
-        Lc.experts = table;
-        Lc.expert_fmt = K3G_EXPERT_MXFP4_TILED;
-        /* the shared expert runs while the misses copy; the routed experts wait */
-        if (c->copies_pending) {
-            k3g_ctx_routed_wait(ctx, c->last_copy);
-            c->copies_pending = 0;
-        }
-        rc = k3g_experts(ctx, &Lc, x, T, idx, wt, out, st);
-    }
+    for (int i = 0; i < nu; i++)
+        if (cache_get(&c->src, layer, uniq[i], NULL) != 0) rc = -1;
     k3gc_step_end(c, st);
     return rc;
 }
+
+int k3gc_chain(K3gCtx *ctx, K3gCache *c, const K3gLayer *layers, const float *const *post_norm,
+               int first_layer, int n_layers, float *h, int T, float rms_eps, void *stream)
+{
+    if (!ctx || !c || !has_device(c) || !layers || !h || n_layers < 1 || T < 1 ||
+        first_layer < 0 || first_layer + n_layers > c->n_layers)
+        return -1;
+    hipStream_t st = stream ? (hipStream_t)stream : (hipStream_t)k3g_ctx_stream(ctx);
+    const int d = layers[0].hidden;
+    int kmax = 1;
+    for (int l = 0; l < n_layers; l++) {
+        if (layers[l].hidden != d) return -1;
+        if (layers[l].topk > kmax) kmax = layers[l].topk;
+    }
+    const size_t act = ((size_t)T * d * 4 + 255) & ~(size_t)255;
+    const size_t rt = ((size_t)T * kmax * 4 + 255) & ~(size_t)255;
+    const size_t need = 2 * act + 2 * rt * (size_t)n_layers;
+    if (need > c->chain_dev_bytes) {
+        if (c->chain_dev) {
+            K3G_CHECK(hipDeviceSynchronize());
+            K3G_CHECK(hipFree(c->chain_dev));
+        }
+        c->chain_dev = NULL;
+        if (hipMalloc((void **)&c->chain_dev, need) != hipSuccess) return -1;
+        c->chain_dev_bytes = need;
+    }
+    const size_t hneed = rt * (size_t)n_layers;
+    if (hneed > c->chain_host_bytes) {
+        if (c->chain_host) {
+            K3G_CHECK(hipDeviceSynchronize());
+            K3G_CHECK(hipHostFree(c->chain_host));
+        }
+        c->chain_host = NULL;
+        if (hipHostMalloc((void **)&c->chain_host, hneed, hipHostMallocDefault) != hipSuccess)
+            return -1;
+        c->chain_host_bytes = hneed;
+    }
+    float *hin = (float *)c->chain_dev, *tmp = (float *)(c->chain_dev + act);
+    unsigned char *rbase = c->chain_dev + 2 * act;
+    /* every expert of every layer resident: the layers run back to back on the cache's
+     * device tables with no host synchronisation, the accounting after them */
+    int resident = c->bank->layout == K3G_EXPERT_MXFP4_TILED;
+    for (int l = 0; l < n_layers && resident; l++)
+        resident = k3gc_layer_all_resident(c, first_layer + l);
+    if (resident) k3gc_wait(c, st);
+    int rc = 0;
+    for (int l = 0; l < n_layers && rc == 0; l++) {
+        const K3gLayer *L = &layers[l];
+        const int layer = first_layer + l, P = T * L->topk;
+        int32_t *idx = (int32_t *)(rbase + 2 * rt * (size_t)l);
+        float *wt = (float *)(rbase + 2 * rt * (size_t)l + rt);
+        /* hin = RMSNorm(h) x post_norm (src/core/k3_ops.c:1015-1016) */
+        const float *in = h;
+        if (post_norm && post_norm[l]) {
+            if (k3k_rmsnorm(hin, h, post_norm[l], d, T, rms_eps, st) != 0) return -1;
+            in = hin;
+        }
+        if (resident) {
+            K3gLayer G = *L;
+            G.experts = k3gc_layer_table(c, layer, st);
+            G.expert_fmt = K3G_EXPERT_MXFP4_TILED;
+            if (!G.experts) return -1;
+            rc = k3g_moe(ctx, &G, in, T, tmp, idx, wt, st);
+            if (rc == 0)
+                K3G_CHECK(hipMemcpyAsync((unsigned char *)c->chain_host + rt * (size_t)l, idx,
+                                         (size_t)P * 4, hipMemcpyDeviceToHost, st));
+        } else {
+            rc = k3gc_moe(ctx, c, L, layer, in, T, tmp, idx, wt, NULL, NULL, st);
+        }
+        /* h += the layer's MoE output (src/core/k3_ops.c:1035-1036) */
+        if (rc == 0) rc = k3k_add(h, tmp, (size_t)T * d, st);
+    }
+    if (resident && rc == 0) {
+        K3G_CHECK(hipStreamSynchronize(st));
+        for (int l = 0; l < n_layers && rc == 0; l++)
+            rc = account_step(c, first_layer + l,
+                              (const int32_t *)((unsigned char *)c->chain_host + rt * (size_t)l),
+                              T * layers[l].topk, st);
+    }
+    return rc;
+}
+

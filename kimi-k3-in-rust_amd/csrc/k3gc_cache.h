@@ -63,6 +63,12 @@ struct K3gCache {
     unsigned char *table_dirty;   /* [n_layers] dev_table row behind the slots */
     int32_t *host_idx;            /* pinned staging of a step's routing */
     int host_idx_cap;
+    /* k3gc_chain's buffers, grow-only: device hin/tmp [T][hidden] and idx/wt per layer;
+     * pinned routing per layer */
+    unsigned char *chain_dev;
+    size_t chain_dev_bytes;
+    int32_t *chain_host;
+    size_t chain_host_bytes;
     /* stats (src/cache/k3_cache.h:74-83) */
     uint64_t hits, misses, evictions, bytes_read, prefetch_reads;
     double load_seconds;

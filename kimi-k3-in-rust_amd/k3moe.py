@@ -239,6 +239,8 @@ def lib() -> C.CDLL:
         L.k3gc_wait.restype = None
         L.k3gc_moe.argtypes = [vp, vp, C.POINTER(K3gLayer), i, vp, i, vp, vp, vp, vp, vp, vp]
         L.k3gc_moe.restype = i
+        L.k3gc_chain.argtypes = [vp, vp, vp, vp, i, i, vp, i, f, vp]
+        L.k3gc_chain.restype = i
         L.k3gc_pin_hottest.argtypes = [vp, vp, i]
         L.k3gc_pin_hottest.restype = i
         L.k3gc_hist.argtypes = [vp]
@@ -831,6 +833,17 @@ class Cache:
                             None if rw is None else rw.ctypes.data, None)
         if rc != 0:
             raise RuntimeError("k3gc_moe failed")
+
+    def chain(self, ctx: "Ctx", layers: list, post_norms: list, first_layer: int, h_ptr: int,
+              T: int, rms_eps: float = 1e-5) -> None:
+        """k3gc_chain: h (device [T][hidden]) through the MoE half of len(layers) layers;
+        post_norms: device pointers of the RMSNorm weights (None entries: no norm)."""
+        arr = (K3gLayer * len(layers))(*layers)
+        pn = (C.c_void_p * len(layers))(*[p if p else None for p in post_norms])
+        rc = lib().k3gc_chain(ctx.ptr, self.ptr, arr, pn, first_layer, len(layers),
+                              C.c_void_p(h_ptr), T, rms_eps, None)
+        if rc != 0:
+            raise RuntimeError("k3gc_chain failed")
 
     def free(self) -> None:
         if self.ptr:
