@@ -396,6 +396,11 @@ int  k3gc_bank_create(K3gcBank **bank, int n_layers, int n_experts, int hidden, 
  * must not copy at the same time. No reference counterpart. */
 int  k3gc_bank_create_ex(K3gcBank **bank, int n_layers, int n_experts, int hidden,
                          int inter, int layout, int max_pinned_layers);
+/* A bank of checkpoint-layout runs of expert_bytes each with no layer shape: it holds and
+ * serves bytes (k3gc_bank_load, a cache's get) but a layer cannot run on it. For
+ * checkpoints whose expert matrices do not form a layer (test fixtures). */
+int  k3gc_bank_create_raw(K3gcBank **bank, int n_layers, int n_experts, int64_t expert_bytes,
+                          int max_pinned_layers);
 /* A bank with the geometry only (no memory), for caches that keep the bookkeeping only
  * (k3gc_init with device < 0): replays of a request trace at any capacity, as the
  * engine's offline simulator does. */
@@ -407,6 +412,41 @@ int64_t k3gc_bank_expert_bytes(const K3gcBank *bank);
 /* layers whose runs sit in pinned memory (the rest are pageable when the driver caps
  * pinned memory below the bank's size) */
 int  k3gc_bank_pinned_layers(const K3gcBank *bank);
+
+/* Routed experts from safetensors checkpoint shards. An index of every tensor of every
+ * *.safetensors file of a directory, shards numbered in name order (the engine's
+ * k3_st_open / k3_st_find, src/io/k3_st.c:364-452). Returns 0, or -1 with a message (no
+ * shards, a malformed header, a span that disagrees with its shape, duplicate names). */
+typedef struct K3gcSt K3gcSt;
+int  k3gc_st_open(K3gcSt **st, const char *dir);
+void k3gc_st_close(K3gcSt *st);
+int  k3gc_st_count(const K3gcSt *st);            /* tensors indexed */
+
+/* One routed expert's six U8 tensors (w1, w2, w3: weight_packed, weight_scale), validated
+ * as the engine's k3_expert_ref does (src/io/k3_load.c:15-100): 2-D, rows agreeing, one
+ * scale byte per 32 elements, one shard. contiguous: the six spans tile one run in the
+ * order w1.packed w1.scale w2.packed w2.scale w3.packed w3.scale (src/io/k3_load.h:3-9). */
+typedef struct {
+    int shard;
+    int64_t off, nbytes;          /* the run: first byte in the shard, total bytes */
+    int contiguous;
+    int rows[3], pcols[3];        /* w1, w2, w3: packed [rows][pcols] */
+    int64_t p_bytes[3], s_bytes[3], p_file[3], s_file[3];
+} K3gcExpertRun;
+int  k3gc_st_expert(const K3gcSt *st, int layer, int expert, K3gcExpertRun *run);
+/* The run's bytes in the checkpoint order into dst (run->nbytes): one read when
+ * contiguous, six otherwise (src/io/k3_load.c:105-136). Returns 0, or -1 on a short read. */
+int  k3gc_st_read_run(const K3gcSt *st, const K3gcExpertRun *run, unsigned char *dst);
+/* Bank layers [bank_layer0, + n_layers) from checkpoint layers [ck_layer0, + n_layers):
+ * every expert's run read straight into the bank's host memory (checkpoint layout), or
+ * read and tiled on the host (tiled layout). A bank with a layer shape takes only experts
+ * of that shape. Returns 0, or -1 with a message. No reference counterpart: the engine
+ * reads experts from the checkpoint on each miss (k3_expert_load_direct). */
+int  k3gc_bank_load(K3gcBank *bank, const K3gcSt *st, int ck_layer0, int bank_layer0,
+                    int n_layers);
+/* The tiled MXFP4 layout of k3g_tile_mxfp4, written by the host (same bytes). */
+int  k3gc_tile_mxfp4_host(unsigned char *dst, const unsigned char *packed,
+                          const unsigned char *scales, int rows, int cols);
 
 /* Replaces k3_cache_init (src/cache/k3_cache.h:97, src/cache/k3_cache.c:263-353):
  * budget_bytes of HBM rounded down to whole slots; fails (-1) below topk + 1 slots.

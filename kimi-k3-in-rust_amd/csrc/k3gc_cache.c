@@ -38,6 +38,9 @@ int k3gc_bank_create(K3gcBank **out, int n_layers, int n_experts, int hidden, in
     return k3gc_bank_create_ex(out, n_layers, n_experts, hidden, inter, layout, -1);
 }
 
+static int bank_alloc(K3gcBank **out, int n_layers, int n_experts, int hidden, int inter,
+                      int layout, int64_t eb, int max_pinned_layers);
+
 int k3gc_bank_create_ex(K3gcBank **out, int n_layers, int n_experts, int hidden, int inter,
                         int layout, int max_pinned_layers)
 {
@@ -53,6 +56,21 @@ int k3gc_bank_create_ex(K3gcBank **out, int n_layers, int n_experts, int hidden,
                 inter);
         return -1;
     }
+    return bank_alloc(out, n_layers, n_experts, hidden, inter, layout, eb, max_pinned_layers);
+}
+
+int k3gc_bank_create_raw(K3gcBank **out, int n_layers, int n_experts, int64_t expert_bytes,
+                         int max_pinned_layers)
+{
+    *out = NULL;
+    if (n_layers < 1 || n_experts < 1 || expert_bytes < 1) return -1;
+    return bank_alloc(out, n_layers, n_experts, 0, 0, K3G_EXPERT_MXFP4, expert_bytes,
+                      max_pinned_layers);
+}
+
+static int bank_alloc(K3gcBank **out, int n_layers, int n_experts, int hidden, int inter,
+                      int layout, int64_t eb, int max_pinned_layers)
+{
     K3gcBank *b = (K3gcBank *)calloc(1, sizeof *b);
     if (!b) return -1;
     b->n_layers = n_layers;
@@ -172,6 +190,13 @@ static void fill_q(const K3gCache *c, int slot, K3ExpertQ *q)
         q->p1 = (const unsigned char *)base;
         q->p3 = (const unsigned char *)(base + t13);
         q->p2 = (const unsigned char *)(base + 2 * t13);
+    } else if (b->hidden == 0) {
+        q->p1 = (const unsigned char *)(base + b->raw_off[0]);
+        q->s1 = (const unsigned char *)(base + b->raw_off[1]);
+        q->p2 = (const unsigned char *)(base + b->raw_off[2]);
+        q->s2 = (const unsigned char *)(base + b->raw_off[3]);
+        q->p3 = (const unsigned char *)(base + b->raw_off[4]);
+        q->s3 = (const unsigned char *)(base + b->raw_off[5]);
     } else {
         const K3gExpertLayout g = k3g_expert_layout(b->hidden, b->inter);
         q->p1 = (const unsigned char *)(base + g.p1_off);

@@ -22,6 +22,10 @@
 struct K3gcBank {
     int n_layers, n_experts, hidden, inter, layout;
     int64_t expert_bytes;
+    /* a bank without a layer shape (hidden == 0): the six matrices' offsets in a run,
+     * w1p w1s w2p w2s w3p w3s, as the checkpoint's runs have them (k3gc_bank_load) */
+    int64_t raw_off[6];
+    int raw_geometry;
     unsigned char **layer_host;   /* [n_layers]: [n_experts][expert_bytes] each */
     unsigned char *layer_pinned;  /* [n_layers]: 1 hipHostMalloc, 0 pageable malloc */
     int pinned_layers;

@@ -79,6 +79,14 @@ class K3MoeW(C.Structure):
     ]
 
 
+class K3gcExpertRun(C.Structure):
+    """include/k3moe.h K3gcExpertRun"""
+    _fields_ = [("shard", C.c_int), ("off", C.c_int64), ("nbytes", C.c_int64),
+                ("contiguous", C.c_int), ("rows", C.c_int * 3), ("pcols", C.c_int * 3),
+                ("p_bytes", C.c_int64 * 3), ("s_bytes", C.c_int64 * 3),
+                ("p_file", C.c_int64 * 3), ("s_file", C.c_int64 * 3)]
+
+
 class K3gExpertLayout(C.Structure):
     _fields_ = [("p1_off", C.c_int64), ("s1_off", C.c_int64), ("p2_off", C.c_int64),
                 ("s2_off", C.c_int64), ("p3_off", C.c_int64), ("s3_off", C.c_int64),
@@ -239,6 +247,22 @@ def lib() -> C.CDLL:
         L.k3gc_wait.restype = None
         L.k3gc_moe.argtypes = [vp, vp, C.POINTER(K3gLayer), i, vp, i, vp, vp, vp, vp, vp, vp]
         L.k3gc_moe.restype = i
+        L.k3gc_bank_create_raw.argtypes = [C.POINTER(vp), i, i, i64, i]
+        L.k3gc_bank_create_raw.restype = i
+        L.k3gc_st_open.argtypes = [C.POINTER(vp), C.c_char_p]
+        L.k3gc_st_open.restype = i
+        L.k3gc_st_close.argtypes = [vp]
+        L.k3gc_st_close.restype = None
+        L.k3gc_st_count.argtypes = [vp]
+        L.k3gc_st_count.restype = i
+        L.k3gc_st_expert.argtypes = [vp, i, i, C.POINTER(K3gcExpertRun)]
+        L.k3gc_st_expert.restype = i
+        L.k3gc_st_read_run.argtypes = [vp, C.POINTER(K3gcExpertRun), vp]
+        L.k3gc_st_read_run.restype = i
+        L.k3gc_bank_load.argtypes = [vp, vp, i, i, i]
+        L.k3gc_bank_load.restype = i
+        L.k3gc_tile_mxfp4_host.argtypes = [vp, vp, vp, i, i]
+        L.k3gc_tile_mxfp4_host.restype = i
         L.k3gc_chain.argtypes = [vp, vp, vp, vp, i, i, vp, i, f, vp]
         L.k3gc_chain.restype = i
         L.k3gc_pin_hottest.argtypes = [vp, vp, i]
@@ -725,9 +749,15 @@ class Bank:
 
     def __init__(self, n_layers: int, n_experts: int, hidden: int = 0, inter: int = 0,
                  layout: int = K3G_EXPERT_MXFP4_TILED, expert_bytes: int = 0,
-                 max_pinned_layers: int = -1):
+                 max_pinned_layers: int = -1, raw: bool = False):
+        """raw: host memory for runs of expert_bytes with no layer shape
+        (k3gc_bank_create_raw); expert_bytes alone: the geometry only."""
         self.ptr = C.c_void_p()
-        if expert_bytes:
+        if raw:
+            rc = lib().k3gc_bank_create_raw(C.byref(self.ptr), n_layers, n_experts, expert_bytes,
+                                            max_pinned_layers)
+            layout = K3G_EXPERT_MXFP4
+        elif expert_bytes:
             rc = lib().k3gc_bank_geometry(C.byref(self.ptr), n_layers, n_experts, expert_bytes)
         else:
             rc = lib().k3gc_bank_create_ex(C.byref(self.ptr), n_layers, n_experts, hidden,
@@ -740,6 +770,14 @@ class Bank:
 
     def expert(self, layer: int, e: int) -> int:
         return lib().k3gc_bank_expert(self.ptr, layer, e)
+
+    def expert_bytes_of(self, layer: int, e: int) -> np.ndarray:
+        """a copy of the run of (layer, e) in the bank's host memory"""
+        return np.frombuffer(C.string_at(self.expert(layer, e), self.expert_bytes), np.uint8).copy()
+
+    def load(self, st: "St", ck_layer0: int, bank_layer0: int, n_layers: int) -> None:
+        if lib().k3gc_bank_load(self.ptr, st.ptr, ck_layer0, bank_layer0, n_layers) != 0:
+            raise RuntimeError("k3gc_bank_load failed")
 
     def fill_from_layer(self, layer_obj: "SynthLayer", layer: int) -> None:
         """copy every expert run of a device-resident SynthLayer into this bank row"""
@@ -762,6 +800,51 @@ class Bank:
             self.free()
         except Exception:
             pass
+
+
+class St:
+    """An index of the safetensors shards of a directory (k3gc_st_open)."""
+
+    def __init__(self, path: str):
+        self.ptr = C.c_void_p()
+        if lib().k3gc_st_open(C.byref(self.ptr), path.encode()) != 0:
+            raise RuntimeError(f"k3gc_st_open({path}) failed")
+
+    def count(self) -> int:
+        return lib().k3gc_st_count(self.ptr)
+
+    def expert(self, layer: int, e: int) -> K3gcExpertRun:
+        r = K3gcExpertRun()
+        if lib().k3gc_st_expert(self.ptr, layer, e, C.byref(r)) != 0:
+            raise KeyError((layer, e))
+        return r
+
+    def read_run(self, r: K3gcExpertRun) -> np.ndarray:
+        out = np.empty(r.nbytes, np.uint8)
+        if lib().k3gc_st_read_run(self.ptr, C.byref(r), out.ctypes.data) != 0:
+            raise IOError("short read")
+        return out
+
+    def close(self) -> None:
+        if self.ptr:
+            lib().k3gc_st_close(self.ptr)
+            self.ptr = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def tile_mxfp4_host(packed: np.ndarray, scales: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """k3gc_tile_mxfp4_host: the tiled layout written by the host"""
+    n = lib().k3g_tiled_mxfp4_bytes(rows, cols)
+    out = np.empty(n, np.uint8)
+    p, s = np.ascontiguousarray(packed, np.uint8), np.ascontiguousarray(scales, np.uint8)
+    if lib().k3gc_tile_mxfp4_host(out.ctypes.data, p.ctypes.data, s.ctypes.data, rows, cols) != 0:
+        raise ValueError("no tiled layout for this shape")
+    return out
 
 
 class Cache:

@@ -10,6 +10,10 @@ reference's tests hold:
   tests/fixtures/ops/MANIFEST.json  tolerances (fp32_abs, fp32_rel)
   tests/fixtures/mxfp4.json         real checkpoint MXFP4 bytes + exact dequant (test_ops.c:743-796)
   tests/fixtures/expert_trace.bin   100,096 (layer, expert) requests (k3_cache.c:244-255)
+  tests/fixtures/cache/model-00001-of-00001.safetensors
+                                    a structurally real checkpoint shard, 24 routed experts
+                                    (144 tensors) of layer 0 (test_cache.c:86-140), copied as
+                                    is into cache_fixture/
 
 plus the byte layout of the engine's public structs, measured by compiling a probe
 against include/k3/k3.h, so the ABI test can check this library's layouts without the
@@ -95,6 +99,13 @@ def trace():
     np.savez_compressed(os.path.join(OUT, "expert_trace.npz"), pairs=raw.reshape(-1, 2))
 
 
+def cache_fixture():
+    import shutil
+    os.makedirs(os.path.join(OUT, "cache_fixture"), exist_ok=True)
+    shutil.copyfile(os.path.join(FX, "cache", "model-00001-of-00001.safetensors"),
+                    os.path.join(OUT, "cache_fixture", "model-00001-of-00001.safetensors"))
+
+
 def layouts():
     fields = {
         "K3Cfg": ["hidden", "rms_eps", "n_experts", "topk", "n_shared", "latent", "moe_inter",
@@ -126,6 +137,6 @@ def layouts():
 
 
 if __name__ == "__main__":
-    router(); moe(); situ(); mxfp4(); manifest(); trace(); layouts()
+    router(); moe(); situ(); mxfp4(); manifest(); trace(); cache_fixture(); layouts()
     for f in sorted(os.listdir(OUT)):
         print(f, os.path.getsize(os.path.join(OUT, f)))

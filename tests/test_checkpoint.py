@@ -1,0 +1,162 @@
+"""Routed experts from safetensors shards into the HBM cache's host bank, on the CPU: the
+index of the engine's own cache fixture (tests/fixtures/cache, 24 experts, 144 tensors)
+and byte-exact runs in a bank; a synthetic checkpoint of the tiny layer (two shards, one
+expert whose tensors are out of order, header entries shuffled, a __metadata__ entry) into
+checkpoint-layout and tiled banks, against the runs it was written from and the tiled
+layout written independently; and the loader's refusals."""
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+import k3moe
+from safetensors_io import expert_tensors, write_shard
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+FIXTURE = os.path.join(GOLDEN, "cache_fixture")
+
+
+def _fixture_runs():
+    """The fixture's expert runs, read independently from the file: for expert e the six
+    tensors' bytes in the order w1.packed w1.scale w2.packed w2.scale w3.packed w3.scale."""
+    raw = open(os.path.join(FIXTURE, "model-00001-of-00001.safetensors"), "rb").read()
+    n = struct.unpack("<Q", raw[:8])[0]
+    head = json.loads(raw[8:8 + n])
+    runs = {}
+    for e in range(24):
+        parts = []
+        for w in ("w1", "w2", "w3"):
+            for kind in ("weight_packed", "weight_scale"):
+                o0, o1 = head[f"language_model.model.layers.0.block_sparse_moe.experts.{e}.{w}.{kind}"]["data_offsets"]
+                parts.append(np.frombuffer(raw[8 + n + o0:8 + n + o1], np.uint8))
+        runs[e] = np.concatenate(parts)
+    return runs
+
+
+def test_index_of_the_engine_fixture():
+    st = k3moe.St(FIXTURE)
+    assert st.count() == 144
+    runs = _fixture_runs()
+    for e in range(24):
+        r = st.expert(0, e)
+        assert r.contiguous == 1 and r.nbytes == 1632
+        assert list(r.rows) == [8, 8, 8] and list(r.pcols) == [64, 64, 64]
+        assert np.array_equal(st.read_run(r), runs[e])
+    with pytest.raises(KeyError):
+        st.expert(0, 24)
+    with pytest.raises(KeyError):
+        st.expert(1, 0)
+
+
+def test_fixture_runs_into_a_bank_byte_exact():
+    runs = _fixture_runs()
+    bank = k3moe.Bank(1, 24, expert_bytes=1632, raw=True)
+    bank.load(k3moe.St(FIXTURE), 0, 0, 1)
+    for e in range(24):
+        assert np.array_equal(bank.expert_bytes_of(0, e), runs[e]), e
+    bank.free()
+
+
+def _tile_py(packed, scales, rows, cols):
+    """The tiled MXFP4 layout, block by block (the layout k3g_tile.hip defines)."""
+    nq = (cols + 511) // 512
+    out = np.zeros((rows // 16) * nq * 4352, np.uint8)
+    for r in range(rows):
+        for b in range(nq * 16):
+            rb, Q, j, g = r // 16, b // 16, (b % 16) // 4, b % 4
+            L = 16 * g + r % 16
+            base = (rb * nq + Q) * 4352
+            live = 32 * b < cols and scales[r, b] != 255
+            out[base + 1024 * j + 16 * L: base + 1024 * j + 16 * L + 16] = (
+                packed[r, 16 * b:16 * b + 16] if live else 0)
+            out[base + 4096 + 4 * L + j] = scales[r, b] if live else 127
+    return out
+
+
+@pytest.mark.parametrize("rows,cols", [(16, 32), (32, 96), (48, 1056)])
+def test_host_tiler_matches_the_layout(rows, cols):
+    packed = k3moe.host_bytes(rows * cols // 2, 3, 1).reshape(rows, cols // 2)
+    scales = k3moe.host_scales(rows * cols // 32, 3, 2, -3, 3).reshape(rows, cols // 32)
+    scales[0, 0] = 255
+    assert np.array_equal(k3moe.tile_mxfp4_host(packed, scales, rows, cols),
+                          _tile_py(packed, scales, rows, cols))
+
+
+def write_checkpoint(d, layer_objs, scramble=(1, 5)):
+    """Two shards for the given layers (checkpoint layers = their .layer): experts 0..7 in
+    shard 1, 8..15 in shard 2; expert `scramble` = (layer, e) has its six tensors written
+    in reverse order (not one run in the checkpoint order); header entries shuffled."""
+    s1, s2 = [], []
+    for lay in layer_objs:
+        s = lay.shape
+        for e in range(s.n_experts):
+            t = expert_tensors(lay.layer, e, lay.expert_host(e), lay.geo, s.inter, s.hidden)
+            if (lay.layer, e) == scramble:
+                t = t[::-1]
+            (s1 if e < 8 else s2).extend(t)
+    rng = np.random.default_rng(1)
+    for name, ts in (("model-00001-of-00002.safetensors", s1),
+                     ("model-00002-of-00002.safetensors", s2)):
+        order = [n for n, _ in ts]
+        rng.shuffle(order)
+        write_shard(os.path.join(d, name), ts, metadata={"format": "pt"}, header_order=order)
+
+
+def test_synthetic_checkpoint_into_banks(tmp_path):
+    layers = [k3moe.SynthLayer(k3moe.TINY, seed=88, layer=l, device=False) for l in range(2)]
+    write_checkpoint(str(tmp_path), layers)
+    st = k3moe.St(str(tmp_path))
+    assert st.count() == 2 * 16 * 6
+    assert st.expert(1, 5).contiguous == 0 and st.expert(1, 4).contiguous == 1
+    assert st.expert(0, 3).shard == 0 and st.expert(0, 12).shard == 1
+    d, I = 256, 128
+    ck = k3moe.Bank(2, 16, d, I, k3moe.K3G_EXPERT_MXFP4)
+    ck.load(st, 0, 0, 2)
+    tb = k3moe.Bank(2, 16, d, I, k3moe.K3G_EXPERT_MXFP4_TILED)
+    tb.load(st, 0, 0, 2)
+    g = layers[0].geo
+    for lay in layers:
+        for e in range(16):
+            run = lay.expert_host(e)
+            assert np.array_equal(ck.expert_bytes_of(lay.layer, e), run), (lay.layer, e)
+            want = np.concatenate([
+                _tile_py(run[g.p1_off:g.s1_off].reshape(I, d // 2), run[g.s1_off:g.p2_off].reshape(I, d // 32), I, d),
+                _tile_py(run[g.p3_off:g.s3_off].reshape(I, d // 2), run[g.s3_off:g.nbytes].reshape(I, d // 32), I, d),
+                _tile_py(run[g.p2_off:g.s2_off].reshape(d, I // 2), run[g.s2_off:g.p3_off].reshape(d, I // 32), d, I)])
+            assert np.array_equal(tb.expert_bytes_of(lay.layer, e), want), (lay.layer, e)
+    # checkpoint layer 1 into bank layer 0
+    one = k3moe.Bank(1, 16, d, I, k3moe.K3G_EXPERT_MXFP4)
+    one.load(st, 1, 0, 1)
+    assert np.array_equal(one.expert_bytes_of(0, 7), layers[1].expert_host(7))
+
+
+def test_loader_refusals(tmp_path):
+    lay = k3moe.SynthLayer(k3moe.TINY, seed=89, device=False)
+    good = expert_tensors(0, 0, lay.expert_host(0), lay.geo, 128, 256)
+    # a span that disagrees with its shape
+    bad = str(tmp_path / "bad")
+    os.makedirs(bad)
+    write_shard(os.path.join(bad, "a.safetensors"), good)
+    raw = bytearray(open(os.path.join(bad, "a.safetensors"), "rb").read())
+    n = struct.unpack("<Q", raw[:8])[0]
+    head = raw[8:8 + n].decode().replace('"shape": [128, 128]', '"shape": [128, 127]', 1)
+    raw[8:8 + n] = head.encode()
+    open(os.path.join(bad, "a.safetensors"), "wb").write(bytes(raw))
+    with pytest.raises(RuntimeError):
+        k3moe.St(bad)
+    # experts missing: the bank wants 16, the shard has 1
+    part = str(tmp_path / "part")
+    os.makedirs(part)
+    write_shard(os.path.join(part, "a.safetensors"), good)
+    b = k3moe.Bank(1, 16, 256, 128, k3moe.K3G_EXPERT_MXFP4)
+    with pytest.raises(RuntimeError):
+        b.load(k3moe.St(part), 0, 0, 1)
+    # an expert of another shape than the bank's
+    b2 = k3moe.Bank(1, 1, 512, 128, k3moe.K3G_EXPERT_MXFP4)
+    with pytest.raises(RuntimeError):
+        b2.load(k3moe.St(part), 0, 0, 1)
+    # no shards at all
+    with pytest.raises(RuntimeError):
+        k3moe.St(str(tmp_path))
