@@ -285,7 +285,7 @@ void k3g_ctx_set_fp8(K3gCtx *ctx, int on);
  * for each ticket its start, the end of its waits and its end as wall-clock stamps
  * (100 MHz counter), then the top-k ticket's stamps after its wait, after its selection
  * and inside the selection. Calls on the grouped GEMMs write 4 uint64 per workgroup of
- * the routed gate/up launch (8 ceil(tiles / 8) ceil(inter / 128) workgroups, tiles =
+ * the routed gate/up launch (8 * 4 ceil(tiles / 32) * ceil(inter / 128) workgroups, tiles =
  * ceil(T topk / 128) + min(n_experts, T topk)), then of the routed down launch: wave 0's
  * start and end, column tile << 32 | feature tile, XCC << 32 | HW_ID. NULL turns it off.
  * No reference counterpart. */

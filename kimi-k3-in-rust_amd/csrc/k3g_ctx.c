@@ -91,6 +91,12 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
         free(c);
         return -1;
     }
+    if (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_in, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&c->ev_routed, hipEventDisableTiming) != hipSuccess) {
+        fprintf(stderr, "k3moe: k3g_ctx_create: cannot create the side stream\n");
+        return -1;
+    }
     const size_t T = (size_t)max_tokens, E = (size_t)c->n_experts, k = (size_t)c->topk;
     const size_t P = T * k, nch = (P + 255) / 256;
     const size_t L = (size_t)c->latent, I = (size_t)c->inter, SI = (size_t)c->shared_inter;
@@ -288,6 +294,10 @@ void k3g_ctx_destroy(K3gCtx *c)
                 hipEventDestroy(c->ev[s][i][1]);
             }
     hipFree(c->ws);
+    hipStreamSynchronize(c->side);
+    hipEventDestroy(c->ev_in);
+    hipEventDestroy(c->ev_routed);
+    hipStreamDestroy(c->side);
     hipStreamDestroy(c->stream);
     free(c);
 }
@@ -370,9 +380,28 @@ static int dense_gemm(K3gCtx *c, const void *W, int rows, int K, const uint16_t 
  * the routed experts on the FP4 x FP8 ones (fp8): dispatch -> column tiles -> x pieces ->
  * [shared gate/up, down] -> routed gate/up (+act) -> down -> [combine]. full = 0 stops at
  * the routed experts' per-pair rows in contrib. */
+static int gemm_body(K3gCtx *c, const K3gLayer *L, const float *x, int T,
+                     const int32_t *idx, const float *wt, float *out, float *contrib, int fp8,
+                     int full, hipEvent_t routed_ready, hipStream_t st);
+
 static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
                         const int32_t *idx, const float *wt, float *out, float *contrib,
                         int fp8, int full, hipStream_t st)
+{
+    int rc = 0;
+    k3g_stage_begin(c, K3G_ST_DISPATCH, st);
+    rc |= k3k_dispatch_tiles(idx, T * L->topk, L->n_experts, c->cnt, c->base, c->off, c->act,
+                             c->nact, c->perm, c->err, c->tiles, c->ntiles, c->xflag, st);
+    k3g_stage_end(c, K3G_ST_DISPATCH, st);
+    return rc | gemm_body(c, L, x, T, idx, wt, out, contrib, fp8, full, NULL, st);
+}
+
+/* The grouped GEMMs after the dispatch (column tiles built, x's piece-1 flag cleared):
+ * x pieces, [latent down], the shared expert, then (once routed_ready, when given) the
+ * routed gate/up and down, [combine, latent up, + shared]. */
+static int gemm_body(K3gCtx *c, const K3gLayer *L, const float *x, int T,
+                     const int32_t *idx, const float *wt, float *out, float *contrib, int fp8,
+                     int full, hipEvent_t routed_ready, hipStream_t st)
 {
     const int d = L->hidden, E = L->n_experts, k = L->topk, I = L->inter;
     const int SI = full ? L->shared_inter : 0, P = T * k;
@@ -380,10 +409,6 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     const int lat = L->latent > 0 ? L->latent : d, lat128 = r128(lat);
     const int projected = L->down != NULL;
     int rc = 0;
-    k3g_stage_begin(c, K3G_ST_DISPATCH, st);
-    rc |= k3k_dispatch_tiles(idx, P, E, c->cnt, c->base, c->off, c->act, c->nact, c->perm,
-                             c->err, c->tiles, c->ntiles, c->xflag, st);
-    k3g_stage_end(c, K3G_ST_DISPATCH, st);
     const int d512 = r512(d), I512 = r512(c->inter);
     k3g_stage_begin(c, K3G_ST_PIECES, st);
     rc |= k3k_xpieces(x, T, d, d128, c->xb, (long long)T * d128, c->xflag, st);
@@ -481,8 +506,9 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
         rc |= k3k_gemm(&s, st);
         k3g_stage_end(c, K3G_ST_SH_DOWN, st);
     }
-    /* routed experts last, after any copies they wait for (the shared expert above
-     * overlaps those copies) */
+    /* routed experts last, after their routing (computed beside the shared expert) and
+     * any copies they wait for (the shared expert above overlaps both) */
+    if (routed_ready && hipStreamWaitEvent(st, routed_ready, 0) != hipSuccess) rc = -1;
     if (c->routed_wait) {
         if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) rc = -1;
         c->routed_wait = NULL;
@@ -507,7 +533,7 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     rc |= fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
     k3g_stage_end(c, K3G_ST_GATEUP, st);
     /* the down launch's stamps follow the widest gate/up launch's (4-wave workgroups) */
-    if (g.trace) g.trace += 4 * 8 * (size_t)((g.max_tiles + 7) / 8) * (size_t)((I + 127) / 128);
+    if (g.trace) g.trace += 4 * 8 * (size_t)K3G_TILE_ROUNDS(g.max_tiles) * (size_t)((I + 127) / 128);
 
     g.mode = 1;
     g.rows = lat;
@@ -787,6 +813,27 @@ int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int
     if (fusable(c, L, T)) {
         c->paths |= 2;
         return run_fused(c, L, x, T, out, idx, wt, 0, st);
+    }
+    if (gemmable(c, L) && !c->routed_wait) {
+        /* the router and the dispatch on the side stream while the shared expert runs on
+         * this one; the routed experts wait for them. The side stream starts after all
+         * earlier work of this stream (the previous call's GEMMs read the dispatch's
+         * buffers). */
+        c->paths |= 4;
+        int rc = 0;
+        if (hipEventRecord(c->ev_in, st) != hipSuccess ||
+            hipStreamWaitEvent(c->side, c->ev_in, 0) != hipSuccess)
+            return -1;
+        rc |= k3g_route(c, L, x, T, idx, wt, c->side);
+        k3g_stage_begin(c, K3G_ST_DISPATCH, c->side);
+        rc |= k3k_dispatch_tiles(idx, T * L->topk, L->n_experts, c->cnt, c->base, c->off,
+                                 c->act, c->nact, c->perm, c->err, c->tiles, c->ntiles,
+                                 c->zflag, c->side);
+        k3g_stage_end(c, K3G_ST_DISPATCH, c->side);
+        if (hipEventRecord(c->ev_routed, c->side) != hipSuccess) return -1;
+        rc |= k3k_set_i32(c->xflag, 0, st);
+        rc |= gemm_body(c, L, x, T, idx, wt, out, c->contrib, c->gemm_fp8, 1, c->ev_routed, st);
+        return rc ? -1 : 0;
     }
     if (k3g_route(c, L, x, T, idx, wt, st) != 0) return -1;
     return k3g_experts(c, L, x, T, idx, wt, out, st);

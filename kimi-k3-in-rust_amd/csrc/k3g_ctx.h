@@ -68,6 +68,10 @@ struct K3gCtx {
     int32_t *tiles, *ntiles, *xflag;
     int max_tiles;
     hipEvent_t routed_wait;      /* the next k3g_experts waits for it before routed work */
+    /* a second compute stream (default priority): the router and dispatch of a grouped
+     * call run on it while the shared expert runs on the call's stream */
+    hipStream_t side;
+    hipEvent_t ev_in, ev_routed;
     int gemm_fp8;                /* routed experts on the FP4 x FP8 matrix cores */
     uint8_t *xq8b, *hq8b;        /* MXFP8 x [T][d512] + scales, h [T*k][I512] + scales */
     unsigned long long *trace;   /* optional per-ticket timestamps of the fused kernel */

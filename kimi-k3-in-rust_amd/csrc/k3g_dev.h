@@ -7,6 +7,7 @@
 #define K3G_WAVE 64
 #define K3G_TILE_COLS 128      /* pairs per column tile of the grouped GEMMs */
 
+
 typedef float k3v2f __attribute__((ext_vector_type(2)));
 
 /* Error codes a kernel may raise into the context's device error word. The host reads

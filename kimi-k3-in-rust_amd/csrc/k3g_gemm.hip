@@ -37,11 +37,13 @@
  * conflicts. K advances 128 per step: one barrier per step, the next step's weights and
  * activations in flight during the current step's matrix work.
  *
- * Workgroup order: column tiles are sorted largest first and dealt to the 8 XCDs in a
- * snake, so every XCD gets the same amount of work and runs its largest tiles first (the
- * contiguous alternative left the busiest XCD ~10% behind on the Zipf-skewed prefill);
- * the feature tiles of one column tile run back to back on one XCD and share the tile's
- * activations in its L2.
+ * Workgroup order: column tiles are sorted largest first (an expert's full tiles next to
+ * each other) and dealt to the 8 XCDs in groups of K3G_TILE_GROUP consecutive tiles, the
+ * groups in a snake, so every XCD gets the same amount of work and runs its largest tiles
+ * first (the contiguous alternative left the busiest XCD ~10% behind on the Zipf-skewed
+ * prefill), and a hot expert's tiles run at once on one XCD, sharing its weights in that
+ * XCD's L2; the feature tiles of one column tile run back to back on one XCD and share
+ * the tile's activations there.
  */
 #include "k3g_dev.h"
 #include "k3g_kernels.h"
@@ -605,10 +607,12 @@ __device__ __forceinline__ void gm_tile_mix(const K3kGemm &g, const GmTile &t,
 
 /* The workgroup's tile and this wave's weight rows. Workgroup b runs on XCD b % 8 and is
  * dispatched there in the order of b / 8. The tiles (largest first) are dealt to the XCDs
- * in a snake: round r gives tile 8 r + x (r even) or 8 r + 7 - x (r odd) to XCD x, so
- * every XCD gets the same mix, largest first; the feature tiles of one column tile run
- * back to back on one XCD, sharing its activations in that XCD's L2. Returns false when
- * the workgroup has no tile. */
+ * in groups of G = K3G_TILE_GROUP consecutive tiles, the groups in a snake: round r of XCD
+ * x takes tile G (8 q + x) + r % G (q = r / G even) or G (8 q + 7 - x) + r % G (q odd), so
+ * every XCD gets the same mix, largest first, and an expert's consecutive full tiles land
+ * on one XCD in consecutive rounds; the feature tiles of one column tile run back to back
+ * on one XCD, sharing its activations in that XCD's L2. Returns false when the workgroup
+ * has no tile. */
 template <int AF, int WV>
 __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *lds, int &nb)
 {
@@ -617,7 +621,8 @@ __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *l
     const int ntl = (g.tiles ? *g.ntiles : (g.dense_rows + GM_COLS - 1) / GM_COLS) * ks_n;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int rnd = slot / g.nft, f = slot - rnd * g.nft;
-    const int tks = 8 * rnd + ((rnd & 1) ? 7 - xcd : xcd);
+    const int grp = rnd / K3G_TILE_GROUP, gi = rnd - grp * K3G_TILE_GROUP;
+    const int tks = K3G_TILE_GROUP * (8 * grp + ((grp & 1) ? 7 - xcd : xcd)) + gi;
     if (tks >= ntl) return false;
     const int tile = tks / ks_n;
     t.ks = tks - tile * ks_n;
@@ -767,10 +772,12 @@ k_gemm(const K3kGemm g)
     if (g.trace && threadIdx.x == 0) {
         const int slot = blockIdx.x >> 3;
         const int rnd = slot / g.nft, xcd = blockIdx.x & 7;
+        const int grp = rnd / K3G_TILE_GROUP, gi = rnd - grp * K3G_TILE_GROUP;
         unsigned long long *o = g.trace + 4 * (size_t)blockIdx.x;
         o[0] = t_start;
         o[1] = wall_clock64();
-        o[2] = (unsigned long long)(8 * rnd + ((rnd & 1) ? 7 - xcd : xcd)) << 32 |
+        o[2] = (unsigned long long)(K3G_TILE_GROUP * (8 * grp + ((grp & 1) ? 7 - xcd : xcd)) +
+                                    gi) << 32 |
                (unsigned)(slot - rnd * g.nft);
         o[3] = (unsigned long long)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15) << 32 |
                (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4);
@@ -1093,7 +1100,7 @@ extern "C" int k3k_gemm_f8(const K3kGemm *g, hipStream_t st)
     if (g->tiles ? (!g->ntiles || g->max_tiles < 1) : g->dense_rows < 1) return -1;
     if ((g->scatter || (g->mode == 0 && g->tiles)) && !g->perm) return -1;
     const long long maxt = g->tiles ? g->max_tiles : (g->dense_rows + GM_COLS - 1) / GM_COLS;
-    const long long grid = 8 * ((maxt + 7) / 8) * g->nft;
+    const long long grid = 8 * (long long)K3G_TILE_ROUNDS(maxt) * g->nft;
     if (grid > 0x7fffffff) return -1;
     hipLaunchKernelGGL(k_gemm_f8, dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
     return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -1125,7 +1132,7 @@ extern "C" int k3k_gemm(const K3kGemm *g, hipStream_t st)
         return -1;
     const long long maxt = g->tiles ? g->max_tiles
                                     : (long long)((g->dense_rows + GM_COLS - 1) / GM_COLS) * ks_n;
-    const long long grid = 8 * ((maxt + 7) / 8) * g->nft;
+    const long long grid = 8 * (long long)K3G_TILE_ROUNDS(maxt) * g->nft;
     if (grid > 0x7fffffff) return -1;
     if (g->afmt == 0 && g->mode == 0) {
         /* gate/up of MXFP4 experts: 4-wave workgroups when x is one piece (the usual case:
@@ -1134,7 +1141,7 @@ extern "C" int k3k_gemm(const K3kGemm *g, hipStream_t st)
         K3kGemm g4 = *g, g8 = *g;
         g4.nft = (g->rows + 127) / 128;
         g8.np_only = 2;
-        const long long grid4 = 8 * ((maxt + 7) / 8) * g4.nft;
+        const long long grid4 = 8 * (long long)K3G_TILE_ROUNDS(maxt) * g4.nft;
         if (grid4 > 0x7fffffff) return -1;
         hipLaunchKernelGGL((k_gemm<0, 4>), dim3((unsigned)grid4), dim3(4 * 64), 0, st, g4);
         if (g->npieces > 1)

@@ -20,6 +20,13 @@ extern "C" {
 
 #define K3G_MAX_TOPK 64
 
+/* The grouped GEMMs deal consecutive column tiles to one XCD in groups of this many (an
+ * expert's full tiles are consecutive, so they run at once on one XCD and share its
+ * weights in that L2); K3G_TILE_ROUNDS(n) is the rounds of workgroups per XCD for up to n
+ * column tiles. */
+#define K3G_TILE_GROUP 4
+#define K3G_TILE_ROUNDS(n) (K3G_TILE_GROUP * (((n) + 8 * K3G_TILE_GROUP - 1) / (8 * K3G_TILE_GROUP)))
+
 /* weight formats */
 enum { K3K_MXFP4 = 0, K3K_F32 = 1, K3K_BF16 = 2 };
 
@@ -209,6 +216,9 @@ int k3k_set_experts(K3ExpertQ *table, const K3kEqSet *s, hipStream_t st);
 /* y = w * x * (float)(1/sqrt(sum x^2 / n + eps)), double sum; one token per block. */
 int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
                 hipStream_t st);
+
+/* *p = v, in stream order */
+int k3k_set_i32(int32_t *p, int32_t v, hipStream_t st);
 
 /* y += a, elementwise */
 int k3k_add(float *y, const float *a, size_t n, hipStream_t st);

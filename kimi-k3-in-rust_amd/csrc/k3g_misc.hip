@@ -292,6 +292,20 @@ extern "C" int k3k_add(float *y, const float *a, size_t n, hipStream_t st)
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+/* *p = v (a flag cleared in stream order by a kernel, which a captured graph replays
+ * the same way every time) */
+__global__ void __launch_bounds__(64) k_set_i32(int32_t *p, int32_t v)
+{
+    if (threadIdx.x == 0) *p = v;
+}
+
+extern "C" int k3k_set_i32(int32_t *p, int32_t v, hipStream_t st)
+{
+    if (!p) return -1;
+    hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(64), 0, st, p, v);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 /* ---------------------------------------------------------------- dequant ---- */
 /* src/core/k3_ops.c:1770-1800: out = E2M1[nibble] * 2^(s-127), s = 255 gives a
  * (signed) zero; element i takes scale i / group of its row. One packed byte per
