@@ -93,7 +93,7 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     }
     if (hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&c->ev_in, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&c->ev_routed, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&c->ev_shared, hipEventDisableTiming) != hipSuccess) {
         fprintf(stderr, "k3moe: k3g_ctx_create: cannot create the side stream\n");
         return -1;
     }
@@ -143,6 +143,13 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
         if (pu > part) part = pu;
     }
     const size_t o_kpart = carve(&at, part ? part : 16);
+    size_t part2 = 0;      /* the shared expert's, when it runs on the side stream */
+    if (SI) {
+        const size_t pg = k3k_gemm_part_bytes((int)((SI + 255) / 256), (int)(2 * SI));
+        const size_t pd = k3k_gemm_part_bytes((int)((d + 511) / 512), (int)d);
+        part2 = pg > pd ? pg : pd;
+    }
+    const size_t o_kpart2 = carve(&at, part2 ? part2 : 16);
     const size_t L128 = (L + 127) / 128 * 128;
     const size_t o_zb = carve(&at, L != d ? 2 * T * L128 * 2 : 16);
     const size_t o_zflag = carve(&at, 4);
@@ -199,6 +206,7 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->zb = (uint16_t *)(b + o_zb);
     c->zflag = (int32_t *)(b + o_zflag);
     c->kpart = (float *)(b + o_kpart);
+    c->kpart2 = (float *)(b + o_kpart2);
     c->rtpart = (double *)(b + o_rtpart);
     c->rtctr = (int32_t *)(b + o_rtctr);
     c->tiles = (int32_t *)(b + o_tiles);
@@ -296,7 +304,7 @@ void k3g_ctx_destroy(K3gCtx *c)
     hipFree(c->ws);
     hipStreamSynchronize(c->side);
     hipEventDestroy(c->ev_in);
-    hipEventDestroy(c->ev_routed);
+    hipEventDestroy(c->ev_shared);
     hipStreamDestroy(c->side);
     hipStreamDestroy(c->stream);
     free(c);
@@ -382,7 +390,7 @@ static int dense_gemm(K3gCtx *c, const void *W, int rows, int K, const uint16_t 
  * the routed experts' per-pair rows in contrib. */
 static int gemm_body(K3gCtx *c, const K3gLayer *L, const float *x, int T,
                      const int32_t *idx, const float *wt, float *out, float *contrib, int fp8,
-                     int full, hipEvent_t routed_ready, hipStream_t st);
+                     int full, int shared_side, hipStream_t st);
 
 static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
                         const int32_t *idx, const float *wt, float *out, float *contrib,
@@ -393,28 +401,92 @@ static int experts_gemm(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     rc |= k3k_dispatch_tiles(idx, T * L->topk, L->n_experts, c->cnt, c->base, c->off, c->act,
                              c->nact, c->perm, c->err, c->tiles, c->ntiles, c->xflag, st);
     k3g_stage_end(c, K3G_ST_DISPATCH, st);
-    return rc | gemm_body(c, L, x, T, idx, wt, out, contrib, fp8, full, NULL, st);
+    return rc | gemm_body(c, L, x, T, idx, wt, out, contrib, fp8, full, 0, st);
+}
+
+/* The shared expert's dense gate/up (+ activation -> h pieces) and down GEMMs on x's
+ * pieces, into c->sh_out; part: the K-slice sums' buffer. */
+static int shared_expert(K3gCtx *c, const K3gLayer *L, int T, float *part, hipStream_t st)
+{
+    const int d = L->hidden, SI = L->shared_inter;
+    const int d128 = r128(d), SI128 = r128(c->shared_inter);
+    int rc = 0;
+    K3kGemm s;
+    memset(&s, 0, sizeof s);
+    s.mode = 0;
+    s.afmt = 1;
+    s.rows = SI;
+    s.K = d;
+    s.ldb = d128;
+    s.b = c->xb;
+    s.bpiece = (long long)T * d128;
+    s.npieces = 2;
+    s.lo_flag = c->xflag;
+    s.wa = (const uint16_t *)L->sh1;
+    s.wb = (const uint16_t *)L->sh3;
+    s.dense_rows = T;
+    s.h = c->hsb;
+    s.hpiece = (long long)T * SI128;
+    s.ldh = SI128;
+    s.b1 = L->act_b1;
+    s.b2 = L->act_b2;
+    s.nft = (SI + 255) / 256;
+    s.ksplit = dense_ksplit(s.nft, T, d);
+    s.part = part;
+    k3g_stage_begin(c, K3G_ST_SH_GATEUP, st);
+    rc |= k3k_gemm(&s, st);
+    k3g_stage_end(c, K3G_ST_SH_GATEUP, st);
+    s.mode = 1;
+    s.rows = d;
+    s.K = SI;
+    s.ldb = SI128;
+    s.wa = (const uint16_t *)L->sh2;
+    s.wb = NULL;
+    s.b = c->hsb;
+    s.bpiece = (long long)T * SI128;
+    s.lo_flag = NULL;
+    s.h = NULL;
+    s.out = c->sh_out;
+    s.ldo = d;
+    s.nft = (d + 511) / 512;
+    s.ksplit = dense_ksplit(s.nft, T, SI);
+    k3g_stage_begin(c, K3G_ST_SH_DOWN, st);
+    rc |= k3k_gemm(&s, st);
+    k3g_stage_end(c, K3G_ST_SH_DOWN, st);
+    return rc;
+}
+
+/* x's two bf16 pieces (the piece-1 flag cleared before) and, for the FP4 x FP8 routed
+ * experts on x itself, its MXFP8 copy. */
+static int gemm_pieces(K3gCtx *c, const K3gLayer *L, const float *x, int T, int fp8,
+                       hipStream_t st)
+{
+    const int d = L->hidden, d128 = r128(d), d512 = r512(d);
+    int rc = 0;
+    k3g_stage_begin(c, K3G_ST_PIECES, st);
+    rc |= k3k_xpieces(x, T, d, d128, c->xb, (long long)T * d128, c->xflag, st);
+    if (fp8 && !L->down)
+        rc |= k3k_xq8(x, T, d, d512, c->xq8b, c->xq8b + (size_t)T * d512, st);
+    k3g_stage_end(c, K3G_ST_PIECES, st);
+    return rc;
 }
 
 /* The grouped GEMMs after the dispatch (column tiles built, x's piece-1 flag cleared):
- * x pieces, [latent down], the shared expert, then (once routed_ready, when given) the
- * routed gate/up and down, [combine, latent up, + shared]. */
+ * x pieces, [latent down], the shared expert, the routed gate/up and down, [combine,
+ * latent up, + shared]. shared_side: x's pieces are already made and the shared expert
+ * runs on the side stream (ev_shared marks its end; the combine waits for it). */
 static int gemm_body(K3gCtx *c, const K3gLayer *L, const float *x, int T,
                      const int32_t *idx, const float *wt, float *out, float *contrib, int fp8,
-                     int full, hipEvent_t routed_ready, hipStream_t st)
+                     int full, int shared_side, hipStream_t st)
 {
     const int d = L->hidden, E = L->n_experts, k = L->topk, I = L->inter;
     const int SI = full ? L->shared_inter : 0, P = T * k;
-    const int d128 = r128(d), I128 = r128(c->inter), SI128 = r128(c->shared_inter);
+    const int d128 = r128(d), I128 = r128(c->inter);
     const int lat = L->latent > 0 ? L->latent : d, lat128 = r128(lat);
     const int projected = L->down != NULL;
     int rc = 0;
-    const int d512 = r512(d), I512 = r512(c->inter);
-    k3g_stage_begin(c, K3G_ST_PIECES, st);
-    rc |= k3k_xpieces(x, T, d, d128, c->xb, (long long)T * d128, c->xflag, st);
-    if (fp8 && !projected)
-        rc |= k3k_xq8(x, T, d, d512, c->xq8b, c->xq8b + (size_t)T * d512, st);
-    k3g_stage_end(c, K3G_ST_PIECES, st);
+    const int I512 = r512(c->inter);
+    if (!shared_side) rc |= gemm_pieces(c, L, x, T, fp8, st);
     /* the routed experts' input: x, or its latent projection z = down x as two bf16
      * pieces (piece 1 always taken) */
     const uint16_t *rb = c->xb;
@@ -458,57 +530,9 @@ static int gemm_body(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     g.b2 = L->act_b2;
     g.nft = (I + 255) / 256;
 
-    K3kGemm s = g;
-    if (SI > 0) {
-        s.afmt = 1;
-        s.rows = SI;
-        s.K = d;
-        s.ldb = d128;
-        s.b = c->xb;
-        s.bpiece = (long long)T * d128;
-        s.lo_flag = c->xflag;
-        s.eq = NULL;
-        s.wa = (const uint16_t *)L->sh1;
-        s.wb = (const uint16_t *)L->sh3;
-        s.perm = NULL;
-        s.tiles = NULL;
-        s.ntiles = NULL;
-        s.dense_rows = T;
-        s.h = c->hsb;
-        s.hpiece = (long long)T * SI128;
-        s.ldh = SI128;
-        s.nft = (SI + 255) / 256;
-        s.ksplit = dense_ksplit(s.nft, T, d);
-        s.part = c->kpart;
-        k3g_stage_begin(c, K3G_ST_SH_GATEUP, st);
-        rc |= k3k_gemm(&s, st);
-        k3g_stage_end(c, K3G_ST_SH_GATEUP, st);
-    }
-
-
-    if (SI > 0) {
-        s.mode = 1;
-        s.rows = d;
-        s.K = SI;
-        s.ldb = SI128;
-        s.wa = (const uint16_t *)L->sh2;
-        s.wb = NULL;
-        s.b = c->hsb;
-        s.bpiece = (long long)T * SI128;
-        s.lo_flag = NULL;
-        s.h = NULL;
-        s.out = c->sh_out;
-        s.ldo = d;
-        s.scatter = 0;
-        s.nft = (d + 511) / 512;
-        s.ksplit = dense_ksplit(s.nft, T, SI);
-        k3g_stage_begin(c, K3G_ST_SH_DOWN, st);
-        rc |= k3k_gemm(&s, st);
-        k3g_stage_end(c, K3G_ST_SH_DOWN, st);
-    }
-    /* routed experts last, after their routing (computed beside the shared expert) and
-     * any copies they wait for (the shared expert above overlaps both) */
-    if (routed_ready && hipStreamWaitEvent(st, routed_ready, 0) != hipSuccess) rc = -1;
+    if (SI > 0 && !shared_side) rc |= shared_expert(c, L, T, c->kpart, st);
+    /* routed experts last, after any copies they wait for (the shared expert above
+     * overlaps them) */
     if (c->routed_wait) {
         if (hipStreamWaitEvent(st, c->routed_wait, 0) != hipSuccess) rc = -1;
         c->routed_wait = NULL;
@@ -562,6 +586,7 @@ static int gemm_body(K3gCtx *c, const K3gLayer *L, const float *x, int T,
     rc |= fp8 ? k3k_gemm_f8(&g, st) : k3k_gemm(&g, st);
     k3g_stage_end(c, K3G_ST_DOWN, st);
 
+    if (SI > 0 && shared_side && hipStreamWaitEvent(st, c->ev_shared, 0) != hipSuccess) rc = -1;
     if (full && !projected && !L->up && !L->latent_norm) {
         k3g_stage_begin(c, K3G_ST_COMBINE, st);
         rc |= k3k_combine(contrib, idx, wt, T, k, d, SI > 0 ? c->sh_out : NULL, out, st);
@@ -815,24 +840,26 @@ int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int
         return run_fused(c, L, x, T, out, idx, wt, 0, st);
     }
     if (gemmable(c, L) && !c->routed_wait) {
-        /* the router and the dispatch on the side stream while the shared expert runs on
-         * this one; the routed experts wait for them. The side stream starts after all
-         * earlier work of this stream (the previous call's GEMMs read the dispatch's
-         * buffers). */
+        /* x's pieces, then the shared expert on the side stream (only the final combine
+         * needs it) beside the router, the dispatch and the routed experts on this one */
         c->paths |= 4;
-        int rc = 0;
-        if (hipEventRecord(c->ev_in, st) != hipSuccess ||
-            hipStreamWaitEvent(c->side, c->ev_in, 0) != hipSuccess)
-            return -1;
-        rc |= k3g_route(c, L, x, T, idx, wt, c->side);
-        k3g_stage_begin(c, K3G_ST_DISPATCH, c->side);
+        int rc = k3k_set_i32(c->xflag, 0, st);
+        rc |= gemm_pieces(c, L, x, T, c->gemm_fp8, st);
+        if (L->shared_inter > 0) {
+            if (hipEventRecord(c->ev_in, st) != hipSuccess ||
+                hipStreamWaitEvent(c->side, c->ev_in, 0) != hipSuccess)
+                rc = -1;
+            rc |= shared_expert(c, L, T, c->kpart2, c->side);
+            if (hipEventRecord(c->ev_shared, c->side) != hipSuccess) rc = -1;
+        }
+        rc |= k3g_route(c, L, x, T, idx, wt, st);
+        /* the dispatch's flag argument (cleared) is the spare one: x's is set above */
+        k3g_stage_begin(c, K3G_ST_DISPATCH, st);
         rc |= k3k_dispatch_tiles(idx, T * L->topk, L->n_experts, c->cnt, c->base, c->off,
                                  c->act, c->nact, c->perm, c->err, c->tiles, c->ntiles,
-                                 c->zflag, c->side);
-        k3g_stage_end(c, K3G_ST_DISPATCH, c->side);
-        if (hipEventRecord(c->ev_routed, c->side) != hipSuccess) return -1;
-        rc |= k3k_set_i32(c->xflag, 0, st);
-        rc |= gemm_body(c, L, x, T, idx, wt, out, c->contrib, c->gemm_fp8, 1, c->ev_routed, st);
+                                 c->zflag, st);
+        k3g_stage_end(c, K3G_ST_DISPATCH, st);
+        rc |= gemm_body(c, L, x, T, idx, wt, out, c->contrib, c->gemm_fp8, 1, 1, st);
         return rc ? -1 : 0;
     }
     if (k3g_route(c, L, x, T, idx, wt, st) != 0) return -1;

@@ -62,16 +62,18 @@ struct K3gCtx {
     uint16_t *xb, *hb, *hsb;     /* bf16 pieces of x [2][T][d128], h [2][T*k][I128], shared h */
     uint16_t *zb;                /* bf16 pieces of the latent input / aggregate [2][T][L128] */
     int32_t *zflag;              /* their piece-1 flag (written, not read) */
-    float *kpart;                /* K-slice sums of the shared expert's GEMMs */
+    float *kpart;                /* K-slice sums of the dense GEMMs */
+    float *kpart2;               /* the shared expert's, when it runs on the side stream */
     double *rtpart;              /* K-slice sums of the router's matrix-core logits */
     int32_t *rtctr;              /* their per-tile arrival counts (zero between calls) */
     int32_t *tiles, *ntiles, *xflag;
     int max_tiles;
     hipEvent_t routed_wait;      /* the next k3g_experts waits for it before routed work */
-    /* a second compute stream (default priority): the router and dispatch of a grouped
-     * call run on it while the shared expert runs on the call's stream */
+    /* a second compute stream (default priority): the shared expert of a grouped call
+     * runs on it beside the router and the routed experts; ev_in orders it after x's
+     * pieces, ev_shared marks its end */
     hipStream_t side;
-    hipEvent_t ev_in, ev_routed;
+    hipEvent_t ev_in, ev_shared;
     int gemm_fp8;                /* routed experts on the FP4 x FP8 matrix cores */
     uint8_t *xq8b, *hq8b;        /* MXFP8 x [T][d512] + scales, h [T*k][I512] + scales */
     unsigned long long *trace;   /* optional per-ticket timestamps of the fused kernel */

@@ -268,6 +268,21 @@ __device__ __noinline__ void gm_act_store_mix(k3v4f g0, k3v4f g1, k3v4f u0, k3v4
     if (g4 == 0) *os = (uint8_t)(sx + 127);
 }
 
+/* Instruction order of one step's matrix work (NR B-operand reads from LDS, 4 MFMAs
+ * each): the reads run two ahead of the MFMAs that use them, and the conversions of the
+ * next sub-step's weights fill the issue slots between MFMAs, so neither an LDS round
+ * trip nor a run of conversions sits between two MFMAs. */
+template <int NR, int GM_AHEAD>
+__device__ __forceinline__ void gm_pipeline()
+{
+    __builtin_amdgcn_sched_group_barrier(0x100, GM_AHEAD, 0);   /* DS read */
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);      /* MFMA */
+        if (i + GM_AHEAD < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+}
+
 /* Everything one workgroup's tile needs, uniform across the workgroup except the
  * per-lane DMA row offsets. */
 struct GmTile {
@@ -378,6 +393,7 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
                     }
                     mma_step(c, 4 * s + t.g4, a);
                 }
+                gm_pipeline<4 * NB * NP, 3>();
             }
         };
         aload(0, ab[0], sb[0]);
