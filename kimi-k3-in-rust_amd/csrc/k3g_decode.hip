@@ -25,19 +25,20 @@
  *      X   x -> FP8 pieces (per token, per 512 columns) and bf16 pieces
  *      R   router logits of one expert row (all tokens), fp64 with an error bound
  *      S   the certified top-k for every token (one ticket); waits for all R
- *      SG  shared gate/up: 16 rows x a K slice; the last slice of a row tile (found
- *          with a returning atomic) sums the slices in slice order, applies the
+ *      SG  shared gate/up: 16 SG_TILES rows x a K slice; the last slice of a row group
+ *          (found with a returning atomic) sums the slices in slice order, applies the
  *          activation and writes the shared h as bf16 pieces
+ *      SD  shared down: 32 rows x a K slice, partial sums per slice
  *      G   routed gate/up of one (token, slot) pair: 32 rows x a K slice of 512-column
  *          quads; the last slice of a tile sums, activates and writes h's FP8 pieces
- *      SD  shared down: 32 rows x a K slice, partial sums per slice
  *      D   routed down of one pair: 32 output rows x a K slice of 512-column quads;
  *          waits for that pair's h. The last arrival of an output tile (over every
  *          pair's slices and the shared expert's) combines it: slots in the engine's
  *          order (float multiply, then add), then + the shared output (its slices
  *          summed in slice order)
  *
- *    The shared expert needs no routing, so SG streams while the router and top-k run.
+ *    The shared expert needs no routing, so SG and then SD stream while the router and
+ *    top-k run.
  *
  * Cross-wave data (logits, routing, partial sums, pieces, per-slot outputs) is written
  * and read at device coherence (sc1 stores and loads) and a producer waits for its stores
@@ -68,6 +69,8 @@ typedef unsigned int k3v4u __attribute__((ext_vector_type(4)));
 #define K3G_BQ 8448       /* FP8 B quad: 4 x 2 KB chunks + 256 B of scales */
 #define NPC8 6            /* FP8 pieces per value */
 #define NPC16 3           /* bf16 pieces per value */
+#define SG_TILES 1        /* shared gate/up: 16-row tiles per ticket */
+#define SG_BATCH 8        /* shared gate/up: 32-column chunks per load batch */
 
 #define SY_LINE 32        /* ints per counter line (128 bytes) */
 #define NSUB 16           /* sub-counters per ticket class with many signalers */
@@ -84,7 +87,7 @@ struct K3Geo {
     int T, P, nQd, nCd, nQi, nCsi;
     int KSS, KSG, KSD, KSR, KSDN; /* K slices of SG, G, SD, R, D tickets */
     int nRc;                     /* router 1024-column chunks */
-    int nSGt, nGt, nSDt, nDt;    /* row tiles */
+    int nSGt, nGt, nSDt, nDt;    /* row tiles (SG: row groups of SG_TILES tiles) */
     int nX, nR, nSG, nG, nSD, nD, total;
     int oSG, oG, oSD, oD;        /* first ticket of each class after S */
     /* counter lines */
@@ -107,7 +110,7 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.nRc = (d + 1023) / 1024;
     g.KSR = K3G_KS_R < g.nRc ? K3G_KS_R : g.nRc;
     g.KSDN = K3G_KS_D < g.nQi ? K3G_KS_D : g.nQi;
-    g.nSGt = SI / 16;
+    g.nSGt = (SI + 16 * SG_TILES - 1) / (16 * SG_TILES);
     g.nGt = I / 32;
     g.nSDt = SI > 0 ? d / 32 : 0;
     g.nDt = d / 32;
@@ -119,9 +122,9 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.nD = g.P * g.nDt * g.KSDN;
     g.total = g.nX + g.nR + 1 + g.nSG + g.nG + g.nSD + g.nD;
     g.oSG = g.nX + g.nR + 1;
-    g.oG = g.oSG + g.nSG;
-    g.oSD = g.oG + g.nG;
-    g.oD = g.oSD + g.nSD;
+    g.oSD = g.oSG + g.nSG;
+    g.oG = g.oSD + g.nSD;
+    g.oD = g.oG + g.nG;
     /* counters: one 128-byte line each; events: a counter plus NREP replicated flags */
     g.lR = 0;
     g.lSD = g.lR + NSUB;
@@ -130,12 +133,13 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.lTG = g.lTSG + g.nSGt;
     g.lRE = g.lTG + g.P * g.nGt;
     g.lDT = g.lRE + E;
+    /* event counters: a top line and NSUB sub-counter lines each (k3d_arrive_event2) */
     g.cX = g.lDT + g.nDt;
-    g.cX16 = g.cX + 1;
-    g.cR = g.cX16 + 1;
-    g.cSGF = g.cR + 1;
-    g.cGF = g.cSGF + 1;
-    g.eX = g.cGF + g.P;
+    g.cX16 = g.cX + 1 + NSUB;
+    g.cR = g.cX16 + 1 + NSUB;
+    g.cSGF = g.cR + 1 + NSUB;
+    g.cGF = g.cSGF + 1 + NSUB;
+    g.eX = g.cGF + g.P * (1 + NSUB);
     g.eX16 = g.eX + K3_EVLINES;
     g.eR = g.eX16 + K3_EVLINES;
     g.eSEL = g.eR + K3_EVLINES;
@@ -226,10 +230,20 @@ __device__ __forceinline__ void k3d_set_event(int *sync, int ev, int lane)
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 
-/* Arrive at an event's counter; the arrival that completes the count sets the event. */
-__device__ __forceinline__ void k3d_arrive_event(int *sync, int ctr, int count, int ev, int lane)
+/* Arrive at an event that `count` arrivals complete, arrival `who` (0 .. count - 1) at
+ * sub-counter line ctr + 1 + who % NSUB; the arrival that completes a sub-counter arrives
+ * at the top line ctr, and the one that completes the top count (one per non-empty
+ * sub-counter) sets the event. Same-address atomics serialise at the memory side, so a
+ * few hundred arrivals on one line would take microseconds; here at most
+ * ceil(count / NSUB) + NSUB meet on one line. */
+__device__ __forceinline__ void k3d_arrive_event2(int *sync, int ctr, int count, int who,
+                                                  int ev, int lane)
 {
-    if (k3d_arrive(k3d_line(sync, ctr), count - 1, lane)) k3d_set_event(sync, ev, lane);
+    const int sub = who % NSUB;
+    const int members = count / NSUB + (sub < count % NSUB ? 1 : 0);
+    if (!k3d_arrive(k3d_line(sync, ctr + 1 + sub), members - 1, lane)) return;
+    const int tops = count < NSUB ? count : NSUB;
+    if (k3d_arrive(k3d_line(sync, ctr), tops - 1, lane)) k3d_set_event(sync, ev, lane);
 }
 
 /* Instrumentation: the moment a ticket's waits are over (its second trace stamp). */
@@ -285,6 +299,24 @@ __device__ __forceinline__ uint32_t k3d_b32(K3Rsrc r, int voff)
 __device__ __forceinline__ float k3d_f32_sc1(K3Rsrc r, int voff)
 {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, K3_SC1));
+}
+
+/* sum over q < n (n <= N) of the fp32 at byte offset off + q * stride, device-coherent,
+ * in q order from 0.0f; every load is issued before the first add (a loop of dependent
+ * loads would cost one memory round trip per term) */
+template <int N>
+__device__ __forceinline__ float k3d_sum_sc1(K3Rsrc r, int off, int stride, int n)
+{
+    float v[N];
+#pragma unroll
+    for (int q = 0; q < N; ++q)
+        v[q] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(r, q < n ? off + q * stride : K3_OOB, 0, K3_SC1));
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < N; ++q)
+        if (q < n) s += v[q];
+    return s;
 }
 
 __device__ __forceinline__ void k3d_st4_sc1(K3Rsrc r, int voff, k3v4f v)
@@ -423,6 +455,50 @@ __device__ __forceinline__ int k3d_b16_off(int k, int col)
     return (k >> 5) * 1024 + (16 * ((k & 31) >> 3) + col) * 16 + 2 * (k & 7);
 }
 
+/* x's bf16 pieces as the B operand of one 32-column chunk, made in registers from fp32 x
+ * (T <= 2, when 3T columns and their 3T neighbours 8 lanes on fit in a 16-lane row).
+ * Lane (kg, col) with col < 3T needs piece col % 3 of token col / 3's values
+ * 32 c + 8 kg .. + 7: lane col loads the first four, lane col + 8 the last four, and a
+ * DPP rotation by 8 inside the row brings the second half over. The pieces are the prep
+ * tickets' (bf16 nearest-even of the value, then of each remainder), so the products are
+ * the same bits. k3d_xb16_off: this lane's load offset (past the end when it loads
+ * nothing); k3d_xb16_make: the operand from the loaded half. */
+__device__ __forceinline__ int k3d_xb16_off(int T, int d, int c, int lane)
+{
+    const int col = lane & 15, half = col >> 3, cl = col & 7;
+    if (cl >= 3 * T) return K3_OOB;
+    return ((cl / 3) * d + 32 * c + 8 * (lane >> 4) + 4 * half) * 4;
+}
+
+__device__ __forceinline__ uint4 k3d_xb16_make(uint4 raw, int T, int lane)
+{
+    typedef __bf16 k3v2bf __attribute__((ext_vector_type(2)));
+    const uint4 up = make_uint4(__builtin_amdgcn_mov_dpp(raw.x, 0x128, 0xf, 0xf, false),
+                                __builtin_amdgcn_mov_dpp(raw.y, 0x128, 0xf, 0xf, false),
+                                __builtin_amdgcn_mov_dpp(raw.z, 0x128, 0xf, 0xf, false),
+                                __builtin_amdgcn_mov_dpp(raw.w, 0x128, 0xf, 0xf, false));
+    float v[8] = {__uint_as_float(raw.x), __uint_as_float(raw.y), __uint_as_float(raw.z),
+                  __uint_as_float(raw.w), __uint_as_float(up.x),  __uint_as_float(up.y),
+                  __uint_as_float(up.z),  __uint_as_float(up.w)};
+    const int col = lane & 15, pc = col % 3;
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int lv = 0; lv < NPC16; ++lv) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const k3v2bf h = {(__bf16)v[2 * m], (__bf16)v[2 * m + 1]};
+            const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+            if (pc == lv) w[m] = hb;
+            if (lv + 1 < NPC16) {
+                v[2 * m] -= __uint_as_float(hb << 16);
+                v[2 * m + 1] -= __uint_as_float(hb & 0xffff0000u);
+            }
+        }
+    }
+    const bool on = col < 3 * T;
+    return on ? make_uint4(w[0], w[1], w[2], w[3]) : make_uint4(0, 0, 0, 0);
+}
+
 /* The kernel's arguments, addressed in the constant address space: a phase function
  * moves the pointer to scalar registers and every field it reads comes back in scalar
  * registers (scalar loads), so buffer descriptors and loop bounds never become per-lane
@@ -459,16 +535,19 @@ struct K3Dec {
         const bool on = col < a.d;
         const float v = on ? a.x[(size_t)t * a.d + col] : 0.0f;
         const int Q = b >> 4;
-        /* the bf16 pieces first: the shared expert's tickets wait only for these */
-        float r2 = v;
+        /* the bf16 pieces first: the shared expert's tickets wait only for these (up to
+         * two tokens they make them themselves) */
+        if (NT > 2) {
+            float r2 = v;
 #pragma unroll
-        for (int pc = 0; pc < NPC16; ++pc) {
-            float back;
-            const uint32_t h = k3d_bf16_rn(r2, back);
-            r2 -= back;
-            if (on) k3d_st16_sc1(r16, k3d_b16_off(col, NPC16 * t + pc), h);
+            for (int pc = 0; pc < NPC16; ++pc) {
+                float back;
+                const uint32_t h = k3d_bf16_rn(r2, back);
+                r2 -= back;
+                if (on) k3d_st16_sc1(r16, k3d_b16_off(col, NPC16 * t + pc), h);
+            }
+            k3d_arrive_event2(a.sync, G.cX16, G.nX, tk, G.eX16, lane);
         }
-        k3d_arrive_event(a.sync, G.cX16, G.nX, G.eX16, lane);
         float r = v;
 #pragma unroll
         for (int pc = 0; pc < NPC8; ++pc) {
@@ -479,7 +558,7 @@ struct K3Dec {
                 if (e == 0) k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_scale(b, pc), sx + 127);
             }
         }
-        k3d_arrive_event(a.sync, G.cX, G.nX, G.eX, lane);
+        k3d_arrive_event2(a.sync, G.cX, G.nX, tk, G.eX, lane);
     }
 
     /* ----------------------------------------------------------------- R ---- */
@@ -569,23 +648,31 @@ struct K3Dec {
         /* the last slice of the row: the slices summed in slice order, then the score
          * interval (any summation order is inside the interval's bound) */
         if (lane < a.T) {
-            double sv = 0.0, bv = 0.0;
-            for (int q = 0; q < G.KSR; ++q) {
-                double2 v;
+            double2 pv[K3G_KS_R];
+#pragma unroll
+            for (int q = 0; q < K3G_KS_R; ++q) {
                 if (wg_slices)
-                    v = make_double2(rl->part[q][lane][0], rl->part[q][lane][1]);
+                    pv[q] = q < G.KSR ? make_double2(rl->part[q][lane][0], rl->part[q][lane][1])
+                                     : make_double2(0.0, 0.0);
                 else
-                    v = __builtin_bit_cast(
+                    pv[q] = __builtin_bit_cast(
                         double2, __builtin_amdgcn_raw_buffer_load_b128(
-                                     rp, ((lane * a.E + e) * G.KSR + q) * 16, 0, K3_SC1));
-                sv += v.x;
-                bv += v.y;
+                                     rp, q < G.KSR ? ((lane * a.E + e) * G.KSR + q) * 16 : K3_OOB,
+                                     0, K3_SC1));
+            }
+            double sv = 0.0, bv = 0.0;
+#pragma unroll
+            for (int q = 0; q < K3G_KS_R; ++q) {
+                if (q < G.KSR) {
+                    sv += pv[q].x;
+                    bv += pv[q].y;
+                }
             }
             const K3Rsrc rr = k3d_rsrc(a.rs, (size_t)a.T * a.E * 16);
             const float4 v = k3d_route_score(sv, bv, a.bias ? a.bias[e] : 0.0f, a.d);
             k3d_st4_sc1(rr, (lane * a.E + e) * 16, k3v4f{v.x, v.y, v.z, v.w});
         }
-        k3d_arrive_event(a.sync, G.cR, a.E, G.eR, lane);
+        k3d_arrive_event2(a.sync, G.cR, a.E, e, G.eR, lane);
     }
 
     /* ----------------------------------------------------------------- S ---- */
@@ -621,69 +708,102 @@ struct K3Dec {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const int tk = k3d_uniform(tk_);
         const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
-        const int st = tk / G.KSS, ks = tk - st * G.KSS;
+        const int rg = tk / G.KSS, ks = tk - rg * G.KSS;    /* row group, K slice */
         const int c0 = ks * G.nCd / G.KSS, c1 = (ks + 1) * G.nCd / G.KSS;
         const size_t mb = (size_t)a.SI * a.d * 2;
         const K3Rsrc r1 = k3d_rsrc(a.sh1, mb), r3 = k3d_rsrc(a.sh3, mb);
         const K3Rsrc rb = k3d_rsrc(a.xq16, (size_t)G.nCd * 1024);
+        const K3Rsrc rx = k3d_rsrc(a.x, (size_t)a.T * a.d * 4);
         const bool bon = (lane & 15) < NPC16 * a.T;
-        k3v4f g = {0, 0, 0, 0}, u = {0, 0, 0, 0};
-        const int abase = st * G.nCd * 1024 + lane * 16;
-        bool first = true;
-        for (int cb = c0; cb < c1; cb += 8) {
-            uint4 A1[8], A3[8], B[8];
+        k3v4f g[SG_TILES], u[SG_TILES];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int c = cb + i;
-                A1[i] = k3d_b128(r1, c < c1 ? abase + c * 1024 : K3_OOB);
-                A3[i] = k3d_b128(r3, c < c1 ? abase + c * 1024 : K3_OOB);
-            }
-            if (first) {
-                /* the first weights stream in while x's bf16 pieces are made */
-                if (!k3d_wait_event(a.sync, G.eX16, tk, a.spin_limit, a.err, lane)) return;
-                k3d_trace_go(a.trace, G.oSG + tk, lane);
-                first = false;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int c = cb + i;
-                B[i] = k3d_b128<K3_BPOL>(rb, bon && c < c1 ? c * 1024 + lane * 16 : K3_OOB);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                g = k3d_mma16(A1[i], B[i], g);
-                u = k3d_mma16(A3[i], B[i], u);
-            }
+        for (int j = 0; j < SG_TILES; ++j) {
+            g[j] = k3v4f{0, 0, 0, 0};
+            u[j] = k3v4f{0, 0, 0, 0};
         }
-        g = k3d_colsum3(g, lane);
-        u = k3d_colsum3(u, lane);
+        /* tile j's chunk c: (SG_TILES rg + j) nCd + c KB in; tiles past SI read zero */
+        const int abase = SG_TILES * rg * G.nCd * 1024 + lane * 16, tstride = G.nCd * 1024;
+        bool first = true;
+        if (NT <= 2) k3d_trace_go(a.trace, G.oSG + tk, lane);
+        for (int cb = c0; cb < c1; cb += SG_BATCH) {
+            uint4 A1[SG_TILES][SG_BATCH], A3[SG_TILES][SG_BATCH], B[SG_BATCH];
+            if (NT <= 2) {
+                /* x's halves first, so they can be used before the weights land */
+#pragma unroll
+                for (int i = 0; i < SG_BATCH; ++i)
+                    B[i] = k3d_b128(rx, cb + i < c1 ? k3d_xb16_off(a.T, a.d, cb + i, lane)
+                                                   : K3_OOB);
+            }
+#pragma unroll
+            for (int i = 0; i < SG_BATCH; ++i) {
+                const int c = cb + i;
+#pragma unroll
+                for (int j = 0; j < SG_TILES; ++j) {
+                    const int o = abase + j * tstride + c * 1024;
+                    A1[j][i] = k3d_b128(r1, c < c1 ? o : K3_OOB);
+                    A3[j][i] = k3d_b128(r3, c < c1 ? o : K3_OOB);
+                }
+            }
+            if (NT <= 2) {
+#pragma unroll
+                for (int i = 0; i < SG_BATCH; ++i) B[i] = k3d_xb16_make(B[i], a.T, lane);
+            } else {
+                if (first) {
+                    /* the first weights stream in while x's bf16 pieces are made */
+                    if (!k3d_wait_event(a.sync, G.eX16, tk, a.spin_limit, a.err, lane))
+                        return;
+                    k3d_trace_go(a.trace, G.oSG + tk, lane);
+                    first = false;
+                }
+#pragma unroll
+                for (int i = 0; i < SG_BATCH; ++i) {
+                    const int c = cb + i;
+                    B[i] = k3d_b128<K3_BPOL>(rb, bon && c < c1 ? c * 1024 + lane * 16 : K3_OOB);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < SG_BATCH; ++i)
+#pragma unroll
+                for (int j = 0; j < SG_TILES; ++j) {
+                    g[j] = k3d_mma16(A1[j][i], B[i], g[j]);
+                    u[j] = k3d_mma16(A3[j][i], B[i], u[j]);
+                }
+        }
         const int t = lane & 15;
         const K3Rsrc rp = k3d_rsrc(a.sgpart, (size_t)G.KSS * a.T * 2 * a.SI * 4);
-        if (t < a.T) {
-            const int row = 16 * st + 4 * (lane >> 4);
-            k3d_st4_sc1(rp, (((ks * a.T + t) * 2 + 0) * a.SI + row) * 4, g);
-            k3d_st4_sc1(rp, (((ks * a.T + t) * 2 + 1) * a.SI + row) * 4, u);
-        }
-        if (!k3d_arrive(k3d_line(a.sync, G.lTSG + st), G.KSS - 1, lane)) return;
-        /* last slice of the tile: h = act(gate, up) for 16 rows x T tokens -> bf16 pieces */
-        const int tt = lane >> 4, row = 16 * st + (lane & 15);
-        if (tt < a.T) {
-            float gs = 0.0f, us = 0.0f;
-            for (int q = 0; q < G.KSS; ++q) {
-                gs += k3d_f32_sc1(rp, (((q * a.T + tt) * 2 + 0) * a.SI + row) * 4);
-                us += k3d_f32_sc1(rp, (((q * a.T + tt) * 2 + 1) * a.SI + row) * 4);
-            }
-            float r2 = k3d_act(gs, us, a.b1, a.b2);
-            const K3Rsrc rh = k3d_rsrc(a.hq16, (size_t)G.nCsi * 1024);
 #pragma unroll
-            for (int pc = 0; pc < NPC16; ++pc) {
-                float back;
-                const uint32_t h = k3d_bf16_rn(r2, back);
-                r2 -= back;
-                k3d_st16_sc1(rh, k3d_b16_off(row, NPC16 * tt + pc), h);
+        for (int j = 0; j < SG_TILES; ++j) {
+            g[j] = k3d_colsum3(g[j], lane);
+            u[j] = k3d_colsum3(u[j], lane);
+            const int row = 16 * (SG_TILES * rg + j) + 4 * (lane >> 4);
+            if (t < a.T && row < a.SI) {
+                k3d_st4_sc1(rp, (((ks * a.T + t) * 2 + 0) * a.SI + row) * 4, g[j]);
+                k3d_st4_sc1(rp, (((ks * a.T + t) * 2 + 1) * a.SI + row) * 4, u[j]);
             }
         }
-        k3d_arrive_event(a.sync, G.cSGF, G.nSGt, G.eSGF, lane);
+        if (!k3d_arrive(k3d_line(a.sync, G.lTSG + rg), G.KSS - 1, lane)) return;
+        /* last slice of the row group: h = act(gate, up) for its 64 rows x T tokens (lane:
+         * row) -> bf16 pieces */
+        const int row = 16 * SG_TILES * rg + lane;
+        const K3Rsrc rh = k3d_rsrc(a.hq16, (size_t)G.nCsi * 1024);
+        for (int tt = 0; tt < a.T; ++tt) {
+            if (lane < 16 * SG_TILES && row < a.SI) {
+                const int qs = a.T * 2 * a.SI * 4;
+                const float gs = k3d_sum_sc1<K3G_KS_SG>(rp, ((tt * 2 + 0) * a.SI + row) * 4, qs,
+                                                        G.KSS);
+                const float us = k3d_sum_sc1<K3G_KS_SG>(rp, ((tt * 2 + 1) * a.SI + row) * 4, qs,
+                                                        G.KSS);
+                float r2 = k3d_act(gs, us, a.b1, a.b2);
+#pragma unroll
+                for (int pc = 0; pc < NPC16; ++pc) {
+                    float back;
+                    const uint32_t h = k3d_bf16_rn(r2, back);
+                    r2 -= back;
+                    k3d_st16_sc1(rh, k3d_b16_off(row, NPC16 * tt + pc), h);
+                }
+            }
+        }
+        k3d_arrive_event2(a.sync, G.cSGF, G.nSGt, rg, G.eSGF, lane);
     }
 
     /* ----------------------------------------------------------------- G ---- */
@@ -767,11 +887,10 @@ struct K3Dec {
             return;
         /* last slice of the tile: 32 rows of h = act(gate, up) -> FP8 pieces (one block) */
         const int r = lane & 31, row = 32 * gt + r;
-        float gs = 0.0f, us = 0.0f;
-        for (int q = 0; q < G.KSG; ++q) {
-            gs += k3d_f32_sc1(rp, (((p * G.KSG + q) * 2 + 0) * a.I + row) * 4);
-            us += k3d_f32_sc1(rp, (((p * G.KSG + q) * 2 + 1) * a.I + row) * 4);
-        }
+        const float gs = k3d_sum_sc1<K3G_KS_G>(rp, ((p * G.KSG * 2 + 0) * a.I + row) * 4,
+                                               2 * a.I * 4, G.KSG);
+        const float us = k3d_sum_sc1<K3G_KS_G>(rp, ((p * G.KSG * 2 + 1) * a.I + row) * 4,
+                                               2 * a.I * 4, G.KSG);
         float h = lane < 32 ? k3d_act(gs, us, a.b1, a.b2) : 0.0f;
         const K3Rsrc rh = k3d_rsrc(a.hq8 + (size_t)p * G.nQi * K3G_BQ, (size_t)G.nQi * K3G_BQ);
         const int Qh = gt >> 4;
@@ -784,7 +903,7 @@ struct K3Dec {
                 if (lane == 0) k3d_st8_sc1(rh, Qh * K3G_BQ + k3d_bq_scale(gt, pc), sx + 127);
             }
         }
-        k3d_arrive_event(a.sync, G.cGF + p, G.nGt, G.eGF + p * K3_EVLINES, lane);
+        k3d_arrive_event2(a.sync, G.cGF + p * (1 + NSUB), G.nGt, gt, G.eGF + p * K3_EVLINES, lane);
     }
 
     /* ---------------------------------------------------------------- SD ---- */
@@ -1007,9 +1126,9 @@ k_decode_fused(K3kDecode a)
         else if ((t -= G.nX) < G.nR) K3Dec<NT>::router(ap, t, lane, &rl, wg_slices);
         else if ((t -= G.nR) < 1) K3Dec<NT>::select(ap, lane, &lds);
         else if ((t -= 1) < G.nSG) K3Dec<NT>::shared_gateup(ap, t, lane);
-        else if ((t -= G.nSG) < G.nG) K3Dec<NT>::routed_gateup(ap, t, lane);
-        else if ((t -= G.nG) < G.nSD) K3Dec<NT>::shared_down(ap, t, lane);
-        else K3Dec<NT>::routed_down(ap, t - G.nSD, lane);
+        else if ((t -= G.nSG) < G.nSD) K3Dec<NT>::shared_down(ap, t, lane);
+        else if ((t -= G.nSD) < G.nG) K3Dec<NT>::routed_gateup(ap, t, lane);
+        else K3Dec<NT>::routed_down(ap, t - G.nG, lane);
         if (a.trace && lane == 0) a.trace[3 * tk + 2] = wall_clock64();
     }
 }
