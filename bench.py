@@ -43,11 +43,11 @@ B_GATEUP_EXPERT = 2 * (I * D // 2 + I * D // 32)   # w1 + w3 of one expert
 # --pmc runs (FETCH_SIZE x 1.9994 + WRITE_SIZE x 1.0, the factors that make a 256 MiB
 # device-to-device copy read 256 MiB); the run and the numbers are in
 # profiles/k_decode_fused_k2_decode.md. Re-measured whenever the kernel changes.
-TRAFFIC_FUSED = 304563580
+TRAFFIC_FUSED = 300037638
 # HBM bytes per launch of the routed gate/up GEMM (k_gemm<0, 4>) of the 4096-token
 # Zipf(0.8) prefill, the same way (FETCH_SIZE x 1.9997 + WRITE_SIZE, mean of 3 launches):
-# 7.804 GB read + 0.204 GB written; profiles/k_gemm_k2_prefill4096.md.
-TRAFFIC_GATEUP_PREFILL = 8008000000
+# 7.666 GB read + 0.204 GB written; profiles/k_gemm_k2_prefill4096.md.
+TRAFFIC_GATEUP_PREFILL = 7869400121
 
 
 def log(msg):
