@@ -150,7 +150,10 @@ size_t k3_moe_scratch(const K3Cfg *c);
  * grouped GEMMs; an HBM expert cache (k3gc_*) with a tiled bank serves its experts in
  * place, any other source's experts are copied and tiled per call. Through an HBM cache
  * the tokens are run in groups whose experts fit the cache's unpinned slots, one cache
- * step each, so a cache of top-k + 1 slots serves any T without dropping an expert. */
+ * step each, so a cache of top-k + 1 slots serves any T without dropping an expert.
+ * fp32 and int8-draft (K3_WI8) shared and latent weights run as per-row GEMVs; the int8
+ * rows are summed in float in the GPU's order, within float rounding of the engine's
+ * k3_matmul_q8 (which itself differs between its AVX2, NEON and plain builds). */
 void k3_moe(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
             int T, int *idx, float *wt, float *scratch);
 
@@ -211,8 +214,11 @@ K3gExpertLayout k3g_expert_layout(int hidden, int inter);
  *                   k3g_tile_mxfp4 writes (they carry their own scales; s1/s3/s2
  *                   unused). The fused decode kernel streams this layout at full line
  *                   granularity into the matrix cores; it serves up to 4 tokens a call.
- *   shared expert, tagged by wdt (K3_WF32 or K3_WBF16): sh1/sh3 [shared_inter][hidden],
- *     sh2 [hidden][shared_inter]; shared_inter == 0 means none. shared_fmt 0: row-major;
+ *   shared expert, tagged by wdt (K3_WF32, K3_WBF16, or K3_WI8: rows of an f32 scale
+ *     then the row's int8 weights, as the engine's draft model stores them, summed in
+ *     float with no bit-exactness promise, as the engine's k3_matmul_q8 gives none):
+ *     sh1/sh3 [shared_inter][hidden], sh2 [hidden][shared_inter]; shared_inter == 0
+ *     means none. shared_fmt 0: row-major;
  *     1: bf16 in the tiled layout k3g_tile_bf16 writes, for the shared expert and the
  *     latent projections alike (goes with expert_fmt 2)
  *   latent projections, tagged by wdt: down [latent][hidden], up [hidden][latent];

@@ -412,7 +412,14 @@ size_t k3_moe_scratch(const K3Cfg *c)
 }
 
 /* ---------------------------------------------------------------- MoE layer ---- */
-static size_t wsz(int wdt) { return wdt == K3_WBF16 ? 2 : 4; }
+/* bytes of a rows x in weight matrix tagged wdt (include/k3/k3.h:299-303: per-row int8
+ * draft rows are an f32 scale then `in` int8 weights) */
+static size_t mat_bytes(int wdt, int rows, int in)
+{
+    const size_t row = wdt == K3_WI8 ? (size_t)4 + (size_t)in
+                                     : (size_t)in * (wdt == K3_WBF16 ? 2u : 4u);
+    return (size_t)rows * row;
+}
 
 /* How a fetched expert reaches the kernels. */
 enum {
@@ -636,7 +643,8 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
 {
     if (T <= 0) return;
     if (c->topk < 1 || c->topk > K3_MAX_TOPK) k3g_fatal("k3_moe: topk outside 1..64");
-    if (w->wdt == K3_WI8) k3g_fatal("k3_moe: int8 draft weights are not on the GPU path");
+    if (w->wdt != K3_WF32 && w->wdt != K3_WBF16 && w->wdt != K3_WI8)
+        k3g_fatal("k3_moe: unknown weight type (wdt)");
     const int d = c->hidden, E = c->n_experts, k = c->topk, I = c->moe_inter;
     const int L = w->down ? c->latent : d;
     const int SI = c->moe_inter * c->n_shared;
@@ -692,12 +700,12 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
             G.sh2 = mirror_tiled(s, w->sh2, d, SI, st);
         }
     } else {
-        G.down = mirror(s, w->down, w->down ? (size_t)L * d * wsz(w->wdt) : 0);
-        G.up = mirror(s, w->up, w->up ? (size_t)d * L * wsz(w->wdt) : 0);
+        G.down = mirror(s, w->down, w->down ? mat_bytes(w->wdt, L, d) : 0);
+        G.up = mirror(s, w->up, w->up ? mat_bytes(w->wdt, d, L) : 0);
         if (SI > 0) {
-            G.sh1 = mirror(s, w->sh1, (size_t)SI * d * wsz(w->wdt));
-            G.sh3 = mirror(s, w->sh3, (size_t)SI * d * wsz(w->wdt));
-            G.sh2 = mirror(s, w->sh2, (size_t)d * SI * wsz(w->wdt));
+            G.sh1 = mirror(s, w->sh1, mat_bytes(w->wdt, SI, d));
+            G.sh3 = mirror(s, w->sh3, mat_bytes(w->wdt, SI, d));
+            G.sh2 = mirror(s, w->sh2, mat_bytes(w->wdt, d, SI));
         }
         if (!w->src) {
             G.expert_fmt = 1;

@@ -662,7 +662,10 @@ int k3g_router(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx
     return k3g_route(c, L, x, T, idx, wt, st);
 }
 
-static int wfmt(int wdt) { return wdt == K3_WBF16 ? K3K_BF16 : K3K_F32; }
+static int wfmt(int wdt)
+{
+    return wdt == K3_WBF16 ? K3K_BF16 : wdt == K3_WI8 ? K3K_I8R : K3K_F32;
+}
 
 /* The routed experts of checkpoint-layout (or fp32) weights as per-expert GEMVs over each
  * expert's pairs (k3g_gemv.hip): dispatch -> gate/up (+act) -> down -> contrib rows. */

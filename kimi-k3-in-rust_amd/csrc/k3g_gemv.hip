@@ -292,6 +292,59 @@ k_dense(const void *Wa, const void *Wb, const uint8_t *Sa, const uint8_t *Sb, in
     }
 }
 
+/* --------------------------------------------------- int8 draft rows (K3_WI8) ---- */
+/* Rows of [f32 scale][int8 x in] (stride 4 + in bytes, so 4-byte aligned when in % 4 == 0):
+ * y[t][r] = (sum_i w[r][i] x[t][i]) * scale[r], summed in float in any order (the engine's
+ * k3_matmul_q8, src/core/k3_ops.c:1198-1272, gives these draft weights no determinism
+ * contract). One wave per row and up to NT tokens, lane l taking columns 4 l + 256 j; with
+ * PAIR the wave also takes the same row of Wb and writes act(a, b). grid (ceil(rows / 4),
+ * ceil(T / NT)), 4 waves per block. */
+template <int NT, bool PAIR>
+__global__ void __launch_bounds__(256)
+k_dense_q8(const uint8_t *Wa, const uint8_t *Wb, int nrows, int in, const float *x, int ldx,
+           int T, float *y, int ldy, float b1, float b2)
+{
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= nrows) return;
+    const int t0 = blockIdx.y * NT;
+    const size_t rowb = (size_t)4 + (size_t)in;
+    const uint8_t *ra = Wa + (size_t)row * rowb;
+    const uint8_t *rb = PAIR ? Wb + (size_t)row * rowb : nullptr;
+    float acc[NT], accb[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) { acc[t] = 0.0f; accb[t] = 0.0f; }
+    for (int i = 4 * lane; i < in; i += 256) {
+        const uint32_t wa = *(const uint32_t *)(ra + 4 + i);
+        const float a[4] = {(float)(int8_t)(wa & 0xff), (float)(int8_t)((wa >> 8) & 0xff),
+                            (float)(int8_t)((wa >> 16) & 0xff), (float)(int8_t)(wa >> 24)};
+        float bw[4] = {0.f, 0.f, 0.f, 0.f};
+        if (PAIR) {
+            const uint32_t wb = *(const uint32_t *)(rb + 4 + i);
+            bw[0] = (float)(int8_t)(wb & 0xff); bw[1] = (float)(int8_t)((wb >> 8) & 0xff);
+            bw[2] = (float)(int8_t)((wb >> 16) & 0xff); bw[3] = (float)(int8_t)(wb >> 24);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t0 + t < T) {
+                const float4 xv = *(const float4 *)(x + (size_t)(t0 + t) * ldx + i);
+                acc[t] = fmaf(a[0], xv.x, fmaf(a[1], xv.y, fmaf(a[2], xv.z, fmaf(a[3], xv.w, acc[t]))));
+                if (PAIR)
+                    accb[t] = fmaf(bw[0], xv.x, fmaf(bw[1], xv.y,
+                                   fmaf(bw[2], xv.z, fmaf(bw[3], xv.w, accb[t]))));
+            }
+        }
+    }
+    const float sa = *(const float *)ra, sb = PAIR ? *(const float *)rb : 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const float va = k3d_wave_sum(acc[t]) * sa;
+        const float vb = PAIR ? k3d_wave_sum(accb[t]) * sb : 0.0f;
+        if (lane == 0 && t0 + t < T)
+            y[(size_t)(t0 + t) * ldy + row] = PAIR ? k3d_act(va, vb, b1, b2) : va;
+    }
+}
+
 /* ------------------------------------------------------------- launchers ---- */
 static bool k3_aligned(const void *p, int a) { return ((uintptr_t)p & (uintptr_t)(a - 1)) == 0; }
 
@@ -348,6 +401,21 @@ extern "C" int k3k_dense(int fmt, const void *Wa, const void *Wb, int rows, int 
                          float b2, hipStream_t st)
 {
     if (rows <= 0 || T <= 0) return 0;
+    if (fmt == K3K_I8R) {
+        /* 4-byte int8 groups and float4 activations: in % 4, 16-byte x rows */
+        if (in % 4 || ldx % 4 || !k3_aligned(x, 16) || !k3_aligned(Wa, 4) ||
+            (Wb && !k3_aligned(Wb, 4)))
+            return -1;
+        constexpr int NT = 4;
+        const dim3 g((rows + 3) / 4, (T + NT - 1) / NT);
+        if (Wb)
+            hipLaunchKernelGGL((k_dense_q8<NT, true>), g, dim3(256), 0, st, (const uint8_t *)Wa,
+                               (const uint8_t *)Wb, rows, in, x, ldx, T, y, ldy, b1, b2);
+        else
+            hipLaunchKernelGGL((k_dense_q8<NT, false>), g, dim3(256), 0, st, (const uint8_t *)Wa,
+                               (const uint8_t *)nullptr, rows, in, x, ldx, T, y, ldy, b1, b2);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if (in % 16 || ldx % 4 || !k3_aligned(x, 16) || !k3_aligned(Wa, 16) ||
         (Wb && !k3_aligned(Wb, 16)))
         return -1;

@@ -28,7 +28,8 @@ extern "C" {
 #define K3G_TILE_ROUNDS(n) (K3G_TILE_GROUP * (((n) + 8 * K3G_TILE_GROUP - 1) / (8 * K3G_TILE_GROUP)))
 
 /* weight formats */
-enum { K3K_MXFP4 = 0, K3K_F32 = 1, K3K_BF16 = 2 };
+enum { K3K_MXFP4 = 0, K3K_F32 = 1, K3K_BF16 = 2,
+       K3K_I8R = 3 };    /* K3K_I8R: rows of [f32 scale][int8 x in] (the engine's K3_WI8) */
 
 /* Everything the routed-expert kernels read, device pointers. */
 typedef struct {
@@ -192,7 +193,7 @@ int k3k_dispatch_tiles(const int32_t *idx, int P, int E, int32_t *cnt, int32_t *
 int k3k_routed_gateup(const K3kRouted *a, int maxU, int maxtok, hipStream_t st);
 int k3k_routed_down(const K3kRouted *a, int maxU, int maxtok, hipStream_t st);
 
-/* y[t][r] = W[r] . x[t] (fmt K3K_F32 or K3K_BF16), or with Wb != NULL
+/* y[t][r] = W[r] . x[t] (fmt K3K_F32, K3K_BF16 or K3K_I8R), or with Wb != NULL
  * y[t][r] = act(Wa[r] . x[t], Wb[r] . x[t]). */
 int k3k_dense(int fmt, const void *Wa, const void *Wb, int rows, int in,
               const float *x, int ldx, int T, float *y, int ldy, float b1, float b2,

@@ -112,7 +112,7 @@ class K3gLayer(C.Structure):
 
 
 K3G_EXPERT_MXFP4, K3G_EXPERT_F32, K3G_EXPERT_MXFP4_TILED = 0, 1, 2
-K3_WF32, K3_WBF16 = 0, 1
+K3_WF32, K3_WBF16, K3_WI8 = 0, 1, 2
 SWIGLU_CAP = float(2.0 ** 100)   # the engine's SwiGLU setting of the SiTU caps
 
 # -------------------------------------------------------------------- libraries ----

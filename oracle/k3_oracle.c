@@ -10,6 +10,9 @@
  *                       fp64 dot within 1e-6 relative (test_expert.c:227)
  *   ork3_matmul_bf16    bench_kernels FNV-1a KAT 83c8504a4cb3fac6 (12288x7168), bit
  *                       identity with ork3_matmul on widened values (test_ops.c:811)
+ *   ork3_matmul_q8      an fp64 dot of the widened rows within 1e-6 of sum|w x| scale,
+ *                       the compiled engine kernel (its AVX2 form) within the same bound,
+ *                       and a planted scale-twice mistake failing it
  *   ork3_situ_glu       ops/situ_glu.json, the |y| <= b1*b2 bound
  *   ork3_router         ops/router.json (index sets, weights 1e-5/1e-4), brute force on
  *                       a stable sort, and bit identity with the compiled engine kernel
@@ -284,17 +287,45 @@ void ork3_router(int *idx, float *w, const float *x, const float *W,
     free(choice);
 }
 
+/* src/core/k3_ops.c:1198-1272, the build without AVX2 or NEON (the engine's flag-free
+ * form): per row, four float accumulators over the columns in steps of four, summed as
+ * (a0 + a1) + (a2 + a3), the tail added one product at a time, then times the row's
+ * scale. The engine gives this kernel no determinism contract (its AVX2 and NEON forms
+ * sum in other orders), so the GPU is held to a tolerance against it, not to bits. */
+void ork3_matmul_q8(float *y, const float *x, const void *W, int in, int out)
+{
+    const unsigned char *base = (const unsigned char *)W;
+    const size_t rowb = (size_t)4 + (size_t)in;
+    for (int o = 0; o < out; o++) {
+        const unsigned char *row = base + (size_t)o * rowb;
+        float scale;
+        memcpy(&scale, row, 4);
+        const signed char *w = (const signed char *)(row + 4);
+        float a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+        int i = 0;
+        for (; i + 3 < in; i += 4) {
+            a0 += (float)w[i] * x[i];
+            a1 += (float)w[i + 1] * x[i + 1];
+            a2 += (float)w[i + 2] * x[i + 2];
+            a3 += (float)w[i + 3] * x[i + 3];
+        }
+        float acc = (a0 + a1) + (a2 + a3);
+        for (; i < in; i++) acc += (float)w[i] * x[i];
+        y[o] = acc * scale;
+    }
+}
+
 /* ------------------------------------------------------- kernel table ---- */
 static OrKernels K = {
     ork3_router, ork3_matmul_mxfp4, ork3_matmul_bf16, ork3_matmul, ork3_situ_glu,
-    ork3_rmsnorm
+    ork3_rmsnorm, ork3_matmul_q8
 };
 
 void ork3_set_kernels(const OrKernels *k)
 {
     static const OrKernels dflt = {
         ork3_router, ork3_matmul_mxfp4, ork3_matmul_bf16, ork3_matmul, ork3_situ_glu,
-        ork3_rmsnorm
+        ork3_rmsnorm, ork3_matmul_q8
     };
     K = k ? *k : dflt;
 }
@@ -305,8 +336,9 @@ static void mmw(float *y, const float *x, const void *W, int wdt, int in, int ou
 {
     if (!W) { if (y != x) memcpy(y, x, (size_t)out * sizeof(float)); return; }
     if (wdt == K3_WBF16) K.matmul_bf16(y, x, (const uint16_t *)W, in, out);
+    else if (wdt == K3_WI8) K.matmul_q8(y, x, W, in, out);
     else if (wdt == K3_WF32) K.matmul(y, x, (const float *)W, in, out);
-    else die("mmw: int8 draft weights are not on this path", wdt);
+    else die("mmw: unknown weight type", wdt);
 }
 
 /* -------------------------------------------------------------- MoE layer ---- */

@@ -29,6 +29,8 @@ void   ork3_mxfp4_dequant(float *out, const unsigned char *packed,
 void   ork3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
                          const unsigned char *scales, int in, int rows, int group);
 void   ork3_matmul_bf16(float *y, const float *x, const uint16_t *W, int in, int out);
+/* per-row int8 draft weights: `out` rows of [f32 scale][int8 * in] */
+void   ork3_matmul_q8(float *y, const float *x, const void *W, int in, int out);
 void   ork3_matmul(float *y, const float *x, const float *W, int in, int out);
 void   ork3_situ_glu(float *y, const float *x, int n, float b1, float b2);
 void   ork3_rmsnorm(float *y, const float *x, const float *w, int n, float eps);
@@ -54,6 +56,7 @@ typedef struct {
     void (*matmul)(float *, const float *, const float *, int, int);
     void (*situ_glu)(float *, const float *, int, float, float);
     void (*rmsnorm)(float *, const float *, const float *, int, float);
+    void (*matmul_q8)(float *, const float *, const void *, int, int);
 } OrKernels;
 void ork3_set_kernels(const OrKernels *k);
 

@@ -44,7 +44,7 @@ class OrMemSrc(C.Structure):
 
 class OrKernels(C.Structure):
     _fields_ = [("router", vp), ("matmul_mxfp4", vp), ("matmul_bf16", vp), ("matmul", vp),
-                ("situ_glu", vp), ("rmsnorm", vp)]
+                ("situ_glu", vp), ("rmsnorm", vp), ("matmul_q8", vp)]
 
 
 def _p(a: np.ndarray | None):
@@ -72,6 +72,8 @@ class Kernels:
         self.f_bf16.argtypes = [vp, vp, vp, i32, i32]
         self.f_mm = g("matmul")
         self.f_mm.argtypes = [vp, vp, vp, i32, i32]
+        self.f_q8 = g("matmul_q8")
+        self.f_q8.argtypes = [vp, vp, vp, i32, i32]
         self.f_situ = g("situ_glu")
         self.f_situ.argtypes = [vp, vp, i32, f32, f32]
         self.f_rms = g("rmsnorm")
@@ -122,6 +124,13 @@ class Kernels:
         x = np.ascontiguousarray(x, np.float32)
         y = np.zeros(out_rows, np.float32)
         self.f_mm(_p(y), _p(x), _p(np.ascontiguousarray(W, np.float32)), x.size, out_rows)
+        return y
+
+    def matmul_q8(self, x, Wrows, out_rows):
+        """Wrows: uint8 [out_rows][4 + in], each row an f32 scale then int8 weights."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(out_rows, np.float32)
+        self.f_q8(_p(y), _p(x), _p(np.ascontiguousarray(Wrows, np.uint8)), x.size, out_rows)
         return y
 
     def situ(self, gu, b1, b2):
@@ -185,7 +194,7 @@ def set_kernels(k: Kernels | None) -> None:
         O.L.ork3_set_kernels(None)
         return
     t = OrKernels(k.addr(k.f_router), k.addr(k.f_mx), k.addr(k.f_bf16), k.addr(k.f_mm),
-                  k.addr(k.f_situ), k.addr(k.f_rms))
+                  k.addr(k.f_situ), k.addr(k.f_rms), k.addr(k.f_q8))
     O.L.ork3_set_kernels(C.byref(t))
 
 

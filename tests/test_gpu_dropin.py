@@ -262,3 +262,71 @@ def test_resident_layer_runs_at_once(gpu, prefill, T, want):
         np.testing.assert_allclose(wt, ow, rtol=1e-6)
     cache.free()
     bank.free()
+
+
+# ------------------------------------------------------- int8 draft weights (K3_WI8) ----
+
+def _q8_rows(rows, inn, seed, stream):
+    """[rows][4 + inn] uint8: per row an f32 scale then int8 weights (K3_WI8)."""
+    rng = np.random.default_rng(seed * 1000 + stream)
+    w = rng.integers(-127, 128, (rows, inn), dtype=np.int8)
+    sc = (rng.uniform(0.5, 2.0, rows) * (0.04 / 127)).astype(np.float32)
+    out = np.empty((rows, 4 + inn), np.uint8)
+    out[:, :4] = sc.view(np.uint8).reshape(rows, 4)
+    out[:, 4:] = w.view(np.uint8)
+    return out
+
+
+@pytest.mark.parametrize("latent,prefill,T", [(True, False, 1), (True, True, 6),
+                                              (False, False, 3), (False, True, 9)])
+def test_int8_draft_weights(gpu, latent, prefill, T):
+    """The draft model's int8 weights (K3_WI8: rows of an f32 scale and int8 weights) for
+    the shared experts and, with a latent width, the down/up projections: per-row GEMVs
+    summed in float (the engine's k3_matmul_q8 promises no bits), routing bit-exact,
+    output within rel-L2 1e-5 of the oracle's k3_moe / k3_moe_prefill."""
+    d, E, k, I = 256, 32, 4, 128
+    Lw = 128 if latent else d
+    SI = 2 * I
+    say(f"case: {'k3_moe_prefill' if prefill else 'k3_moe'} int8 draft weights, d={d}, "
+        f"E={E}, top-{k}, latent {Lw}, I={I}, shared {SI}, T={T}, host source")
+    shape = k3moe.Shape("int8 draft", Lw, E, k, I, n_shared=2, routed_scale=1.0, x_bf16=False)
+    experts = k3moe.SynthLayer(shape, seed=57, device=False)
+    gate = np.ascontiguousarray(k3moe.host_normal(E * d, 57, 701, 0.0, 0.05))
+    bias = k3moe.host_normal(E, 57, 702, 0.0, 0.01)
+    lnorm = k3moe.host_normal(Lw, 57, 703, 1.0, 0.1)
+    down, up = _q8_rows(Lw, d, 57, 704), _q8_rows(d, Lw, 57, 705)
+    sh1, sh3, sh2 = _q8_rows(SI, d, 57, 706), _q8_rows(SI, d, 57, 707), _q8_rows(d, SI, 57, 708)
+    x = np.ascontiguousarray(k3moe.host_normal(T * d, 57, 709, 0.0, 1.0).reshape(T, d))
+    runs = {(0, e): experts.expert_host(e) for e in range(E)}
+
+    def weights():
+        src = O.MemSrc(runs, 1, E, experts.geo)
+        w = k3moe.K3MoeW()
+        w.gate, w.bias = gate.ctypes.data, bias.ctypes.data
+        if latent:
+            w.latent_norm = lnorm.ctypes.data
+            w.down, w.up = down.ctypes.data, up.ctypes.data
+        w.sh1, w.sh3, w.sh2 = sh1.ctypes.data, sh3.ctypes.data, sh2.ctypes.data
+        w.wdt = k3moe.K3_WI8
+        w.src, w.layer = src.ptr, 0
+        return w, src
+
+    cfg = k3moe.K3Cfg()
+    cfg.hidden, cfg.latent, cfg.moe_inter = d, Lw, I
+    cfg.n_experts, cfg.topk, cfg.n_shared = E, k, 2
+    cfg.routed_scale, cfg.moe_renorm, cfg.latent_norm = 1.0, 1, 1 if latent else 0
+    cfg.rms_eps, cfg.situ_b1, cfg.situ_b2, cfg.n_layers = 1e-6, 4.0, 25.0, 1
+    w, src = weights()
+    d0 = drops()
+    out, idx, wt, paths = dropin(w, cfg, x, prefill)
+    k3moe.lib().k3moe_forget_weights()
+    w2, src2 = weights()
+    oo, oi, ow = O.oracle().moe(w2, cfg, x, prefill=prefill)
+    r = rel_l2(out, oo)
+    say(f"  kernels {paths}, rel-L2 {r:.3e}")
+    assert paths == STAGED
+    assert drops() == d0
+    assert np.isfinite(out).all() and r <= 1e-5
+    if not prefill:
+        assert np.array_equal(idx, oi)
+        np.testing.assert_allclose(wt, ow, rtol=1e-6)

@@ -241,6 +241,57 @@ def test_k2_weights_sum_to_routed_scale():
     assert np.isfinite(out).all()
 
 
+# --------------------------------------------------------- int8 draft rows (K3_WI8) ----
+
+def q8_rows(rng, rows, inn):
+    """[rows][4 + inn] uint8: an f32 scale then int8 weights per row (K3_WI8)."""
+    w = rng.integers(-127, 128, (rows, inn), dtype=np.int8)
+    sc = rng.uniform(0.5, 2.0, rows).astype(np.float32) * np.float32(0.02 / 127)
+    out = np.empty((rows, 4 + inn), np.uint8)
+    out[:, :4] = sc.view(np.uint8).reshape(rows, 4)
+    out[:, 4:] = w.view(np.uint8)
+    return out, w, sc
+
+
+def q8_bound(w, sc, x):
+    """|float k3_matmul_q8 - exact| for the engine's forms (four float accumulators of
+    ceil(in / 4) terms, or sixteen vector lanes and a reduction tree): every product is
+    rounded once and passes through at most ceil(in / 4) + 8 roundings on its way to the
+    result, so gamma_m sum|w x| scale with m = ceil(in / 4) + 8, plus the scale multiply's
+    rounding (gamma_m = m u / (1 - m u), u = 2^-24)."""
+    inn = w.shape[1]
+    m = (inn + 3) // 4 + 8
+    u = 2.0 ** -24
+    gam = m * u / (1 - m * u)
+    mag = np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    exact = (w.astype(np.float64) @ x.astype(np.float64)) * sc.astype(np.float64)
+    return exact, gam * mag * sc.astype(np.float64) + np.abs(exact) * u
+
+
+@pytest.mark.parametrize("inn", [7168, 1003, 12])
+def test_q8_matmul_within_its_float_bound(inn):
+    """ork3_matmul_q8 (src/core/k3_ops.c:1198-1272) against an fp64 dot of the widened
+    rows times the row scale: inside the float-summation bound; a scale applied twice, a
+    row stride without the scale's 4 bytes, and a dropped tail each fall outside it."""
+    rng = np.random.default_rng(inn)
+    rows = 48
+    W, w, sc = q8_rows(rng, rows, inn)
+    x = rng.normal(0, 1, inn).astype(np.float32)
+    y = O.oracle().matmul_q8(x, W, rows)
+    exact, bound = q8_bound(w, sc, x)
+    assert np.all(np.abs(y - exact) <= bound)
+    # planted mistakes, computed from the same inputs: each must leave the bound
+    twice = exact * sc.astype(np.float64)
+    assert not np.all(np.abs(twice - exact) <= bound)
+    flat = W.reshape(-1)[4:4 + rows * inn].view(np.int8).reshape(rows, inn)
+    wrong_stride = (flat.astype(np.float64) @ x.astype(np.float64)) * sc.astype(np.float64)
+    assert not np.all(np.abs(wrong_stride - exact) <= bound)
+    if inn % 4:
+        n4 = inn - inn % 4
+        no_tail = (w[:, :n4].astype(np.float64) @ x[:n4].astype(np.float64)) * sc
+        assert not np.all(np.abs(no_tail - exact) <= bound)
+
+
 # -------------------------------------------------------- against the engine itself ----
 
 ref = O.ref()
@@ -269,6 +320,22 @@ def test_ref_mxfp4_and_bf16_bit_identical():
     assert np.array_equal(O.oracle().matmul_mxfp4(x, pk, sc, 257), ref.matmul_mxfp4(x, pk, sc, 257))
     Wb = O.kat_bf16(129 * 3584, 8)
     assert np.array_equal(O.oracle().matmul_bf16(x, Wb, 129), ref.matmul_bf16(x, Wb, 129))
+
+
+@needs_ref
+def test_ref_q8_within_the_float_bound():
+    """The engine's compiled k3_matmul_q8 (its AVX2 form: other accumulators, fused
+    products) and the oracle's flag-free form both sit inside the float-summation bound
+    around the exact dot, so they are within twice the bound of each other."""
+    rng = np.random.default_rng(17)
+    rows, inn = 64, 7168
+    W, w, sc = q8_rows(rng, rows, inn)
+    x = rng.normal(0, 1, inn).astype(np.float32)
+    exact, bound = q8_bound(w, sc, x)
+    a = O.oracle().matmul_q8(x, W, rows)
+    r = ref.matmul_q8(x, W, rows)
+    assert np.all(np.abs(r - exact) <= bound)
+    assert np.all(np.abs(a - r) <= 2 * bound)
 
 
 @needs_ref
