@@ -167,8 +167,11 @@ void k3_mxfp4_dequant(float *out, const unsigned char *packed,
                       const unsigned char *scales, int rows, int pcols, int group);
 
 /* Replaces include/k3/k3.h:565-566 (src/core/k3_ops.c:1363-1768). Aborts on odd `in`
- * or group > 64, as the engine does. group must be 32 on the GPU path (the format
- * K3_MXFP4_GROUP fixes); another group aborts with a message. */
+ * or group > 64, as the engine does (and on group < 1, which the engine divides by).
+ * Each row carries ceil(in / group) E8M0 scale bytes; group 32 (the format's block,
+ * K3_MXFP4_GROUP) runs the vectorised kernel, any other group one wave per row, reading
+ * the nibbles as the engine's grouped path does (group g from byte g * (group / 2)).
+ * Sums in float, within float rounding of the engine's double sums. */
 void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
                      const unsigned char *scales, int in, int rows, int group);
 

@@ -942,9 +942,9 @@ void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
                 group);
         abort();
     }
-    if (group != K3_MXFP4_GROUP) {
-        fprintf(stderr, "k3moe: FATAL, k3_matmul_mxfp4 on the GPU needs group 32, got %d.\n",
-                group);
+    if (group < 1) {
+        /* the engine divides by it (src/core/k3_ops.c:1387) */
+        fprintf(stderr, "k3moe: FATAL, k3_matmul_mxfp4 called with group=%d.\n", group);
         abort();
     }
     if (rows <= 0 || in <= 0) return;
@@ -958,7 +958,7 @@ void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
     L.topk = 1;
     L.inter = 16;
     K3gCtx *c = ctx_for(s, &L, 1);
-    const size_t pb = (size_t)rows * (in / 2), sb = (size_t)rows * ((in + 31) / 32);
+    const size_t pb = (size_t)rows * (in / 2), sb = (size_t)rows * ((in + group - 1) / group);
     const size_t xb = (size_t)in * 4, yb = (size_t)rows * 4;
     const size_t a0 = 0, a1 = (pb + 255) & ~(size_t)255, a2 = a1 + ((sb + 255) & ~(size_t)255);
     const size_t a3 = a2 + ((xb + 255) & ~(size_t)255);
@@ -967,7 +967,7 @@ void k3_matmul_mxfp4(float *y, const float *x, const unsigned char *packed,
     K3G_CHECK(hipMemcpyAsync(b + a1, scales, sb, hipMemcpyHostToDevice, c->stream));
     K3G_CHECK(hipMemcpyAsync(b + a2, x, xb, hipMemcpyHostToDevice, c->stream));
     if (k3k_mxfp4_gemv((float *)(b + a3), (const float *)(b + a2), b + a0, b + a1, in, rows,
-                       c->stream) != 0)
+                       group, c->stream) != 0)
         k3g_fatal("k3_matmul_mxfp4: launch failed");
     K3G_CHECK(hipMemcpyAsync(y, b + a3, yb, hipMemcpyDeviceToHost, c->stream));
     K3G_CHECK(hipStreamSynchronize(c->stream));

@@ -460,20 +460,24 @@ extern "C" int k3k_dense(int fmt, const void *Wa, const void *Wb, int rows, int 
 }
 
 /* One MXFP4 matrix times one vector (k3_matmul_mxfp4 on the GPU). Fast path for
- * in % 16 == 0 with aligned operands; otherwise one wave per row decoding nibbles one
- * at a time. */
+ * group 32, in % 16 == 0 with aligned operands; otherwise one wave per row decoding
+ * nibbles one at a time the way the engine's grouped path does (src/core/k3_ops.c:
+ * 1386-1388, 1515-1520): a row has ceil(in / group) scale bytes, element j of group g
+ * is nibble j of the bytes from g * (group / 2) on (low nibble first) scaled by byte g --
+ * for an even group the row's plain packing, for an odd one what the engine reads. */
 __global__ void __launch_bounds__(64)
 k_mxfp4_gemv_any(float *y, const float *x, const uint8_t *packed, const uint8_t *scales,
-                 int in, int rows)
+                 int in, int rows, int group)
 {
     const int r = blockIdx.x, lane = threadIdx.x;
     const uint8_t *pr = packed + (size_t)r * (in / 2);
-    const uint8_t *sr = scales + (size_t)r * ((in + 31) / 32);
+    const uint8_t *sr = scales + (size_t)r * ((in + group - 1) / group);
     float acc = 0.0f;
     for (int i = lane; i < in; i += 64) {
-        const uint8_t b = pr[i >> 1];
-        const uint32_t code = (i & 1) ? (b >> 4) : (b & 15);
-        const float m = k3d_e8m0(sr[i >> 5]);
+        const int g = i / group, j = i - g * group;
+        const uint8_t b = pr[g * (group >> 1) + (j >> 1)];
+        const uint32_t code = (j & 1) ? (b >> 4) : (b & 15);
+        const float m = k3d_e8m0(sr[g]);
         const float mag = (code & 7) == 0 ? 0.0f
                         : (code & 7) == 1 ? 0.5f
                         : __uint_as_float((((code & 7) >> 1) + 126u) << 23 | (code & 1u) << 22);
@@ -485,10 +489,12 @@ k_mxfp4_gemv_any(float *y, const float *x, const uint8_t *packed, const uint8_t 
 }
 
 extern "C" int k3k_mxfp4_gemv(float *y, const float *x, const uint8_t *packed,
-                              const uint8_t *scales, int in, int rows, hipStream_t st)
+                              const uint8_t *scales, int in, int rows, int group,
+                              hipStream_t st)
 {
     if (rows <= 0 || in <= 0) return 0;
-    if (in % 16 == 0 && k3_aligned(x, 16) && k3_aligned(packed, 8)) {
+    if (group < 1) return -1;
+    if (group == 32 && in % 16 == 0 && k3_aligned(x, 16) && k3_aligned(packed, 8)) {
         constexpr int NR = 16;
         hipLaunchKernelGGL((k_dense<K3K_MXFP4, NR, 1, false>),
                            dim3((rows + 4 * NR - 1) / (4 * NR), 1), dim3(256), 0, st,
@@ -496,7 +502,7 @@ extern "C" int k3k_mxfp4_gemv(float *y, const float *x, const uint8_t *packed,
                            in, x, in, 1, y, rows, 0.f, 0.f);
     } else {
         hipLaunchKernelGGL(k_mxfp4_gemv_any, dim3(rows), dim3(64), 0, st, y, x, packed, scales,
-                           in, rows);
+                           in, rows, group);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -230,7 +230,7 @@ int k3k_dequant(float *out, const uint8_t *packed, const uint8_t *scales, int ro
 
 /* y[rows] = W x for one MXFP4 matrix (group 32), any even `in`. */
 int k3k_mxfp4_gemv(float *y, const float *x, const uint8_t *packed, const uint8_t *scales,
-                   int in, int rows, hipStream_t st);
+                   int in, int rows, int group, hipStream_t st);
 
 int k3k_fill_bytes(uint8_t *dst, size_t n, uint64_t seed, uint64_t stream, uint64_t first,
                    hipStream_t st);

@@ -128,6 +128,29 @@ def test_matmul_mxfp4_shapes(gpu, rows, inn, lo, hi):
     assert rel_l2(y, ref) < 1e-6
 
 
+@pytest.mark.parametrize("rows,inn,group", [(40, 512, 16), (33, 1000, 64), (21, 90, 10),
+                                           (9, 64, 1), (12, 100, 9)])
+def test_matmul_mxfp4_other_groups(gpu, rows, inn, group):
+    """group != 32 (the engine's grouped path: ceil(in / group) scale bytes per row,
+    group g read from byte g * (group / 2) on, which for the odd groups 1 and 9 is not the
+    plain packing), against the oracle's restatement of it (bit-identical to the
+    engine's compiled kernel in the CPU tests)."""
+    say(f"case: k3_matmul_mxfp4 rows={rows} in={inn} group={group}")
+    ng = (inn + group - 1) // group
+    pk = k3moe.host_bytes(rows * inn // 2, 6, 950 + inn)
+    sc = k3moe.host_scales(rows * ng, 6, 951 + inn, -4, 2)
+    x = k3moe.host_normal(inn, 6, 952 + inn)
+    y = np.zeros(rows, np.float32)
+    k3moe.lib().k3_matmul_mxfp4(y.ctypes.data, x.ctypes.data, pk.ctypes.data, sc.ctypes.data,
+                                inn, rows, group)
+    ref = O.oracle().matmul_mxfp4(x, pk, sc, rows, group)
+    assert rel_l2(y, ref) < 1e-6
+    # a kernel that kept 32-element scale blocks reads other bytes
+    sc32 = np.ascontiguousarray(np.resize(sc, rows * ((inn + 31) // 32)))
+    wrong = O.oracle().matmul_mxfp4(x, pk, sc32, rows, 32)
+    assert rel_l2(wrong, ref) > 1e-3
+
+
 # ------------------------------------------------------------------------ router ----
 
 def test_router_golden(gpu):

@@ -339,6 +339,20 @@ def test_ref_q8_within_the_float_bound():
 
 
 @needs_ref
+@pytest.mark.parametrize("group", [16, 64, 10, 1, 9])
+def test_ref_mxfp4_other_groups_bit_identical(group):
+    """The restatement's general group path (ceil(in / group) scale bytes per row) is the
+    engine's, bit for bit."""
+    rows, inn = 37, 640
+    ng = (inn + group - 1) // group
+    pk = O.kat_b(rows * inn // 2, 11 + group)
+    sc = (O.kat_b(rows * ng, 12 + group) % 9 + 122).astype(np.uint8)
+    x = O.kat_f(inn, 13 + group)
+    assert np.array_equal(O.oracle().matmul_mxfp4(x, pk, sc, rows, group),
+                          ref.matmul_mxfp4(x, pk, sc, rows, group))
+
+
+@needs_ref
 def test_ref_moe_golden_bit_identical():
     w, cfg, keep = _moe_golden()
     x = keep["in"].reshape(-1, cfg.hidden)
