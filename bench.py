@@ -410,7 +410,7 @@ def prefill(a):
     ctx.profile(False)
     out = dout.download(np.float32, T * D)
     assert np.isfinite(out).all()
-    reroutes = ctx.stats()[0]
+    reroutes, recomputed = ctx.stats()[:2]
     # the FP4 x FP8 variant of the routed experts, reported separately
     ctx.set_fp8(True)
     for _ in range(a.prefill_warmup):
@@ -455,7 +455,8 @@ def prefill(a):
         "routing": {"experts_used": int(len(act)), "max_tokens": int(cnt.max()),
                     "min_tokens": int(act.min()),
                     "p90_over_p10": round(float(np.percentile(act, 90) / max(np.percentile(act, 10), 1)), 2),
-                    "certificate_reroutes": int(reroutes)},
+                    "certificate_reroutes": int(reroutes),
+                    "unsettled_scores_recomputed": int(recomputed)},
         "stage_us": stage_us,
         "fp4xfp8_variant": {
             "ms_per_step": round(ms8, 4), "tokens_per_s": round(T / (ms8 * 1e-3), 1),

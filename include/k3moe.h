@@ -267,7 +267,8 @@ void k3g_ctx_destroy(K3gCtx *ctx);
 void *k3g_ctx_stream(K3gCtx *ctx);   /* the context's compute stream (hipStream_t) */
 
 /* Routing statistics since the context was created: [0] tokens whose certificate
- * failed and were re-routed in the engine's serial order. */
+ * failed and were re-routed in the engine's serial order, [1] selected experts of
+ * certified tokens whose score the bound left unsettled and was recomputed exactly. */
 void k3g_ctx_stats(K3gCtx *ctx, int64_t *out, int n);
 
 /* Per-stage timing with HIP events on the call's stream (off by default; turning it on

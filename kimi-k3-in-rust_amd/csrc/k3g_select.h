@@ -243,6 +243,59 @@ __device__ __forceinline__ void k3d_fast_dots_staged(uint8_t *stage,
     }
 }
 
+/* The engine's float logit for one row, from a wave. The engine adds the row's d exact
+ * products p_i serially in double, s^_i = fl(s^_(i-1) + p_i), and that sum is within
+ * u sum_i |s^_i| of the exact one (u = 2^-53; Higham, Accuracy and Stability, 4.2) --
+ * a bound in the partial sums' magnitudes, far tighter than one in sum |p_i|. Lane l adds
+ * a contiguous block of the row in the engine's order, keeping its block sum b_l and the
+ * sum L_l of its local partial sums' magnitudes; a wave scan gives each block its starting
+ * partial sum P_l, so sum_i |s_i| <= sum_l (n_l |P_l| + L_l). The lanes' own sums err by
+ * at most u L_l each and the scan by gamma_7 sum_l |b_l|. When s -/+ that total bound
+ * round to the same float, that float is the engine's; returns false otherwise. d a
+ * multiple of 4, w and x 16-byte aligned. */
+__device__ __forceinline__ bool k3d_row_logit(const float *w, const float *x, int d, int lane,
+                                             float *f)
+{
+    const float4 *w4 = (const float4 *)w, *x4 = (const float4 *)x;
+    const int n4 = d / 4, per = (n4 + 63) / 64;
+    const int q0 = min(lane * per, n4), q1 = min(q0 + per, n4);
+    double b = 0.0, L = 0.0;
+    for (int q = q0; q < q1; q += 8) {
+        float4 wv[8], xv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int qq = min(q + u, q1 - 1);
+            wv[u] = w4[qq];
+            xv[u] = x4[qq];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (q + u < q1) {
+                b += (double)wv[u].x * xv[u].x; L += fabs(b);
+                b += (double)wv[u].y * xv[u].y; L += fabs(b);
+                b += (double)wv[u].z * xv[u].z; L += fabs(b);
+                b += (double)wv[u].w * xv[u].w; L += fabs(b);
+            }
+        }
+    }
+    /* inclusive scan of the block sums; P = the partial sum before this block */
+    double inc = b;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const double o = __shfl_up(inc, m, K3G_WAVE);
+        if (lane >= m) inc += o;
+    }
+    const double P = inc - b;
+    const double nl = 4.0 * (q1 - q0);
+    const double part = nl * fabs(P) + 2.0 * L, mag = fabs(b);
+    const double sp = k3d_wave_sumd(part), sm = k3d_wave_sumd(mag);
+    const double sum = __shfl(inc, 63, K3G_WAVE);
+    const double B = 1.05 * 0x1p-53 * sp + 8.0 * 0x1p-53 * sm + fabs(sum) * 0x1p-52 + 0x1p-1060;
+    const float lo = (float)(sum - B), hi = (float)(sum + B);
+    *f = lo;
+    return lo == hi;
+}
+
 /* The float the engine casts its serial fp64 sum to, from a sum s of the same n exact
  * products in another order and the sum a of their magnitudes: true when the bound
  * settles it (*f set), false when s lies too close to a float rounding boundary. */
@@ -264,9 +317,11 @@ __device__ __forceinline__ bool k3d_settled_float(double s, double a, int n, flo
  * value, then lower index). The certificate is checked along the way: with the rounds in
  * choice order, "every selected lo above the hi of everything ranked after it" is "each
  * new hi below the smallest lo selected before it" plus "the smallest selected lo above
- * the largest unselected hi". LDS is only used when the certificate fails. */
+ * the largest unselected hi". LDS is only used when the certificate fails. Returns the
+ * certified selections whose scores are not settled (bit j: round j; 0 after the exact
+ * path), for k3d_fix_unsettled. */
 template <int NPL>
-__device__ __noinline__ void
+__device__ __noinline__ uint64_t
 k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
                    const float *W, const float *x, int d, int E, int k, int renorm,
                    float routed_scale, int32_t *idx, float *wt, int force, int *stats,
@@ -299,7 +354,7 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
     float minlo = INFINITY;
     double wsum = 0.0;
     int my_sel = -1;          /* lane j: the j-th selected expert */
-    float my_score = 0.0f;
+    float my_score = 0.0f, my_hi = 0.0f;
     for (int j = 0; j < k; ++j) {
         /* this lane's best untaken key: a tree over the slots */
         uint64_t m[NPL];
@@ -332,8 +387,10 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
         } else {
             ok = false;
         }
-        if (lane == j) { my_sel = w; my_score = w >= 0 ? wsc : 0.0f; }
+        if (lane == j) { my_sel = w; my_score = w >= 0 ? wsc : 0.0f; my_hi = whi; }
     }
+    /* the selections whose score is not settled (bit j: round j) */
+    const uint64_t unsettled = __ballot(lane < k && my_sel >= 0 && !k3d_settled(my_hi));
     float hrest = -INFINITY;
 #pragma unroll
     for (int i = 0; i < NPL; ++i)
@@ -465,22 +522,70 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
         __hip_atomic_store(&wt[(size_t)t * k + lane], __fmul_rn(w, routed_scale),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    /* the exact path formed every score it selected from the engine's float logit */
+    return ok ? unsettled : 0;
 }
 
-/* k3d_select_token_n with the per-lane count chosen for E (<= K3G_MAX_E). */
+/* A certified selection's weights are its scores, and a score the bound left unsettled
+ * may not be the engine's (its float logit within the bound of a rounding boundary): the
+ * order stands (the intervals hold the engine's choices), so only those scores are
+ * recomputed -- k3d_row_logit reads the row straight from memory, one block per lane, and
+ * its partial-sum bound settles the engine's float logit; the serial chain only when it
+ * does not -- and the token's weights are formed again from all k scores (the engine's
+ * sequential double sum in selection order). Out of line and after the selection, so the
+ * selection's common path keeps its registers. */
+__device__ __noinline__ void k3d_fix_unsettled(int t, const float4 *rs, const float *W,
+                                               const float *x, int d, int E, int k, int renorm,
+                                               float routed_scale, int32_t *idx, float *wt,
+                                               int *stats, int lane, uint64_t unsettled)
+{
+    if (stats && lane == 0) atomicAdd(&stats[1], __popcll(unsettled));
+    const float *xt = x + (size_t)t * d;
+    int sel = 0;
+    float score = 0.0f;
+    if (lane < k) {
+        sel = __hip_atomic_load(&idx[(size_t)t * k + lane], __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+        score = rs[(size_t)t * E + sel].w;
+    }
+    const bool vec = d % 4 == 0 && ((((uintptr_t)W | (uintptr_t)x) & 15) == 0);
+    for (uint64_t m = unsettled; m; m &= m - 1) {
+        const int j = __builtin_ctzll(m);
+        const int e = __builtin_amdgcn_readlane(sel, j);
+        float logit;
+        if (!vec || !k3d_row_logit(W + (size_t)e * d, xt, d, lane, &logit))
+            logit = (float)k3d_serial_dot(W + (size_t)e * d, xt, d);
+        if (lane == j) score = k3d_sigmoid(logit);
+    }
+    double wsum = 0.0;
+    for (int j = 0; j < k; ++j)
+        wsum += (double)__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(score), j));
+    if (lane < k) {
+        float w = score;
+        if (renorm && k > 1) w = __fmul_rn(w, (float)(1.0 / (wsum + 1e-20)));
+        __hip_atomic_store(&wt[(size_t)t * k + lane], __fmul_rn(w, routed_scale),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+/* k3d_select_token_n with the per-lane count chosen for E (<= K3G_MAX_E), then the
+ * unsettled scores of a certified selection recomputed. */
 __device__ __forceinline__ void
 k3d_select_token(K3SelectLds *s, int t, const float4 *rs, const float *bias, const float *W,
                  const float *x, int d, int E, int k, int renorm, float routed_scale,
                  int32_t *idx, float *wt, int force, int *stats, int lane,
                  unsigned long long *stamp = nullptr, uint8_t *stage = nullptr)
 {
+    uint64_t um;
     if (E <= 256)
-        k3d_select_token_n<4>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                              force, stats, lane, stamp, stage);
+        um = k3d_select_token_n<4>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx,
+                                   wt, force, stats, lane, stamp, stage);
     else if (E <= 512)
-        k3d_select_token_n<8>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                              force, stats, lane, stamp, stage);
+        um = k3d_select_token_n<8>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx,
+                                   wt, force, stats, lane, stamp, stage);
     else
-        k3d_select_token_n<16>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                               force, stats, lane, stamp, stage);
+        um = k3d_select_token_n<16>(s, t, rs, bias, W, x, d, E, k, renorm, routed_scale, idx,
+                                    wt, force, stats, lane, stamp, stage);
+    if (um)
+        k3d_fix_unsettled(t, rs, W, x, d, E, k, renorm, routed_scale, idx, wt, stats, lane, um);
 }

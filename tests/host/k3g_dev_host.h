@@ -92,6 +92,20 @@ inline T emu_shfl_xor(T v, int m)
 }
 #define __shfl_xor(v, m, w) emu_shfl_xor(v, m)
 
+/* lane l takes lane l - m (lanes below m keep their own value), and any lane's value */
+template <typename T>
+inline T emu_shfl_from(T v, int from)
+{
+    uint64_t u = 0;
+    std::memcpy(&u, &v, sizeof(T));
+    const uint64_t o = emu_exchange(u, from);
+    T r;
+    std::memcpy(&r, &o, sizeof(T));
+    return r;
+}
+#define __shfl_up(v, m, w) emu_shfl_from(v, t_lane >= (m) ? t_lane - (m) : t_lane)
+#define __shfl(v, l, w) emu_shfl_from(v, (l))
+
 inline uint32_t emu_readlane(uint32_t v, int l) { return (uint32_t)emu_exchange(v, l); }
 #define __builtin_amdgcn_readlane(v, l) emu_readlane((uint32_t)(v), (l))
 /* every lane of the selection code is active wherever it reads the first lane */
@@ -142,6 +156,7 @@ inline void emu_wave_barrier() { g_wave->bar.arrive_and_wait(); }
 /* stores other waves read at device coherence: plain stores here (one wave) */
 #define __HIP_MEMORY_SCOPE_AGENT 0
 #define __hip_atomic_store(p, v, order, scope) (*(p) = (v))
+#define __hip_atomic_load(p, order, scope) (*(p))
 inline int atomicAdd(int *p, int v)
 {
     return std::atomic_ref<int>(*p).fetch_add(v);

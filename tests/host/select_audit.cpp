@@ -10,10 +10,11 @@
  * carry duplicated router rows and tied biases (exact ties in the choice scores, which fail
  * the certificate and exercise the exact path and its lowest-index rule).
  *
- * usage: select_audit E k d T ties seed      (prints one line per case; exit 1 on a
+ * usage: select_audit E k d T ties seed [wide]   (prints one line per case; exit 1 on a
  *                                             mismatch, the sanitizers abort on a fault) */
 #include "k3g_select.h"
 
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <random>
@@ -51,10 +52,14 @@ static void strided_dot(const float *w, const float *x, int d, double *s, double
 
 int main(int argc, char **argv)
 {
-    if (argc != 7) {
-        std::fprintf(stderr, "usage: select_audit E k d T ties seed\n");
+    if (argc != 7 && argc != 8) {
+        std::fprintf(stderr, "usage: select_audit E k d T ties seed [wide]\n");
         return 2;
     }
+    /* wide: every interval's bound is widened to many float ulps of the logit and its best
+     * guess moved by 0.7 of the bound (still inside it), so no score is settled and the
+     * guessed scores are not the engine's: a weight taken from a guess is a mismatch */
+    const int wide = argc == 8 ? std::atoi(argv[7]) : 0;
     const int E = std::atoi(argv[1]), k = std::atoi(argv[2]), d = std::atoi(argv[3]);
     const int T = std::atoi(argv[4]), ties = std::atoi(argv[5]);
     const unsigned seed = (unsigned)std::atoi(argv[6]);
@@ -83,7 +88,13 @@ int main(int argc, char **argv)
         for (int e = 0; e < E; ++e) {
             double s, a;
             strided_dot(W + (size_t)e * d, x + (size_t)t * d, d, &s, &a);
-            rs[(size_t)t * E + e] = k3d_route_score(s, a, bias[e], d);
+            if (wide) {
+                const double nr = 1e8, B = nr * 0x1p-53 * 1.01 * a + std::fabs(s) * 0x1p-51;
+                rs[(size_t)t * E + e] = k3d_route_score_n(s + ((e & 1) ? 0.7 : -0.7) * B, a,
+                                                          bias[e], nr);
+            } else {
+                rs[(size_t)t * E + e] = k3d_route_score(s, a, bias[e], d);
+            }
         }
 
     std::vector<int> ref_idx((size_t)T * k);
@@ -122,8 +133,9 @@ int main(int argc, char **argv)
             const int npl = E <= 256 ? 4 : E <= 512 ? 8 : 16;
             const long deliberate = (long)T * (64L * npl - E);
             std::printf("E=%d k=%d d=%d T=%d ties=%d staged=%d force=%d: rerouted %d, "
-                        "dma %ld, range-checked loads %ld (deliberate %ld), mismatches %d\n",
-                        E, k, d, T, ties, staged, force, stats[0], (long)wave.dma_ops,
+                        "recomputed %d, dma %ld, range-checked loads %ld (deliberate %ld), "
+                        "mismatches %d\n",
+                        E, k, d, T, ties, staged, force, stats[0], stats[1], (long)wave.dma_ops,
                         (long)wave.oob_loads, deliberate, mism);
             if (mism || wave.oob_loads != deliberate) bad = 1;
             delete[] idx;

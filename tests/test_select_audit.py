@@ -56,3 +56,26 @@ def test_select_in_bounds_and_bit_exact(audit, E, k, ties):
         # the duplicated rows put exact ties at the top-k boundary: the certificate fails
         # and the exact path picks the lower index, as the engine does
         assert all("force=0: rerouted 0" not in l for l in lines if "force=0" in l), r.stdout
+
+
+@pytest.mark.parametrize("E,k,ties", [(384, 8, 0), (1024, 64, 1), (16, 4, 0)])
+def test_unsettled_scores_never_become_weights(audit, E, k, ties):
+    """Intervals whose bound spans several float ulps of the logit, with the best guess
+    moved inside them: the certificate may still order the experts, but a selected score
+    that is not settled is not the engine's (here each guess sits 0.7 of the bound from the
+    true sum, several float ulps of the logit). Every such score is recomputed (or the
+    token re-routed), and indices and weights come out bit-exact with the oracle."""
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1")
+    r = subprocess.run([audit, str(E), str(k), "256", "2", str(ties), "5", "1"],
+                       capture_output=True, text=True, timeout=240, env=env)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    lines = [l for l in r.stdout.splitlines() if l.startswith("E=")]
+    assert len(lines) == 8, r.stdout
+    assert all(l.endswith("mismatches 0") for l in lines), r.stdout
+    for l in lines:
+        if "force=0" in l:
+            rer = int(l.split("rerouted ")[1].split(",")[0])
+            rec = int(l.split("recomputed ")[1].split(",")[0])
+            # each token either failed its certificate or had its k scores recomputed
+            assert rer + rec // k >= 2 and rec % k == 0, l
+
