@@ -104,7 +104,7 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     size_t at = 0;
     const size_t o_rs = carve(&at, T * E * 16);
     const size_t o_idx = carve(&at, P * 4), o_wt = carve(&at, P * 4);
-    const size_t o_cnt = carve(&at, nch * E * 4), o_base = carve(&at, nch * E * 4);
+    const size_t o_cnt = carve(&at, nch * E * 4), o_base = carve(&at, (nch + 1) * E * 4);
     const size_t o_off = carve(&at, (E + 1) * 4), o_act = carve(&at, E * 4);
     const size_t o_nact = carve(&at, 4), o_perm = carve(&at, P * 4);
     const size_t o_z = carve(&at, T * L * 4), o_h = carve(&at, P * I * 4);

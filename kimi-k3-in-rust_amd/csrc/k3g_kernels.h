@@ -177,8 +177,8 @@ int k3k_router(const float *x, int T, const float *W, const float *bias, int d, 
  * lines, 16384 ints) */
 size_t k3k_router_part_bytes(void);
 
-/* Stable counting sort of the T*k (token, slot) pairs by expert. cnt/base are
- * [ceil(P/256)][E] ints of workspace. */
+/* Stable counting sort of the T*k (token, slot) pairs by expert. cnt is [ceil(P/256)][E]
+ * ints of workspace, base [ceil(P/256) + 1][E] (the experts' totals in its last row). */
 int k3k_dispatch(const int32_t *idx, int P, int E, int32_t *cnt, int32_t *base,
                  int32_t *off, int32_t *act, int32_t *nact, int32_t *perm, int *err,
                  hipStream_t st);

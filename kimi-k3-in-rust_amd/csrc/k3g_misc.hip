@@ -100,84 +100,104 @@ k_disp_sort(const int32_t *idx, int P, int E, int32_t *off, int32_t *act, int32_
     if (tiles) k3d_build_tiles(tid, E, ce, v[0], tiles, ntiles, flag, red);
 }
 
-/* Large P, three passes over chunks of 256 pairs. */
+/* Large P: three passes over chunks of 256 pairs, no single-block step (a lone large
+ * block waits long for a CU when other kernels fill the GPU beside it):
+ *   count   one block per chunk: the chunk's per-expert counts from LDS atomics;
+ *   scan    one wave per 64 experts, a lane per expert: its counts over all chunks (every
+ *           load of a batch in flight), their running sum as each chunk's base within the
+ *           expert, and the expert's total;
+ *   scatter one block per chunk: the expert ranges from a block scan of the totals (block
+ *           0 also writes them and the active list), then each pair's place = its expert's
+ *           start + its chunk's base + its rank among the chunk's earlier pairs of that
+ *           expert (ballots over the key bits within a wave, per-wave counts in LDS across
+ *           waves), so the order within an expert is the pair order. */
 __global__ void __launch_bounds__(256)
 k_disp_count(const int32_t *idx, int P, int E, int32_t *cnt, int *err)
 {
-    __shared__ int keys[K3G_DCH];
+    __shared__ int h[K3G_MAX_EXPERTS];
     const int c = blockIdx.x;
-    keys[threadIdx.x] = k3d_key(idx, c * K3G_DCH + threadIdx.x, P, E, err);
+    for (int e = threadIdx.x; e < E; e += 256) h[e] = 0;
     __syncthreads();
-    const int n = min(K3G_DCH, P - c * K3G_DCH);
-    for (int e = threadIdx.x; e < E; e += 256) {
-        int m = 0;
-        for (int i = 0; i < n; ++i) m += keys[i] == e;
-        cnt[(size_t)c * E + e] = m;
-    }
+    const int key = k3d_key(idx, c * K3G_DCH + threadIdx.x, P, E, err);
+    if (key >= 0) atomicAdd(&h[key], 1);
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += 256) cnt[(size_t)c * E + e] = h[e];
 }
 
-/* One block, a thread per expert: per-chunk bases of each expert's pairs, the expert
- * ranges and the active list. The chunk counts are read 8 at a time so the loads of a
- * thread overlap instead of forming one long dependent chain. */
-__global__ void __launch_bounds__(1024)
-k_disp_scan(const int32_t *cnt, int nch, int E, int32_t *base, int32_t *off,
-            int32_t *act, int32_t *nact)
+__global__ void __launch_bounds__(64)
+k_disp_scan(const int32_t *cnt, int nch, int E, int32_t *base, int32_t *tot)
 {
-    __shared__ int sc[1024], sa[1024];
-    const int e = threadIdx.x;
-    int tot = 0;
-    if (e < E) {
-        int c = 0;
-        for (; c + 8 <= nch; c += 8) {
-            int v[8];
+    const int e = blockIdx.x * 64 + threadIdx.x;
+    if (e >= E) return;
+    int b = 0;
+    for (int c = 0; c < nch; c += 32) {
+        int v[32];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = cnt[(size_t)(c + u) * E + e];
+        for (int u = 0; u < 32; ++u) v[u] = c + u < nch ? cnt[(size_t)(c + u) * E + e] : 0;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) tot += v[u];
-        }
-        for (; c < nch; ++c) tot += cnt[(size_t)c * E + e];
+        for (int u = 0; u < 32; ++u)
+            if (c + u < nch) { base[(size_t)(c + u) * E + e] = b; b += v[u]; }
     }
-    /* block-wide inclusive scans of the totals and of the active flags */
-    sc[e] = tot;
-    sa[e] = tot > 0;
-    __syncthreads();
-    for (int d = 1; d < 1024; d <<= 1) {
-        const int a = e >= d ? sc[e - d] : 0, b = e >= d ? sa[e - d] : 0;
-        __syncthreads();
-        sc[e] += a;
-        sa[e] += b;
-        __syncthreads();
-    }
-    if (e < E) {
-        const int first = sc[e] - tot;
-        off[e] = first;
-        if (tot > 0) act[sa[e] - 1] = e;
-        int s = first;
-        int c = 0;
-        for (; c + 8 <= nch; c += 8) {
-            int v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = cnt[(size_t)(c + u) * E + e];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) { base[(size_t)(c + u) * E + e] = s; s += v[u]; }
-        }
-        for (; c < nch; ++c) { base[(size_t)c * E + e] = s; s += cnt[(size_t)c * E + e]; }
-    }
-    if (e == 1023) { off[E] = sc[1023]; *nact = sa[1023]; }
+    tot[e] = b;
 }
 
 __global__ void __launch_bounds__(256)
-k_disp_scatter(const int32_t *idx, int P, int E, const int32_t *base, int32_t *perm)
+k_disp_scatter(const int32_t *idx, int P, int E, const int32_t *base, const int32_t *tot,
+               int32_t *off, int32_t *act, int32_t *nact, int32_t *perm)
 {
-    __shared__ int keys[K3G_DCH];
-    const int c = blockIdx.x;
-    keys[threadIdx.x] = k3d_key(idx, c * K3G_DCH + threadIdx.x, P, E, nullptr);
+    __shared__ int wc[4][K3G_MAX_EXPERTS];
+    __shared__ int first[K3G_MAX_EXPERTS];
+    __shared__ int red[5 * 2];
+    const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    for (int e = tid; e < E; e += 256) wc[0][e] = wc[1][e] = wc[2][e] = wc[3][e] = 0;
+    /* the expert ranges: thread i scans experts 4 i .. 4 i + 3 (E <= 1024) */
+    {
+        int t4[4], run = 0, nz = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = 4 * tid + u;
+            t4[u] = e < E ? tot[e] : 0;
+            run += t4[u];
+            nz += t4[u] > 0;
+        }
+        int v[2] = {run, nz}, all[2];
+        k3d_block_exscan_n<2, 4>(v, all, red);
+        int s0 = v[0], a0 = v[1];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = 4 * tid + u;
+            if (e < E) {
+                first[e] = s0;
+                if (c == 0) {
+                    off[e] = s0;
+                    if (t4[u] > 0) act[a0] = e;
+                }
+            }
+            s0 += t4[u];
+            a0 += t4[u] > 0;
+        }
+        if (c == 0 && tid == 0) { off[E] = all[0]; *nact = all[1]; }
+    }
+    const int key = k3d_key(idx, c * K3G_DCH + tid, P, E, nullptr);
+    /* the lanes of this wave holding the same key: ballots over the key's bits (skipped
+     * slots, key -1, form their own group and are not placed) */
+    uint64_t peers = __ballot(key >= 0);
+    if (key < 0) peers = ~peers;
+    const int nb = 32 - __clz(E > 1 ? E - 1 : 1);
+    for (int b = 0; b < nb; ++b) {
+        const bool one = key >= 0 && ((key >> b) & 1);
+        const uint64_t m = __ballot(one);
+        peers &= one ? m : ~m;
+    }
+    const uint64_t lt = (1ull << lane) - 1;
+    const int r = __popcll(peers & lt);
     __syncthreads();
-    const int n = min(K3G_DCH, P - c * K3G_DCH);
-    for (int e = threadIdx.x; e < E; e += 256) {
-        int pos = base[(size_t)c * E + e];
-        for (int i = 0; i < n; ++i)
-            if (keys[i] == e) perm[pos++] = c * K3G_DCH + i;
+    if (key >= 0 && r == 0) wc[w][key] = __popcll(peers);
+    __syncthreads();
+    if (key >= 0) {
+        int before = r;
+        for (int q = 0; q < w; ++q) before += wc[q][key];
+        perm[first[key] + base[(size_t)c * E + key] + before] = c * K3G_DCH + tid;
     }
 }
 
@@ -193,10 +213,13 @@ extern "C" int k3k_dispatch_tiles(const int32_t *idx, int P, int E, int32_t *cnt
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     const int nch = (P + K3G_DCH - 1) / K3G_DCH;
+    /* the experts' totals follow the chunk bases (base holds (nch + 1) E entries) */
+    int32_t *tot = base + (size_t)nch * E;
     hipLaunchKernelGGL(k_disp_count, dim3(nch), dim3(256), 0, st, idx, P, E, cnt, err);
-    hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, st, cnt, nch, E, base, off, act,
-                       nact);
-    hipLaunchKernelGGL(k_disp_scatter, dim3(nch), dim3(256), 0, st, idx, P, E, base, perm);
+    hipLaunchKernelGGL(k_disp_scan, dim3((E + 63) / 64), dim3(64), 0, st, cnt, nch, E, base,
+                       tot);
+    hipLaunchKernelGGL(k_disp_scatter, dim3(nch), dim3(256), 0, st, idx, P, E, base, tot, off,
+                       act, nact, perm);
     if (hipGetLastError() != hipSuccess) return -1;
     return tiles ? k3k_gemm_tiles(off, E, tiles, ntiles, flag, st) : 0;
 }
