@@ -21,7 +21,7 @@ CSRC = os.path.join(ROOT, "kimi-k3-in-rust_amd", "csrc")
 HOST = os.path.join(ROOT, "tests", "host")
 
 CASES = [(E, k, ties) for E in (16, 384, 1024) for k in (1, 8, 64) for ties in (0, 1)] + [
-    (896, 16, 1)]
+    (896, 16, 1), (384, 16, 0), (1024, 16, 1), (16, 4, 0), (384, 9, 1)]
 
 
 @pytest.fixture(scope="module")
