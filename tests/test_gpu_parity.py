@@ -494,7 +494,8 @@ def _dispatch_expected(idx, E):
 
 
 @pytest.mark.parametrize("T,E,k", [(1, 384, 8), (20, 384, 8), (32, 384, 8), (33, 384, 8),
-                                   (300, 384, 8), (512, 384, 8), (4096, 384, 8), (50, 16, 4)])
+                                   (300, 384, 8), (512, 384, 8), (4096, 384, 8), (50, 16, 4),
+                                   (600, 896, 16), (1537, 1024, 4), (4100, 64, 2)])
 def test_dispatch_is_a_stable_sort(gpu, T, E, k):
     P = T * k
     path = "one block" if P <= 256 else "one 1024-thread block" if P <= 4096 else "three passes"
@@ -513,12 +514,13 @@ def test_dispatch_is_a_stable_sort(gpu, T, E, k):
     ctx.destroy()
 
 
-def test_dispatch_all_dropped(gpu):
-    say("case: k3g_dispatch, every slot dropped (idx -1)")
-    ctx = k3moe.Ctx(_shape_only_layer(128, 64, 4, 128), max_tokens=8)
-    didx = k3moe.DevBuf.from_array(np.full((8, 4), -1, np.int32))
-    dperm, doff = k3moe.DevBuf(32 * 4), k3moe.DevBuf(65 * 4)
-    ctx.dispatch(didx.ptr, 8, 4, 64, dperm.ptr, doff.ptr)
+@pytest.mark.parametrize("T", [8, 2000])
+def test_dispatch_all_dropped(gpu, T):
+    say(f"case: k3g_dispatch, every slot of {T} tokens dropped (idx -1)")
+    ctx = k3moe.Ctx(_shape_only_layer(128, 64, 4, 128), max_tokens=T)
+    didx = k3moe.DevBuf.from_array(np.full((T, 4), -1, np.int32))
+    dperm, doff = k3moe.DevBuf(T * 4 * 4), k3moe.DevBuf(65 * 4)
+    ctx.dispatch(didx.ptr, T, 4, 64, dperm.ptr, doff.ptr)
     ctx.sync()
     assert not np.any(doff.download(np.int32, 65))
     ctx.destroy()
