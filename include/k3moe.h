@@ -266,9 +266,14 @@ int  k3g_ctx_create(K3gCtx **ctx, int device, const K3gLayer *shape, int max_tok
 void k3g_ctx_destroy(K3gCtx *ctx);
 void *k3g_ctx_stream(K3gCtx *ctx);   /* the context's compute stream (hipStream_t) */
 
-/* Routing statistics since the context was created: [0] tokens whose certificate
- * failed and were re-routed in the engine's serial order, [1] selected experts of
- * certified tokens whose score the bound left unsettled and was recomputed exactly. */
+/* Routing statistics since the context was created. Calls of up to 511 tokens (fp64
+ * logits and a certified selection): [0] tokens whose certificate failed and were
+ * re-routed in the engine's serial order, [1] selected experts of certified tokens whose
+ * score the bound left unsettled and was recomputed exactly. Calls of 512 tokens or more
+ * (bounded bf16 logits, then fp64 logits for the candidates only): [0] tokens with more
+ * candidates than k, [1] candidate logits the any-order bound left open (settled by the
+ * partial-sum bound or the serial chain), [2] candidates whose fp64 logit fell outside
+ * its bounded interval (a live check of the bound; never expected). */
 void k3g_ctx_stats(K3gCtx *ctx, int64_t *out, int n);
 
 /* Per-stage timing with HIP events on the call's stream (off by default; turning it on

@@ -155,6 +155,8 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t o_zflag = carve(&at, 4);
     const size_t o_rtpart = carve(&at, k3k_router_part_bytes());
     const size_t o_rtctr = carve(&at, 512 * 128);
+    const size_t rbf = k3k_router_bf3_floats((int)T, (int)E);
+    const size_t o_rbpart = carve(&at, rbf ? rbf * 4 : 16);
     const size_t o_tiles = carve(&at, maxt * 16), o_ntiles = carve(&at, 4);
     const size_t o_xflag = carve(&at, 4);
     const size_t d512 = (d + 511) / 512 * 512, I512 = (I + 511) / 512 * 512;
@@ -209,6 +211,8 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->kpart2 = (float *)(b + o_kpart2);
     c->rtpart = (double *)(b + o_rtpart);
     c->rtctr = (int32_t *)(b + o_rtctr);
+    c->rbpart = rbf ? (float *)(b + o_rbpart) : NULL;
+    c->rbpart_floats = rbf;
     c->tiles = (int32_t *)(b + o_tiles);
     c->ntiles = (int32_t *)(b + o_ntiles);
     c->xflag = (int32_t *)(b + o_xflag);
@@ -650,7 +654,8 @@ int k3g_route(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx,
     k3g_stage_begin(c, K3G_ST_ROUTER, st);
     const int rc = k3k_router(x, T, L->gate, L->bias, L->hidden, L->n_experts, L->topk,
                               L->renorm, L->routed_scale, c->rs, idx, wt, c->force_exact,
-                              c->stats, c->rtpart, c->rtctr, st);
+                              c->stats, c->rtpart, c->rtctr, c->rbpart, c->rbpart_floats,
+                              st);
     k3g_stage_end(c, K3G_ST_ROUTER, st);
     return rc;
 }

@@ -66,6 +66,8 @@ struct K3gCtx {
     float *kpart2;               /* the shared expert's, when it runs on the side stream */
     double *rtpart;              /* K-slice sums of the router's matrix-core logits */
     int32_t *rtctr;              /* their per-tile arrival counts (zero between calls) */
+    float *rbpart;               /* the bounded bf16 logits' K-slice sums and norms */
+    size_t rbpart_floats;
     int32_t *tiles, *ntiles, *xflag;
     int max_tiles;
     hipEvent_t routed_wait;      /* the next k3g_experts waits for it before routed work */

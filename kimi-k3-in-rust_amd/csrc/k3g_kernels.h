@@ -172,10 +172,13 @@ int k3k_tile_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols, hipStr
 /* rs: [T][E] float4 {choice, lo, hi, score} workspace */
 int k3k_router(const float *x, int T, const float *W, const float *bias, int d, int E,
                int k, int renorm, float routed_scale, float *rs, int32_t *idx, float *wt,
-               int force, int *stats, double *part, int32_t *ctr, hipStream_t st);
+               int force, int *stats, double *part, int32_t *ctr, float *bpart,
+               size_t bpart_floats, hipStream_t st);
 /* bytes of the part buffer k3k_router's sliced logits use (ctr: 512 zeroed 128-byte
  * lines, 16384 ints) */
 size_t k3k_router_part_bytes(void);
+/* floats of the bpart buffer the bounded bf16 logits of T tokens use (0: not taken) */
+size_t k3k_router_bf3_floats(int T, int E);
 
 /* Stable counting sort of the T*k (token, slot) pairs by expert. cnt is [ceil(P/256)][E]
  * ints of workspace, base [ceil(P/256) + 1][E] (the experts' totals in its last row). */

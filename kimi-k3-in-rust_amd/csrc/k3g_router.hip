@@ -254,6 +254,490 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
     }
 }
 
+/* ------------------------------ many tokens: bounded logits on the bf16 matrix cores ---- */
+/* From a few hundred tokens on, the fp64 logits of every (token, expert) pair cost more
+ * than the routing needs: only the k selected scores must be the engine's exactly, and
+ * which experts those are is decided by a handful per token. So the logits are first
+ * formed on the bf16 matrix cores with a rigorous error bound (k_router_bf3), and only the
+ * experts whose bounded choice score can reach the token's top-k get their fp64 logit
+ * (k_router_pick).
+ *
+ * With w = w0 + w1 + ew and x = x0 + x1 + ex split into bf16 pieces, each rounded to
+ * nearest even (|w1| <= 2^-8 |w|, |ew| <= 2^-16 |w|, likewise for x), the three products
+ * w0 x0 + w0 x1 + w1 x0 differ from w x by at most 3.02 2^-16 |w x|, and each is exact in
+ * fp32. v_mfma_f32_16x16x32_bf16 sums them into fp32 accumulators that restart every 128
+ * columns (384 terms per chunk); the chunk sums are added in fp32, within a K slice and
+ * then over the slices in slice order. With each addition within 2^-23 of its result (an
+ * accumulator that aligns and truncates its products stays within that per product), the
+ * total errs by at most 1.02 (384 + d/128) 2^-23 sum |w x|. The bound used is twice the sum
+ * of both terms, on ||w|| ||x|| >= sum |w x| (norms from fp32 sums of squares, widened by
+ * 2^-10); it also covers the engine's own double rounding (< 2^-40 relative). */
+#define RB_TILE 128                 /* experts x tokens per workgroup tile */
+#define RB_OPB 16384                /* one operand's two pieces, 128 rows x 64 B each */
+#define RB_MIN_T 512                /* from this many tokens on */
+#define RP_RB 8                     /* candidate rows per pass of the exact logits */
+
+typedef __bf16 k3v2bfr __attribute__((ext_vector_type(2)));
+typedef __bf16 k3v8bfr __attribute__((ext_vector_type(8)));
+typedef float k3v4fr __attribute__((ext_vector_type(4)));
+
+static double rb_bound(int d)
+{
+    return 2.0 * (3.02 * 0x1p-16 + 1.02 * (400.0 + d / 128) * 0x1p-23);
+}
+
+/* 8 fp32 values -> their two bf16 pieces, 16 bytes each */
+__device__ __forceinline__ void rb_pieces(float4 a, float4 b, uint4 &p0, uint4 &p1)
+{
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const k3v2f f = {v[2 * i], v[2 * i + 1]};
+        const k3v2bfr hb = __builtin_convertvector(f, k3v2bfr);
+        const k3v2f r = f - __builtin_convertvector(hb, k3v2f);      /* exact */
+        const k3v2bfr lb = __builtin_convertvector(r, k3v2bfr);
+        h[i] = __builtin_bit_cast(uint32_t, hb);
+        l[i] = __builtin_bit_cast(uint32_t, lb);
+    }
+    p0 = make_uint4(h[0], h[1], h[2], h[3]);
+    p1 = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
+__device__ __forceinline__ float rb_sq(float4 a, float4 b, float s)
+{
+    s = fmaf(a.x, a.x, s); s = fmaf(a.y, a.y, s); s = fmaf(a.z, a.z, s); s = fmaf(a.w, a.w, s);
+    s = fmaf(b.x, b.x, s); s = fmaf(b.y, b.y, s); s = fmaf(b.z, b.z, s); s = fmaf(b.w, b.w, s);
+    return s;
+}
+
+__device__ __forceinline__ k3v4fr rb_mma(uint4 a, uint4 b, k3v4fr c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(k3v8bfr, a),
+                                                   __builtin_bit_cast(k3v8bfr, b), c, 0, 0, 0);
+}
+
+/* One workgroup = a 128-expert x 128-token tile over one K slice of whole 128-column
+ * chunks; wave w takes experts 64 (w >> 1) .. + 63 and tokens 64 (w & 1) .. + 63 as 4 x 4
+ * blocks of 16 x 16. Per 32-column step the workgroup converts its W and x rows to bf16
+ * pieces in registers and stores them in LDS (two stages; each row's four 16-byte column
+ * groups XOR-swizzled by (row >> 2) & 3, so that the operand reads of 16 consecutive rows
+ * hit 64 distinct banks); the next step's rows are loaded before the current step's matrix
+ * work. Partial sums go to part[s][t][e]; the workgroups of expert tile 0 also sum x's
+ * squares (xn2[s][t]) and those of token tile 0 W's (wn2[s][e]). Workgroups of one token
+ * tile and slice are consecutive on one XCD, sharing its x rows in that L2. */
+__global__ void __launch_bounds__(256, 2)
+k_router_bf3(const float *__restrict__ x, int T, const float *__restrict__ W, int d, int E,
+             int S, float *__restrict__ part, float *__restrict__ xn2, float *__restrict__ wn2)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * RB_OPB];
+    const int nte = (E + RB_TILE - 1) / RB_TILE, ntt = (T + RB_TILE - 1) / RB_TILE;
+    const int N = nte * ntt * S, per = (N + 7) >> 3;
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    const int lam = xcd * per + slot;
+    if (slot >= per || lam >= N) return;
+    const int et = lam % nte, rest = lam / nte, s = rest % S, tt = rest / S;
+    const int e0 = RB_TILE * et, t0 = RB_TILE * tt;
+    const int nch = d / 128, cps = (nch + S - 1) / S;
+    const int cb = min(nch, s * cps), ce = min(nch, cb + cps);
+    const int nst = 4 * (ce - cb);
+    const int tid = threadIdx.x, w = tid >> 6, L = tid & 63;
+
+    /* staging units tid and tid + 256: row u >> 2, columns 8 (u & 3) .. + 7 of the step */
+    const int r0 = tid >> 2, r1 = r0 + 64, cc = tid & 3;
+    const bool we0 = e0 + r0 < E, we1 = e0 + r1 < E, xe0 = t0 + r0 < T, xe1 = t0 + r1 < T;
+    const size_t kb = (size_t)cb * 128 + 8 * cc;
+    const float *wp0 = W + (size_t)min(e0 + r0, E - 1) * d + kb;
+    const float *wp1 = W + (size_t)min(e0 + r1, E - 1) * d + kb;
+    const float *xp0 = x + (size_t)min(t0 + r0, T - 1) * d + kb;
+    const float *xp1 = x + (size_t)min(t0 + r1, T - 1) * d + kb;
+    const uint32_t so0 = r0 * 64 + 16 * (cc ^ ((r0 >> 2) & 3));
+    const uint32_t so1 = r1 * 64 + 16 * (cc ^ ((r1 >> 2) & 3));
+    const bool do_x = et == 0, do_w = tt == 0;
+    float xs0 = 0.0f, xs1 = 0.0f, ws0 = 0.0f, ws1 = 0.0f;
+
+    float4 g[8];
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    /* rows past E or T load a valid row (the pointers are clamped) and are zeroed after */
+    auto gload = [&](int st) {
+        const int k = 32 * st;
+        g[0] = *(const float4 *)(wp0 + k);
+        g[1] = *(const float4 *)(wp0 + k + 4);
+        g[2] = *(const float4 *)(wp1 + k);
+        g[3] = *(const float4 *)(wp1 + k + 4);
+        g[4] = *(const float4 *)(xp0 + k);
+        g[5] = *(const float4 *)(xp0 + k + 4);
+        g[6] = *(const float4 *)(xp1 + k);
+        g[7] = *(const float4 *)(xp1 + k + 4);
+    };
+    auto stage = [&](int buf) {
+        uint8_t *b = lds + buf * 2 * RB_OPB;
+        if (!we0) { g[0] = z4; g[1] = z4; }
+        if (!we1) { g[2] = z4; g[3] = z4; }
+        if (!xe0) { g[4] = z4; g[5] = z4; }
+        if (!xe1) { g[6] = z4; g[7] = z4; }
+        uint4 p0, p1;
+        rb_pieces(g[0], g[1], p0, p1);
+        *(uint4 *)(b + so0) = p0;
+        *(uint4 *)(b + 8192 + so0) = p1;
+        rb_pieces(g[2], g[3], p0, p1);
+        *(uint4 *)(b + so1) = p0;
+        *(uint4 *)(b + 8192 + so1) = p1;
+        rb_pieces(g[4], g[5], p0, p1);
+        *(uint4 *)(b + RB_OPB + so0) = p0;
+        *(uint4 *)(b + RB_OPB + 8192 + so0) = p1;
+        rb_pieces(g[6], g[7], p0, p1);
+        *(uint4 *)(b + RB_OPB + so1) = p0;
+        *(uint4 *)(b + RB_OPB + 8192 + so1) = p1;
+        if (do_w) { ws0 = rb_sq(g[0], g[1], ws0); ws1 = rb_sq(g[2], g[3], ws1); }
+        if (do_x) { xs0 = rb_sq(g[4], g[5], xs0); xs1 = rb_sq(g[6], g[7], xs1); }
+    };
+
+    const int wr = w >> 1, wc = w & 1, rr = L & 15, cq = L >> 4;
+    const uint32_t sw = 16 * (cq ^ ((rr >> 2) & 3));
+    const uint32_t ao = (64 * wr + rr) * 64 + sw, bo = RB_OPB + (64 * wc + rr) * 64 + sw;
+    k3v4fr acc[4][4], tot[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tot[i][j] = k3v4fr{0.0f, 0.0f, 0.0f, 0.0f};
+
+    if (nst > 0) {
+        gload(0);
+        stage(0);
+        if (nst > 1) gload(1);
+        __syncthreads();
+    }
+    for (int st0 = 0; st0 < nst; st0 += 4) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int st = st0 + q;
+            /* the next step's rows into the other stage (free since the last barrier), the
+             * one after into registers, then this step's matrix work */
+            if (st + 1 < nst) stage((st + 1) & 1);
+            if (st + 2 < nst) gload(st + 2);
+            const uint8_t *b = lds + (st & 1) * 2 * RB_OPB;
+            uint4 b0[4], b1[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                b0[j] = *(const uint4 *)(b + bo + j * 1024);
+                b1[j] = *(const uint4 *)(b + bo + 8192 + j * 1024);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 a0 = *(const uint4 *)(b + ao + i * 1024);
+                const uint4 a1 = *(const uint4 *)(b + ao + 8192 + i * 1024);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    k3v4fr c = q == 0 ? k3v4fr{0.0f, 0.0f, 0.0f, 0.0f} : acc[i][j];
+                    c = rb_mma(a0, b0[j], c);
+                    c = rb_mma(a0, b1[j], c);
+                    acc[i][j] = rb_mma(a1, b0[j], c);
+                }
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) tot[i][j] += acc[i][j];
+    }
+
+    /* lane L of block (i, j): experts 4 (L >> 4) + 0..3, token L & 15 */
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int t = t0 + 64 * wc + 16 * j + rr;
+        if (t < T) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = e0 + 64 * wr + 16 * i + 4 * cq;
+                if (e < E) *(k3v4fr *)(part + ((size_t)s * T + t) * E + e) = tot[i][j];
+            }
+        }
+    }
+    if (do_x || do_w) {
+        /* the four units of a row are lanes 4m .. 4m + 3 */
+        xs0 += __shfl_xor(xs0, 1, K3G_WAVE); xs0 += __shfl_xor(xs0, 2, K3G_WAVE);
+        xs1 += __shfl_xor(xs1, 1, K3G_WAVE); xs1 += __shfl_xor(xs1, 2, K3G_WAVE);
+        ws0 += __shfl_xor(ws0, 1, K3G_WAVE); ws0 += __shfl_xor(ws0, 2, K3G_WAVE);
+        ws1 += __shfl_xor(ws1, 1, K3G_WAVE); ws1 += __shfl_xor(ws1, 2, K3G_WAVE);
+        if (cc == 0) {
+            if (do_x && xe0) xn2[(size_t)s * T + t0 + r0] = xs0;
+            if (do_x && xe1) xn2[(size_t)s * T + t0 + r1] = xs1;
+            if (do_w && we0) wn2[(size_t)s * E + e0 + r0] = ws0;
+            if (do_w && we1) wn2[(size_t)s * E + e0 + r1] = ws1;
+        }
+    }
+}
+
+/* The K slices' sums of k_router_bf3 added in slice order into slice 0 (the logits four
+ * experts per thread, then the squared norms), so that the per-token pass reads one value
+ * per expert. */
+__global__ void __launch_bounds__(256)
+k_router_bf3_sum(float *__restrict__ part, int S, int T, int E, float *__restrict__ xn2,
+                 float *__restrict__ wn2)
+{
+    const size_t n4 = (size_t)T * E / 4, stride = (size_t)gridDim.x * 256;
+    const size_t TE = (size_t)T * E;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4 + T + E; i += stride) {
+        if (i < n4) {
+            k3v4fr a = *(const k3v4fr *)(part + 4 * i);
+            for (int s = 1; s < S; ++s) a += *(const k3v4fr *)(part + s * TE + 4 * i);
+            *(k3v4fr *)(part + 4 * i) = a;
+        } else if (i < n4 + T) {
+            const size_t t = i - n4;
+            float a = xn2[t];
+            for (int s = 1; s < S; ++s) a += xn2[(size_t)s * T + t];
+            xn2[t] = a;
+        } else {
+            const size_t e = i - n4 - T;
+            float a = wn2[e];
+            for (int s = 1; s < S; ++s) a += wn2[(size_t)s * E + e];
+            wn2[e] = a;
+        }
+    }
+}
+
+/* a candidate's float logit the any-order bound left open: the partial-sum bound, else the
+ * engine's serial chain (always the chain when force > 2). Inline, so that the kernel's
+ * register budget holds for it too (a call would size the kernel by its callee). */
+__device__ __forceinline__ float rp_open_logit(const float *row, const float *xt, int d,
+                                               int lane, int force)
+{
+    float g;
+    if (force <= 2 && k3d_row_logit(row, xt, d, lane, &g)) return g;
+    const float4 *w4 = (const float4 *)row, *x4 = (const float4 *)xt;
+    double acc = 0.0;
+#pragma unroll 8
+    for (int q = 0; q < d / 4; ++q) {
+        const float4 wv = w4[q], xv = x4[q];
+        acc = fma((double)wv.x, (double)xv.x, acc);
+        acc = fma((double)wv.y, (double)xv.y, acc);
+        acc = fma((double)wv.z, (double)xv.z, acc);
+        acc = fma((double)wv.w, (double)xv.w, acc);
+    }
+    return (float)acc;
+}
+
+/* One wave per token after k_router_bf3: the score intervals from the bounded logits, the
+ * top-k on their best guesses, the candidates (every expert whose interval reaches the
+ * weakest selected lower end: the engine's top-k lies among them; all experts when the
+ * guesses cannot select k or are not numbers), their fp64 logits (the engine's float
+ * logit settled by the any-order bound, else by the partial-sum bound, else the serial
+ * chain), and the engine's selection among the candidates with its weights. Candidate
+ * rows stream straight from memory, RP_RB rows per pass beside one pass over x.
+ * stats: [0] tokens with more candidates than k, [1] candidate logits the any-order bound
+ * left open, [2] candidates whose fp64 logit fell outside its bounded interval (never
+ * expected: a check of the bound on live data). */
+template <int NPL>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
+              const float *__restrict__ wn2, const float *__restrict__ bias,
+              const float *__restrict__ W, const float *__restrict__ x, int d, int E, int k,
+              int renorm, float routed_scale, int32_t *__restrict__ idx,
+              float *__restrict__ wt, int force, int *__restrict__ stats, double nround)
+{
+    __shared__ int cand[K3G_MAX_E];
+    __shared__ float cch[K3G_MAX_E], csc[K3G_MAX_E];
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const double xn = sqrt((double)xn2[t]) * (1.0 + 0x1p-10);
+    /* the approximate logit and its norm product */
+    auto approx = [&](int e, float &a, double &ab) {
+        a = part[(size_t)t * E + e];
+        ab = sqrt((double)wn2[e]) * (1.0 + 0x1p-10) * xn;
+    };
+    /* every load issued before any is used */
+    float av[NPL], wv[NPL], bv[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int e = min(lane + 64 * i, E - 1);
+        av[i] = part[(size_t)t * E + e];
+        wv[i] = wn2[e];
+        bv[i] = bias ? bias[e] : 0.0f;
+    }
+    float4 v[NPL];
+    uint64_t key[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int e = lane + 64 * i;
+        v[i] = make_float4(-INFINITY, -INFINITY, -INFINITY, 0.0f);
+        key[i] = 0;
+        if (e < E) {
+            const double ab = sqrt((double)wv[i]) * (1.0 + 0x1p-10) * xn;
+            v[i] = k3d_route_score_n((double)av[i], ab, bv[i], nround);
+            if (v[i].x > -INFINITY)
+                key[i] = ((uint64_t)k3d_ordered(v[i].x) << 32) | (uint32_t)~e;
+        }
+    }
+    /* top-k on the guesses: theta = the weakest selected lower end */
+    uint32_t taken = 0;
+    bool valid = true;
+    float theta = INFINITY;
+    for (int j = 0; j < k; ++j) {
+        uint64_t m[NPL];
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) m[i] = key[i];
+#pragma unroll
+        for (int h = NPL / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int i = 0; i < h; ++i) m[i] = m[i + h] > m[i] ? m[i + h] : m[i];
+        const uint64_t win = k3d_wave_max_u64(m[0]);
+        if (!win) { valid = false; break; }
+        const int w = (int)~(uint32_t)win, slot = w >> 6, wl = w & 63;
+        float lo = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i)
+            if (i == slot) {
+                lo = v[i].y;
+                if (lane == wl) { key[i] = 0; taken |= 1u << i; }
+            }
+        const float wlo = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(lo), wl));
+        if (__builtin_isnan(wlo)) valid = false;
+        theta = fminf(theta, wlo);
+    }
+    if (!valid || force >= 2) theta = -INFINITY;
+    /* candidates in expert order (a NaN upper end is a candidate) */
+    int nc = 0;
+    const uint64_t lt = (1ull << lane) - 1;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int e = lane + 64 * i;
+        const bool cf = e < E && (((taken >> i) & 1u) || !(v[i].z < theta));
+        const uint64_t cm = __ballot(cf);
+        if (cf) cand[nc + __popcll(cm & lt)] = e;
+        nc += __popcll(cm);
+    }
+    __syncthreads();
+
+    /* the candidates' float logits */
+    const float *xt = x + (size_t)t * d;
+    int nopen = 0, nviol = 0;
+    for (int c0 = 0; c0 < nc; c0 += RP_RB) {
+        const int nb = min(RP_RB, nc - c0);
+        const float *rows[RP_RB];
+#pragma unroll
+        for (int j = 0; j < RP_RB; ++j)
+            rows[j] = W + (size_t)__builtin_amdgcn_readfirstlane(cand[c0 + min(j, nb - 1)]) * d;
+        double acc[2 * RP_RB];
+#pragma unroll
+        for (int j = 0; j < 2 * RP_RB; ++j) acc[j] = 0.0;
+        /* every row loads (rows past nb repeat a candidate's) and the next 256 columns are
+         * in flight while these are summed; rows past nb are not summed */
+        const float4 *x4 = (const float4 *)xt;
+        const int nq = d / 256;
+        float4 xa = x4[lane], wa[RP_RB];
+#pragma unroll
+        for (int j = 0; j < RP_RB; ++j) wa[j] = ((const float4 *)rows[j])[lane];
+        for (int q = 0; q < nq; ++q) {
+            const int qn = (q + 1 < nq ? q + 1 : q) * 64 + lane;
+            const float4 xb = x4[qn];
+            float4 wb[RP_RB];
+#pragma unroll
+            for (int j = 0; j < RP_RB; ++j) wb[j] = ((const float4 *)rows[j])[qn];
+            const double x0 = xa.x, x1 = xa.y, x2 = xa.z, x3 = xa.w;
+#pragma unroll
+            for (int j = 0; j < RP_RB; ++j) {
+                if (j < nb) {
+                    const double w0 = wa[j].x, w1 = wa[j].y, w2 = wa[j].z, w3 = wa[j].w;
+                    double s = acc[2 * j], a = acc[2 * j + 1];
+                    s = fma(w0, x0, s); s = fma(w1, x1, s); s = fma(w2, x2, s); s = fma(w3, x3, s);
+                    a = fma(fabs(w0), fabs(x0), a); a = fma(fabs(w1), fabs(x1), a);
+                    a = fma(fabs(w2), fabs(x2), a); a = fma(fabs(w3), fabs(x3), a);
+                    acc[2 * j] = s;
+                    acc[2 * j + 1] = a;
+                }
+            }
+            xa = xb;
+#pragma unroll
+            for (int j = 0; j < RP_RB; ++j) wa[j] = wb[j];
+        }
+        /* lane l then holds value l >> 2: row j's sum at lane 8 j, its magnitude at 8 j + 4 */
+        k3d_transpose_reduce<2 * RP_RB>(acc, lane);
+        const double sj = __shfl(acc[0], (8 * lane) & 63, K3G_WAVE);
+        const double aj = __shfl(acc[0], (8 * lane + 4) & 63, K3G_WAVE);
+        float f = 0.0f;
+        bool ok = false;
+        if (lane < nb) ok = force <= 2 && k3d_settled_float(sj, aj, d, &f);
+        const uint64_t um = __ballot(lane < nb && !ok);
+        nopen += __popcll(um);
+        for (uint64_t m = um; m; m &= m - 1) {
+            const int j = __builtin_ctzll(m);
+            const float *row = W + (size_t)__builtin_amdgcn_readfirstlane(cand[c0 + j]) * d;
+            const float g = rp_open_logit(row, xt, d, lane, force);
+            if (lane == j) f = g;
+        }
+        bool viol = false;
+        if (lane < nb) {
+            const int e = cand[c0 + lane];
+            const float sc = k3d_sigmoid(f);
+            csc[c0 + lane] = sc;
+            cch[c0 + lane] = __fadd_rn(sc, bias ? bias[e] : 0.0f);
+            float a;
+            double ab;
+            approx(e, a, ab);
+            const double B = nround * 0x1p-53 * 1.01 * ab + fabs((double)a) * 0x1p-51;
+            const double df = fabs((double)f - (double)a);
+            viol = __builtin_isfinite(f) && __builtin_isfinite(a) && __builtin_isfinite(B) &&
+                   df > B + fabs((double)f) * 0x1p-23;
+        }
+        nviol += __popcll(__ballot(viol));
+    }
+    __syncthreads();
+
+    /* the engine's selection among the candidates: larger choice, then lower index (the
+     * candidates are in expert order, so the lower candidate slot); NaN and -inf never win */
+    const int nsl = (nc + 63) >> 6;
+    uint32_t tk = 0;
+    int my_sel = -1;
+    float my_score = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        uint64_t best = 0;
+        for (int q = 0; q < nsl; ++q) {
+            const int c = lane + 64 * q;
+            if (c < nc && !((tk >> q) & 1u)) {
+                const float ch = cch[c];
+                if (ch > -INFINITY) {
+                    const uint64_t kk = ((uint64_t)k3d_ordered(ch) << 32) | (uint32_t)~c;
+                    best = kk > best ? kk : best;
+                }
+            }
+        }
+        const uint64_t win = k3d_wave_max_u64(best);
+        int sel = -1;
+        float sc = 0.0f;
+        if (win) {
+            const int c = (int)~(uint32_t)win;
+            sel = cand[c];
+            sc = csc[c];
+            if (lane == (c & 63)) tk |= 1u << (c >> 6);
+        }
+        if (lane == j) { my_sel = sel; my_score = sc; }
+    }
+    /* weights from the unbiased scores, renormalised by the engine's sequential double sum
+     * in selection order, then scaled */
+    double wsum = 0.0;
+    for (int j = 0; j < k; ++j)
+        wsum += (double)__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_score), j));
+    if (lane < k) {
+        float wgt = my_score;
+        if (renorm && k > 1) wgt = __fmul_rn(wgt, (float)(1.0 / (wsum + 1e-20)));
+        idx[(size_t)t * k + lane] = my_sel >= 0 ? my_sel : 0;
+        wt[(size_t)t * k + lane] = __fmul_rn(wgt, routed_scale);
+    }
+    if (stats && lane == 0) {
+        if (nc > k) atomicAdd(&stats[0], 1);
+        if (nopen) atomicAdd(&stats[1], nopen);
+        if (nviol) atomicAdd(&stats[2], nviol);
+    }
+}
+
+/* floats of workspace the bounded-logit path needs for T tokens (0 below its range) */
+extern "C" size_t k3k_router_bf3_floats(int T, int E)
+{
+    if (T < RB_MIN_T) return 0;
+    return 8 * ((size_t)T * E + T + E);
+}
+
 /* ------------------------------------------------------------------ select ---- */
 /* One wave per token; a token whose certificate fails computes its candidates' exact
  * logits from rows staged through LDS. */
@@ -286,12 +770,50 @@ static int router_slices(int N)
 extern "C" int k3k_router(const float *x, int T, const float *W, const float *bias, int d,
                           int E, int k, int renorm, float routed_scale, float *rs,
                           int32_t *idx, float *wt, int force, int *stats, double *part,
-                          int32_t *ctr, hipStream_t st)
+                          int32_t *ctr, float *bpart, size_t bpart_floats, hipStream_t st)
 {
     if (E > K3G_MAX_E || k > K3G_MAX_TOPK || k < 1 || T < 1 || d < 1) return -1;
-    /* the score intervals of token t live at [t][E] */
     /* float4 loads need 16-byte aligned rows; anything else takes the scalar loop */
     const int vec = ((((uintptr_t)x | (uintptr_t)W) & 15) == 0) && ((d & 3) == 0);
+    if (bpart && T >= RB_MIN_T && vec && E % 16 == 0 && d % 256 == 0) {
+        /* bounded bf16 logits, then the candidates' fp64 logits: about two workgroups per
+         * CU of K slices, whole 128-column chunks each, no empty slice */
+        const int nmn = ((E + RB_TILE - 1) / RB_TILE) * ((T + RB_TILE - 1) / RB_TILE);
+        const int nch = d / 128;
+        const size_t per_s = (size_t)T * E + T + E;
+        int S = 512 / nmn;
+        if ((size_t)S * per_s > bpart_floats) S = (int)(bpart_floats / per_s);
+        if (S > nch) S = nch;
+        if (S >= 1) {
+            const int cps = (nch + S - 1) / S;
+            S = (nch + cps - 1) / cps;
+            float *xn2 = bpart + (size_t)S * T * E, *wn2 = xn2 + (size_t)S * T;
+            const long long N = (long long)nmn * S;
+            hipLaunchKernelGGL(k_router_bf3, dim3((unsigned)(8 * ((N + 7) / 8))), dim3(256), 0,
+                               st, x, T, W, d, E, S, bpart, xn2, wn2);
+            if (S > 1) {
+                const size_t n = (size_t)T * E / 4 + T + E;
+                const unsigned g = (unsigned)((n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048);
+                hipLaunchKernelGGL(k_router_bf3_sum, dim3(g), dim3(256), 0, st, bpart, S, T, E,
+                                   xn2, wn2);
+            }
+            const double nround = rb_bound(d) / (1.01 * 0x1p-53);
+            if (E <= 256)
+                hipLaunchKernelGGL(k_router_pick<4>, dim3(T), dim3(64), 0, st, bpart, xn2,
+                                   wn2, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
+                                   force, stats, nround);
+            else if (E <= 512)
+                hipLaunchKernelGGL(k_router_pick<8>, dim3(T), dim3(64), 0, st, bpart, xn2,
+                                   wn2, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
+                                   force, stats, nround);
+            else
+                hipLaunchKernelGGL(k_router_pick<16>, dim3(T), dim3(64), 0, st, bpart, xn2,
+                                   wn2, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
+                                   force, stats, nround);
+            return hipGetLastError() == hipSuccess ? 0 : -1;
+        }
+    }
+    /* the score intervals of token t live at [t][E] */
     const long long N1 = (long long)(E / 16) * ((T + 31) / 32);
     const bool mfma_ok = T >= 16 && vec && E >= 16 && E % 16 == 0 && d % 64 == 0;
     int S = (mfma_ok && part && ctr && N1 < 512) ? router_slices((int)N1) : 1;

@@ -260,6 +260,77 @@ def test_router_k3_shape(gpu, T, force):
     ctx.destroy()
 
 
+@pytest.mark.parametrize("T,force", [(1200, 0), (512, 2)])
+def test_router_bounded_logits_k2(k2_layer, T, force):
+    """From 512 tokens the logits are formed on the bf16 matrix cores with a rigorous bound
+    and only the experts whose bounded score can reach a token's top-k get an fp64 logit
+    (force 2: every expert, so the bound is checked on every (token, expert) pair). The
+    selection and weights are the engine's bit for bit on sampled tokens, and no fp64 logit
+    lies outside its bounded interval (stats[2])."""
+    say(f"case: k3g_router bounded bf16 logits d=7168 E=384 k=8, {T} tokens, force_exact={force}")
+    layer = k2_layer
+    x = layer.tokens(T, stream_base=900)
+    ctx = k3moe.Ctx(layer.dev, max_tokens=T)
+    ctx.force_exact(force)
+    dx = k3moe.DevBuf.from_array(x)
+    didx, dwt = k3moe.DevBuf(T * 8 * 4), k3moe.DevBuf(T * 8 * 4)
+    ctx.router(layer.dev, dx.ptr, T, didx.ptr, dwt.ptr)
+    ctx.sync()
+    extra, opened, viol = ctx.stats()[:3]
+    say(f"  tokens with extra candidates {extra}, open logits {opened}, bound violations {viol}")
+    assert viol == 0
+    if force:
+        assert extra == T
+    else:
+        assert extra < T // 2
+    idx = didx.download(np.int32, T * 8).reshape(T, 8)
+    wt = dwt.download(np.float32, T * 8).reshape(T, 8)
+    rng = np.random.default_rng(T + force)
+    for t in np.unique(np.concatenate([[0, T - 1], rng.choice(T, 24, replace=False)])):
+        oi, ow = O.oracle().router(x[t], layer.gate, layer.bias, 384, 8, 1, 2.5)
+        assert np.array_equal(idx[t], oi), (t, idx[t], oi)
+        assert np.array_equal(wt[t].view(np.uint32), ow.view(np.uint32)), t
+    ctx.destroy()
+
+
+@pytest.mark.parametrize("E,k", [(64, 4), (16, 4), (144, 9)])
+def test_router_bounded_logits_ties(gpu, E, k):
+    """The bounded-logit path on exact ties and odd inputs, every token against the
+    engine: duplicated router rows with equal biases (tied choices, lowest index wins),
+    zero tokens (every logit 0), a token of tiny values and one of huge values, expert
+    counts below and not a multiple of the 128-expert tile, a ragged last token tile."""
+    d, T = 256, 520
+    say(f"case: k3g_router bounded bf16 logits with ties E={E} k={k} d={d}, {T} tokens")
+    W = np.ascontiguousarray(k3moe.host_normal(E * d, 13, 601, 0, 0.02).reshape(E, d))
+    bias = k3moe.host_normal(E, 13, 602, 0, 0.01)
+    for a, b in ((3, 10), (3, E - 6), (0, E - 1)):
+        W[b] = W[a]
+        bias[b] = bias[a]
+    x = np.ascontiguousarray(k3moe.host_normal(T * d, 13, 603, 0, 1.0).reshape(T, d))
+    x[5] = 0.0
+    x[100] = 0.0
+    x[200] *= np.float32(2.0 ** -60)
+    x[300] *= np.float32(2.0 ** 40)
+    x[301] = x[302]
+    L = k3moe.K3gLayer()
+    L.hidden, L.n_experts, L.topk, L.inter, L.latent = d, E, k, 128, d
+    L.renorm, L.routed_scale = 1, 2.5
+    dW, db, dx = (k3moe.DevBuf.from_array(a) for a in (W, bias, x))
+    L.gate, L.bias = dW.ptr, db.ptr
+    ctx = k3moe.Ctx(L, max_tokens=T)
+    didx, dwt = k3moe.DevBuf(T * k * 4), k3moe.DevBuf(T * k * 4)
+    ctx.router(L, dx.ptr, T, didx.ptr, dwt.ptr)
+    ctx.sync()
+    assert ctx.stats()[2] == 0
+    idx = didx.download(np.int32, T * k).reshape(T, k)
+    wt = dwt.download(np.float32, T * k).reshape(T, k)
+    for t in range(T):
+        oi, ow = O.oracle().router(x[t], W, bias, E, k, 1, 2.5)
+        assert np.array_equal(idx[t], oi), (t, idx[t], oi)
+        assert np.array_equal(wt[t].view(np.uint32), ow.view(np.uint32)), t
+    ctx.destroy()
+
+
 # ------------------------------------------------------------------- tiled layouts ----
 
 def _tile_mxfp4_host(packed, scales, rows, cols):
