@@ -519,6 +519,45 @@ __device__ __forceinline__ float rp_open_logit(const float *row, const float *xt
     return (float)acc;
 }
 
+/* 1 / (1 + e^-v) with the hardware exponential: within a few float ulps */
+__device__ __forceinline__ float rp_sig(float v) { return 1.0f / (1.0f + __expf(-v)); }
+
+/* Row j < NB's fp64 dot product with x (acc[2 j]) and the sum of its products' magnitudes
+ * (acc[2 j + 1]), this lane's share: columns 2 lane + 128 q, two per 128-column stage,
+ * with three stages in flight. d a multiple of 256, rows and x 8-byte aligned. */
+template <int NB>
+__device__ __forceinline__ void rp_dots(const float *const *rows, const float *xt, int d,
+                                        int lane, double *acc)
+{
+    const float2 *x2 = (const float2 *)xt;
+    const int nq = d / 128;
+    float2 xs[4], ws[4][NB];
+    auto ld = [&](int slot, int q) {
+        const int o = min(q, nq - 1) * 64 + lane;
+        xs[slot] = x2[o];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) ws[slot][j] = ((const float2 *)rows[j])[o];
+    };
+    ld(0, 0);
+    ld(1, 1);
+    ld(2, 2);
+    for (int q0 = 0; q0 < nq; q0 += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            ld((u + 3) & 3, q0 + u + 3);
+            if (q0 + u < nq) {
+                const double x0 = xs[u].x, x1 = xs[u].y;
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const double w0 = ws[u][j].x, w1 = ws[u][j].y;
+                    acc[2 * j] = fma(w1, x1, fma(w0, x0, acc[2 * j]));
+                    acc[2 * j + 1] = fma(fabs(w1), fabs(x1), fma(fabs(w0), fabs(x0), acc[2 * j + 1]));
+                }
+            }
+        }
+    }
+}
+
 /* One wave per token after k_router_bf3: the score intervals from the bounded logits, the
  * top-k on their best guesses, the candidates (every expert whose interval reaches the
  * weakest selected lower end: the engine's top-k lies among them; all experts when the
@@ -563,8 +602,18 @@ k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
         v[i] = make_float4(-INFINITY, -INFINITY, -INFINITY, 0.0f);
         key[i] = 0;
         if (e < E) {
-            const double ab = sqrt((double)wv[i]) * (1.0 + 0x1p-10) * xn;
-            v[i] = k3d_route_score_n((double)av[i], ab, bv[i], nround);
+            /* the engine's float logit lies in [fl(a - B), fl(a + B)] (rounding is
+             * monotone); the choice bounds follow in fast float arithmetic with 2^-16
+             * (1 + |bias|) of slack, which covers the fast exp, the engine's expf and the
+             * roundings of the sigmoid and the bias add. Only the candidate set depends on
+             * them. */
+            const double a = av[i];
+            const double B = nround * 0x1p-53 * 1.01 * (sqrt((double)wv[i]) * (1.0 + 0x1p-10) * xn) +
+                             fabs(a) * 0x1p-51 + 0x1p-1000;
+            const float slack = 0x1p-16f * (1.0f + fabsf(bv[i]));
+            v[i].x = rp_sig((float)a) + bv[i];
+            v[i].y = rp_sig((float)(a - B)) + bv[i] - slack;
+            v[i].z = rp_sig((float)(a + B)) + bv[i] + slack;
             if (v[i].x > -INFINITY)
                 key[i] = ((uint64_t)k3d_ordered(v[i].x) << 32) | (uint32_t)~e;
         }
@@ -621,35 +670,15 @@ k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
         double acc[2 * RP_RB];
 #pragma unroll
         for (int j = 0; j < 2 * RP_RB; ++j) acc[j] = 0.0;
-        /* every row loads (rows past nb repeat a candidate's) and the next 256 columns are
-         * in flight while these are summed; rows past nb are not summed */
-        const float4 *x4 = (const float4 *)xt;
-        const int nq = d / 256;
-        float4 xa = x4[lane], wa[RP_RB];
-#pragma unroll
-        for (int j = 0; j < RP_RB; ++j) wa[j] = ((const float4 *)rows[j])[lane];
-        for (int q = 0; q < nq; ++q) {
-            const int qn = (q + 1 < nq ? q + 1 : q) * 64 + lane;
-            const float4 xb = x4[qn];
-            float4 wb[RP_RB];
-#pragma unroll
-            for (int j = 0; j < RP_RB; ++j) wb[j] = ((const float4 *)rows[j])[qn];
-            const double x0 = xa.x, x1 = xa.y, x2 = xa.z, x3 = xa.w;
-#pragma unroll
-            for (int j = 0; j < RP_RB; ++j) {
-                if (j < nb) {
-                    const double w0 = wa[j].x, w1 = wa[j].y, w2 = wa[j].z, w3 = wa[j].w;
-                    double s = acc[2 * j], a = acc[2 * j + 1];
-                    s = fma(w0, x0, s); s = fma(w1, x1, s); s = fma(w2, x2, s); s = fma(w3, x3, s);
-                    a = fma(fabs(w0), fabs(x0), a); a = fma(fabs(w1), fabs(x1), a);
-                    a = fma(fabs(w2), fabs(x2), a); a = fma(fabs(w3), fabs(x3), a);
-                    acc[2 * j] = s;
-                    acc[2 * j + 1] = a;
-                }
-            }
-            xa = xb;
-#pragma unroll
-            for (int j = 0; j < RP_RB; ++j) wa[j] = wb[j];
+        switch (nb) {
+        case 1: rp_dots<1>(rows, xt, d, lane, acc); break;
+        case 2: rp_dots<2>(rows, xt, d, lane, acc); break;
+        case 3: rp_dots<3>(rows, xt, d, lane, acc); break;
+        case 4: rp_dots<4>(rows, xt, d, lane, acc); break;
+        case 5: rp_dots<5>(rows, xt, d, lane, acc); break;
+        case 6: rp_dots<6>(rows, xt, d, lane, acc); break;
+        case 7: rp_dots<7>(rows, xt, d, lane, acc); break;
+        default: rp_dots<8>(rows, xt, d, lane, acc); break;
         }
         /* lane l then holds value l >> 2: row j's sum at lane 8 j, its magnitude at 8 j + 4 */
         k3d_transpose_reduce<2 * RP_RB>(acc, lane);
