@@ -524,14 +524,14 @@ __device__ __forceinline__ float rp_sig(float v) { return 1.0f / (1.0f + __expf(
 
 /* Row j < NB's fp64 dot product with x (acc[2 j]) and the sum of its products' magnitudes
  * (acc[2 j + 1]), this lane's share: columns 2 lane + 128 q, two per 128-column stage,
- * with three stages in flight. d a multiple of 256, rows and x 8-byte aligned. */
+ * with two stages in flight. d a multiple of 256, rows and x 8-byte aligned. */
 template <int NB>
 __device__ __forceinline__ void rp_dots(const float *const *rows, const float *xt, int d,
                                         int lane, double *acc)
 {
     const float2 *x2 = (const float2 *)xt;
     const int nq = d / 128;
-    float2 xs[4], ws[4][NB];
+    float2 xs[3], ws[3][NB];
     auto ld = [&](int slot, int q) {
         const int o = min(q, nq - 1) * 64 + lane;
         xs[slot] = x2[o];
@@ -540,11 +540,10 @@ __device__ __forceinline__ void rp_dots(const float *const *rows, const float *x
     };
     ld(0, 0);
     ld(1, 1);
-    ld(2, 2);
-    for (int q0 = 0; q0 < nq; q0 += 4) {
+    for (int q0 = 0; q0 < nq; q0 += 3) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            ld((u + 3) & 3, q0 + u + 3);
+        for (int u = 0; u < 3; ++u) {
+            ld((u + 2) % 3, q0 + u + 2);
             if (q0 + u < nq) {
                 const double x0 = xs[u].x, x1 = xs[u].y;
 #pragma unroll
@@ -569,16 +568,21 @@ __device__ __forceinline__ void rp_dots(const float *const *rows, const float *x
  * left open, [2] candidates whose fp64 logit fell outside its bounded interval (never
  * expected: a check of the bound on live data). */
 template <int NPL>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
               const float *__restrict__ wn2, const float *__restrict__ bias,
-              const float *__restrict__ W, const float *__restrict__ x, int d, int E, int k,
+              const float *__restrict__ W, const float *__restrict__ x, int T, int d, int E, int k,
               int renorm, float routed_scale, int32_t *__restrict__ idx,
-              float *__restrict__ wt, int force, int *__restrict__ stats, double nround)
+              float *__restrict__ wt, int force, int *__restrict__ tstat, double nround)
 {
-    __shared__ int cand[K3G_MAX_E];
-    __shared__ float cch[K3G_MAX_E], csc[K3G_MAX_E];
-    const int t = blockIdx.x, lane = threadIdx.x;
+    /* four tokens per workgroup, one per wave, each with its own LDS lists */
+    __shared__ int cand_s[4][K3G_MAX_E];
+    __shared__ float cch_s[4][K3G_MAX_E], csc_s[4][K3G_MAX_E];
+    const int wq = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = 4 * blockIdx.x + wq;
+    if (t >= T) return;
+    int *cand = cand_s[wq];
+    float *cch = cch_s[wq], *csc = csc_s[wq];
     const double xn = sqrt((double)xn2[t]) * (1.0 + 0x1p-10);
     /* the approximate logit and its norm product */
     auto approx = [&](int e, float &a, double &ab) {
@@ -656,7 +660,8 @@ k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
         if (cf) cand[nc + __popcll(cm & lt)] = e;
         nc += __popcll(cm);
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
 
     /* the candidates' float logits */
     const float *xt = x + (size_t)t * d;
@@ -711,7 +716,8 @@ k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
         }
         nviol += __popcll(__ballot(viol));
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
 
     /* the engine's selection among the candidates: larger choice, then lower index (the
      * candidates are in expert order, so the lower candidate slot); NaN and -inf never win */
@@ -753,18 +759,42 @@ k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
         idx[(size_t)t * k + lane] = my_sel >= 0 ? my_sel : 0;
         wt[(size_t)t * k + lane] = __fmul_rn(wgt, routed_scale);
     }
-    if (stats && lane == 0) {
-        if (nc > k) atomicAdd(&stats[0], 1);
-        if (nopen) atomicAdd(&stats[1], nopen);
-        if (nviol) atomicAdd(&stats[2], nviol);
+    /* per-token counts (4096 waves adding into one address would queue at the L2) */
+    if (lane == 0) *(int4 *)(tstat + 4 * (size_t)t) = make_int4(nc > k, nopen, nviol, 0);
+}
+
+/* The per-token counts of k_router_pick added into the context's statistics */
+__global__ void __launch_bounds__(256)
+k_router_stats(const int4 *__restrict__ tstat, int T, int *__restrict__ stats)
+{
+    __shared__ int red[3][4];
+    int a = 0, b = 0, c = 0;
+    for (int t = threadIdx.x; t < T; t += 256) {
+        const int4 v = tstat[t];
+        a += v.x; b += v.y; c += v.z;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        a += __shfl_xor(a, m, K3G_WAVE);
+        b += __shfl_xor(b, m, K3G_WAVE);
+        c += __shfl_xor(c, m, K3G_WAVE);
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { red[0][w] = a; red[1][w] = b; red[2][w] = c; }
+    __syncthreads();
+    if (threadIdx.x < 3) {
+        const int s = red[threadIdx.x][0] + red[threadIdx.x][1] + red[threadIdx.x][2] +
+                      red[threadIdx.x][3];
+        if (s) atomicAdd(&stats[threadIdx.x], s);
     }
 }
 
-/* floats of workspace the bounded-logit path needs for T tokens (0 below its range) */
+/* floats of workspace the bounded-logit path needs for T tokens (0 below its range): up
+ * to 8 K slices of partial sums and norms, then 4 ints of counts per token */
 extern "C" size_t k3k_router_bf3_floats(int T, int E)
 {
     if (T < RB_MIN_T) return 0;
-    return 8 * ((size_t)T * E + T + E);
+    return 8 * ((size_t)T * E + T + E) + 4 * (size_t)T;
 }
 
 /* ------------------------------------------------------------------ select ---- */
@@ -810,8 +840,10 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
         const int nmn = ((E + RB_TILE - 1) / RB_TILE) * ((T + RB_TILE - 1) / RB_TILE);
         const int nch = d / 128;
         const size_t per_s = (size_t)T * E + T + E;
+        const size_t room = bpart_floats > 4 * (size_t)T ? bpart_floats - 4 * (size_t)T : 0;
+        int *tstat = (int *)(bpart + room);
         int S = 512 / nmn;
-        if ((size_t)S * per_s > bpart_floats) S = (int)(bpart_floats / per_s);
+        if ((size_t)S * per_s > room) S = (int)(room / per_s);
         if (S > nch) S = nch;
         if (S >= 1) {
             const int cps = (nch + S - 1) / S;
@@ -828,17 +860,20 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
             }
             const double nround = rb_bound(d) / (1.01 * 0x1p-53);
             if (E <= 256)
-                hipLaunchKernelGGL(k_router_pick<4>, dim3(T), dim3(64), 0, st, bpart, xn2,
-                                   wn2, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                                   force, stats, nround);
+                hipLaunchKernelGGL(k_router_pick<4>, dim3((T + 3) / 4), dim3(256), 0, st, bpart,
+                                   xn2, wn2, bias, W, x, T, d, E, k, renorm, routed_scale, idx, wt,
+                                   force, tstat, nround);
             else if (E <= 512)
-                hipLaunchKernelGGL(k_router_pick<8>, dim3(T), dim3(64), 0, st, bpart, xn2,
-                                   wn2, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                                   force, stats, nround);
+                hipLaunchKernelGGL(k_router_pick<8>, dim3((T + 3) / 4), dim3(256), 0, st, bpart,
+                                   xn2, wn2, bias, W, x, T, d, E, k, renorm, routed_scale, idx, wt,
+                                   force, tstat, nround);
             else
-                hipLaunchKernelGGL(k_router_pick<16>, dim3(T), dim3(64), 0, st, bpart, xn2,
-                                   wn2, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
-                                   force, stats, nround);
+                hipLaunchKernelGGL(k_router_pick<16>, dim3((T + 3) / 4), dim3(256), 0, st, bpart,
+                                   xn2, wn2, bias, W, x, T, d, E, k, renorm, routed_scale, idx, wt,
+                                   force, tstat, nround);
+            if (stats)
+                hipLaunchKernelGGL(k_router_stats, dim3(1), dim3(256), 0, st, (const int4 *)tstat,
+                                   T, stats);
             return hipGetLastError() == hipSuccess ? 0 : -1;
         }
     }
