@@ -275,7 +275,6 @@ k_router_logits_mfma(const float *__restrict__ x, int T, const float *__restrict
 #define RB_TILE 128                 /* experts x tokens per workgroup tile */
 #define RB_OPB 16384                /* one operand's two pieces, 128 rows x 64 B each */
 #define RB_MIN_T 512                /* from this many tokens on */
-#define RP_RB 8                     /* candidate rows per pass of the exact logits */
 
 typedef __bf16 k3v2bfr __attribute__((ext_vector_type(2)));
 typedef __bf16 k3v8bfr __attribute__((ext_vector_type(8)));
@@ -498,75 +497,7 @@ k_router_bf3_sum(float *__restrict__ part, int S, int T, int E, float *__restric
     }
 }
 
-/* a candidate's float logit the any-order bound left open: the partial-sum bound, else the
- * engine's serial chain (always the chain when force > 2). Inline, so that the kernel's
- * register budget holds for it too (a call would size the kernel by its callee). */
-__device__ __forceinline__ float rp_open_logit(const float *row, const float *xt, int d,
-                                               int lane, int force)
-{
-    float g;
-    if (force <= 2 && k3d_row_logit(row, xt, d, lane, &g)) return g;
-    const float4 *w4 = (const float4 *)row, *x4 = (const float4 *)xt;
-    double acc = 0.0;
-#pragma unroll 8
-    for (int q = 0; q < d / 4; ++q) {
-        const float4 wv = w4[q], xv = x4[q];
-        acc = fma((double)wv.x, (double)xv.x, acc);
-        acc = fma((double)wv.y, (double)xv.y, acc);
-        acc = fma((double)wv.z, (double)xv.z, acc);
-        acc = fma((double)wv.w, (double)xv.w, acc);
-    }
-    return (float)acc;
-}
-
-/* 1 / (1 + e^-v) with the hardware exponential: within a few float ulps */
-__device__ __forceinline__ float rp_sig(float v) { return 1.0f / (1.0f + __expf(-v)); }
-
-/* Row j < NB's fp64 dot product with x (acc[2 j]) and the sum of its products' magnitudes
- * (acc[2 j + 1]), this lane's share: columns 2 lane + 128 q, two per 128-column stage,
- * with two stages in flight. d a multiple of 256, rows and x 8-byte aligned. */
-template <int NB>
-__device__ __forceinline__ void rp_dots(const float *const *rows, const float *xt, int d,
-                                        int lane, double *acc)
-{
-    const float2 *x2 = (const float2 *)xt;
-    const int nq = d / 128;
-    float2 xs[3], ws[3][NB];
-    auto ld = [&](int slot, int q) {
-        const int o = min(q, nq - 1) * 64 + lane;
-        xs[slot] = x2[o];
-#pragma unroll
-        for (int j = 0; j < NB; ++j) ws[slot][j] = ((const float2 *)rows[j])[o];
-    };
-    ld(0, 0);
-    ld(1, 1);
-    for (int q0 = 0; q0 < nq; q0 += 3) {
-#pragma unroll
-        for (int u = 0; u < 3; ++u) {
-            ld((u + 2) % 3, q0 + u + 2);
-            if (q0 + u < nq) {
-                const double x0 = xs[u].x, x1 = xs[u].y;
-#pragma unroll
-                for (int j = 0; j < NB; ++j) {
-                    const double w0 = ws[u][j].x, w1 = ws[u][j].y;
-                    acc[2 * j] = fma(w1, x1, fma(w0, x0, acc[2 * j]));
-                    acc[2 * j + 1] = fma(fabs(w1), fabs(x1), fma(fabs(w0), fabs(x0), acc[2 * j + 1]));
-                }
-            }
-        }
-    }
-}
-
-/* One wave per token after k_router_bf3: the score intervals from the bounded logits, the
- * top-k on their best guesses, the candidates (every expert whose interval reaches the
- * weakest selected lower end: the engine's top-k lies among them; all experts when the
- * guesses cannot select k or are not numbers), their fp64 logits (the engine's float
- * logit settled by the any-order bound, else by the partial-sum bound, else the serial
- * chain), and the engine's selection among the candidates with its weights. Candidate
- * rows stream straight from memory, RP_RB rows per pass beside one pass over x.
- * stats: [0] tokens with more candidates than k, [1] candidate logits the any-order bound
- * left open, [2] candidates whose fp64 logit fell outside its bounded interval (never
- * expected: a check of the bound on live data). */
+/* One wave per token after k_router_bf3 (k3d_pick_token), four tokens per workgroup. */
 template <int NPL>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
@@ -575,192 +506,17 @@ k_router_pick(const float *__restrict__ part, const float *__restrict__ xn2,
               int renorm, float routed_scale, int32_t *__restrict__ idx,
               float *__restrict__ wt, int force, int *__restrict__ tstat, double nround)
 {
-    /* four tokens per workgroup, one per wave, each with its own LDS lists */
+    /* each wave with its own LDS lists */
     __shared__ int cand_s[4][K3G_MAX_E];
     __shared__ float cch_s[4][K3G_MAX_E], csc_s[4][K3G_MAX_E];
     const int wq = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int t = 4 * blockIdx.x + wq;
     if (t >= T) return;
-    int *cand = cand_s[wq];
-    float *cch = cch_s[wq], *csc = csc_s[wq];
-    const double xn = sqrt((double)xn2[t]) * (1.0 + 0x1p-10);
-    /* the approximate logit and its norm product */
-    auto approx = [&](int e, float &a, double &ab) {
-        a = part[(size_t)t * E + e];
-        ab = sqrt((double)wn2[e]) * (1.0 + 0x1p-10) * xn;
-    };
-    /* every load issued before any is used */
-    float av[NPL], wv[NPL], bv[NPL];
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const int e = min(lane + 64 * i, E - 1);
-        av[i] = part[(size_t)t * E + e];
-        wv[i] = wn2[e];
-        bv[i] = bias ? bias[e] : 0.0f;
-    }
-    float4 v[NPL];
-    uint64_t key[NPL];
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const int e = lane + 64 * i;
-        v[i] = make_float4(-INFINITY, -INFINITY, -INFINITY, 0.0f);
-        key[i] = 0;
-        if (e < E) {
-            /* the engine's float logit lies in [fl(a - B), fl(a + B)] (rounding is
-             * monotone); the choice bounds follow in fast float arithmetic with 2^-16
-             * (1 + |bias|) of slack, which covers the fast exp, the engine's expf and the
-             * roundings of the sigmoid and the bias add. Only the candidate set depends on
-             * them. */
-            const double a = av[i];
-            const double B = nround * 0x1p-53 * 1.01 * (sqrt((double)wv[i]) * (1.0 + 0x1p-10) * xn) +
-                             fabs(a) * 0x1p-51 + 0x1p-1000;
-            const float slack = 0x1p-16f * (1.0f + fabsf(bv[i]));
-            v[i].x = rp_sig((float)a) + bv[i];
-            v[i].y = rp_sig((float)(a - B)) + bv[i] - slack;
-            v[i].z = rp_sig((float)(a + B)) + bv[i] + slack;
-            if (v[i].x > -INFINITY)
-                key[i] = ((uint64_t)k3d_ordered(v[i].x) << 32) | (uint32_t)~e;
-        }
-    }
-    /* top-k on the guesses: theta = the weakest selected lower end */
-    uint32_t taken = 0;
-    bool valid = true;
-    float theta = INFINITY;
-    for (int j = 0; j < k; ++j) {
-        uint64_t m[NPL];
-#pragma unroll
-        for (int i = 0; i < NPL; ++i) m[i] = key[i];
-#pragma unroll
-        for (int h = NPL / 2; h >= 1; h /= 2)
-#pragma unroll
-            for (int i = 0; i < h; ++i) m[i] = m[i + h] > m[i] ? m[i + h] : m[i];
-        const uint64_t win = k3d_wave_max_u64(m[0]);
-        if (!win) { valid = false; break; }
-        const int w = (int)~(uint32_t)win, slot = w >> 6, wl = w & 63;
-        float lo = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NPL; ++i)
-            if (i == slot) {
-                lo = v[i].y;
-                if (lane == wl) { key[i] = 0; taken |= 1u << i; }
-            }
-        const float wlo = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(lo), wl));
-        if (__builtin_isnan(wlo)) valid = false;
-        theta = fminf(theta, wlo);
-    }
-    if (!valid || force >= 2) theta = -INFINITY;
-    /* candidates in expert order (a NaN upper end is a candidate) */
-    int nc = 0;
-    const uint64_t lt = (1ull << lane) - 1;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const int e = lane + 64 * i;
-        const bool cf = e < E && (((taken >> i) & 1u) || !(v[i].z < theta));
-        const uint64_t cm = __ballot(cf);
-        if (cf) cand[nc + __popcll(cm & lt)] = e;
-        nc += __popcll(cm);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-
-    /* the candidates' float logits */
-    const float *xt = x + (size_t)t * d;
-    int nopen = 0, nviol = 0;
-    for (int c0 = 0; c0 < nc; c0 += RP_RB) {
-        const int nb = min(RP_RB, nc - c0);
-        const float *rows[RP_RB];
-#pragma unroll
-        for (int j = 0; j < RP_RB; ++j)
-            rows[j] = W + (size_t)__builtin_amdgcn_readfirstlane(cand[c0 + min(j, nb - 1)]) * d;
-        double acc[2 * RP_RB];
-#pragma unroll
-        for (int j = 0; j < 2 * RP_RB; ++j) acc[j] = 0.0;
-        switch (nb) {
-        case 1: rp_dots<1>(rows, xt, d, lane, acc); break;
-        case 2: rp_dots<2>(rows, xt, d, lane, acc); break;
-        case 3: rp_dots<3>(rows, xt, d, lane, acc); break;
-        case 4: rp_dots<4>(rows, xt, d, lane, acc); break;
-        case 5: rp_dots<5>(rows, xt, d, lane, acc); break;
-        case 6: rp_dots<6>(rows, xt, d, lane, acc); break;
-        case 7: rp_dots<7>(rows, xt, d, lane, acc); break;
-        default: rp_dots<8>(rows, xt, d, lane, acc); break;
-        }
-        /* lane l then holds value l >> 2: row j's sum at lane 8 j, its magnitude at 8 j + 4 */
-        k3d_transpose_reduce<2 * RP_RB>(acc, lane);
-        const double sj = __shfl(acc[0], (8 * lane) & 63, K3G_WAVE);
-        const double aj = __shfl(acc[0], (8 * lane + 4) & 63, K3G_WAVE);
-        float f = 0.0f;
-        bool ok = false;
-        if (lane < nb) ok = force <= 2 && k3d_settled_float(sj, aj, d, &f);
-        const uint64_t um = __ballot(lane < nb && !ok);
-        nopen += __popcll(um);
-        for (uint64_t m = um; m; m &= m - 1) {
-            const int j = __builtin_ctzll(m);
-            const float *row = W + (size_t)__builtin_amdgcn_readfirstlane(cand[c0 + j]) * d;
-            const float g = rp_open_logit(row, xt, d, lane, force);
-            if (lane == j) f = g;
-        }
-        bool viol = false;
-        if (lane < nb) {
-            const int e = cand[c0 + lane];
-            const float sc = k3d_sigmoid(f);
-            csc[c0 + lane] = sc;
-            cch[c0 + lane] = __fadd_rn(sc, bias ? bias[e] : 0.0f);
-            float a;
-            double ab;
-            approx(e, a, ab);
-            const double B = nround * 0x1p-53 * 1.01 * ab + fabs((double)a) * 0x1p-51;
-            const double df = fabs((double)f - (double)a);
-            viol = __builtin_isfinite(f) && __builtin_isfinite(a) && __builtin_isfinite(B) &&
-                   df > B + fabs((double)f) * 0x1p-23;
-        }
-        nviol += __popcll(__ballot(viol));
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-
-    /* the engine's selection among the candidates: larger choice, then lower index (the
-     * candidates are in expert order, so the lower candidate slot); NaN and -inf never win */
-    const int nsl = (nc + 63) >> 6;
-    uint32_t tk = 0;
-    int my_sel = -1;
-    float my_score = 0.0f;
-    for (int j = 0; j < k; ++j) {
-        uint64_t best = 0;
-        for (int q = 0; q < nsl; ++q) {
-            const int c = lane + 64 * q;
-            if (c < nc && !((tk >> q) & 1u)) {
-                const float ch = cch[c];
-                if (ch > -INFINITY) {
-                    const uint64_t kk = ((uint64_t)k3d_ordered(ch) << 32) | (uint32_t)~c;
-                    best = kk > best ? kk : best;
-                }
-            }
-        }
-        const uint64_t win = k3d_wave_max_u64(best);
-        int sel = -1;
-        float sc = 0.0f;
-        if (win) {
-            const int c = (int)~(uint32_t)win;
-            sel = cand[c];
-            sc = csc[c];
-            if (lane == (c & 63)) tk |= 1u << (c >> 6);
-        }
-        if (lane == j) { my_sel = sel; my_score = sc; }
-    }
-    /* weights from the unbiased scores, renormalised by the engine's sequential double sum
-     * in selection order, then scaled */
-    double wsum = 0.0;
-    for (int j = 0; j < k; ++j)
-        wsum += (double)__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(my_score), j));
-    if (lane < k) {
-        float wgt = my_score;
-        if (renorm && k > 1) wgt = __fmul_rn(wgt, (float)(1.0 / (wsum + 1e-20)));
-        idx[(size_t)t * k + lane] = my_sel >= 0 ? my_sel : 0;
-        wt[(size_t)t * k + lane] = __fmul_rn(wgt, routed_scale);
-    }
+    int cnt[3];
+    k3d_pick_token<NPL>(t, part, xn2, wn2, bias, W, x, d, E, k, renorm, routed_scale, idx, wt,
+                        force, nround, cand_s[wq], cch_s[wq], csc_s[wq], lane, cnt);
     /* per-token counts (4096 waves adding into one address would queue at the L2) */
-    if (lane == 0) *(int4 *)(tstat + 4 * (size_t)t) = make_int4(nc > k, nopen, nviol, 0);
+    if (lane == 0) *(int4 *)(tstat + 4 * (size_t)t) = make_int4(cnt[0], cnt[1], cnt[2], 0);
 }
 
 /* The per-token counts of k_router_pick added into the context's statistics */

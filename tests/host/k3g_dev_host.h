@@ -192,6 +192,33 @@ inline double k3d_wave_sumd(double v)
     return v;
 }
 
+/* the device's hardware exponential stands in as the host's float exp */
+inline float __expf(float v) { return std::exp(v); }
+
+/* Transposed wave reduction of V partial sums per lane (the device helper's halving
+ * rounds): lane l ends with the 64-lane sum of value index l >> (6 - log2 V) in v[0]. */
+template <int V, typename A>
+inline void k3d_transpose_reduce(A *v, int lane)
+{
+    int n = V;
+    for (int m = 32; m >= 1; m >>= 1) {
+        if (n > 1) {
+            const int h = n >> 1;
+            const bool upper = (lane & m) != 0;
+            for (int i = 0; i < V / 2; ++i) {
+                if (i < h) {
+                    const A send = upper ? v[i] : v[i + h];
+                    const A keep = upper ? v[i + h] : v[i];
+                    v[i] = keep + __shfl_xor(send, m, K3G_WAVE);
+                }
+            }
+            n = h;
+        } else {
+            v[0] += __shfl_xor(v[0], m, K3G_WAVE);
+        }
+    }
+}
+
 /* global_load_lds_dwordx4: lane l's 16 bytes land at LDS byte address lds + 16 l; the
  * address is the low 32 bits of a pointer into the host block standing in for the LDS */
 inline void k3d_dma16(const void *src, uint32_t lds)

@@ -9,7 +9,13 @@ K3_MAX_TOPK (64, also above n_experts), exact ties in the choice scores (duplica
 rows and biases, which fail the certificate and run the exact path), both exact-path
 variants (LDS-staged candidate rows as the router kernel runs it, unstaged as the fused
 decode kernel runs it) and the four forced modes. Any out-of-bounds access to the LDS
-arrays, the score intervals, the router rows or the outputs aborts the run."""
+arrays, the score intervals, the router rows or the outputs aborts the run.
+
+The many-token selection (k3d_pick_token, run by k_router_pick after the bounded bf16
+logits) is audited the same way (tests/host/pick_audit.cpp): approximate logits placed
+adversarially inside their bound (0.9 of it, up for odd experts and down for even ones,
+rounded to float), with the bound the GPU path uses and a 200 times tighter one, in the
+normal and two forced modes."""
 import os
 import shutil
 import subprocess
@@ -79,3 +85,37 @@ def test_unsettled_scores_never_become_weights(audit, E, k, ties):
             # each token either failed its certificate or had its k scores recomputed
             assert rer + rec // k >= 2 and rec % k == 0, l
 
+
+
+@pytest.fixture(scope="module")
+def pick_audit(tmp_path_factory):
+    if not shutil.which("g++") or not shutil.which("gcc"):
+        pytest.skip("no host compiler")
+    d = tmp_path_factory.mktemp("pick_audit")
+    shutil.copy(os.path.join(CSRC, "k3g_select.h"), d / "k3g_select.h")
+    shutil.copy(os.path.join(HOST, "k3g_dev_host.h"), d / "k3g_dev.h")
+    san = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all"]
+    subprocess.run(["gcc", "-O1", "-g", "-ffp-contract=off", *san, "-c",
+                    os.path.join(ROOT, "oracle", "k3_oracle.c"), "-I",
+                    os.path.join(ROOT, "include"), "-o", str(d / "oracle.o")], check=True)
+    exe = d / "pick_audit"
+    subprocess.run(["g++", "-std=c++20", "-O1", "-g", "-ffp-contract=off", *san,
+                    "-fsanitize=bounds-strict", "-Wno-attributes", "-I", str(d),
+                    os.path.join(HOST, "pick_audit.cpp"), str(d / "oracle.o"), "-o",
+                    str(exe), "-lpthread"], check=True)
+    return str(exe)
+
+
+@pytest.mark.parametrize("E,k,ties,mode", [(384, 8, 0, 0), (384, 8, 1, 1), (16, 4, 1, 0),
+                                           (1024, 64, 1, 0), (896, 16, 0, 1), (384, 9, 1, 0),
+                                           (64, 1, 1, 1), (512, 16, 1, 0)])
+def test_many_token_pick_bit_exact(pick_audit, E, k, ties, mode):
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=1")
+    r = subprocess.run([pick_audit, str(E), str(k), "256", "3", str(ties), "13", str(mode)],
+                       capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    lines = [l for l in r.stdout.splitlines() if l.startswith("E=")]
+    assert len(lines) == 3, r.stdout
+    assert all(l.endswith("violations 0, mismatches 0") for l in lines), r.stdout
+    # forced mode 2 makes every expert a candidate: every token counts as having extras
+    assert all("extra 3," in l for l in lines if "force=2" in l), r.stdout
