@@ -655,7 +655,7 @@ int k3g_route(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx,
     const int rc = k3k_router(x, T, L->gate, L->bias, L->hidden, L->n_experts, L->topk,
                               L->renorm, L->routed_scale, c->rs, idx, wt, c->force_exact,
                               c->stats, c->rtpart, c->rtctr, c->rbpart, c->rbpart_floats,
-                              st);
+                              c->route_x1flag, st);
     k3g_stage_end(c, K3G_ST_ROUTER, st);
     return rc;
 }
@@ -860,7 +860,11 @@ int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int
             rc |= shared_expert(c, L, T, c->kpart2, c->side);
             if (hipEventRecord(c->ev_shared, c->side) != hipSuccess) rc = -1;
         }
+        /* x's piece-1 flag is this x's: the router skips the product of x's second piece
+         * when every x is a bf16 value */
+        c->route_x1flag = c->xflag;
         rc |= k3g_route(c, L, x, T, idx, wt, st);
+        c->route_x1flag = NULL;
         /* the dispatch's flag argument (cleared) is the spare one: x's is set above */
         k3g_stage_begin(c, K3G_ST_DISPATCH, st);
         rc |= k3k_dispatch_tiles(idx, T * L->topk, L->n_experts, c->cnt, c->base, c->off,

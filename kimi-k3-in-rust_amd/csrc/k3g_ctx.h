@@ -67,6 +67,7 @@ struct K3gCtx {
     double *rtpart;              /* K-slice sums of the router's matrix-core logits */
     int32_t *rtctr;              /* their per-tile arrival counts (zero between calls) */
     float *rbpart;               /* the bounded bf16 logits' K-slice sums and norms */
+    const int32_t *route_x1flag; /* x's piece-1 flag for the call being routed, or NULL */
     size_t rbpart_floats;
     int32_t *tiles, *ntiles, *xflag;
     int max_tiles;

@@ -173,7 +173,7 @@ int k3k_tile_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols, hipStr
 int k3k_router(const float *x, int T, const float *W, const float *bias, int d, int E,
                int k, int renorm, float routed_scale, float *rs, int32_t *idx, float *wt,
                int force, int *stats, double *part, int32_t *ctr, float *bpart,
-               size_t bpart_floats, hipStream_t st);
+               size_t bpart_floats, const int32_t *x1flag, hipStream_t st);
 /* bytes of the part buffer k3k_router's sliced logits use (ctr: 512 zeroed 128-byte
  * lines, 16384 ints) */
 size_t k3k_router_part_bytes(void);

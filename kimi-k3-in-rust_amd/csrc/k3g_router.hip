@@ -325,11 +325,11 @@ __device__ __forceinline__ k3v4fr rb_mma(uint4 a, uint4 b, k3v4fr c)
  * work. Partial sums go to part[s][t][e]; the workgroups of expert tile 0 also sum x's
  * squares (xn2[s][t]) and those of token tile 0 W's (wn2[s][e]). Workgroups of one token
  * tile and slice are consecutive on one XCD, sharing its x rows in that L2. */
-__global__ void __launch_bounds__(256, 2)
-k_router_bf3(const float *__restrict__ x, int T, const float *__restrict__ W, int d, int E,
-             int S, float *__restrict__ part, float *__restrict__ xn2, float *__restrict__ wn2)
+template <bool X1>
+__device__ __forceinline__ void
+rb_tile(const float *__restrict__ x, int T, const float *__restrict__ W, int d, int E, int S,
+        float *__restrict__ part, float *__restrict__ xn2, float *__restrict__ wn2, uint8_t *lds)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * RB_OPB];
     const int nte = (E + RB_TILE - 1) / RB_TILE, ntt = (T + RB_TILE - 1) / RB_TILE;
     const int N = nte * ntt * S, per = (N + 7) >> 3;
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
@@ -420,7 +420,7 @@ k_router_bf3(const float *__restrict__ x, int T, const float *__restrict__ W, in
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 b0[j] = *(const uint4 *)(b + bo + j * 1024);
-                b1[j] = *(const uint4 *)(b + bo + 8192 + j * 1024);
+                if (X1) b1[j] = *(const uint4 *)(b + bo + 8192 + j * 1024);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -430,7 +430,7 @@ k_router_bf3(const float *__restrict__ x, int T, const float *__restrict__ W, in
                 for (int j = 0; j < 4; ++j) {
                     k3v4fr c = q == 0 ? k3v4fr{0.0f, 0.0f, 0.0f, 0.0f} : acc[i][j];
                     c = rb_mma(a0, b0[j], c);
-                    c = rb_mma(a0, b1[j], c);
+                    if (X1) c = rb_mma(a0, b1[j], c);
                     acc[i][j] = rb_mma(a1, b0[j], c);
                 }
             }
@@ -467,6 +467,20 @@ k_router_bf3(const float *__restrict__ x, int T, const float *__restrict__ W, in
             if (do_w && we1) wn2[(size_t)s * E + e0 + r1] = ws1;
         }
     }
+}
+
+/* x1flag (optional): nonzero when some x has a nonzero second bf16 piece; when it reads
+ * zero every x is a bf16 value and its w0 x1 product is skipped (it would add zeros). */
+__global__ void __launch_bounds__(256, 2)
+k_router_bf3(const float *__restrict__ x, int T, const float *__restrict__ W, int d, int E,
+             int S, float *__restrict__ part, float *__restrict__ xn2, float *__restrict__ wn2,
+             const int32_t *__restrict__ x1flag)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[4 * RB_OPB];
+    if (!x1flag || *x1flag)
+        rb_tile<true>(x, T, W, d, E, S, part, xn2, wn2, lds);
+    else
+        rb_tile<false>(x, T, W, d, E, S, part, xn2, wn2, lds);
 }
 
 /* The K slices' sums of k_router_bf3 added in slice order into slice 0 (the logits four
@@ -585,7 +599,8 @@ static int router_slices(int N)
 extern "C" int k3k_router(const float *x, int T, const float *W, const float *bias, int d,
                           int E, int k, int renorm, float routed_scale, float *rs,
                           int32_t *idx, float *wt, int force, int *stats, double *part,
-                          int32_t *ctr, float *bpart, size_t bpart_floats, hipStream_t st)
+                          int32_t *ctr, float *bpart, size_t bpart_floats,
+                          const int32_t *x1flag, hipStream_t st)
 {
     if (E > K3G_MAX_E || k > K3G_MAX_TOPK || k < 1 || T < 1 || d < 1) return -1;
     /* float4 loads need 16-byte aligned rows; anything else takes the scalar loop */
@@ -607,7 +622,7 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
             float *xn2 = bpart + (size_t)S * T * E, *wn2 = xn2 + (size_t)S * T;
             const long long N = (long long)nmn * S;
             hipLaunchKernelGGL(k_router_bf3, dim3((unsigned)(8 * ((N + 7) / 8))), dim3(256), 0,
-                               st, x, T, W, d, E, S, bpart, xn2, wn2);
+                               st, x, T, W, d, E, S, bpart, xn2, wn2, x1flag);
             if (S > 1) {
                 const size_t n = (size_t)T * E / 4 + T + E;
                 const unsigned g = (unsigned)((n + 255) / 256 < 2048 ? (n + 255) / 256 : 2048);
