@@ -559,12 +559,22 @@ k_router_stats(const int4 *__restrict__ tstat, int T, int *__restrict__ stats)
     }
 }
 
-/* floats of workspace the bounded-logit path needs for T tokens (0 below its range): up
- * to 8 K slices of partial sums and norms, then 4 ints of counts per token */
+/* K slices of the bounded logits wanted for T tokens: about 512 (tile, slice) workgroups,
+ * at least one slice (the launch further bounds it by the workspace and by d / 128) */
+static int rb_slices(int T, int E)
+{
+    const int nmn = ((E + RB_TILE - 1) / RB_TILE) * ((T + RB_TILE - 1) / RB_TILE);
+    const int s = 512 / nmn;
+    return s < 1 ? 1 : s;
+}
+
+/* floats of workspace the bounded-logit path needs for T tokens (0 below its range): its
+ * K slices of partial sums and norms, then 4 ints of counts per token */
 extern "C" size_t k3k_router_bf3_floats(int T, int E)
 {
     if (T < RB_MIN_T) return 0;
-    return 8 * ((size_t)T * E + T + E) + 4 * (size_t)T;
+    const int S = rb_slices(T, E);
+    return (size_t)(S < 8 ? S : 8) * ((size_t)T * E + T + E) + 4 * (size_t)T;
 }
 
 /* ------------------------------------------------------------------ select ---- */
@@ -613,7 +623,7 @@ extern "C" int k3k_router(const float *x, int T, const float *W, const float *bi
         const size_t per_s = (size_t)T * E + T + E;
         const size_t room = bpart_floats > 4 * (size_t)T ? bpart_floats - 4 * (size_t)T : 0;
         int *tstat = (int *)(bpart + room);
-        int S = 512 / nmn;
+        int S = rb_slices(T, E);
         if ((size_t)S * per_s > room) S = (int)(room / per_s);
         if (S > nch) S = nch;
         if (S >= 1) {

@@ -566,7 +566,8 @@ def _dispatch_expected(idx, E):
 
 @pytest.mark.parametrize("T,E,k", [(1, 384, 8), (20, 384, 8), (32, 384, 8), (33, 384, 8),
                                    (300, 384, 8), (512, 384, 8), (4096, 384, 8), (50, 16, 4),
-                                   (600, 896, 16), (1537, 1024, 4), (4100, 64, 2)])
+                                   (600, 896, 16), (1537, 1024, 4), (4100, 64, 2),
+                                   (4096, 896, 16)])
 def test_dispatch_is_a_stable_sort(gpu, T, E, k):
     P = T * k
     path = "one block" if P <= 256 else "one 1024-thread block" if P <= 4096 else "three passes"
