@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "k3g_expf.h"
+
 #define K3G_WAVE 64
 #define K3G_TILE_COLS 128      /* pairs per column tile of the grouped GEMMs */
 
@@ -203,16 +205,16 @@ __device__ __forceinline__ void k3d_transpose_reduce(A *v, int lane)
     }
 }
 
-/* Float expf, correctly rounded except for ~2^-28 of inputs: the double exp is within an
- * ulp of double, far inside a float rounding interval. glibc's expf is within 0.502 ulp,
- * so the two agree but on a vanishing set of near-midpoint inputs. */
-__device__ __forceinline__ float k3d_expf_cr(float v) { return (float)exp((double)v); }
+/* The engine's expf bit for bit (the C library's algorithm, k3g_expf.h), and tanhf
+ * correctly rounded but for a vanishing set of near-midpoint inputs (the double tanh is
+ * within an ulp of double, far inside a float rounding interval). */
+__device__ __forceinline__ float k3d_expf(float v) { return k3x_expf(v); }
 __device__ __forceinline__ float k3d_tanhf_cr(float v) { return (float)tanh((double)v); }
 
 /* 1/(1+expf(-v)) with the engine's float operation order (src/core/k3_ops.c:105) */
 __device__ __forceinline__ float k3d_sigmoid(float v)
 {
-    return __fdiv_rn(1.0f, __fadd_rn(1.0f, k3d_expf_cr(-v)));
+    return __fdiv_rn(1.0f, __fadd_rn(1.0f, k3d_expf(-v)));
 }
 
 /* SiTU-GLU on one (gate, up) pair, src/core/k3_ops.c:110-123, in the engine's float

@@ -17,6 +17,8 @@
  * The test copies this file next to a copy of k3g_select.h as "k3g_dev.h". */
 #pragma once
 
+#include "k3g_expf.h"
+
 #include <atomic>
 #include <cmath>
 #include <cstdint>
@@ -183,8 +185,8 @@ inline emu_u4 __builtin_amdgcn_raw_buffer_load_b128(__amdgpu_buffer_rsrc_t r, in
 }
 
 /* ------------------------------------------------------------------ helpers ---- */
-inline float k3d_expf_cr(float v) { return (float)std::exp((double)v); }
-inline float k3d_sigmoid(float v) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, k3d_expf_cr(-v))); }
+inline float k3d_expf(float v) { return k3x_expf(v); }
+inline float k3d_sigmoid(float v) { return __fdiv_rn(1.0f, __fadd_rn(1.0f, k3d_expf(-v))); }
 
 inline double k3d_wave_sumd(double v)
 {

@@ -37,6 +37,7 @@ def audit(tmp_path_factory):
     d = tmp_path_factory.mktemp("select_audit")
     shutil.copy(os.path.join(CSRC, "k3g_select.h"), d / "k3g_select.h")
     shutil.copy(os.path.join(HOST, "k3g_dev_host.h"), d / "k3g_dev.h")
+    shutil.copy(os.path.join(CSRC, "k3g_expf.h"), d / "k3g_expf.h")
     san = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all"]
     subprocess.run(["gcc", "-O1", "-g", "-ffp-contract=off", *san, "-c",
                     os.path.join(ROOT, "oracle", "k3_oracle.c"), "-I",
@@ -94,6 +95,7 @@ def pick_audit(tmp_path_factory):
     d = tmp_path_factory.mktemp("pick_audit")
     shutil.copy(os.path.join(CSRC, "k3g_select.h"), d / "k3g_select.h")
     shutil.copy(os.path.join(HOST, "k3g_dev_host.h"), d / "k3g_dev.h")
+    shutil.copy(os.path.join(CSRC, "k3g_expf.h"), d / "k3g_expf.h")
     san = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all"]
     subprocess.run(["gcc", "-O1", "-g", "-ffp-contract=off", *san, "-c",
                     os.path.join(ROOT, "oracle", "k3_oracle.c"), "-I",
