@@ -535,16 +535,21 @@ int  k3gc_moe(K3gCtx *ctx, K3gCache *cache, const K3gLayer *L, int layer, const 
               int T, float *out, int32_t *idx, float *wt, const int32_t *route_idx,
               const float *route_wt, void *stream);
 
-/* The MoE half of n_layers consecutive decoder layers on a hidden state h [T][hidden]
- * (device, fp32) that stays in HBM: for each layer l, hin = RMSNorm(h) x post_norm[l]
- * (double sum, as the engine's k3_rmsnorm; skipped when post_norm or post_norm[l] is
- * NULL), then h += the layer's MoE output on hin through the cache (cache layer
- * first_layer + l), as k3_decoder_layer_inc does around its k3_moe_prefill call
- * (src/core/k3_ops.c:1015-1036) and forward() walks the layers with the cache as their
- * expert source (src/cli/k3_run.c:582-618). Only each layer's routing crosses to the host
- * (for the cache's get calls). When every expert of every layer in the chain is resident,
- * the layers run back to back with no host synchronisation and the cache's get calls
- * follow, one step per layer, all hits. Layers in the tiled layout of the cache's bank. */
+/* A synthetic stack of MoE halves on a hidden state h [T][hidden] (device, fp32) that
+ * stays in HBM, with no attention and no AttnRes aggregation between them: for each
+ * layer l, hin = RMSNorm(h) x post_norm[l] (double sum, as the engine's k3_rmsnorm;
+ * skipped when post_norm or post_norm[l] is NULL), the layer's MoE output on hin through
+ * the cache (cache layer first_layer + l), then h += that output. The norm and MoE call
+ * are k3_decoder_layer_inc's (src/core/k3_ops.c:1015-1024), the layer walk with the cache
+ * as every layer's expert source is forward()'s (src/cli/k3_run.c:582-618); the engine
+ * adds the MoE output to its block prefix pref (src/core/k3_ops.c:1035-1036), which its
+ * attention and AttnRes steps keep apart from h, where this chain adds it to h itself.
+ * Between layers the residual add and the next layer's norm are one launch. Only the
+ * routing crosses to the host (for the cache's get calls). When every expert of every
+ * layer in the chain is resident, the layers run back to back with no host
+ * synchronisation, every layer's routing comes back in one copy, and the cache's get
+ * calls follow, one step per layer, all hits. Layers in the tiled layout of the cache's
+ * bank. */
 int  k3gc_chain(K3gCtx *ctx, K3gCache *cache, const K3gLayer *layers,
                 const float *const *post_norm, int first_layer, int n_layers, float *h,
                 int T, float rms_eps, void *stream);

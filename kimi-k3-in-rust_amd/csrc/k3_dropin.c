@@ -115,6 +115,17 @@ static void host_copy(void *dst, const void *src, size_t n)
     }
 }
 
+/* Activations between the call's pinned staging and HBM: up to 1 MB by a copy kernel on
+ * the compute stream (the kernels before and after it need no hand-over to a copy engine
+ * and back, ~10 us each way at one token), larger ones by the copy engine. */
+#define XFER_KERNEL_MAX ((size_t)1 << 20)
+static void xfer(void *dst, const void *src, size_t n, hipMemcpyKind kind, hipStream_t st)
+{
+    if (!n) return;
+    if (n <= XFER_KERNEL_MAX && k3k_copy(dst, src, n, st) == 0) return;
+    K3G_CHECK(hipMemcpyAsync(dst, src, n, kind, st));
+}
+
 /* pinned host memory of at least `bytes`, grow-only */
 static unsigned char *pinned(DevState *s, size_t bytes)
 {
@@ -757,7 +768,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     float *rwt = (float *)(pin + o_wt), *pout = (float *)(pin + o_out);
     float *px = (float *)(pin + io_n);
     host_copy(px, x, xbytes);
-    K3G_CHECK(hipMemcpyAsync(xd, px, xbytes, hipMemcpyHostToDevice, st));
+    xfer(xd, px, xbytes, hipMemcpyHostToDevice, st);
     ctx->paths = 0;
     host_scratch(s, (size_t)T * k, E);
     int last[K3_MAX_TOPK];
@@ -775,7 +786,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         G.experts = k3gc_layer_table(hc, w->layer, st);
         if (!G.experts) k3g_fatal("k3_moe: expert table update failed");
         if (k3g_moe(ctx, &G, xd, T, od, didx, dwt, st) != 0) k3g_fatal("k3_moe: launch failed");
-        K3G_CHECK(hipMemcpyAsync(pin, io, io_n, hipMemcpyDeviceToHost, st));
+        xfer(pin, io, io_n, hipMemcpyDeviceToHost, st);
         K3G_CHECK(hipStreamSynchronize(st));
         if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error");
         f.table = s->table;
@@ -797,7 +808,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     }
 
     if (k3g_route(ctx, &G, xd, T, didx, dwt, st) != 0) k3g_fatal("k3_moe: router launch");
-    K3G_CHECK(hipMemcpyAsync(pin, io, o_out, hipMemcpyDeviceToHost, st));
+    xfer(pin, io, o_out, hipMemcpyDeviceToHost, st);
     K3G_CHECK(hipStreamSynchronize(st));
     if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error in the router");
     memcpy(last, ridx + (size_t)(T - 1) * k, (size_t)k * sizeof(int));
@@ -878,8 +889,8 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
                 k3g_fatal("k3_moe: expert table update failed");
             const size_t pk = (size_t)t0 * k, np = (size_t)(t1 - t0) * k;
             if (cache_only || drops0 != k3_expert_drops) {
-                K3G_CHECK(hipMemcpyAsync(didx + pk, ridx + pk, np * 4, hipMemcpyHostToDevice, st));
-                K3G_CHECK(hipMemcpyAsync(dwt + pk, rwt + pk, np * 4, hipMemcpyHostToDevice, st));
+                xfer(didx + pk, ridx + pk, np * 4, hipMemcpyHostToDevice, st);
+                xfer(dwt + pk, rwt + pk, np * 4, hipMemcpyHostToDevice, st);
             }
             /* the misses copy on the cache's stream: the routed experts wait for them
              * (the shared expert does not) */
@@ -896,8 +907,8 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
             t0 = t1;
         }
     }
-    K3G_CHECK(hipMemcpyAsync(pout, od, xbytes, hipMemcpyDeviceToHost, st));
-    K3G_CHECK(hipMemcpyAsync(perr, io, 4, hipMemcpyDeviceToHost, st));
+    xfer(pout, od, xbytes, hipMemcpyDeviceToHost, st);
+    xfer(perr, io, 4, hipMemcpyDeviceToHost, st);
     K3G_CHECK(hipStreamSynchronize(st));
     if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error");
     host_copy(out, pout, xbytes);

@@ -647,6 +647,21 @@ static int fits(const K3gCtx *c, const K3gLayer *L, int T)
     return 1;
 }
 
+/* fits() for the calls that read the routed experts: a layer whose experts are missing
+ * (no table for the MXFP4 formats, no w1/w3/w2 for the fp32 bank; a caller that freed
+ * its experts and serves them from an HBM cache passes the cache's table instead) is
+ * refused here rather than read on the device */
+static int fits_experts(const K3gCtx *c, const K3gLayer *L, int T)
+{
+    const int have = L->expert_fmt == K3G_EXPERT_F32 ? (L->w1 && L->w3 && L->w2)
+                                                     : L->experts != NULL;
+    if (!have) {
+        fprintf(stderr, "k3moe: the layer has no routed experts (table or fp32 bank)\n");
+        return 0;
+    }
+    return fits(c, L, T);
+}
+
 int k3g_route(K3gCtx *c, const K3gLayer *L, const float *x, int T, int32_t *idx, float *wt,
               hipStream_t st)
 {
@@ -716,7 +731,7 @@ static int routed_staged(K3gCtx *c, const K3gLayer *L, const float *z, int lat, 
 int k3g_experts(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
                 const float *wt, float *out, hipStream_t st)
 {
-    if (!fits(c, L, T)) return -1;
+    if (!fits_experts(c, L, T)) return -1;
     const int d = L->hidden, k = L->topk;
     const int SI = L->shared_inter, lat = L->latent > 0 ? L->latent : d;
     const int projected = L->down != NULL;
@@ -842,7 +857,7 @@ int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int
     hipStream_t st = stream ? (hipStream_t)stream : c->stream;
     if (!idx) idx = c->idx;
     if (!wt) wt = c->wt;
-    if (!fits(c, L, T)) return -1;
+    if (!fits_experts(c, L, T)) return -1;
     if (fusable(c, L, T)) {
         c->paths |= 2;
         return run_fused(c, L, x, T, out, idx, wt, 0, st);
@@ -920,7 +935,7 @@ int k3g_dispatch(K3gCtx *c, const int32_t *idx, int T, int topk, int n_experts, 
 int k3g_expert_gemv(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
                     float *contrib, void *stream)
 {
-    if (!c || !L || !x || !idx || !contrib || !fits(c, L, T)) return -1;
+    if (!c || !L || !x || !idx || !contrib || !fits_experts(c, L, T)) return -1;
     if (L->expert_fmt == K3G_EXPERT_MXFP4_TILED || L->down ||
         (L->latent > 0 && L->latent != L->hidden)) {
         fprintf(stderr, "k3g_expert_gemv: needs checkpoint-layout (or fp32) experts and no "
@@ -935,7 +950,7 @@ int k3g_expert_gemv(K3gCtx *c, const K3gLayer *L, const float *x, int T, const i
 static int grouped(K3gCtx *c, const K3gLayer *L, const float *x, int T, const int32_t *idx,
                    float *contrib, int fp8, void *stream)
 {
-    if (!c || !L || !x || !idx || !contrib || !fits(c, L, T)) return -1;
+    if (!c || !L || !x || !idx || !contrib || !fits_experts(c, L, T)) return -1;
     if (L->expert_fmt != K3G_EXPERT_MXFP4_TILED || L->down || L->up || L->latent_norm ||
         (L->latent > 0 && L->latent != L->hidden) || L->hidden % 32 || L->inter % 32) {
         fprintf(stderr, "k3g_grouped_gemm: needs experts in the tiled MXFP4 layout and no "

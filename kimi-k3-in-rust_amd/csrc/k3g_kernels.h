@@ -227,6 +227,15 @@ int k3k_set_i32(int32_t *p, int32_t v, hipStream_t st);
 /* y += a, elementwise */
 int k3k_add(float *y, const float *a, size_t n, hipStream_t st);
 
+/* Per token (rows of n): h += a when a is given (stored back), then y = RMSNorm(h) * w
+ * when w is given (k3k_rmsnorm's arithmetic); y may alias h. */
+int k3k_add_rmsnorm(float *h, const float *a, float *y, const float *w, int n, int T, float eps,
+                    hipStream_t st);
+
+/* dst <- src, n bytes, by a kernel on the stream (16-byte aligned pointers; either side may
+ * be pinned host memory). -1 on misaligned pointers. */
+int k3k_copy(void *dst, const void *src, size_t n, hipStream_t st);
+
 /* MXFP4 -> fp32, exact (k3_mxfp4_dequant semantics). */
 int k3k_dequant(float *out, const uint8_t *packed, const uint8_t *scales, int rows,
                 int pcols, int group, hipStream_t st);

@@ -273,30 +273,132 @@ extern "C" int k3k_combine(const float *contrib, const int32_t *idx, const float
 }
 
 /* ---------------------------------------------------------------- rmsnorm ---- */
-/* src/core/k3_ops.c:94-102; one token per block. */
-__global__ void __launch_bounds__(256)
-k_rmsnorm(float *y, const float *x, const float *w, int n, float eps)
+/* One token per block of 1024 threads: h += a (when a is given, stored back: the residual
+ * add of src/core/k3_ops.c:1035-1036), then y = w * h * inv with
+ * inv = (float)(1 / sqrt(sum_double h^2 / n + eps)) (src/core/k3_ops.c:94-102, float
+ * multiplies in the engine's order) when w is given. Every load of the token is issued
+ * before the first use; each thread owns elements 4 (tid + 1024 j) .. + 3 and is the only
+ * one to read or write them, so y may alias h. The sum of squares is fp64 (the squares of
+ * floats are exact in it) in a fixed order: per thread, then the wave, then the 16 waves
+ * in index order. NV = float4s per thread held in registers (n <= 4096 NV). */
+template <int NV>
+__global__ void __launch_bounds__(1024)
+k_add_rmsnorm(float *h, const float *a, float *y, const float *w, int n, float eps)
 {
-    __shared__ double part[4];
-    const float *xt = x + (size_t)blockIdx.x * n;
-    float *yt = y + (size_t)blockIdx.x * n;
+    __shared__ double part[16];
+    const size_t base = (size_t)blockIdx.x * n;
+    float4 *h4 = (float4 *)(h + base);
+    const float4 *a4 = a ? (const float4 *)(a + base) : nullptr;
+    const int n4 = n >> 2, tid = threadIdx.x;
+    float4 v[NV], av[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = tid + 1024 * j;
+        if (i < n4) {
+            v[j] = h4[i];
+            if (a4) av[j] = a4[i];
+        }
+    }
     double ss = 0.0;
-    for (int i = threadIdx.x; i < n; i += 256) ss = fma((double)xt[i], (double)xt[i], ss);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = tid + 1024 * j;
+        if (i < n4) {
+            if (a4) {
+                v[j].x = __fadd_rn(v[j].x, av[j].x);
+                v[j].y = __fadd_rn(v[j].y, av[j].y);
+                v[j].z = __fadd_rn(v[j].z, av[j].z);
+                v[j].w = __fadd_rn(v[j].w, av[j].w);
+                h4[i] = v[j];
+            }
+            ss = fma((double)v[j].x, (double)v[j].x, ss);
+            ss = fma((double)v[j].y, (double)v[j].y, ss);
+            ss = fma((double)v[j].z, (double)v[j].z, ss);
+            ss = fma((double)v[j].w, (double)v[j].w, ss);
+        }
+    }
+    if (!w) return;
     ss = k3d_wave_sumd(ss);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
     __syncthreads();
-    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    double tot = 0.0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) tot += part[q];
     const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 256) yt[i] = __fmul_rn(__fmul_rn(w[i], xt[i]), inv);
+    float4 *y4 = (float4 *)(y + base);
+    const float4 *w4 = (const float4 *)w;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int i = tid + 1024 * j;
+        if (i < n4) {
+            const float4 wv = w4[i];
+            float4 o;
+            o.x = __fmul_rn(__fmul_rn(wv.x, v[j].x), inv);
+            o.y = __fmul_rn(__fmul_rn(wv.y, v[j].y), inv);
+            o.z = __fmul_rn(__fmul_rn(wv.z, v[j].z), inv);
+            o.w = __fmul_rn(__fmul_rn(wv.w, v[j].w), inv);
+            y4[i] = o;
+        }
+    }
 }
 
+/* Any width: the same sums and products, element by element, in the same per-thread
+ * order (thread tid owns elements tid + 1024 j). */
+__global__ void __launch_bounds__(1024)
+k_add_rmsnorm_any(float *h, const float *a, float *y, const float *w, int n, float eps)
+{
+    __shared__ double part[16];
+    const size_t base = (size_t)blockIdx.x * n;
+    float *ht = h + base;
+    const float *at = a ? a + base : nullptr;
+    const int tid = threadIdx.x;
+    double ss = 0.0;
+    for (int i = tid; i < n; i += 1024) {
+        float v = ht[i];
+        if (at) {
+            v = __fadd_rn(v, at[i]);
+            ht[i] = v;
+        }
+        ss = fma((double)v, (double)v, ss);
+    }
+    if (!w) return;
+    ss = k3d_wave_sumd(ss);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) tot += part[q];
+    const float inv = (float)(1.0 / sqrt(tot / (double)n + (double)eps));
+    float *yt = y + base;
+    for (int i = tid; i < n; i += 1024) yt[i] = __fmul_rn(__fmul_rn(w[i], ht[i]), inv);
+}
+
+extern "C" int k3k_add_rmsnorm(float *h, const float *a, float *y, const float *w, int n, int T,
+                               float eps, hipStream_t st)
+{
+    if (T < 1 || n < 1) return 0;
+    if (!a && !w) return 0;
+    const bool v4 = n % 4 == 0 && (((uintptr_t)h | (uintptr_t)a | (uintptr_t)y | (uintptr_t)w) & 15) == 0;
+    const int nv = (n / 4 + 1023) / 1024;
+    if (v4 && nv <= 1)
+        hipLaunchKernelGGL(k_add_rmsnorm<1>, dim3(T), dim3(1024), 0, st, h, a, y, w, n, eps);
+    else if (v4 && nv <= 2)
+        hipLaunchKernelGGL(k_add_rmsnorm<2>, dim3(T), dim3(1024), 0, st, h, a, y, w, n, eps);
+    else if (v4 && nv <= 4)
+        hipLaunchKernelGGL(k_add_rmsnorm<4>, dim3(T), dim3(1024), 0, st, h, a, y, w, n, eps);
+    else
+        hipLaunchKernelGGL(k_add_rmsnorm_any, dim3(T), dim3(1024), 0, st, h, a, y, w, n, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+/* y = RMSNorm(x) * w, one token per block (y may alias x) */
 extern "C" int k3k_rmsnorm(float *y, const float *x, const float *w, int n, int T, float eps,
                            hipStream_t st)
 {
     if (T < 1 || n < 1) return 0;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), 0, st, y, x, w, n, eps);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+    if (!w) return -1;
+    /* with no addend the kernel only reads x */
+    return k3k_add_rmsnorm(const_cast<float *>(x), nullptr, y, w, n, T, eps, st);
 }
 
 __global__ void k_add(float *y, const float *a, size_t n)
@@ -312,6 +414,32 @@ extern "C" int k3k_add(float *y, const float *a, size_t n, hipStream_t st)
     const size_t blocks = (n + 255) / 256;
     hipLaunchKernelGGL(k_add, dim3(blocks < 4096 ? (unsigned)blocks : 4096u), dim3(256), 0, st,
                        y, a, n);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+/* dst <- src (n bytes) by a kernel on the stream: between pinned host memory and device
+ * memory this stays on the compute queue, with no hand-over to a copy engine and back.
+ * Both 16-byte aligned. */
+__global__ void __launch_bounds__(256) k_copy(uint4 *dst, const uint4 *src, size_t n16,
+                                              uint8_t *dtail, const uint8_t *stail, int ntail)
+{
+    const size_t g = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+    for (size_t i = g; i < n16; i += stride) dst[i] = src[i];
+    if (g < (size_t)ntail) dtail[g] = stail[g];
+}
+
+extern "C" int k3k_copy(void *dst, const void *src, size_t n, hipStream_t st)
+{
+    if (!n) return 0;
+    if ((((uintptr_t)dst | (uintptr_t)src) & 15) != 0) return -1;
+    const size_t n16 = n / 16;
+    const int ntail = (int)(n - 16 * n16);
+    size_t blocks = (n16 + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 1024) blocks = 1024;
+    hipLaunchKernelGGL(k_copy, dim3((unsigned)blocks), dim3(256), 0, st, (uint4 *)dst,
+                       (const uint4 *)src, n16, (uint8_t *)dst + 16 * n16,
+                       (const uint8_t *)src + 16 * n16, ntail);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

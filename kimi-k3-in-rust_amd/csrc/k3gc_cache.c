@@ -852,6 +852,7 @@ int k3gc_chain(K3gCtx *ctx, K3gCache *c, const K3gLayer *layers, const float *co
         c->chain_host_bytes = hneed;
     }
     float *hin = (float *)c->chain_dev, *tmp = (float *)(c->chain_dev + act);
+    /* the layers' routing: idx of layer l at rbase + rt l, its weights after all idx */
     unsigned char *rbase = c->chain_dev + 2 * act;
     /* every expert of every layer resident: the layers run back to back on the cache's
      * device tables with no host synchronisation, the accounting after them */
@@ -860,33 +861,36 @@ int k3gc_chain(K3gCtx *ctx, K3gCache *c, const K3gLayer *layers, const float *co
         resident = k3gc_layer_all_resident(c, first_layer + l);
     if (resident) k3gc_wait(c, st);
     int rc = 0;
+    /* hin = RMSNorm(h) x post_norm (src/core/k3_ops.c:1015-1016); between layers the
+     * residual add and the next layer's norm are one launch */
+    if (post_norm && post_norm[0] &&
+        k3k_add_rmsnorm(h, NULL, hin, post_norm[0], d, T, rms_eps, st) != 0)
+        return -1;
     for (int l = 0; l < n_layers && rc == 0; l++) {
         const K3gLayer *L = &layers[l];
-        const int layer = first_layer + l, P = T * L->topk;
-        int32_t *idx = (int32_t *)(rbase + 2 * rt * (size_t)l);
-        float *wt = (float *)(rbase + 2 * rt * (size_t)l + rt);
-        /* hin = RMSNorm(h) x post_norm (src/core/k3_ops.c:1015-1016) */
-        const float *in = h;
-        if (post_norm && post_norm[l]) {
-            if (k3k_rmsnorm(hin, h, post_norm[l], d, T, rms_eps, st) != 0) return -1;
-            in = hin;
-        }
+        const int layer = first_layer + l;
+        int32_t *idx = (int32_t *)(rbase + rt * (size_t)l);
+        float *wt = (float *)(rbase + rt * (size_t)(n_layers + l));
+        const float *in = post_norm && post_norm[l] ? hin : h;
         if (resident) {
             K3gLayer G = *L;
             G.experts = k3gc_layer_table(c, layer, st);
             G.expert_fmt = K3G_EXPERT_MXFP4_TILED;
             if (!G.experts) return -1;
             rc = k3g_moe(ctx, &G, in, T, tmp, idx, wt, st);
-            if (rc == 0)
-                K3G_CHECK(hipMemcpyAsync((unsigned char *)c->chain_host + rt * (size_t)l, idx,
-                                         (size_t)P * 4, hipMemcpyDeviceToHost, st));
         } else {
             rc = k3gc_moe(ctx, c, L, layer, in, T, tmp, idx, wt, NULL, NULL, st);
         }
-        /* h += the layer's MoE output (src/core/k3_ops.c:1035-1036) */
-        if (rc == 0) rc = k3k_add(h, tmp, (size_t)T * d, st);
+        /* h += the layer's MoE output (src/core/k3_ops.c:1035-1036), then the next
+         * layer's hin */
+        const float *next = post_norm && l + 1 < n_layers ? post_norm[l + 1] : NULL;
+        if (rc == 0) rc = k3k_add_rmsnorm(h, tmp, next ? hin : NULL, next, d, T, rms_eps, st);
     }
     if (resident && rc == 0) {
+        /* every layer's routing to the host in one copy on the compute stream */
+        if (k3k_copy(c->chain_host, rbase, rt * (size_t)n_layers, st) != 0)
+            K3G_CHECK(hipMemcpyAsync(c->chain_host, rbase, rt * (size_t)n_layers,
+                                     hipMemcpyDeviceToHost, st));
         K3G_CHECK(hipStreamSynchronize(st));
         for (int l = 0; l < n_layers && rc == 0; l++)
             rc = account_step(c, first_layer + l,

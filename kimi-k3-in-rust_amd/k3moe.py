@@ -604,6 +604,12 @@ class SynthLayer:
             if b is not None:
                 b.free()
                 setattr(self, name, None)
+        # the layer descriptors no longer name an expert table: a call that needs one is
+        # refused by the library instead of reading freed memory
+        for name in ("dev", "dev_tiled"):
+            L = getattr(self, name, None)
+            if L is not None:
+                L.experts = None
 
     def k3g_layer(self, tiled: bool = False) -> K3gLayer:
         s = self.shape
