@@ -61,8 +61,11 @@ typedef struct {
     int nmir, capmir;
     size_t mir_bytes;            /* device bytes the mirrors hold */
     uint64_t calls;
-    void *stage;                 /* scratch device buffer, grow-only */
+    void *stage;                 /* scratch device buffer of a call, grow-only */
     size_t stage_bytes;
+    void *mstage;                /* the mirrors' upload buffer, grow-only: a mirror checked
+                                    while a call runs uploads without touching its stage */
+    size_t mstage_bytes;
     K3ExpertQ *eq_dev;           /* [cap_e] device expert table */
     int cap_e;
     /* host scratch of a call, grow-only; the routing and the activations travel through
@@ -78,6 +81,7 @@ typedef struct {
     K3ExpertQ *table;
     unsigned char *have, *seen;
     int cap_host_e;
+    int defer;                   /* mirror lookups skip the fingerprint (checked later) */
 } DevState;
 
 #define K3_MAX_DEV 16
@@ -236,8 +240,17 @@ static void mirror_upload(DevState *s, Mirror *m, hipStream_t st)
         K3G_CHECK(hipMemcpy(m->dev, m->host, m->bytes, hipMemcpyHostToDevice));
         return;
     }
-    /* row-major bf16 to the staging buffer, then tiled into the mirror */
-    void *tmp = stage(s, m->bytes);
+    /* row-major bf16 to the mirrors' upload buffer, then tiled into the mirror */
+    if (m->bytes > s->mstage_bytes) {
+        if (s->mstage) {
+            K3G_CHECK(hipDeviceSynchronize());
+            K3G_CHECK(hipFree(s->mstage));
+        }
+        s->mstage = NULL;
+        K3G_CHECK(hipMalloc(&s->mstage, m->bytes));
+        s->mstage_bytes = m->bytes;
+    }
+    void *tmp = s->mstage;
     K3G_CHECK(hipMemcpy(tmp, m->host, m->bytes, hipMemcpyHostToDevice));
     if (k3k_tile_bf16((uint16_t *)m->dev, (const uint16_t *)tmp, m->rows, m->cols, st) != 0)
         k3g_fatal("tiling a bf16 weight matrix failed");
@@ -251,19 +264,22 @@ static const void *mirror_kind(DevState *s, const void *host, size_t bytes, int 
                                int cols, hipStream_t st)
 {
     if (!host || !bytes) return NULL;
-    const uint64_t fp = fingerprint(host, bytes);
     for (int i = 0; i < s->nmir; i++) {
         Mirror *m = &s->mir[i];
         if (m->host == host && m->bytes == bytes && m->kind == kind && m->rows == rows &&
             m->cols == cols) {
             m->used = s->calls;
-            if (m->print != fp) {
-                m->print = fp;
-                mirror_upload(s, m, st);
+            if (!s->defer) {
+                const uint64_t fp = fingerprint(host, bytes);
+                if (m->print != fp) {
+                    m->print = fp;
+                    mirror_upload(s, m, st);
+                }
             }
             return m->dev;
         }
     }
+    const uint64_t fp = fingerprint(host, bytes);
     const size_t db = kind == MIR_ROWMAJOR ? bytes : k3k_tiled_bf16_bytes(rows, cols);
     if (!db) k3g_fatal("a bf16 weight matrix has no tiled layout (rows % 16, cols % 32)");
     mirror_make_room(s, db);
@@ -300,6 +316,25 @@ static const void *mirror_tiled(DevState *s, const void *host, int rows, int col
     return mirror_kind(s, host, (size_t)rows * cols * 2, MIR_TILED_BF16, rows, cols, st);
 }
 
+/* The fingerprints of the mirrors this call uses, checked while its kernels run: on a
+ * change the stream is drained (the kernels read the old bytes) and the changed mirrors
+ * are uploaded again. Returns how many were; the caller then runs its work again. */
+static int verify_mirrors(DevState *s, hipStream_t st)
+{
+    int n = 0;
+    for (int i = 0; i < s->nmir; i++) {
+        Mirror *m = &s->mir[i];
+        if (m->used != s->calls) continue;
+        const uint64_t fp = fingerprint(m->host, m->bytes);
+        if (fp == m->print) continue;
+        if (!n) K3G_CHECK(hipStreamSynchronize(st));
+        m->print = fp;
+        mirror_upload(s, m, st);
+        n++;
+    }
+    return n;
+}
+
 static void *stage(DevState *s, size_t bytes)
 {
     if (bytes > s->stage_bytes) {
@@ -328,6 +363,9 @@ void k3moe_forget_weights(void)
         for (int i = 0; i < s->nmir; i++) hipFree(s->mir[i].dev);
         s->nmir = 0;
         s->mir_bytes = 0;
+        if (s->mstage) hipFree(s->mstage);
+        s->mstage = NULL;
+        s->mstage_bytes = 0;
     }
     hipSetDevice(cur);
     pthread_mutex_unlock(&g_lock);
@@ -696,6 +734,12 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     /* sizes first (the context may be recreated), then the mirrors on its stream */
     K3gCtx *ctx = ctx_for(s, &G, T);
     hipStream_t st = ctx->stream;
+    const int cache_only = w->cache_only && w->src && w->src->resident;
+    /* Every expert of the layer in the HBM cache: the whole layer runs at once (below);
+     * the mirrors' fingerprints are then checked while it runs */
+    const int resident = hc && fast && hc->bank->layout == K3G_EXPERT_MXFP4_TILED &&
+                         !cache_only && k3gc_layer_all_resident(hc, w->layer);
+    s->defer = resident;
     G.gate = (const float *)mirror(s, w->gate, (size_t)E * d * 4);
     G.bias = (const float *)mirror(s, w->bias, w->bias ? (size_t)E * 4 : 0);
     G.latent_norm = c->latent_norm ? (const float *)mirror(s, w->latent_norm, (size_t)L * 4)
@@ -725,6 +769,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
             G.w2 = (const float *)mirror(s, w->w2, (size_t)E * L * I * 4);
         }
     }
+    s->defer = 0;
 
     /* how fetched experts reach the kernels, and the staging this call needs */
     Fetcher f;
@@ -773,20 +818,22 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     host_scratch(s, (size_t)T * k, E);
     int last[K3_MAX_TOPK];
     float lastw[K3_MAX_TOPK];
-    const int cache_only = w->cache_only && w->src && w->src->resident;
 
     /* Every expert of the layer in the HBM cache: the whole layer runs at once against
      * the cache's device expert table (the fused decode kernel routes inside), and the
      * engine's getmany/get calls follow on the host in the engine's order, all hits: the
-     * same results and the same cache state and accounting as fetching first. */
-    const int resident = hc && fast && hc->bank->layout == K3G_EXPERT_MXFP4_TILED &&
-                         !cache_only && k3gc_layer_all_resident(hc, w->layer);
+     * same results and the same cache state and accounting as fetching first. A weight
+     * buffer found changed while the layer ran is uploaded again and the layer rerun. */
     if (resident) {
         k3gc_wait(hc, st);
         G.experts = k3gc_layer_table(hc, w->layer, st);
         if (!G.experts) k3g_fatal("k3_moe: expert table update failed");
-        if (k3g_moe(ctx, &G, xd, T, od, didx, dwt, st) != 0) k3g_fatal("k3_moe: launch failed");
-        xfer(pin, io, io_n, hipMemcpyDeviceToHost, st);
+        for (int pass = 0;; pass++) {
+            if (k3g_moe(ctx, &G, xd, T, od, didx, dwt, st) != 0)
+                k3g_fatal("k3_moe: launch failed");
+            xfer(pin, io, io_n, hipMemcpyDeviceToHost, st);
+            if (pass > 0 || !verify_mirrors(s, st)) break;
+        }
         K3G_CHECK(hipStreamSynchronize(st));
         if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error");
         f.table = s->table;

@@ -151,6 +151,43 @@ def test_weights_rewritten_in_place(gpu):
     assert rel_l2(out_c, oc) <= REL
 
 
+def test_resident_weights_rewritten_in_place(gpu):
+    """Every expert in a tiled HBM cache: the layer runs at once and the mirrors'
+    fingerprints are checked while it runs. Gate, bias and shared weights rewritten in
+    place with another layer's values between two calls: the second call must match the
+    oracle on the new weights (the changed mirrors upload again and the layer reruns)."""
+    say("case: k3_moe tiny layer T=1 through a tiled HBM cache holding every expert, "
+        "gate/bias/shared rewritten in place between calls")
+    a = k3moe.SynthLayer(k3moe.TINY, seed=53, layout="tiled")
+    b = k3moe.SynthLayer(k3moe.TINY, seed=54, device=False)
+    E = a.shape.n_experts
+    bank = tiled_bank(a)
+    slot = (bank.expert_bytes + 65535) // 65536 * 65536
+    cache = k3moe.Cache(bank, topk=a.shape.topk, budget_bytes=E * slot)
+    for e in range(E):
+        cache.prefetch(a.layer, e)
+    w = cache_weights(a, cache)
+    cfg = a.cfg()
+    x = a.tokens(1, stream_base=610)
+    out_a, idx_a, _, paths = dropin(w, cfg, x)
+    oa, oia, _ = O.k2_forward(a, x)
+    assert paths == FUSED
+    assert np.array_equal(idx_a, oia) and rel_l2(out_a, oa) <= REL
+    for name in ("gate", "bias", "sh1", "sh3", "sh2"):
+        np.copyto(getattr(a, name), getattr(b, name))
+    d0 = drops()
+    out_b, idx_b, _, paths = dropin(w, cfg, x)
+    ob, oib, _ = O.k2_forward(a, x)
+    say(f"  after the rewrite: rel-L2 {rel_l2(out_b, ob):.3e} "
+        f"(the first call's output against it: {rel_l2(out_a, ob):.3e})")
+    assert paths == FUSED and drops() == d0
+    assert rel_l2(out_a, ob) > 1e-2
+    assert np.array_equal(idx_b, oib)
+    assert rel_l2(out_b, ob) <= REL
+    cache.free()
+    bank.free()
+
+
 # ------------------------------------------------------------- HBM expert cache ----
 
 @pytest.mark.parametrize("layout", ["tiled", "checkpoint"])
