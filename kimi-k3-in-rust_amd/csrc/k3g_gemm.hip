@@ -147,6 +147,48 @@ __device__ __forceinline__ void gm_dma16(const void *src, uint32_t lds)
                  : "=&s"(keep) : "v"(src), "s"(lds) : "memory");
 }
 
+/* The same DMA with a wave-uniform base in scalar registers and this lane's 32-bit byte
+ * offset in one vector register: no per-lane 64-bit address to build or keep. */
+__device__ __forceinline__ void gm_dma16s(const void *sbase, uint32_t voff, uint32_t lds)
+{
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %3\n\t"
+                 "global_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+
+__device__ __forceinline__ void gm_dma4s(const void *sbase, uint32_t voff, uint32_t lds)
+{
+    uint32_t keep;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %3\n\t"
+                 "global_load_lds_dword %1, %2\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep) : "v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+
+/* a wave-uniform pointer, in scalar registers */
+template <typename P>
+__device__ __forceinline__ P *gm_uniform_ptr(P *p)
+{
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (P *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+/* raw buffer descriptor over `bytes` at p (p wave-uniform): loads take a scalar offset
+ * and this lane's vector offset */
+typedef __amdgpu_buffer_rsrc_t gm_rsrc;
+__device__ __forceinline__ gm_rsrc gm_make_rsrc(const void *p, size_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(bytes < 0x7fffffffu ? bytes : 0x7fffffffu),
+                                             0x00020000);
+}
+
 /* s_waitcnt vmcnt(N) (expcnt, lgkmcnt not waited on) */
 template <int N>
 __device__ __forceinline__ void gm_wait_vm()
@@ -294,6 +336,7 @@ struct GmTile {
     uint32_t boff[8];          /* element offsets of this lane's DMA rows (+ swizzled slot) */
     uint32_t lds;              /* LDS byte address of the staging buffers */
     uint8_t *ldsp;
+    uint32_t rbb;              /* bytes of one 16-row block of the weight matrix */
 };
 
 /* The tile's GEMM with NB 16-column blocks and NP activation pieces in a workgroup of WV
@@ -505,17 +548,41 @@ __device__ __forceinline__ void gm_tile(const K3kGemm &g, const GmTile &t)
     }
 }
 
+/* Instruction order of one step of the down GEMM's matrix work: NB FP8 groups (the
+ * remainder: 3 LDS reads, 4 scaled MFMAs each), then 4 NB bf16 groups (piece 0: 1 LDS
+ * read, 4 MFMAs each), the reads AH groups ahead of the MFMAs that use them. */
+template <int NB, int AH>
+__device__ __forceinline__ void gm_pipeline_mix()
+{
+    constexpr int NG = 5 * NB;
+    constexpr int PRO = AH <= NB ? 3 * AH : 3 * NB + (AH - NB);
+    __builtin_amdgcn_sched_group_barrier(0x100, PRO, 0);     /* DS read */
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);   /* MFMA */
+        if (j + AH < NB) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+        else if (j + AH < NG) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+}
+
 /* The down GEMM of MXFP4 experts with h as bf16 piece 0 (bf16 matrix cores, as gm_tile)
  * plus its MX remainder (scaled FP8 matrix cores, one 16x16x128 instruction per step
  * on the same weight registers, at twice the bf16 rate): three quarters of the matrix
  * time of two bf16 pieces. Stage c % 2: piece 0 (GM_PIECE, gm_tile's layout), then the
  * remainder's bytes and scales (GM_F8_STAGE, k_gemm_f8's layout). The weight and DMA
  * pipeline is gm_tile's with two stages: a step waits for all but the 8 weight loads
- * issued after its stage's DMA. */
+ * issued after its stage's DMA.
+ *
+ * The tile's B rows are sorted positions p0 .. p0 + 127, contiguous: every DMA takes a
+ * uniform base in scalar registers (the tile's first row, advanced per step) and a
+ * loop-invariant byte offset per lane (bofb: piece 0, doff: remainder bytes, soff:
+ * remainder scales, all relative to row p0); the weights load through one buffer
+ * descriptor per row group with the step in the scalar offset. No per-lane 64-bit
+ * address is kept, which leaves the registers for the LDS read-ahead. */
 template <int NB>
 __device__ __forceinline__ void gm_tile_mix(const K3kGemm &g, const GmTile &t,
-                                            const uint32_t (&doff)[2], uint32_t soff, int nd,
-                                            int ns)
+                                            const uint32_t (&bofb)[4], const uint32_t (&doff)[2],
+                                            uint32_t soff, int nd, int ns)
 {
     k3v4f acc[4][NB];
 #pragma unroll
@@ -524,29 +591,36 @@ __device__ __forceinline__ void gm_tile_mix(const K3kGemm &g, const GmTile &t,
         for (int cb = 0; cb < NB; ++cb) acc[r][cb] = k3v4f{0.f, 0.f, 0.f, 0.f};
     const int lane = t.lane;
     constexpr uint32_t ST = GM_PIECE + GM_F8_STAGE;
+    const uint8_t *b0 = gm_uniform_ptr((const uint8_t *)(g.b + (size_t)t.p0 * g.ldb));
+    const uint8_t *q0 = gm_uniform_ptr(g.bq + (size_t)t.p0 * g.ldhq);
+    const uint8_t *s0 = gm_uniform_ptr(g.bs + (size_t)t.p0 * (g.ldhq / 32));
     auto dma = [&](int c) {
         const uint32_t st = t.lds + (c & 1) * ST;
-        const uint16_t *b = g.b + (size_t)c * GM_KC;
+        const uint8_t *b = b0 + (size_t)c * (2 * GM_KC);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            if (i < t.ndma) gm_dma16(b + t.boff[i], st + t.w * 1024 + i * 8 * 1024);
-        const uint8_t *q = g.bq + (size_t)c * GM_KC;
+            if (i < t.ndma) gm_dma16s(b, bofb[i], st + t.w * 1024 + i * 8 * 1024);
+        const uint8_t *q = q0 + (size_t)c * GM_KC;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            if (i < nd) gm_dma16(q + doff[i], st + GM_PIECE + (8 * i + t.w) * 1024);
-        if (t.w < ns) gm_dma4(g.bs + soff + 4 * c, st + GM_PIECE + GM_F8_DATA + t.w * 256);
+            if (i < nd) gm_dma16s(q, doff[i], st + GM_PIECE + (8 * i + t.w) * 1024);
+        if (t.w < ns) gm_dma4s(s0 + 4 * c, soff, st + GM_PIECE + GM_F8_DATA + t.w * 256);
     };
     const uint8_t *brow = t.ldsp + (lane & 15) * 256;
     const int q4 = lane >> 4, c0 = lane & 15;
+    gm_rsrc ar[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ar[r] = gm_make_rsrc(t.abase[r], t.rbb);
+    const int v16 = 16 * lane, v4 = 4 * lane;
     uint4 ab[3][4];
     uint32_t sbuf[3][4];
     auto aload = [&](int c, uint4 (&dst)[4], uint32_t (&sdst)[4]) {
-        const size_t qo = (size_t)(c >> 2) * GM_QT;
+        const int so = (c >> 2) * GM_QT;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint8_t *p = t.abase[r] + qo;
-            dst[r] = gm_ld16(p + 1024 * (c & 3) + 16 * lane);
-            sdst[r] = gm_ld4(p + 4096 + 4 * lane);
+            dst[r] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(ar[r], v16, so + 1024 * (c & 3), 0));
+            sdst[r] = __builtin_amdgcn_raw_buffer_load_b32(ar[r], v4, so + 4096, 0);
         }
     };
     auto step = [&](int c, const uint4 (&cur)[4], const uint32_t (&scl)[4], uint4 (&nxt)[4],
@@ -574,7 +648,6 @@ __device__ __forceinline__ void gm_tile_mix(const K3kGemm &g, const GmTile &t,
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     acc[r][cb] = gm_mma_f8(cur[r], (scl[r] >> (8 * j)) & 0xffu, bv, sb, acc[r][cb]);
-                if (cb & 1) __builtin_amdgcn_sched_barrier(0);
             }
             float sc[4];
 #pragma unroll
@@ -596,6 +669,9 @@ __device__ __forceinline__ void gm_tile_mix(const K3kGemm &g, const GmTile &t,
                     for (int r = 0; r < 4; ++r) acc[r][cb] = gm_mma(a[r], bv, acc[r][cb]);
                 }
             }
+            /* the reads three groups ahead (where the registers allow it: a full tile of 8
+             * column blocks keeps the compiler's own order, without spilling) */
+            gm_pipeline_mix<NB, 3>();
         }
     };
     aload(0, ab[0], sbuf[0]);
@@ -645,7 +721,7 @@ __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *l
     int e = 0;
     if (g.tiles) {
         const int4 tv = ((const int4 *)g.tiles)[tile];
-        e = tv.x; t.p0 = tv.y; t.np = tv.z;
+        e = gm_uniform(tv.x); t.p0 = gm_uniform(tv.y); t.np = gm_uniform(tv.z);
     } else {
         t.p0 = tile * GM_COLS;
         t.np = min(GM_COLS, g.dense_rows - t.p0);
@@ -673,13 +749,14 @@ __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *l
     }
     /* bytes per 16-row block */
     const size_t rbb = AF == 0 ? (size_t)((g.K + 511) / 512) * GM_QT : (size_t)(g.K / 32) * 1024;
+    t.rbb = (uint32_t)rbb;
     if (g.mode == 0) {
         t.orow0 = 32 * WV * f + 32 * t.w;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int row = t.orow0 + 16 * (r & 1);
             t.rv[r] = t.orow0 < g.rows;
-            t.abase[r] = (r < 2 ? m0 : m1) + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
+            t.abase[r] = gm_uniform_ptr((r < 2 ? m0 : m1) + (size_t)(t.rv[r] ? row / 16 : 0) * rbb);
         }
     } else {
         t.orow0 = 64 * WV * f + 64 * t.w;
@@ -687,7 +764,7 @@ __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *l
         for (int r = 0; r < 4; ++r) {
             const int row = t.orow0 + 16 * r;
             t.rv[r] = row < g.rows;
-            t.abase[r] = m0 + (size_t)(t.rv[r] ? row / 16 : 0) * rbb;
+            t.abase[r] = gm_uniform_ptr(m0 + (size_t)(t.rv[r] ? row / 16 : 0) * rbb);
         }
     }
     return true;
@@ -742,27 +819,35 @@ k_gemm(const K3kGemm g)
              * fills rows 8 (8 i + w) .. + 7; waves 0 and 1 fill the scales of rows 0 .. 63
              * and 64 .. 127 */
             mixed = true;
+            /* offsets relative to the tile's first row p0 (its rows are p0 .. p0 + 127) */
+            auto rel = [&](int r) { return r < t.np ? r : 0; };
+            uint32_t bofb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * (8 * i + t.w) + (t.lane >> 4);
+                bofb[i] = 2u * ((uint32_t)rel(r) * (uint32_t)g.ldb + (uint32_t)qoff);
+            }
             uint32_t doff[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int r = 8 * (8 * i + t.w) + (t.lane >> 3);
                 const int ls = (t.lane & 7) ^ ((r >> 1) & 7);
                 const int u = (ls & 1) ? 4 + (ls >> 1) : (ls >> 1);
-                doff[i] = (uint32_t)gm_src_row(g, t, r) * (uint32_t)g.ldhq + 16 * u;
+                doff[i] = (uint32_t)rel(r) * (uint32_t)g.ldhq + 16 * u;
             }
             const int nd = min(2, (2 * nb + 7 - t.w) / 8);
             const int ns = nb > 4 ? 2 : 1;
             const uint32_t soff =
-                (uint32_t)gm_src_row(g, t, 64 * min(t.w, 1) + t.lane) * (uint32_t)(g.ldhq / 32);
+                (uint32_t)rel(64 * min(t.w, 1) + t.lane) * (uint32_t)(g.ldhq / 32);
             switch (nb) {
-                case 1: gm_tile_mix<1>(g, t, doff, soff, nd, ns); break;
-                case 2: gm_tile_mix<2>(g, t, doff, soff, nd, ns); break;
-                case 3: gm_tile_mix<3>(g, t, doff, soff, nd, ns); break;
-                case 4: gm_tile_mix<4>(g, t, doff, soff, nd, ns); break;
-                case 5: gm_tile_mix<5>(g, t, doff, soff, nd, ns); break;
-                case 6: gm_tile_mix<6>(g, t, doff, soff, nd, ns); break;
-                case 7: gm_tile_mix<7>(g, t, doff, soff, nd, ns); break;
-                case 8: gm_tile_mix<8>(g, t, doff, soff, nd, ns); break;
+                case 1: gm_tile_mix<1>(g, t, bofb, doff, soff, nd, ns); break;
+                case 2: gm_tile_mix<2>(g, t, bofb, doff, soff, nd, ns); break;
+                case 3: gm_tile_mix<3>(g, t, bofb, doff, soff, nd, ns); break;
+                case 4: gm_tile_mix<4>(g, t, bofb, doff, soff, nd, ns); break;
+                case 5: gm_tile_mix<5>(g, t, bofb, doff, soff, nd, ns); break;
+                case 6: gm_tile_mix<6>(g, t, bofb, doff, soff, nd, ns); break;
+                case 7: gm_tile_mix<7>(g, t, bofb, doff, soff, nd, ns); break;
+                case 8: gm_tile_mix<8>(g, t, bofb, doff, soff, nd, ns); break;
                 default: break;
             }
         }
