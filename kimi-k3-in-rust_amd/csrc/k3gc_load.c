@@ -18,6 +18,7 @@
 
 #include <dirent.h>
 #include <fcntl.h>
+#include <limits.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -165,7 +166,8 @@ static int scan_shard(K3gcSt *st, int shard, const char *path)
     uint64_t hlen = 0;
     for (int i = 7; i >= 0; i--) hlen = (hlen << 8) | lb[i];
     struct stat sb;
-    if (fstat(fd, &sb) != 0 || hlen == 0 || (uint64_t)sb.st_size < 8 + hlen) {
+    if (fstat(fd, &sb) != 0 || hlen == 0 || sb.st_size < 8 ||
+        hlen > (uint64_t)sb.st_size - 8) {
         fprintf(stderr, "k3gc: %s: impossible header length %llu\n", path, (unsigned long long)hlen);
         return -1;
     }
@@ -212,7 +214,8 @@ static int scan_shard(K3gcSt *st, int shard, const char *path)
                     if (!js_lit(&s, '[')) goto done;
                     if (!js_lit(&s, ']')) for (;;) {
                         int64_t dim;
-                        if (!js_i64(&s, &dim) || dim < 0) goto done;
+                        /* the expert API takes dimensions as int */
+                        if (!js_i64(&s, &dim) || dim < 0 || dim > INT_MAX) goto done;
                         if (t.ndim >= 4) { fprintf(stderr, "k3gc: %s: rank > 4\n", name); goto done; }
                         t.shape[t.ndim++] = dim;
                         if (js_lit(&s, ',')) continue;
@@ -231,18 +234,24 @@ static int scan_shard(K3gcSt *st, int shard, const char *path)
                 if (js_lit(&s, '}')) break;
                 goto done;
             }
-            if (!have_dt || !have_off || o1 < o0) {
-                fprintf(stderr, "k3gc: %s: %s lacks dtype or data_offsets\n", path, name);
+            if (!have_dt || !have_off || o0 < 0 || o1 < o0) {
+                fprintf(stderr, "k3gc: %s: %s lacks dtype or valid data_offsets\n", path, name);
                 goto done;
             }
-            int64_t numel = 1;
-            for (int i = 0; i < t.ndim; i++) numel *= t.shape[i];
+            /* elements x element size and the span's end, with every product and sum
+             * checked (an untrusted header must not overflow them) */
+            int64_t numel = 1, span = 0, end = 0;
+            for (int i = 0; i < t.ndim; i++)
+                if (__builtin_mul_overflow(numel, t.shape[i], &numel)) goto overflow;
+            if (__builtin_mul_overflow(numel, elem, &span) ||
+                __builtin_add_overflow(base, o1, &end))
+                goto overflow;
             t.off = base + o0;
             t.nbytes = o1 - o0;
             /* the span must equal elements x element size, and lie inside the file */
-            if (t.nbytes != numel * elem || base + o1 > (int64_t)sb.st_size) {
+            if (t.nbytes != span || end > (int64_t)sb.st_size) {
                 fprintf(stderr, "k3gc: %s: %s spans %lld bytes, its shape %lld\n", path, name,
-                        (long long)t.nbytes, (long long)(numel * elem));
+                        (long long)t.nbytes, (long long)span);
                 goto done;
             }
             t.name = strdup(name);
@@ -253,6 +262,9 @@ static int scan_shard(K3gcSt *st, int shard, const char *path)
         goto done;
     }
     rc = 0;
+    goto done;
+overflow:
+    fprintf(stderr, "k3gc: %s: a tensor's size overflows\n", path);
 done:
     if (rc) fprintf(stderr, "k3gc: %s: malformed header near byte %ld\n", path, (long)(s.p - json));
     free(json);

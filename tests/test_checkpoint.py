@@ -160,3 +160,37 @@ def test_loader_refusals(tmp_path):
     # no shards at all
     with pytest.raises(RuntimeError):
         k3moe.St(str(tmp_path))
+
+
+def _raw_shard(path, header: str, data: bytes = b"", hlen=None):
+    h = header.encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h) if hlen is None else hlen))
+        f.write(h)
+        f.write(data)
+
+
+@pytest.mark.parametrize("case", ["negative_offset", "numel_overflow", "dim_past_int",
+                                  "span_past_file", "header_length_wraps"])
+def test_loader_refuses_crafted_headers(tmp_path, case):
+    """Headers an untrusted shard could carry: an offset before the data section (a read
+    into the header), a shape whose element count overflows 64 bits, a dimension past what
+    the expert API's int holds, a span past the end of the file, and a header length that
+    would wrap the size check. Each shard must be refused, not indexed."""
+    d = str(tmp_path / case)
+    os.makedirs(d)
+    f = os.path.join(d, "a.safetensors")
+    if case == "negative_offset":
+        _raw_shard(f, '{"t": {"dtype": "U8", "shape": [16], "data_offsets": [-8, 8]}}', bytes(8))
+    elif case == "numel_overflow":
+        _raw_shard(f, '{"t": {"dtype": "U8", "shape": [2147483647, 2147483647, 2147483647], '
+                      '"data_offsets": [0, 8]}}', bytes(8))
+    elif case == "dim_past_int":
+        _raw_shard(f, '{"t": {"dtype": "U8", "shape": [2147483648, 0], "data_offsets": [0, 0]}}')
+    elif case == "span_past_file":
+        _raw_shard(f, '{"t": {"dtype": "U8", "shape": [64], "data_offsets": [0, 64]}}', bytes(8))
+    else:
+        _raw_shard(f, '{"t": {"dtype": "U8", "shape": [8], "data_offsets": [0, 8]}}', bytes(8),
+                   hlen=(1 << 64) - 1)
+    with pytest.raises(RuntimeError):
+        k3moe.St(d)
