@@ -436,6 +436,10 @@ typedef struct K3gcSt K3gcSt;
 int  k3gc_st_open(K3gcSt **st, const char *dir);
 void k3gc_st_close(K3gcSt *st);
 int  k3gc_st_count(const K3gcSt *st);            /* tensors indexed */
+/* Shards read with O_DIRECT (contiguous runs, through the enclosing 4096-byte window, as
+ * the engine's k3_st_read_aligned, src/io/k3_st.c:457-497); the others, and every shard
+ * when K3GC_NO_DIRECT is set at open, use ordinary reads. */
+int  k3gc_st_direct(const K3gcSt *st);
 
 /* One routed expert's six U8 tensors (w1, w2, w3: weight_packed, weight_scale), validated
  * as the engine's k3_expert_ref does (src/io/k3_load.c:15-100): 2-D, rows agreeing, one

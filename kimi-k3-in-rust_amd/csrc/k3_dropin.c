@@ -595,9 +595,12 @@ static void fetch_tokens(Fetcher *f, DevState *s, int *ridx, int k, int E, int t
         return;
     }
     /* src/core/k3_ops.c:707-766: 64-token chunks, unique experts in first-seen order,
-     * one get() each */
-    for (int c0 = t0; c0 < t1; c0 += 64) {
-        const int n = t1 - c0 < 64 ? t1 - c0 : 64;
+     * one get() each; the chunks are the engine's [64 m, 64 m + 64) whatever token a
+     * group starts at (a group that began inside a chunk the cache could not hold at
+     * once ends at its boundary) */
+    for (int c0 = t0, c1; c0 < t1; c0 = c1) {
+        c1 = (c0 / 64 + 1) * 64 < t1 ? (c0 / 64 + 1) * 64 : t1;
+        const int n = c1 - c0;
         if (n == 1) {
             /* a one-token chunk takes k3_moe's per-slot path (:709-710) */
             fetch_tokens(f, s, ridx, k, E, c0, c0 + 1, 0, 0);
@@ -643,8 +646,10 @@ static void settle_tokens(unsigned char *seen, const int *ridx, int k, int E, in
 }
 
 /* The end of the next token group from t0: whole units (one token, or a 64-token prefill
- * chunk) while the group's distinct experts fit in cap slots; a unit that alone exceeds
- * cap is split into tokens (at least one: the cache holds top-k + 1 slots). */
+ * chunk, the engine's [64 m, 64 m + 64)) while the group's distinct experts fit in cap
+ * slots; a unit that alone exceeds cap is split into tokens (at least one: the cache
+ * holds top-k + 1 slots), and the group after a split ends at the chunk's boundary, so
+ * later chunks keep the engine's alignment. */
 static int next_group(DevState *s, const int *ridx, int k, int E, int T, int t0, int unit,
                       int cap)
 {
@@ -652,7 +657,8 @@ static int next_group(DevState *s, const int *ridx, int k, int E, int T, int t0,
     memset(seen, 0, (size_t)E);
     int n = 0, t1 = t0;
     while (t1 < T) {
-        const int u1 = t1 + unit < T ? t1 + unit : T;
+        const int ue = (t1 / unit + 1) * unit;
+        const int u1 = ue < T ? ue : T;
         const int add = add_tokens(seen, ridx, k, E, t1, u1);
         const int fits = n + add <= cap;
         settle_tokens(seen, ridx, k, E, t1, u1, fits);

@@ -453,7 +453,10 @@ int k3gc_init(K3gCache **out, int device, K3gcBank *bank, int topk, int64_t budg
     K3gCache *c = (K3gCache *)calloc(1, sizeof *c);
     if (!c) return -1;
     c->src.get = cache_get;
-    c->src.getmany = cache_getmany;
+    /* K3_NOPREFETCH set: no batch path (src/cache/k3_cache.c:268-274), so one binary can
+     * time the layer with and without it; get() then copies each miss itself */
+    c->src.getmany = getenv("K3_NOPREFETCH") ? NULL : cache_getmany;
+    if (!c->src.getmany) fprintf(stderr, "k3gc: batch prefetch disabled by K3_NOPREFETCH\n");
     c->src.resident = cache_resident;
     c->src.ctx = c;
     c->bank = bank;
@@ -758,7 +761,8 @@ int k3gc_moe(K3gCtx *ctx, K3gCache *c, const K3gLayer *L, int layer, const float
         }
         k3gc_step_begin(c);
         for (int i = 0; i < nu; i += K3_MAX_TOPK)
-            cache_getmany(&c->src, layer, uniq + i, nu - i < K3_MAX_TOPK ? nu - i : K3_MAX_TOPK);
+            if (c->src.getmany)
+                c->src.getmany(&c->src, layer, uniq + i, nu - i < K3_MAX_TOPK ? nu - i : K3_MAX_TOPK);
         K3kEqSet set;
         memset(&set, 0, sizeof set);
         for (int i = 0; i < nu && rc == 0; i++) {
@@ -808,7 +812,8 @@ static int account_step(K3gCache *c, int layer, const int32_t *idx, int P, hipSt
     }
     k3gc_step_begin(c);
     for (int i = 0; i < nu; i += K3_MAX_TOPK)
-        cache_getmany(&c->src, layer, uniq + i, nu - i < K3_MAX_TOPK ? nu - i : K3_MAX_TOPK);
+        if (c->src.getmany)
+            c->src.getmany(&c->src, layer, uniq + i, nu - i < K3_MAX_TOPK ? nu - i : K3_MAX_TOPK);
     for (int i = 0; i < nu; i++)
         if (cache_get(&c->src, layer, uniq[i], NULL) != 0) rc = -1;
     k3gc_step_end(c, st);

@@ -12,7 +12,15 @@
  * (src/io/k3_load.c:15-100, src/io/k3_load.h:3-9). Here the run goes straight into the
  * bank: one read when contiguous (six reads in the run order otherwise, :123-135), into
  * the bank's pinned memory for the checkpoint layout, or through a buffer and the host
- * tiler for the tiled layout the matrix cores stream. */
+ * tiler for the tiled layout the matrix cores stream.
+ *
+ * A contiguous run is read with O_DIRECT where the filesystem takes it, as the engine's
+ * k3_expert_load_direct does (src/io/k3_st.c:457-497, K3_ST_ALIGN 4096): the read is
+ * widened to the enclosing 4096-byte window of the file, lands in a 4096-aligned buffer,
+ * and the run is copied out of it. Several hundred GB of experts then do not pass through
+ * (and evict everything else from) the page cache. Shards whose filesystem refuses
+ * O_DIRECT, and scattered runs, use ordinary reads. */
+#define _GNU_SOURCE            /* O_DIRECT */
 #include "k3gc_cache.h"
 #include "k3g_kernels.h"
 
@@ -32,10 +40,14 @@ typedef struct {
     int64_t off, nbytes;          /* absolute file offset, bytes */
 } StTensor;
 
+#define ST_ALIGN 4096
+#define ST_READ_MAX ((int64_t)1 << 30)
+
 struct K3gcSt {
     int nshard;
     char **path;
     int *fd;
+    int *dfd;                     /* O_DIRECT descriptor of each shard, or -1 */
     StTensor *t;                  /* sorted by name */
     int nt, capt;
 };
@@ -286,10 +298,12 @@ void k3gc_st_close(K3gcSt *st)
     if (!st) return;
     for (int i = 0; i < st->nshard; i++) {
         if (st->fd && st->fd[i] >= 0) close(st->fd[i]);
+        if (st->dfd && st->dfd[i] >= 0) close(st->dfd[i]);
         if (st->path) free(st->path[i]);
     }
     for (int i = 0; i < st->nt; i++) free(st->t[i].name);
     free(st->fd);
+    free(st->dfd);
     free(st->path);
     free(st->t);
     free(st);
@@ -328,8 +342,13 @@ int k3gc_st_open(K3gcSt **out, const char *dir)
     /* shard numbers stable across machines: sorted by name, not readdir order */
     qsort(st->path, (size_t)st->nshard, sizeof *st->path, cmp_path);
     st->fd = (int *)malloc((size_t)st->nshard * sizeof(int));
-    if (!st->fd) { k3gc_st_close(st); return -1; }
-    for (int i = 0; i < st->nshard; i++) st->fd[i] = -1;
+    st->dfd = (int *)malloc((size_t)st->nshard * sizeof(int));
+    if (!st->fd || !st->dfd) { k3gc_st_close(st); return -1; }
+    for (int i = 0; i < st->nshard; i++) st->fd[i] = st->dfd[i] = -1;
+    /* K3GC_NO_DIRECT set: ordinary reads only (one binary, both read paths) */
+    const int direct = getenv("K3GC_NO_DIRECT") == NULL;
+    for (int i = 0; i < st->nshard && direct; i++)
+        st->dfd[i] = open(st->path[i], O_RDONLY | O_DIRECT);   /* -1: not supported */
     for (int i = 0; i < st->nshard; i++)
         if (scan_shard(st, i, st->path[i]) != 0) { k3gc_st_close(st); return -1; }
     qsort(st->t, (size_t)st->nt, sizeof *st->t, cmp_name);
@@ -423,12 +442,46 @@ static int read_full(int fd, unsigned char *dst, int64_t n, int64_t off)
     return 0;
 }
 
-/* The run's bytes in the checkpoint order into dst: one read when contiguous, six
- * otherwise (src/io/k3_load.c:105-136). */
+/* The 4096-byte-aligned window around [off, off + n) with O_DIRECT into an aligned
+ * buffer, then the span into dst. Returns 0, or -1 (the caller then reads buffered). The
+ * last window of a shard may run past its end: a short read is fine once the span is in. */
+static int read_direct(int dfd, unsigned char *dst, int64_t n, int64_t off)
+{
+    const int64_t lo = off & ~(int64_t)(ST_ALIGN - 1);
+    const int64_t hi = (off + n + ST_ALIGN - 1) & ~(int64_t)(ST_ALIGN - 1);
+    const int64_t len = hi - lo, pad = off - lo;
+    void *buf = NULL;
+    if (posix_memalign(&buf, ST_ALIGN, (size_t)len) != 0) return -1;
+    int64_t got = 0;
+    while (got < len) {
+        const int64_t want = len - got < ST_READ_MAX ? len - got : ST_READ_MAX;
+        const ssize_t r = pread(dfd, (char *)buf + got, (size_t)want, (off_t)(lo + got));
+        if (r <= 0) break;
+        got += r;
+    }
+    const int ok = got >= pad + n;
+    if (ok) memcpy(dst, (char *)buf + pad, (size_t)n);
+    free(buf);
+    return ok ? 0 : -1;
+}
+
+int k3gc_st_direct(const K3gcSt *st)
+{
+    int n = 0;
+    for (int i = 0; st && st->dfd && i < st->nshard; i++) n += st->dfd[i] >= 0;
+    return n;
+}
+
+/* The run's bytes in the checkpoint order into dst: one read when contiguous (O_DIRECT
+ * where the shard has it), six otherwise (src/io/k3_load.c:105-136). */
 int k3gc_st_read_run(const K3gcSt *st, const K3gcExpertRun *r, unsigned char *dst)
 {
     const int fd = st->fd[r->shard];
-    if (r->contiguous) return read_full(fd, dst, r->nbytes, r->off);
+    if (r->contiguous) {
+        const int dfd = st->dfd ? st->dfd[r->shard] : -1;
+        if (dfd >= 0 && read_direct(dfd, dst, r->nbytes, r->off) == 0) return 0;
+        return read_full(fd, dst, r->nbytes, r->off);
+    }
     int64_t o = 0;
     for (int i = 0; i < 3; i++) {
         if (read_full(fd, dst + o, r->p_bytes[i], r->p_file[i]) != 0) return -1;

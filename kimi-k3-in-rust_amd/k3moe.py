@@ -255,6 +255,8 @@ def lib() -> C.CDLL:
         L.k3gc_st_close.restype = None
         L.k3gc_st_count.argtypes = [vp]
         L.k3gc_st_count.restype = i
+        L.k3gc_st_direct.argtypes = [vp]
+        L.k3gc_st_direct.restype = i
         L.k3gc_st_expert.argtypes = [vp, i, i, C.POINTER(K3gcExpertRun)]
         L.k3gc_st_expert.restype = i
         L.k3gc_st_read_run.argtypes = [vp, C.POINTER(K3gcExpertRun), vp]
@@ -819,6 +821,10 @@ class St:
     def count(self) -> int:
         return lib().k3gc_st_count(self.ptr)
 
+    def direct(self) -> int:
+        """shards read with O_DIRECT"""
+        return lib().k3gc_st_direct(self.ptr)
+
     def expert(self, layer: int, e: int) -> K3gcExpertRun:
         r = K3gcExpertRun()
         if lib().k3gc_st_expert(self.ptr, layer, e, C.byref(r)) != 0:
@@ -865,7 +871,8 @@ class Cache:
         self.src_ptr = lib().k3gc_src(self.ptr)
         src = K3ExpertSrc.from_address(self.src_ptr)
         self._get = SRC_GET(src.get)
-        self._getmany = SRC_GETMANY(src.getmany)
+        # no batch path when the cache was made with K3_NOPREFETCH set
+        self._getmany = SRC_GETMANY(src.getmany) if src.getmany else None
         self._resident = SRC_RESIDENT(src.resident)
 
     def get(self, layer: int, e: int):
@@ -874,6 +881,8 @@ class Cache:
         return q if rc == 0 else None
 
     def getmany(self, layer: int, experts) -> int:
+        if self._getmany is None:
+            return 0
         a = np.ascontiguousarray(experts, np.int32)
         return self._getmany(self.src_ptr, layer, a.ctypes.data, a.size)
 
@@ -903,6 +912,16 @@ class Cache:
 
     def reset_stats(self) -> None:
         lib().k3gc_reset_stats(self.ptr)
+
+    def trace(self) -> np.ndarray:
+        """The (layer, expert) pairs of every get() so far, in order, [n][2] int32 (the
+        engine's expert_trace.bin format, through k3gc_dump_trace)."""
+        import tempfile
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "trace.bin")
+            if lib().k3gc_dump_trace(self.ptr, path.encode()) != 0:
+                return np.zeros((0, 2), np.int32)
+            return np.fromfile(path, np.int32).reshape(-1, 2)
 
     def report(self, label: str = "") -> None:
         lib().k3gc_report(self.ptr, label.encode())

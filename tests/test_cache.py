@@ -126,6 +126,23 @@ def test_device_src_vtable_is_exposed():
     assert src.get and src.getmany and src.resident
 
 
+def test_no_prefetch_switch(monkeypatch):
+    """src/cache/k3_cache.c:268-274: K3_NOPREFETCH set at init leaves the source without
+    its batch path (getmany NULL), so one binary times the layer both ways; get() still
+    serves every request."""
+    monkeypatch.setenv("K3_NOPREFETCH", "1")
+    c = dry_cache(1, 6, 4)
+    src = k3moe.K3ExpertSrc.from_address(c.src_ptr)
+    assert src.get and src.resident and not src.getmany
+    for e in (0, 1, 0, 2):
+        assert c.get(0, e) is not None
+    st = c.stats()
+    assert (st.hits, st.misses, st.prefetch_reads) == (1, 3, 0)
+    monkeypatch.delenv("K3_NOPREFETCH")
+    c2 = dry_cache(1, 6, 4)
+    assert k3moe.K3ExpertSrc.from_address(c2.src_ptr).getmany
+
+
 # ------------------------------------------------------------ policy beyond LRU ----
 # docs/data/expert-cache-capacity.txt:20-28 (the engine's tools/sim_cache.py on its
 # recorded trace): capacity in GB, slots of one K3 expert, LRU / BELADY / PIN+LRU hit rates

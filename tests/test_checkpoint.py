@@ -50,6 +50,25 @@ def test_index_of_the_engine_fixture():
         st.expert(1, 0)
 
 
+@pytest.mark.parametrize("direct", [True, False])
+def test_fixture_runs_with_and_without_o_direct(monkeypatch, direct):
+    """Contiguous runs read with O_DIRECT (the enclosing 4096-byte window into an aligned
+    buffer, src/io/k3_st.c:457-497) and with ordinary reads (K3GC_NO_DIRECT) give the same
+    bytes: the fixture's 1632-byte runs start at offsets that are not 4096-aligned, so the
+    window's padding is exercised. Where the filesystem refuses O_DIRECT the reader falls
+    back and the bytes still match."""
+    if not direct:
+        monkeypatch.setenv("K3GC_NO_DIRECT", "1")
+    st = k3moe.St(FIXTURE)
+    if not direct:
+        assert st.direct() == 0
+    print(f"shards read with O_DIRECT: {st.direct()}")
+    runs = _fixture_runs()
+    assert any(st.expert(0, e).off % 4096 for e in range(24))
+    for e in range(24):
+        assert np.array_equal(st.read_run(st.expert(0, e)), runs[e]), e
+
+
 def test_fixture_runs_into_a_bank_byte_exact():
     runs = _fixture_runs()
     bank = k3moe.Bank(1, 24, expert_bytes=1632, raw=True)

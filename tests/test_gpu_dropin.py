@@ -224,6 +224,59 @@ def test_small_cache_never_drops(gpu, layout):
     bank.free()
 
 
+def test_prefill_chunks_keep_engine_alignment(gpu):
+    """k3_moe_prefill through a cache too small for some 64-token chunks: those chunks run
+    in token groups, and every chunk the cache can hold still asks for its experts as the
+    engine does (src/core/k3_ops.c:707-766): its unique experts in first-seen order, one
+    get() each, as one run of the cache's request trace, chunks in order. A group that
+    starts inside a split chunk must end at that chunk's boundary for this to hold."""
+    shape = k3moe.Shape("d=256 E=64 k=2 I=128", 256, 64, 2, 128, x_bf16=False)
+    layer = k3moe.SynthLayer(shape, seed=67, layout="tiled")
+    T, k = 640, shape.topk
+    x = layer.tokens(T, stream_base=680)
+    uniq = []
+    for c0 in range(0, T, 64):
+        seen = []
+        for t in range(c0, c0 + 64):
+            idx, _ = O.oracle().router(x[t], layer.gate, layer.bias, shape.n_experts, k,
+                                       shape.renorm, shape.routed_scale)
+            for e in idx:
+                if int(e) not in seen:
+                    seen.append(int(e))
+        uniq.append(seen)
+    counts = [len(u) for u in uniq]
+    # a capacity with a chunk that splits before a chunk that fits
+    cap = next((c for c in sorted(set(counts))
+                if any(counts[i] > c >= counts[j] for i in range(len(counts))
+                       for j in range(i + 1, len(counts)))), None)
+    assert cap is not None and cap >= k + 1, counts
+    say(f"case: k3_moe_prefill T={T}, E=64 top-2, chunks' distinct experts {counts}, "
+        f"cache of {cap} slots")
+    bank = tiled_bank(layer)
+    slot = (bank.expert_bytes + 65535) // 65536 * 65536
+    cache = k3moe.Cache(bank, topk=k, budget_bytes=cap * slot)
+    assert cache.stats().nslot == cap
+    w = cache_weights(layer, cache)
+    d0 = drops()
+    out, _, _, paths = dropin(w, layer.cfg(), x, prefill=True)
+    wo, cfgo, keepo = O.k2_weights(layer, list(range(shape.n_experts)))
+    oo, _, _ = O.oracle().moe(wo, cfgo, x, prefill=True)
+    assert drops() == d0 and rel_l2(out, oo) <= REL
+    trace = [int(e) for e in cache.trace()[:, 1]]
+    at, held = 0, 0
+    for m, u in enumerate(uniq):
+        if counts[m] > cap:
+            continue
+        n = len(u)
+        pos = next((p for p in range(at, len(trace) - n + 1) if trace[p:p + n] == u), None)
+        assert pos is not None, f"chunk {m}'s requests are not the engine's"
+        at, held = pos + n, held + 1
+    say(f"  {held} chunks that fit ask for their experts in the engine's order; "
+        f"{len(trace)} get() calls")
+    cache.free()
+    bank.free()
+
+
 def test_k2_through_tiled_cache(gpu):
     """The K2 layer through the drop-in with its experts in a tiled HBM cache: one token on
     the fused decode kernel, 8 tokens on the grouped GEMMs, and a 64-token prefill through
