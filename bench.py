@@ -589,8 +589,8 @@ def k3_shape(a):
     """The real Kimi-K3 LatentMoE layer on the device API: d 7168, 896 MXFP4 experts top-16
     at latent 3584 x I 3072, bf16 latent down/up projections, RMSNorm of the aggregate, two
     shared experts fused (6144), SiTU(4, 25), routed scale 1.0; synthetic seeded weights.
-    Decode (1 token, 2 layers round-robin) and a --k3-prefill-tokens prefill, on the
-    grouped matrix-core GEMMs."""
+    Decode (1 token, 2 layers round-robin) on the fused decode kernel and a
+    --k3-prefill-tokens prefill on the grouped matrix-core GEMMs."""
     import ctypes as C
     import numpy as np
     import k3moe
@@ -661,7 +661,9 @@ def k3_shape(a):
     res = {"decode": {"us_per_token": round(us, 2), "bytes_per_token": tok_bytes,
                       "hbm_GBps": round(tok_bytes / (us * 1e-6) / 1e9, 1),
                       "hbm_frac": round(tok_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                      "steps": a.steps, "kernels": "router + grouped GEMMs (latent)"}}
+                      "steps": a.steps,
+                      "kernels": "fused decode kernel: router, top-k, latent down, routed "
+                                 "experts on z, aggregate + RMSNorm, latent up, shared"}}
     if Tp > 0:
         def run():
             ctx.moe(Ls[0], dx.ptr, Tp, dout.ptr, didx.ptr, dwt.ptr)

@@ -288,6 +288,9 @@ int  k3g_ctx_stage_ms(K3gCtx *ctx, double *ms, int64_t *count, int n);
 /* k3g_moe runs a Kimi-K2-shaped layer at up to 4 tokens as one fused persistent kernel
  * (default on); off forces the staged kernels. No reference counterpart. */
 void k3g_ctx_set_fused(K3gCtx *ctx, int on);
+/* The kernels the context's calls ran since the last clear: bit 0 the staged VALU kernels,
+ * bit 1 the fused decode kernel, bit 2 the grouped GEMMs; clear != 0 resets it. */
+int  k3g_ctx_paths(K3gCtx *ctx, int clear);
 
 /* Routed experts of calls beyond the fused decode kernel on the FP4 x FP8 matrix cores
  * (v_mfma_scale_f32_16x16x128_f8f6f4): MXFP4 weights as stored, x and the activation h

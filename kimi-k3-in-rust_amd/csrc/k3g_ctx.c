@@ -121,7 +121,18 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t o_sgpart = carve(&at, (size_t)K3G_KS_SG * T4 * 2 * (SI ? SI : 1) * 4);
     const size_t o_shpart = carve(&at, (size_t)K3G_KS_SD * T4 * d * 4);
     const size_t o_rpart = carve(&at, (size_t)T4 * E * K3G_KS_R * 16);
-    const size_t o_dcontrib = carve(&at, P4 * K3G_KS_D * d * 4);
+    const size_t dl = d > L ? d : L;       /* the routed down's output rows */
+    const size_t o_dcontrib = carve(&at, P4 * K3G_KS_D * dl * 4);
+    /* the latent layer's: z's slices and FP8 pieces, the aggregate, its tiles' sums of
+     * squares, its bf16 pieces, the latent up's slices */
+    const int lat = L != d;
+    const size_t nQL = (L + 511) / 512;
+    const size_t o_dzpart = carve(&at, lat ? (size_t)K3G_KS_LD * T4 * L * 4 : 16);
+    const size_t o_dzq8 = carve(&at, lat ? (size_t)T4 * nQL * 8448 : 16);
+    const size_t o_daccl = carve(&at, lat ? (size_t)T4 * L * 4 : 16);
+    const size_t o_dnss = carve(&at, lat ? (size_t)T4 * (L / 32) * 8 : 16);
+    const size_t o_daq16 = carve(&at, lat ? (L / 32 + 1) * 1024 : 16);
+    const size_t o_dupart = carve(&at, lat ? (size_t)K3G_KS_LU * T4 * d * 4 : 16);
     /* the grouped GEMMs' activation pieces and column tiles */
     const size_t d128 = (d + 127) / 128 * 128, I128 = (I + 127) / 128 * 128;
     const size_t SI128 = (SI + 127) / 128 * 128;
@@ -164,8 +175,11 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t o_xq8b = carve(&at, T * q512 + T * q512 / 32);
     const size_t o_hq8b = carve(&at, P * I512 + P * I512 / 32);
     /* two banks of counters, one per call in turn; each a multiple of 256 bytes */
-    c->sync_bytes = (k3k_decode_sync_bytes(T4, (int)d, (int)E, (int)k, (int)I, (int)SI) + 255) &
-                    ~(size_t)255;
+    /* the larger of the latent layer's geometry and the plain one (a layer without the
+     * latent projections may run on a context sized for them) */
+    const size_t sb_l = k3k_decode_sync_bytes(T4, (int)d, (int)E, (int)k, (int)I, (int)SI, (int)L);
+    const size_t sb_d = k3k_decode_sync_bytes(T4, (int)d, (int)E, (int)k, (int)I, (int)SI, (int)d);
+    c->sync_bytes = ((sb_l > sb_d ? sb_l : sb_d) + 255) & ~(size_t)255;
     const size_t o_sync = carve(&at, 2 * c->sync_bytes);
     c->ws_bytes = at;
     if (hipMalloc(&c->ws, at) != hipSuccess) {
@@ -201,6 +215,12 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     c->shpart = (float *)(b + o_shpart);
     c->rpart = (double *)(b + o_rpart);
     c->dcontrib = (float *)(b + o_dcontrib);
+    c->dzpart = (float *)(b + o_dzpart);
+    c->dzq8 = (uint8_t *)(b + o_dzq8);
+    c->daccl = (float *)(b + o_daccl);
+    c->dnss = (double *)(b + o_dnss);
+    c->daq16 = (uint16_t *)(b + o_daq16);
+    c->dupart = (float *)(b + o_dupart);
     c->sync = (int *)(b + o_sync);
     c->xb = (uint16_t *)(b + o_xb);
     c->hb = (uint16_t *)(b + o_hb);
@@ -320,16 +340,28 @@ void k3g_ctx_force_exact(K3gCtx *c, int mode) { if (c) c->force_exact = mode; }
 
 void k3g_ctx_set_fused(K3gCtx *c, int on) { if (c) c->fused = on; }
 
+int k3g_ctx_paths(K3gCtx *c, int clear)
+{
+    if (!c) return 0;
+    const int p = c->paths;
+    if (clear) c->paths = 0;
+    return p;
+}
+
 void k3g_ctx_set_trace(K3gCtx *c, void *dev_buf) { if (c) c->trace = (unsigned long long *)dev_buf; }
 
-/* The fused kernel covers the Kimi-K2 layer shape at decode token counts, with the
- * routed experts and the shared expert in the tiled layouts. */
+/* The fused kernel covers decode token counts with the routed experts and the shared
+ * expert in the tiled layouts: the Kimi-K2 layer shape (no latent), and the LatentMoE
+ * layer (Kimi-K3: both latent projections in the tiled bf16 layout, the aggregate's
+ * RMSNorm when given). */
 static int fusable(const K3gCtx *c, const K3gLayer *L, int T)
 {
     const int lat = L->latent > 0 ? L->latent : L->hidden;
-    return c->fused && T <= 4 && L->expert_fmt == K3G_EXPERT_MXFP4_TILED && !L->down &&
-           !L->up && !L->latent_norm && lat == L->hidden && L->hidden % 32 == 0 &&
-           L->inter % 32 == 0 &&
+    const int plain = !L->down && !L->up && !L->latent_norm && lat == L->hidden;
+    const int latent = L->down && L->up && lat != L->hidden && lat % 32 == 0 &&
+                       lat <= c->latent && L->wdt == K3_WBF16 && L->shared_fmt == 1;
+    return c->fused && T <= 4 && L->expert_fmt == K3G_EXPERT_MXFP4_TILED && (plain || latent) &&
+           L->hidden % 32 == 0 && L->inter % 32 == 0 &&
            (L->shared_inter == 0 || (L->wdt == K3_WBF16 && L->shared_fmt == 1 &&
                                      L->shared_inter % 32 == 0));
 }
@@ -834,6 +866,20 @@ static int run_fused(K3gCtx *c, const K3gLayer *L, const float *x, int T, float 
     a.contrib = c->dcontrib;
     a.shpart = c->shpart;
     a.rpart = c->rpart;
+    const int lat = L->latent > 0 ? L->latent : L->hidden;
+    a.L = lat;
+    if (lat != L->hidden) {
+        a.down = (const uint16_t *)L->down;
+        a.up = (const uint16_t *)L->up;
+        a.lnorm = L->latent_norm;
+        a.rms_eps = L->rms_eps;
+        a.zpart = c->dzpart;
+        a.zq8 = c->dzq8;
+        a.accl = c->daccl;
+        a.nss = c->dnss;
+        a.aq16 = c->daq16;
+        a.upart = c->dupart;
+    }
     const int words = (int)(c->sync_bytes / 4);
     a.sync = c->sync + (size_t)(c->epoch & 1) * words;
     a.sync_clear = c->sync + (size_t)((c->epoch & 1) ^ 1) * words;

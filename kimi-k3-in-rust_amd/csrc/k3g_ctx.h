@@ -50,6 +50,11 @@ struct K3gCtx {
     uint8_t *xq8, *hq8;
     uint16_t *xq16, *hq16;
     float *gpart, *sgpart, *shpart, *dcontrib;
+    /* the fused kernel's latent-layer buffers (k3g_decode.hip) */
+    float *dzpart, *daccl, *dupart;
+    uint8_t *dzq8;
+    double *dnss;
+    uint16_t *daq16;
     double *rpart;
     int *sync;
     size_t sync_bytes;

@@ -83,6 +83,13 @@ typedef unsigned int k3v4u __attribute__((ext_vector_type(4)));
 #define K3_EVLINES (NREP * REP_STRIDE)
 
 /* ------------------------------------------------------------ geometry ---- */
+/* Ticket classes in order: X R S [LD] SG SD G D [NR LU]. The bracketed ones exist only for
+ * the LatentMoE layer (L != d): LD the latent down projection z = down x (32 rows x a K
+ * slice; the last slice of a row tile writes z's FP8 pieces for the routed gate/up), NR
+ * the aggregate's RMSNorm into bf16 pieces (64 columns each), LU the latent up projection
+ * (32 output rows x a K slice; the last arrival of an output tile, over LU's and the shared
+ * down's slices, writes out). There the routed gate/up reads z (K = L), the routed down
+ * produces L rows, and its last arrival per 32 rows writes the slot-order aggregate. */
 struct K3Geo {
     int T, P, nQd, nCd, nQi, nCsi;
     int KSS, KSG, KSD, KSR, KSDN; /* K slices of SG, G, SD, R, D tickets */
@@ -90,41 +97,60 @@ struct K3Geo {
     int nSGt, nGt, nSDt, nDt;    /* row tiles (SG: row groups of SG_TILES tiles) */
     int nX, nR, nSG, nG, nSD, nD, total;
     int oSG, oG, oSD, oD;        /* first ticket of each class after S */
+    /* the latent layer */
+    int lat, L, Dout, nQk;       /* L; D's output rows (L or d); G's K in 512-column quads */
+    int nCL, KSLD, KSLU, nLDt, nLUt, nNR, nLD, nLU, oLD, oNR, oLU;
     /* counter lines */
-    int lR, lSD, lD, lTSG, lTG, lRE, lDT, cX, cX16, cR, cSGF, cGF, eX, eX16, eR, eSEL, eSGF,
-        eGF, nlines;
+    int lR, lSD, lD, lTSG, lTG, lRE, lDT, lLD, lLU, cX, cX16, cR, cSGF, cGF, cZ, cA, cN, eX,
+        eX16, eR, eSEL, eSGF, eGF, eZ, eA, eN, nlines;
 };
 
-__host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int SI)
+__host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int SI, int L)
 {
     K3Geo g;
     g.T = T;
     g.P = T * k;
+    if (L <= 0) L = d;           /* 0: no latent layer */
+    g.lat = L != d;
+    g.L = L;
+    g.Dout = g.lat ? L : d;
     g.nQd = (d + 511) / 512;
+    g.nQk = g.lat ? (L + 511) / 512 : g.nQd;
     g.nCd = d / 32;
+    g.nCL = L / 32;
     g.nQi = (I + 511) / 512;
     g.nCsi = SI / 32;
     g.KSS = SI > 0 ? (K3G_KS_SG < g.nCd ? K3G_KS_SG : g.nCd) : 0;
-    g.KSG = K3G_KS_G < g.nQd ? K3G_KS_G : g.nQd;
+    g.KSG = K3G_KS_G < g.nQk ? K3G_KS_G : g.nQk;
     g.KSD = SI > 0 ? (K3G_KS_SD < g.nCsi ? K3G_KS_SD : g.nCsi) : 0;
     g.nRc = (d + 1023) / 1024;
     g.KSR = K3G_KS_R < g.nRc ? K3G_KS_R : g.nRc;
     g.KSDN = K3G_KS_D < g.nQi ? K3G_KS_D : g.nQi;
+    g.KSLD = g.lat ? (K3G_KS_LD < g.nCd ? K3G_KS_LD : g.nCd) : 0;
+    g.KSLU = g.lat ? (K3G_KS_LU < g.nCL ? K3G_KS_LU : g.nCL) : 0;
     g.nSGt = (SI + 16 * SG_TILES - 1) / (16 * SG_TILES);
     g.nGt = I / 32;
     g.nSDt = SI > 0 ? d / 32 : 0;
-    g.nDt = d / 32;
+    g.nDt = g.Dout / 32;
+    g.nLDt = g.lat ? L / 32 : 0;
+    g.nLUt = g.lat ? d / 32 : 0;
+    g.nNR = g.lat ? (L + 63) / 64 : 0;
     g.nX = T * ((g.nCd + 1) / 2);
     g.nR = E * g.KSR;
+    g.nLD = g.nLDt * g.KSLD;
     g.nSG = g.nSGt * g.KSS;
     g.nG = g.P * g.nGt * g.KSG;
     g.nSD = g.nSDt * g.KSD;
     g.nD = g.P * g.nDt * g.KSDN;
-    g.total = g.nX + g.nR + 1 + g.nSG + g.nG + g.nSD + g.nD;
-    g.oSG = g.nX + g.nR + 1;
+    g.nLU = g.nLUt * g.KSLU;
+    g.oLD = g.nX + g.nR + 1;
+    g.oSG = g.oLD + g.nLD;
     g.oSD = g.oSG + g.nSG;
     g.oG = g.oSD + g.nSD;
     g.oD = g.oG + g.nG;
+    g.oNR = g.oD + g.nD;
+    g.oLU = g.oNR + g.nNR;
+    g.total = g.oLU + g.nLU;
     /* counters: one 128-byte line each; events: a counter plus NREP replicated flags */
     g.lR = 0;
     g.lSD = g.lR + NSUB;
@@ -133,18 +159,26 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.lTG = g.lTSG + g.nSGt;
     g.lRE = g.lTG + g.P * g.nGt;
     g.lDT = g.lRE + E;
+    g.lLD = g.lDT + g.nDt;
+    g.lLU = g.lLD + g.nLDt;
     /* event counters: a top line and NSUB sub-counter lines each (k3d_arrive_event2) */
-    g.cX = g.lDT + g.nDt;
+    g.cX = g.lLU + g.nLUt;
     g.cX16 = g.cX + 1 + NSUB;
     g.cR = g.cX16 + 1 + NSUB;
     g.cSGF = g.cR + 1 + NSUB;
-    g.cGF = g.cSGF + 1 + NSUB;
+    g.cZ = g.cSGF + 1 + NSUB;
+    g.cA = g.cZ + 1 + NSUB;
+    g.cN = g.cA + 1 + NSUB;
+    g.cGF = g.cN + 1 + NSUB;
     g.eX = g.cGF + g.P * (1 + NSUB);
     g.eX16 = g.eX + K3_EVLINES;
     g.eR = g.eX16 + K3_EVLINES;
     g.eSEL = g.eR + K3_EVLINES;
     g.eSGF = g.eSEL + K3_EVLINES;
-    g.eGF = g.eSGF + K3_EVLINES;
+    g.eZ = g.eSGF + K3_EVLINES;
+    g.eA = g.eZ + K3_EVLINES;
+    g.eN = g.eA + K3_EVLINES;
+    g.eGF = g.eN + K3_EVLINES;
     g.nlines = g.eGF + g.P * K3_EVLINES;
     return g;
 }
@@ -524,7 +558,7 @@ struct K3Dec {
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const int tk = k3d_uniform(tk_);
-        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
         const int npair = (G.nCd + 1) / 2;
         const int t = tk / npair, i = tk - t * npair;
         const K3Rsrc r8 = k3d_rsrc(a.xq8 + (size_t)t * G.nQd * K3G_BQ, (size_t)G.nQd * K3G_BQ);
@@ -548,14 +582,18 @@ struct K3Dec {
             }
             k3d_arrive_event2(a.sync, G.cX16, G.nX, tk, G.eX16, lane);
         }
-        float r = v;
+        /* x's FP8 pieces feed the routed gate/up; the latent layer's routed experts read
+         * z's instead (the LD tickets make them) */
+        if (!G.lat) {
+            float r = v;
 #pragma unroll
-        for (int pc = 0; pc < NPC8; ++pc) {
-            int sx;
-            const uint32_t q = k3d_fp8_piece(r, sx);
-            if (on) {
-                k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_data(b, e, pc), q);
-                if (e == 0) k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_scale(b, pc), sx + 127);
+            for (int pc = 0; pc < NPC8; ++pc) {
+                int sx;
+                const uint32_t q = k3d_fp8_piece(r, sx);
+                if (on) {
+                    k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_data(b, e, pc), q);
+                    if (e == 0) k3d_st8_sc1(r8, Q * K3G_BQ + k3d_bq_scale(b, pc), sx + 127);
+                }
             }
         }
         k3d_arrive_event2(a.sync, G.cX, G.nX, tk, G.eX, lane);
@@ -568,7 +606,7 @@ struct K3Dec {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         if (a.given) return;
         const int tk = k3d_uniform(tk_);
-        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
         const int e = tk / G.KSR, r = tk - e * G.KSR;
         const int ch0 = r * G.nRc / G.KSR, ch1 = (r + 1) * G.nRc / G.KSR;
         const K3Rsrc rg = k3d_rsrc(a.gate + (size_t)e * a.d, (size_t)a.d * 4);
@@ -679,7 +717,7 @@ struct K3Dec {
     static __device__ __noinline__ void select(K3ArgPtr ap, int lane, K3SelectLds *lds)
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
-        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
         if (a.given) {
             /* the routing came with the call: publish it once x's pieces exist */
             if (!k3d_wait_event(a.sync, G.eX, 0, a.spin_limit, a.err, lane)) return;
@@ -707,7 +745,7 @@ struct K3Dec {
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const int tk = k3d_uniform(tk_);
-        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
         const int rg = tk / G.KSS, ks = tk - rg * G.KSS;    /* row group, K slice */
         const int c0 = ks * G.nCd / G.KSS, c1 = (ks + 1) * G.nCd / G.KSS;
         const size_t mb = (size_t)a.SI * a.d * 2;
@@ -811,12 +849,14 @@ struct K3Dec {
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const int tk = k3d_uniform(tk_);
-        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
         const int per = G.nGt * G.KSG;
         const int p = tk / per, rem = tk - p * per;
         const int gt = rem / G.KSG, ks = rem - gt * G.KSG;
-        const int q0 = ks * G.nQd / G.KSG, q1 = (ks + 1) * G.nQd / G.KSG;
+        const int q0 = ks * G.nQk / G.KSG, q1 = (ks + 1) * G.nQk / G.KSG;
         if (!k3d_wait_event(a.sync, G.eSEL, tk, a.spin_limit, a.err, lane)) return;
+        /* the latent layer's routed input is z = down x */
+        if (G.lat && !k3d_wait_event(a.sync, G.eZ, tk, a.spin_limit, a.err, lane)) return;
         k3d_trace_go(a.trace, G.oG + tk, lane);
         const int e = k3d_uniform(__hip_atomic_load(&a.idx[p], __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT));
@@ -825,11 +865,12 @@ struct K3Dec {
         if (e >= 0 && e < a.E) {
             const uint8_t *w1 = k3d_uniform_ptr((const uint8_t *)a.eq[e].p1);
             const uint8_t *w3 = k3d_uniform_ptr((const uint8_t *)a.eq[e].p3);
-            const size_t mb = (size_t)(a.I / 16) * G.nQd * K3G_QT;
+            const size_t mb = (size_t)(a.I / 16) * G.nQk * K3G_QT;
             const K3Rsrc r1 = k3d_rsrc(w1, mb), r3 = k3d_rsrc(w3, mb);
-            const K3Rsrc rb = k3d_rsrc(a.xq8 + (size_t)t * G.nQd * K3G_BQ, (size_t)G.nQd * K3G_BQ);
+            const uint8_t *bsrc = G.lat ? a.zq8 : a.xq8;
+            const K3Rsrc rb = k3d_rsrc(bsrc + (size_t)t * G.nQk * K3G_BQ, (size_t)G.nQk * K3G_BQ);
             const bool bon = (lane & 15) < NPC8;
-            const int rs = G.nQd * K3G_QT;                    /* bytes per row block */
+            const int rs = G.nQk * K3G_QT;                    /* bytes per row block */
             const int o0 = 2 * gt * rs + lane * 16, o1 = o0 + rs;
             for (int Q = q0; Q < q1; ++Q) {
                 const int qo = Q * K3G_QT;
@@ -911,7 +952,7 @@ struct K3Dec {
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const int tk = k3d_uniform(tk_);
-        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
         const int rt = tk / G.KSD, ks = tk - rt * G.KSD;
         const int c0 = ks * G.nCsi / G.KSD, c1 = (ks + 1) * G.nCsi / G.KSD;
         const K3Rsrc r2 = k3d_rsrc(a.sh2, (size_t)a.d * a.SI * 2);
@@ -953,8 +994,12 @@ struct K3Dec {
             k3d_st4_sc1(rp, ((ks * a.T + t) * a.d + row) * 4, y0);
             k3d_st4_sc1(rp, ((ks * a.T + t) * a.d + row + 16) * 4, y1);
         }
-        if (k3d_arrive(k3d_line(a.sync, G.lDT + rt), G.P * G.KSDN + G.KSD - 1, lane))
+        if (G.lat) {
+            if (k3d_arrive(k3d_line(a.sync, G.lLU + rt), G.KSLU + G.KSD - 1, lane))
+                combine_out(a, G, rt, lane);
+        } else if (k3d_arrive(k3d_line(a.sync, G.lDT + rt), G.P * G.KSDN + G.KSD - 1, lane)) {
             combine_rows(a, G, rt, lane);
+        }
     }
 
     /* ----------------------------------------------------------------- D ---- */
@@ -962,7 +1007,7 @@ struct K3Dec {
     {
         const K3kDecode a = *k3d_uniform_cptr(ap);
         const int tk = k3d_uniform(tk_);
-        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
         const int per = G.nDt * G.KSDN;
         const int p = tk / per, rem = tk - p * per;
         const int dt = rem / G.KSDN, ks = rem - dt * G.KSDN;
@@ -973,7 +1018,7 @@ struct K3Dec {
         k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
         if (e >= 0 && e < a.E) {
             const uint8_t *w2 = k3d_uniform_ptr((const uint8_t *)a.eq[e].p2);
-            const K3Rsrc r2 = k3d_rsrc(w2, (size_t)(a.d / 16) * G.nQi * K3G_QT);
+            const K3Rsrc r2 = k3d_rsrc(w2, (size_t)(G.Dout / 16) * G.nQi * K3G_QT);
             const K3Rsrc rb = k3d_rsrc(a.hq8 + (size_t)p * G.nQi * K3G_BQ, (size_t)G.nQi * K3G_BQ);
             const bool bon = (lane & 15) < NPC8;
             const int rs = G.nQi * K3G_QT;
@@ -1018,13 +1063,291 @@ struct K3Dec {
         y0 = k3d_colsum(y0);
         y1 = k3d_colsum(y1);
         if ((lane & 15) == 0) {
-            const K3Rsrc rc = k3d_rsrc(a.contrib, (size_t)G.P * G.KSDN * a.d * 4);
+            const K3Rsrc rc = k3d_rsrc(a.contrib, (size_t)G.P * G.KSDN * G.Dout * 4);
             const int row = 32 * dt + 4 * (lane >> 4);
-            k3d_st4_sc1(rc, ((p * G.KSDN + ks) * a.d + row) * 4, y0);
-            k3d_st4_sc1(rc, ((p * G.KSDN + ks) * a.d + row + 16) * 4, y1);
+            k3d_st4_sc1(rc, ((p * G.KSDN + ks) * G.Dout + row) * 4, y0);
+            k3d_st4_sc1(rc, ((p * G.KSDN + ks) * G.Dout + row + 16) * 4, y1);
         }
-        if (k3d_arrive(k3d_line(a.sync, G.lDT + dt), G.P * G.KSDN + G.KSD - 1, lane))
+        if (G.lat) {
+            /* the latent layer: the slots' aggregate (the shared expert joins after up) */
+            if (k3d_arrive(k3d_line(a.sync, G.lDT + dt), G.P * G.KSDN - 1, lane))
+                combine_latent(a, G, dt, lane);
+        } else if (k3d_arrive(k3d_line(a.sync, G.lDT + dt), G.P * G.KSDN + G.KSD - 1, lane)) {
             combine_rows(a, G, dt, lane);
+        }
+    }
+
+    /* ---------------------------------------------------------------- LD ---- */
+    /* z = down x for 32 latent rows x a K slice (tiled bf16 down [L][d], B = x's bf16
+     * pieces, as the shared gate/up reads them); the last slice of a row tile sums the
+     * slices in slice order and writes the 32 values' FP8 pieces (one MX block) for the
+     * routed gate/up (src/core/k3_ops.c:600: z = down x). */
+    static __device__ __noinline__ void latent_down(K3ArgPtr ap, int tk_, int lane)
+    {
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
+        const int rt = tk / G.KSLD, ks = tk - rt * G.KSLD;
+        const int c0 = ks * G.nCd / G.KSLD, c1 = (ks + 1) * G.nCd / G.KSLD;
+        const K3Rsrc rw = k3d_rsrc(a.down, (size_t)G.L * a.d * 2);
+        const K3Rsrc rb = k3d_rsrc(a.xq16, (size_t)G.nCd * 1024);
+        const K3Rsrc rx = k3d_rsrc(a.x, (size_t)a.T * a.d * 4);
+        const bool bon = (lane & 15) < NPC16 * a.T;
+        k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
+        const int o0 = 2 * rt * G.nCd * 1024 + lane * 16, o1 = o0 + G.nCd * 1024;
+        bool first = true;
+        if (NT <= 2) k3d_trace_go(a.trace, G.oLD + tk, lane);
+        for (int cb = c0; cb < c1; cb += 8) {
+            uint4 A0[8], A1[8], B[8];
+            if (NT <= 2) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    B[i] = k3d_b128(rx, cb + i < c1 ? k3d_xb16_off(a.T, a.d, cb + i, lane)
+                                                   : K3_OOB);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = cb + i;
+                A0[i] = k3d_b128(rw, c < c1 ? o0 + c * 1024 : K3_OOB);
+                A1[i] = k3d_b128(rw, c < c1 ? o1 + c * 1024 : K3_OOB);
+            }
+            if (NT <= 2) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) B[i] = k3d_xb16_make(B[i], a.T, lane);
+            } else {
+                if (first) {
+                    if (!k3d_wait_event(a.sync, G.eX16, tk, a.spin_limit, a.err, lane))
+                        return;
+                    k3d_trace_go(a.trace, G.oLD + tk, lane);
+                    first = false;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int c = cb + i;
+                    B[i] = k3d_b128<K3_BPOL>(rb, bon && c < c1 ? c * 1024 + lane * 16 : K3_OOB);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                y0 = k3d_mma16(A0[i], B[i], y0);
+                y1 = k3d_mma16(A1[i], B[i], y1);
+            }
+        }
+        y0 = k3d_colsum3(y0, lane);
+        y1 = k3d_colsum3(y1, lane);
+        const K3Rsrc rp = k3d_rsrc(a.zpart, (size_t)G.KSLD * a.T * G.L * 4);
+        if ((lane & 15) < a.T) {
+            const int t = lane & 15, row = 32 * rt + 4 * (lane >> 4);
+            k3d_st4_sc1(rp, ((ks * a.T + t) * G.L + row) * 4, y0);
+            k3d_st4_sc1(rp, ((ks * a.T + t) * G.L + row + 16) * 4, y1);
+        }
+        if (!k3d_arrive(k3d_line(a.sync, G.lLD + rt), G.KSLD - 1, lane)) return;
+        /* last slice of the row tile: rows 32 rt + r (lane r < 32) of z -> FP8 pieces */
+        const int r = lane & 31, row = 32 * rt + r;
+        const K3Rsrc rz = k3d_rsrc(a.zq8, (size_t)a.T * G.nQk * K3G_BQ);
+        const int Qz = rt >> 4;
+        for (int tt = 0; tt < a.T; ++tt) {
+            const float zs = k3d_sum_sc1<K3G_KS_LD>(rp, (tt * G.L + row) * 4, a.T * G.L * 4,
+                                                    G.KSLD);
+            float h = lane < 32 ? zs : 0.0f;
+            const int qb = (tt * G.nQk + Qz) * K3G_BQ;
+#pragma unroll
+            for (int pc = 0; pc < NPC8; ++pc) {
+                int sx;
+                const uint32_t q = k3d_fp8_piece(h, sx);
+                if (lane < 32) {
+                    k3d_st8_sc1(rz, qb + k3d_bq_data(rt, r, pc), q);
+                    if (lane == 0) k3d_st8_sc1(rz, qb + k3d_bq_scale(rt, pc), sx + 127);
+                }
+            }
+        }
+        k3d_arrive_event2(a.sync, G.cZ, G.nLDt, rt, G.eZ, lane);
+    }
+
+    /* ---------------------------------------------------------------- NR ---- */
+    /* The aggregate's RMSNorm for 64 latent columns of every token (src/core/k3_ops.c:
+     * 94-102 on accL, :646): inv = (float)(1 / sqrt(sum_double a^2 / L + eps)) from the
+     * row tiles' sums (added in tile order), y = lnorm * a * inv (float, the engine's
+     * order), then y's bf16 pieces (the latent up's B operand). No lnorm: y = a. */
+    static __device__ __noinline__ void norm(K3ArgPtr ap, int tk_, int lane)
+    {
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
+        if (!k3d_wait_event(a.sync, G.eA, tk, a.spin_limit, a.err, lane)) return;
+        k3d_trace_go(a.trace, G.oNR + tk, lane);
+        const int col = 64 * tk + lane;
+        const bool on = col < G.L;
+        const K3Rsrc rn = k3d_rsrc(a.nss, (size_t)a.T * G.nDt * 8);
+        const K3Rsrc ra = k3d_rsrc(a.accl, (size_t)a.T * G.L * 4);
+        const K3Rsrc rq = k3d_rsrc(a.aq16, (size_t)G.nCL * 1024);
+        for (int t = 0; t < a.T; ++t) {
+            float inv = 1.0f;
+            if (a.lnorm) {
+                /* every tile's sum, lane l taking tiles l, l + 64, ..., in that order, then
+                 * the wave's fixed-order reduction: the same sum in every NR ticket */
+                double s = 0.0;
+                for (int q = lane; q < G.nDt; q += 64)
+                    s += __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(
+                                                        rn, (t * G.nDt + q) * 8, 0, K3_SC1));
+                s = k3d_wave_sumd(s);
+                inv = (float)(1.0 / sqrt(s / (double)G.L + (double)a.rms_eps));
+            }
+            const float v = k3d_f32_sc1(ra, on ? (t * G.L + col) * 4 : K3_OOB);
+            float y = a.lnorm && on ? __fmul_rn(__fmul_rn(a.lnorm[col], v), inv) : v;
+#pragma unroll
+            for (int pc = 0; pc < NPC16; ++pc) {
+                float back;
+                const uint32_t h = k3d_bf16_rn(y, back);
+                y -= back;
+                if (on) k3d_st16_sc1(rq, k3d_b16_off(col, NPC16 * t + pc), h);
+            }
+        }
+        k3d_arrive_event2(a.sync, G.cN, G.nNR, tk, G.eN, lane);
+    }
+
+    /* ---------------------------------------------------------------- LU ---- */
+    /* out = up * aggregate for 32 output rows x a K slice (tiled bf16 up [d][L], B = the
+     * normalised aggregate's bf16 pieces): the first weights stream in while the norm
+     * finishes. The last arrival of an output tile (LU's and the shared down's slices)
+     * writes out (src/core/k3_ops.c:647-654). */
+    static __device__ __noinline__ void latent_up(K3ArgPtr ap, int tk_, int lane)
+    {
+        const K3kDecode a = *k3d_uniform_cptr(ap);
+        const int tk = k3d_uniform(tk_);
+        const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
+        const int rt = tk / G.KSLU, ks = tk - rt * G.KSLU;
+        const int c0 = ks * G.nCL / G.KSLU, c1 = (ks + 1) * G.nCL / G.KSLU;
+        const K3Rsrc rw = k3d_rsrc(a.up, (size_t)a.d * G.L * 2);
+        const K3Rsrc rb = k3d_rsrc(a.aq16, (size_t)G.nCL * 1024);
+        const bool bon = (lane & 15) < NPC16 * a.T;
+        k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
+        const int o0 = 2 * rt * G.nCL * 1024 + lane * 16, o1 = o0 + G.nCL * 1024;
+        bool first = true;
+        for (int cb = c0; cb < c1; cb += 8) {
+            uint4 A0[8], A1[8], B[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = cb + i;
+                A0[i] = k3d_b128(rw, c < c1 ? o0 + c * 1024 : K3_OOB);
+                A1[i] = k3d_b128(rw, c < c1 ? o1 + c * 1024 : K3_OOB);
+            }
+            if (first) {
+                if (!k3d_wait_event(a.sync, G.eN, tk, a.spin_limit, a.err, lane)) return;
+                k3d_trace_go(a.trace, G.oLU + tk, lane);
+                first = false;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int c = cb + i;
+                B[i] = k3d_b128<K3_BPOL>(rb, bon && c < c1 ? c * 1024 + lane * 16 : K3_OOB);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                y0 = k3d_mma16(A0[i], B[i], y0);
+                y1 = k3d_mma16(A1[i], B[i], y1);
+            }
+        }
+        y0 = k3d_colsum3(y0, lane);
+        y1 = k3d_colsum3(y1, lane);
+        if ((lane & 15) < a.T) {
+            const K3Rsrc rp = k3d_rsrc(a.upart, (size_t)G.KSLU * a.T * a.d * 4);
+            const int t = lane & 15, row = 32 * rt + 4 * (lane >> 4);
+            k3d_st4_sc1(rp, ((ks * a.T + t) * a.d + row) * 4, y0);
+            k3d_st4_sc1(rp, ((ks * a.T + t) * a.d + row + 16) * 4, y1);
+        }
+        if (k3d_arrive(k3d_line(a.sync, G.lLU + rt), G.KSLU + G.KSD - 1, lane))
+            combine_out(a, G, rt, lane);
+    }
+
+    /* The latent layer's aggregate for latent rows 32 dt .. + 31, once every slot's
+     * down-projection slices are in: slots in the engine's order (float multiply, then
+     * add, src/core/k3_ops.c:641-642), stored for the norm, with the rows' sum of squares
+     * (fp64; a float's square is exact in it). Lane r < 32 owns row 32 dt + r. */
+    static __device__ void combine_latent(const K3kDecode &a, const K3Geo &G, int dt, int lane)
+    {
+        const int row = 32 * dt + (lane & 31);
+        const K3Rsrc rc = k3d_rsrc(a.contrib, (size_t)G.P * G.KSDN * G.Dout * 4);
+        const K3Rsrc ra = k3d_rsrc(a.accl, (size_t)a.T * G.L * 4);
+        const K3Rsrc rn = k3d_rsrc(a.nss, (size_t)a.T * G.nDt * 8);
+        for (int t = 0; t < a.T; ++t) {
+            int ev = -1;
+            float wv = 0.0f;
+            if (lane < a.k) {
+                ev = __hip_atomic_load(&a.idx[t * a.k + lane], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                wv = __hip_atomic_load(&a.wt[t * a.k + lane], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+            float c = 0.0f;
+            for (int j0 = 0; j0 < a.k; j0 += 8) {
+                float y[8][K3G_KS_D];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj)
+#pragma unroll
+                    for (int q = 0; q < K3G_KS_D; ++q) {
+                        const int p = t * a.k + j0 + jj;
+                        y[jj][q] = __uint_as_float(k3d_b32<K3_BPOL>(
+                            rc, j0 + jj < a.k && q < G.KSDN
+                                    ? ((p * G.KSDN + q) * G.Dout + row) * 4 : K3_OOB));
+                    }
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int j = j0 + jj;
+                    if (j >= a.k) break;
+                    const int e = __builtin_amdgcn_readlane(ev, j);
+                    if (e < 0 || e >= a.E) continue;
+                    const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), j));
+                    float yy = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < K3G_KS_D; ++q)
+                        if (q < G.KSDN) yy += y[jj][q];
+                    c = __fadd_rn(c, __fmul_rn(w, yy));
+                }
+            }
+            if (lane < 32)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(c), ra, (t * G.L + row) * 4,
+                                                      0, K3_SC1);
+            const double sq = k3d_wave_sumd(lane < 32 ? (double)c * (double)c : 0.0);
+            if (lane == 0)
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    __builtin_bit_cast(unsigned int __attribute__((ext_vector_type(2))), sq), rn,
+                    (t * G.nDt + dt) * 8, 0, K3_SC1);
+        }
+        k3d_arrive_event2(a.sync, G.cA, G.nDt, dt, G.eA, lane);
+    }
+
+    /* The latent layer's output rows 32 rt .. + 31, once the latent up's and the shared
+     * down's slices for them are in: up * aggregate (slices in order), then + the shared
+     * output (slices in order), one float add (src/core/k3_ops.c:654). */
+    static __device__ void combine_out(const K3kDecode &a, const K3Geo &G, int rt, int lane)
+    {
+        const int row = 32 * rt + (lane & 31);
+        const K3Rsrc ru = k3d_rsrc(a.upart, (size_t)G.KSLU * a.T * a.d * 4);
+        const K3Rsrc rs = k3d_rsrc(a.shpart, (size_t)(G.KSD > 0 ? G.KSD : 1) * a.T * a.d * 4);
+        for (int t = 0; t < a.T; ++t) {
+            float uv[K3G_KS_LU], sh[K3G_KS_SD];
+#pragma unroll
+            for (int q = 0; q < K3G_KS_LU; ++q)
+                uv[q] = __uint_as_float(k3d_b32<K3_BPOL>(
+                    ru, q < G.KSLU ? ((q * a.T + t) * a.d + row) * 4 : K3_OOB));
+#pragma unroll
+            for (int q = 0; q < K3G_KS_SD; ++q)
+                sh[q] = __uint_as_float(k3d_b32<K3_BPOL>(
+                    rs, a.SI > 0 && q < G.KSD ? ((q * a.T + t) * a.d + row) * 4 : K3_OOB));
+            float c = 0.0f;
+#pragma unroll
+            for (int q = 0; q < K3G_KS_LU; ++q)
+                if (q < G.KSLU) c += uv[q];
+            if (a.SI > 0) {
+                float s2 = 0.0f;
+#pragma unroll
+                for (int q = 0; q < K3G_KS_SD; ++q)
+                    if (q < G.KSD) s2 += sh[q];
+                c = __fadd_rn(c, s2);
+            }
+            if (lane < 32) a.out[(size_t)t * a.d + row] = c;
+        }
     }
 
     /* ------------------------------------------------------------ combine ---- */
@@ -1099,7 +1422,7 @@ k_decode_fused(K3kDecode a)
     __shared__ K3RouterLds rl;
     const int lane = threadIdx.x & 63;
     const K3ArgPtr ap = (K3ArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
-    const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI);
+    const K3Geo G = k3_geo(a.T, a.d, a.E, a.k, a.I, a.SI, a.L);
     const int W = gridDim.x * (blockDim.x >> 6);
     const int w = k3d_uniform(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
     {
@@ -1125,23 +1448,26 @@ k_decode_fused(K3kDecode a)
         if (t < G.nX) K3Dec<NT>::prep(ap, t, lane);
         else if ((t -= G.nX) < G.nR) K3Dec<NT>::router(ap, t, lane, &rl, wg_slices);
         else if ((t -= G.nR) < 1) K3Dec<NT>::select(ap, lane, &lds);
-        else if ((t -= 1) < G.nSG) K3Dec<NT>::shared_gateup(ap, t, lane);
+        else if ((t -= 1) < G.nLD) K3Dec<NT>::latent_down(ap, t, lane);
+        else if ((t -= G.nLD) < G.nSG) K3Dec<NT>::shared_gateup(ap, t, lane);
         else if ((t -= G.nSG) < G.nSD) K3Dec<NT>::shared_down(ap, t, lane);
         else if ((t -= G.nSD) < G.nG) K3Dec<NT>::routed_gateup(ap, t, lane);
-        else K3Dec<NT>::routed_down(ap, t - G.nG, lane);
+        else if ((t -= G.nG) < G.nD) K3Dec<NT>::routed_down(ap, t, lane);
+        else if ((t -= G.nD) < G.nNR) K3Dec<NT>::norm(ap, t, lane);
+        else K3Dec<NT>::latent_up(ap, t - G.nNR, lane);
         if (a.trace && lane == 0) a.trace[3 * tk + 2] = wall_clock64();
     }
 }
 
-extern "C" size_t k3k_decode_sync_bytes(int T, int d, int E, int k, int I, int SI)
+extern "C" size_t k3k_decode_sync_bytes(int T, int d, int E, int k, int I, int SI, int L)
 {
-    const K3Geo G = k3_geo(T, d, E, k, I, SI);
+    const K3Geo G = k3_geo(T, d, E, k, I, SI, L);
     return (size_t)G.nlines * SY_LINE * 4;
 }
 
-extern "C" int k3k_decode_tickets(int T, int d, int E, int k, int I, int SI)
+extern "C" int k3k_decode_tickets(int T, int d, int E, int k, int I, int SI, int L)
 {
-    return k3_geo(T, d, E, k, I, SI).total;
+    return k3_geo(T, d, E, k, I, SI, L).total;
 }
 
 extern "C" int k3k_decode_fused(const K3kDecode *a, hipStream_t st)
@@ -1149,7 +1475,14 @@ extern "C" int k3k_decode_fused(const K3kDecode *a, hipStream_t st)
     if (a->T < 1 || a->T > 4 || a->d % 32 || a->I % 32 || a->SI % 32 || a->k < 1 ||
         a->k > K3G_MAX_TOPK || a->E < 1 || a->E > K3G_MAX_E || a->T * a->k > 256 ||
         !a->sync || !a->sync_clear ||
-        (size_t)a->sync_words * 4 < k3k_decode_sync_bytes(a->T, a->d, a->E, a->k, a->I, a->SI))
+        (size_t)a->sync_words * 4 <
+            k3k_decode_sync_bytes(a->T, a->d, a->E, a->k, a->I, a->SI, a->L))
+        return -1;
+    /* the latent layer: both projections, widths the tiles and blocks divide, and every
+     * buffer its tickets write */
+    if (a->L > 0 && a->L != a->d &&
+        (a->L % 32 || !a->down || !a->up || !a->zpart || !a->zq8 || !a->accl || !a->nss ||
+         !a->aq16 || !a->upart))
         return -1;
     /* the co-resident grid, per device and token-count instance, found once */
     static int grids[16][5];

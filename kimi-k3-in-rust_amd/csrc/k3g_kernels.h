@@ -80,6 +80,21 @@ typedef struct {
                                    * left out); the router tickets do nothing */
     long long spin_limit;
     unsigned long long *trace;    /* optional: [ticket][2] start/end wall-clock stamps */
+    /* the LatentMoE layer (Kimi-K3: src/core/k3_ops.c:556-656): L != d turns on the latent
+     * projections. The routed experts then run on z = down x (width L), their slot-order
+     * aggregate (width L) is RMSNorm-ed with lnorm (when given) and projected back by up,
+     * and the shared expert's output is added to that. L == d: the Kimi-K2 shape, none of
+     * the fields below is read. */
+    int L;
+    const uint16_t *down, *up;    /* tiled bf16 [L][d] and [d][L] */
+    const float *lnorm;           /* [L], or NULL: no RMSNorm of the aggregate */
+    float rms_eps;
+    float *zpart;                 /* [K3G_KS_LD][T][L] latent down partial sums */
+    uint8_t *zq8;                 /* [T][ceil(L/512)][8448]: z's FP8 pieces, B layout */
+    float *accl;                  /* [T][L] the routed experts' slot-order aggregate */
+    double *nss;                  /* [T][L/32] the aggregate's sums of squares per 32 rows */
+    uint16_t *aq16;               /* [L/32][64][8]: the normalised aggregate's bf16 pieces */
+    float *upart;                 /* [K3G_KS_LU][T][d] latent up partial sums */
 } K3kDecode;
 
 /* One grouped GEMM on the bf16 matrix cores (k3g_gemm.hip). Columns are (token, slot)
@@ -155,11 +170,13 @@ int k3k_xpieces(const float *x, int T, int d, int ldb, uint16_t *xb, long long p
 #define K3G_KS_SD 2               /* shared down: over 32-column chunks of SI */
 #define K3G_KS_R 4                /* router: over 1024-column chunks of d */
 #define K3G_KS_D 2                /* routed down: over 512-column quads of I */
+#define K3G_KS_LD 7               /* latent down: over 32-column chunks of d */
+#define K3G_KS_LU 4               /* latent up: over 32-column chunks of L */
 #define K3G_DEC_WAVES_PER_EU 4
 
 /* bytes of counters and tickets per call of the fused kernel at this shape */
-size_t k3k_decode_sync_bytes(int T, int d, int E, int k, int I, int SI);
-int k3k_decode_tickets(int T, int d, int E, int k, int I, int SI);
+size_t k3k_decode_sync_bytes(int T, int d, int E, int k, int I, int SI, int L);
+int k3k_decode_tickets(int T, int d, int E, int k, int I, int SI, int L);
 int k3k_decode_fused(const K3kDecode *a, hipStream_t st);
 
 /* Repack into the tiled layouts (k3g_tile.hip). Sizes are 0 for unsupported shapes. */

@@ -105,7 +105,7 @@ extern "C" int k3g_moe_noalloc(const K3gLayer *L, const float *x, int T, float *
     }
     const int d = L->hidden, E = L->n_experts, k = L->topk, I = L->inter, SI = L->shared_inter;
     const NoallocLayout lo = layout_for(d, E, k, I, SI);
-    const size_t sync_bytes = k3k_decode_sync_bytes(4, d, E, k, I, SI);
+    const size_t sync_bytes = k3k_decode_sync_bytes(4, d, E, k, I, SI, d);
     if (lo.total > K3G_NOALLOC_BYTES || sync_bytes > K3G_NOALLOC_BANK) {
         fprintf(stderr, "k3g_moe_noalloc: the layer needs %zu bytes of scratch (%zu of "
                         "counters), beyond the fixed %u (%u per counter bank)\n",

@@ -163,6 +163,8 @@ def lib() -> C.CDLL:
         L.k3g_ctx_force_exact.restype = None
         L.k3g_ctx_set_fused.argtypes = [vp, i]
         L.k3g_ctx_set_fused.restype = None
+        L.k3g_ctx_paths.argtypes = [vp, i]
+        L.k3g_ctx_paths.restype = i
         L.k3g_ctx_set_fp8.argtypes = [vp, i]
         L.k3g_ctx_set_fp8.restype = None
         L.k3g_ctx_profile.argtypes = [vp, i]
@@ -711,6 +713,10 @@ class Ctx:
 
     def force_exact(self, mode: int) -> None:
         lib().k3g_ctx_force_exact(self.ptr, mode)
+
+    def paths(self, clear: bool = True) -> int:
+        """kernels run since the last clear: 1 staged, 2 fused decode, 4 grouped GEMMs"""
+        return lib().k3g_ctx_paths(self.ptr, int(clear))
 
     def set_fused(self, on: bool) -> None:
         lib().k3g_ctx_set_fused(self.ptr, 1 if on else 0)

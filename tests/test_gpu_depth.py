@@ -316,22 +316,29 @@ def k3_layer(gpu):
     del lay
 
 
-@pytest.mark.parametrize("T,nsample", [(64, 10), (600, 8)])
+@pytest.mark.parametrize("T,nsample", [(1, 1), (2, 2), (4, 4), (64, 10), (600, 8)])
 def test_k3_latent_moe_device(k3_layer, T, nsample):
+    """Up to 4 tokens: the fused decode kernel with its latent tickets (z = down x, the
+    routed experts on z, the slot-order aggregate, its RMSNorm, up, + shared); more: the
+    grouped GEMMs with the latent projections."""
     lay = k3_layer
-    say(f"case: k3g_moe K3 LatentMoE, {T} tokens, grouped GEMMs with latent projections: "
+    kind = "fused decode kernel" if T <= 4 else "grouped GEMMs"
+    say(f"case: k3g_moe K3 LatentMoE, {T} tokens, {kind} with latent projections: "
         f"routing bit-exact for every token, {nsample} sampled rows vs the oracle")
     x = np.ascontiguousarray(k3moe.host_normal(T * lay.d, 31, 609 + T, 0.0, 1.0).reshape(T, lay.d))
     ctx = k3moe.Ctx(lay.L, max_tokens=T)
     dx = k3moe.DevBuf.from_array(x)
     dout = k3moe.DevBuf(T * lay.d * 4)
     didx, dwt = k3moe.DevBuf(T * lay.k * 4), k3moe.DevBuf(T * lay.k * 4)
+    ctx.paths()
     ctx.moe(lay.L, dx.ptr, T, dout.ptr, didx.ptr, dwt.ptr)
     ctx.sync()
+    paths = ctx.paths()
     out = dout.download(np.float32, T * lay.d).reshape(T, lay.d)
     idx = didx.download(np.int32, T * lay.k).reshape(T, lay.k)
     wt = dwt.download(np.float32, T * lay.k).reshape(T, lay.k)
     ctx.destroy()
+    assert paths == (2 if T <= 4 else 4), paths
     kk = O.oracle()
     for t in range(T):
         oi, ow = kk.router(x[t], lay.gate, lay.bias, lay.E, lay.k, 1, 1.0)

@@ -870,11 +870,13 @@ def test_dropin_k3_shape_latent_moe(gpu):
     wt = np.zeros(k, np.float32)
     k3moe.lib().k3_moe(out.ctypes.data, x.ctypes.data, C.byref(w), C.byref(cfg), T,
                        idx.ctypes.data, wt.ctypes.data, None)
+    paths = k3moe.lib().k3moe_last_kernels()
     k3moe.lib().k3moe_forget_weights()
     w2, src2 = weights()
     oo, oi, ow = kk.moe(w2, cfg, x)
     r = rel_l2(out, oo)
-    say(f"  rel-L2 {r:.3e}, {len(used)} experts")
+    say(f"  rel-L2 {r:.3e}, {len(used)} experts, kernels {paths}")
+    assert paths == 2          # the fused decode kernel, latent tickets, routing given
     assert np.array_equal(idx, oi)
     np.testing.assert_allclose(wt, ow, rtol=1e-6)
     assert r <= REL_L2
