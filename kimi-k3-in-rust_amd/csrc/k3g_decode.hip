@@ -69,6 +69,11 @@ typedef unsigned int k3v4u __attribute__((ext_vector_type(4)));
 #define K3G_BQ 8448       /* FP8 B quad: 4 x 2 KB chunks + 256 B of scales */
 #define NPC8 6            /* FP8 pieces per value */
 #define NPC16 3           /* bf16 pieces per value */
+/* up to this many tokens the shared gate/up and latent down tickets make x's bf16 pieces
+ * in registers from fp32 x; above it they read the prep tickets' pieces */
+#ifndef K3G_XREG
+#define K3G_XREG 2
+#endif
 #define SG_TILES 1        /* shared gate/up: 16-row tiles per ticket */
 #define SG_BATCH 8        /* shared gate/up: 32-column chunks per load batch */
 
@@ -551,6 +556,22 @@ __device__ __forceinline__ K3ArgPtr k3d_uniform_cptr(K3ArgPtr p)
     return (K3ArgPtr)(((uint64_t)hi << 32) | lo);
 }
 
+/* The slices of the bf16 ticket classes start at multiples of 32 KB of their tiled
+ * matrices, and every wave of a class streams its slice from the first 8 KB batch to the
+ * last at about the same pace: left alone, the waves' reads would all fall in the same
+ * 8 KB of every 32 KB at once. Batch bi of a ticket's nb is taken at position
+ * (bi + rot) mod nb, rot = ticket mod nb, so waves running together start at different
+ * offsets. */
+#ifndef K3G_ROT
+#define K3G_ROT 1
+#endif
+__device__ __forceinline__ int k3d_batch_rot(int tk, int nb) { return K3G_ROT && nb > 0 ? tk % nb : 0; }
+__device__ __forceinline__ int k3d_batch_at(int bi, int nb, int rot)
+{
+    const int b = bi + rot;
+    return b >= nb ? b - nb : b;
+}
+
 template <int NT>
 struct K3Dec {
     /* ----------------------------------------------------------------- X ---- */
@@ -571,7 +592,7 @@ struct K3Dec {
         const int Q = b >> 4;
         /* the bf16 pieces first: the shared expert's tickets wait only for these (up to
          * two tokens they make them themselves) */
-        if (NT > 2) {
+        if (NT > K3G_XREG) {
             float r2 = v;
 #pragma unroll
             for (int pc = 0; pc < NPC16; ++pc) {
@@ -762,10 +783,12 @@ struct K3Dec {
         /* tile j's chunk c: (SG_TILES rg + j) nCd + c KB in; tiles past SI read zero */
         const int abase = SG_TILES * rg * G.nCd * 1024 + lane * 16, tstride = G.nCd * 1024;
         bool first = true;
-        if (NT <= 2) k3d_trace_go(a.trace, G.oSG + tk, lane);
-        for (int cb = c0; cb < c1; cb += SG_BATCH) {
+        if (NT <= K3G_XREG) k3d_trace_go(a.trace, G.oSG + tk, lane);
+        const int nb = (c1 - c0 + SG_BATCH - 1) / SG_BATCH, rot = k3d_batch_rot(tk, nb);
+        for (int bi = 0; bi < nb; ++bi) {
+            const int cb = c0 + SG_BATCH * k3d_batch_at(bi, nb, rot);
             uint4 A1[SG_TILES][SG_BATCH], A3[SG_TILES][SG_BATCH], B[SG_BATCH];
-            if (NT <= 2) {
+            if (NT <= K3G_XREG) {
                 /* x's halves first, so they can be used before the weights land */
 #pragma unroll
                 for (int i = 0; i < SG_BATCH; ++i)
@@ -782,7 +805,7 @@ struct K3Dec {
                     A3[j][i] = k3d_b128(r3, c < c1 ? o : K3_OOB);
                 }
             }
-            if (NT <= 2) {
+            if (NT <= K3G_XREG) {
 #pragma unroll
                 for (int i = 0; i < SG_BATCH; ++i) B[i] = k3d_xb16_make(B[i], a.T, lane);
             } else {
@@ -961,7 +984,9 @@ struct K3Dec {
         k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
         const int o0 = 2 * rt * G.nCsi * 1024 + lane * 16, o1 = o0 + G.nCsi * 1024;
         bool first = true;
-        for (int cb = c0; cb < c1; cb += 8) {
+        const int nb = (c1 - c0 + 7) / 8, rot = k3d_batch_rot(tk, nb);
+        for (int bi = 0; bi < nb; ++bi) {
+            const int cb = c0 + 8 * k3d_batch_at(bi, nb, rot);
             uint4 A0[8], A1[8], B[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -1096,10 +1121,12 @@ struct K3Dec {
         k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
         const int o0 = 2 * rt * G.nCd * 1024 + lane * 16, o1 = o0 + G.nCd * 1024;
         bool first = true;
-        if (NT <= 2) k3d_trace_go(a.trace, G.oLD + tk, lane);
-        for (int cb = c0; cb < c1; cb += 8) {
+        if (NT <= K3G_XREG) k3d_trace_go(a.trace, G.oLD + tk, lane);
+        const int nb = (c1 - c0 + 7) / 8, rot = k3d_batch_rot(tk, nb);
+        for (int bi = 0; bi < nb; ++bi) {
+            const int cb = c0 + 8 * k3d_batch_at(bi, nb, rot);
             uint4 A0[8], A1[8], B[8];
-            if (NT <= 2) {
+            if (NT <= K3G_XREG) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
                     B[i] = k3d_b128(rx, cb + i < c1 ? k3d_xb16_off(a.T, a.d, cb + i, lane)
@@ -1111,7 +1138,7 @@ struct K3Dec {
                 A0[i] = k3d_b128(rw, c < c1 ? o0 + c * 1024 : K3_OOB);
                 A1[i] = k3d_b128(rw, c < c1 ? o1 + c * 1024 : K3_OOB);
             }
-            if (NT <= 2) {
+            if (NT <= K3G_XREG) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) B[i] = k3d_xb16_make(B[i], a.T, lane);
             } else {
@@ -1224,7 +1251,9 @@ struct K3Dec {
         k3v4f y0 = {0, 0, 0, 0}, y1 = {0, 0, 0, 0};
         const int o0 = 2 * rt * G.nCL * 1024 + lane * 16, o1 = o0 + G.nCL * 1024;
         bool first = true;
-        for (int cb = c0; cb < c1; cb += 8) {
+        const int nb = (c1 - c0 + 7) / 8, rot = k3d_batch_rot(tk, nb);
+        for (int bi = 0; bi < nb; ++bi) {
+            const int cb = c0 + 8 * k3d_batch_at(bi, nb, rot);
             uint4 A0[8], A1[8], B[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {

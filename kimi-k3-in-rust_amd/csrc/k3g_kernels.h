@@ -164,14 +164,29 @@ int k3k_gemm_tiles(const int32_t *off, int E, int32_t *tiles, int32_t *ntiles,
 int k3k_xpieces(const float *x, int T, int d, int ldb, uint16_t *xb, long long piece,
                 int32_t *flag, hipStream_t st);
 
-/* K slices of the fused kernel's ticket classes (fewer when K is short) */
+/* K slices of the fused kernel's ticket classes (fewer when K is short); each may be set
+ * at build time (-DK3G_KS_SG=...) */
+#ifndef K3G_KS_G
 #define K3G_KS_G 7                /* routed gate/up: over 512-column quads of d */
+#endif
+#ifndef K3G_KS_SG
 #define K3G_KS_SG 7               /* shared gate/up: over 32-column chunks of d */
+#endif
+#ifndef K3G_KS_SD
 #define K3G_KS_SD 2               /* shared down: over 32-column chunks of SI */
+#endif
+#ifndef K3G_KS_R
 #define K3G_KS_R 4                /* router: over 1024-column chunks of d */
+#endif
+#ifndef K3G_KS_D
 #define K3G_KS_D 2                /* routed down: over 512-column quads of I */
+#endif
+#ifndef K3G_KS_LD
 #define K3G_KS_LD 7               /* latent down: over 32-column chunks of d */
+#endif
+#ifndef K3G_KS_LU
 #define K3G_KS_LU 4               /* latent up: over 32-column chunks of L */
+#endif
 #define K3G_DEC_WAVES_PER_EU 4
 
 /* bytes of counters and tickets per call of the fused kernel at this shape */

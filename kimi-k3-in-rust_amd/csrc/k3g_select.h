@@ -15,6 +15,11 @@
 
 #define K3G_MAX_E 1024
 
+/* 0: always the k rounds of k3d_select_token_n (the threshold path is skipped) */
+#ifndef K3G_SELECT_FAST
+#define K3G_SELECT_FAST 1
+#endif
+
 struct K3SelectLds {
     float choice[K3G_MAX_E];
     float lo[K3G_MAX_E];
@@ -27,6 +32,11 @@ struct K3SelectLds {
     int ncand, nredo;
     int cert;
     double wsum;
+    /* k3d_select_fast: the candidates (keys, lo, hi, score) and the selection by rank */
+    unsigned long long ckey[64], rkey[64];
+    float clo[64], chi[64], csc[64];
+    float rlo[64], rhi[64], rsc[64];
+    int rsel[64];
 };
 
 /* {choice, lo, hi, score} of one expert from its fp64 logit sum `acc` and a bound `ab` on
@@ -309,6 +319,104 @@ __device__ __forceinline__ bool k3d_settled_float(double s, double a, int n, flo
     return lo == hi;
 }
 
+/* The top-k and its certificate without k dependent rounds. th = the k-th largest of the
+ * 64 lanes' best ordered choices (a bitwise search on ballot counts) is at most the k-th
+ * largest choice overall, so the keys whose ordered choice reaches th hold the top k.
+ * When there are at most 64 of them they go to LDS, and each one's rank is the number of
+ * candidates with a larger key (the keys are distinct: they carry the index), which is
+ * its round in the engine's order. Lane r < k then holds the r-th selection, and the
+ * certificate is the rounds' one: every selected hi (r > 0) below the smallest lo
+ * selected before it (a prefix minimum over the lanes), no NaN lo. Returns false, with
+ * nothing changed, when fewer than k lanes hold a key or the candidates are more than 64;
+ * the rounds then run as before. */
+template <int NPL>
+__device__ __forceinline__ bool k3d_select_fast(K3SelectLds *s, const uint64_t (&key)[NPL],
+                                                const float4 (&v)[NPL], int k, int lane,
+                                                uint32_t &taken, bool &ok, float &minlo,
+                                                double &wsum, int &my_sel, float &my_score,
+                                                float &my_hi)
+{
+    uint64_t m = key[0];
+#pragma unroll
+    for (int i = 1; i < NPL; ++i) m = key[i] > m ? key[i] : m;
+    const uint32_t mh = (uint32_t)(m >> 32);
+    uint32_t th = 0;
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t c = th | (1u << b);
+        if (__popcll(__ballot(mh >= c)) >= k) th = c;
+    }
+    if (th == 0) return false;              /* fewer than k lanes hold a valid key */
+    int total = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) total += __popcll(__ballot((uint32_t)(key[i] >> 32) >= th));
+    if (total > 64) return false;
+    const uint64_t lt = (1ull << lane) - 1;
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const bool c = (uint32_t)(key[i] >> 32) >= th;
+        const uint64_t bm = __ballot(c);
+        if (c) {
+            const int pos = base + __popcll(bm & lt);
+            s->ckey[pos] = key[i];
+            s->clo[pos] = v[i].y;
+            s->chi[pos] = v[i].z;
+            s->csc[pos] = v[i].w;
+        }
+        base += __popcll(bm);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t mine = lane < total ? s->ckey[lane] : 0;
+    int rank = 0;
+    for (int q = 0; q < total; ++q) rank += s->ckey[q] > mine ? 1 : 0;
+    if (lane < total && rank < k) {
+        s->rkey[rank] = mine;
+        s->rsel[rank] = (int)~(uint32_t)mine;
+        s->rlo[rank] = s->clo[lane];
+        s->rhi[rank] = s->chi[lane];
+        s->rsc[rank] = s->csc[lane];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    float lo = INFINITY, hi = 0.0f, sc = 0.0f;
+    if (lane < k) {
+        my_sel = s->rsel[lane];
+        lo = s->rlo[lane];
+        hi = s->rhi[lane];
+        sc = s->rsc[lane];
+        my_score = sc;
+        my_hi = hi;
+    }
+    /* inclusive prefix minimum of the selected lo (fminf: NaN ignored, as the rounds'
+     * running minimum ignores it), and the exclusive one for the check */
+    float inc = lo;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float u = __shfl_up(inc, o, K3G_WAVE);
+        if (lane >= o) inc = fminf(inc, u);
+    }
+    float ex = __shfl_up(inc, 1, K3G_WAVE);
+    if (lane == 0) ex = INFINITY;
+    const bool bad = lane < k && ((lane > 0 && !__builtin_isnan(hi) && !(hi < ex)) ||
+                                  __builtin_isnan(lo));
+    if (__ballot(bad)) ok = false;
+    minlo = __shfl(inc, k - 1, K3G_WAVE);
+    /* the engine's sequential double sum in selection order */
+    double ws = 0.0;
+    for (int r = 0; r < k; ++r)
+        ws += (double)__uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sc), r));
+    wsum = ws;
+    /* the k-th selected key (readfirstlane returns int: widen each half unsigned) */
+    const uint32_t kh = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(s->rkey[k - 1] >> 32));
+    const uint32_t kl = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)s->rkey[k - 1]);
+    const uint64_t kth = ((uint64_t)kh << 32) | kl;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i)
+        if (key[i] != 0 && key[i] >= kth) taken |= 1u << i;
+    return true;
+}
+
 /* Selection for token t from rs [T][E] {choice, lo, hi, score} (read at device
  * coherence: the fused kernel's router tickets write them in the same launch). Each lane
  * owns experts lane, lane + 64, ... (NPL of them); all loads are issued before any is
@@ -355,7 +463,10 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
     double wsum = 0.0;
     int my_sel = -1;          /* lane j: the j-th selected expert */
     float my_score = 0.0f, my_hi = 0.0f;
-    for (int j = 0; j < k; ++j) {
+    const bool fast = K3G_SELECT_FAST &&
+                      k3d_select_fast<NPL>(s, key, v, k, lane, taken, ok, minlo, wsum, my_sel,
+                                           my_score, my_hi);
+    for (int j = 0; j < (fast ? 0 : k); ++j) {
         /* this lane's best untaken key: a tree over the slots */
         uint64_t m[NPL];
 #pragma unroll

@@ -316,6 +316,34 @@ def k3_layer(gpu):
     del lay
 
 
+def test_k3_decode_certificate_ordinary_tokens(k3_layer):
+    """The decode kernel's top-k at 896 experts, top-16 certifies ordinary tokens on its
+    own: six seeded single-token decodes never enter the exact path (stats[0]), and the
+    routing is the engine's."""
+    lay = k3_layer
+    T = 6
+    say(f"case: fused decode K3 E=896 k=16, {T} single-token calls: certificate without the "
+        "exact path")
+    x = np.ascontiguousarray(k3moe.host_normal(T * lay.d, 31, 4343, 0.0, 1.0).reshape(T, lay.d))
+    ctx = k3moe.Ctx(lay.L, max_tokens=1)
+    dx = k3moe.DevBuf.from_array(x)
+    dout = k3moe.DevBuf(T * lay.d * 4)
+    didx, dwt = k3moe.DevBuf(T * lay.k * 4), k3moe.DevBuf(T * lay.k * 4)
+    for t in range(T):
+        ctx.moe(lay.L, dx.ptr + t * lay.d * 4, 1, dout.ptr + t * lay.d * 4,
+                didx.ptr + t * lay.k * 4, dwt.ptr + t * lay.k * 4)
+    ctx.sync()
+    extra = ctx.stats()[0]
+    idx = didx.download(np.int32, T * lay.k).reshape(T, lay.k)
+    ctx.destroy()
+    say(f"  tokens through the exact path: {extra}")
+    assert extra == 0
+    kk = O.oracle()
+    for t in range(T):
+        oi, _ = kk.router(x[t], lay.gate, lay.bias, lay.E, lay.k, 1, 1.0)
+        assert np.array_equal(idx[t], oi), t
+
+
 @pytest.mark.parametrize("T,nsample", [(1, 1), (2, 2), (4, 4), (64, 10), (600, 8)])
 def test_k3_latent_moe_device(k3_layer, T, nsample):
     """Up to 4 tokens: the fused decode kernel with its latent tickets (z = down x, the

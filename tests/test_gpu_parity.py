@@ -260,6 +260,35 @@ def test_router_k3_shape(gpu, T, force):
     ctx.destroy()
 
 
+def test_decode_certificate_ordinary_tokens(k2_layer):
+    """The decode kernel's top-k (384 experts, top-8) certifies ordinary tokens on its own:
+    eight seeded single-token decodes never enter the exact path (stats[0] counts the
+    tokens that do), and routing and weights are the engine's bit for bit."""
+    T, d = 8, 7168
+    say(f"case: fused decode d=7168 E=384 k=8, {T} single-token calls: certificate without "
+        "the exact path")
+    layer = k2_layer
+    x = layer.tokens(T, stream_base=4242)
+    ctx = k3moe.Ctx(layer.dev_tiled, max_tokens=1)
+    dx = k3moe.DevBuf.from_array(x)
+    dout = k3moe.DevBuf(T * d * 4)
+    didx, dwt = k3moe.DevBuf(T * 8 * 4), k3moe.DevBuf(T * 8 * 4)
+    for t in range(T):
+        ctx.moe(layer.dev_tiled, dx.ptr + t * d * 4, 1, dout.ptr + t * d * 4,
+                didx.ptr + t * 32, dwt.ptr + t * 32)
+    ctx.sync()
+    extra = ctx.stats()[0]
+    idx = didx.download(np.int32, T * 8).reshape(T, 8)
+    wt = dwt.download(np.float32, T * 8).reshape(T, 8)
+    ctx.destroy()
+    say(f"  tokens through the exact path: {extra}")
+    assert extra == 0
+    for t in range(T):
+        oi, ow = O.oracle().router(x[t], layer.gate, layer.bias, 384, 8, 1, 2.5)
+        assert np.array_equal(idx[t], oi), (t, idx[t], oi)
+        assert np.array_equal(wt[t].view(np.uint32), ow.view(np.uint32)), t
+
+
 @pytest.mark.parametrize("T,force", [(1200, 0), (512, 2)])
 def test_router_bounded_logits_k2(k2_layer, T, force):
     """From 512 tokens the logits are formed on the bf16 matrix cores with a rigorous bound
