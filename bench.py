@@ -48,6 +48,9 @@ TRAFFIC_FUSED = 300037638
 # Zipf(0.8) prefill, the same way (FETCH_SIZE x 1.9997 + WRITE_SIZE, mean of 3 launches):
 # 7.666 GB read + 0.204 GB written; profiles/k_gemm_k2_prefill4096.md.
 TRAFFIC_GATEUP_PREFILL = 7869400121
+# the same for the fp32-x sub-leg's routed gate/up (x in two bf16 pieces); None until a
+# counter run measures it
+TRAFFIC_GATEUP_PREFILL_FP32 = None
 
 
 def log(msg):
@@ -75,15 +78,23 @@ def host_cpu():
     return info
 
 
-def cpu_baseline(seconds: float, max_tokens: int, seed: int, legs=("decode", "batch", "prefill")):
+def cpu_baseline(seconds: float, max_tokens: int, seed: int,
+                 legs=("decode", "identity", "batch", "prefill", "streamed")):
     """The engine's CPU kernels (k3_router, k3_matmul_mxfp4, k3_situ_glu, k3_matmul_bf16,
     compiled from the engine's src/core/k3_ops.c with its flags: kind "reference"; the C
     restatement when that library is absent: kind "port") composed as k3_moe /
-    k3_moe_prefill for the same K2 layers without identity latent projections. Expert
-    regeneration on the host is outside the timed regions.
-      decode: median over a bounded sample of 1-token calls (the c1 workload);
+    k3_moe_prefill (src/core/k3_ops.c:556-808) for the same K2 layers. Expert
+    regeneration on the host is outside the timed regions; every routed expert the timed
+    call reads is in host RAM.
+      decode: median over a bounded sample of 1-token calls (the c1 workload), without
+        the latent projections (down = up = NULL);
+      identity_latent: the same tokens through the full k3_moe with bf16 identity latent
+        matrices (7168 x 7168, as the engine must express a K2 layer);
       batch: one 64-token k3_moe_prefill call (64-token chunk) on the Zipf(1.1) layer;
-      prefill: 128 tokens (two 64-token chunks) of the Zipf(0.8) 4096-token prefill."""
+      prefill: 128 tokens (two 64-token chunks) of the Zipf(0.8) 4096-token prefill, three
+        calls;
+      streamed: the 16-layer x batch-8 workload, one 8-token k3_moe_prefill call per
+        layer, as many of the 16 layers as a bounded sample allows."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import k3moe
@@ -96,7 +107,9 @@ def cpu_baseline(seconds: float, max_tokens: int, seed: int, legs=("decode", "ba
     cpu = host_cpu()
     what = ("the engine's own kernels compiled from src/core/k3_ops.c" if ref else
             "the C restatement of the engine's kernels")
-    res = {"cores": threads, "kind": kind, "cpu": cpu}
+    res = {"cores": threads, "kind": kind, "cpu": cpu,
+           "omp": {v: os.environ.get(v, "unset") for v in
+                   ("OMP_NUM_THREADS", "OMP_PROC_BIND", "OMP_PLACES")}}
     if "decode" in legs:
         layer = k3moe.SynthLayer(k3moe.K2, seed=seed, layer=0, device=False)
         times = []
@@ -118,23 +131,78 @@ def cpu_baseline(seconds: float, max_tokens: int, seed: int, legs=("decode", "ba
                     "tokens_per_s": round(1.0 / med, 2),
                     "GBps": round((K * B_EXPERT + B_SHARED + B_ROUTER + B_TOKEN) / med / 1e9, 2)})
         del layer
-    for leg, shape, T, base in (("batch", k3moe.K2_BATCH, 64, 1900),
-                                ("prefill", k3moe.K2_PREFILL, 128, 900)):
+    if "identity" in legs:
+        # the full k3_moe as the engine runs a K2 layer: bf16 identity latent down and up
+        layer = k3moe.SynthLayer(k3moe.K2, seed=seed, layer=0, device=False)
+        times = []
+        for i in range(max_tokens):
+            x = layer.tokens(1, stream_base=5000 + i)
+            experts = O.routed_union(layer, x)
+            w, cfg, keep = O.k2_weights(layer, experts, identity=True)
+            t0 = time.perf_counter()
+            O.oracle().moe(w, cfg, x)
+            times.append(time.perf_counter() - t0)
+            del keep
+            if sum(times) >= seconds / 2 and len(times) >= 3:
+                break
+        med = float(np.median(times))
+        res["identity_latent"] = {
+            "value": round(1e6 * med, 1), "unit": "us/token",
+            "tokens_per_s": round(1.0 / med, 2),
+            "sample": f"{len(times)} decode tokens (the decode sample's first ones, median) "
+                      f"through the full k3_moe with bf16 identity latent matrices "
+                      f"(7168 x 7168 down and up), {what}, OpenMP {threads} threads"}
+        del layer
+    for leg, shape, T, base, reps in (("batch", k3moe.K2_BATCH, 64, 1900, 1),
+                                      ("prefill", k3moe.K2_PREFILL, 128, 900, 3)):
         if leg not in legs:
             continue
         layer = k3moe.SynthLayer(shape, seed=seed, layer=0, device=False)
         x = layer.tokens(T, stream_base=base)
         experts = O.routed_union(layer, x)
         w, cfg, keep = O.k2_weights(layer, experts)
-        t0 = time.perf_counter()
-        O.oracle().moe(w, cfg, x, prefill=True)
-        dt = time.perf_counter() - t0
+        runs = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            O.oracle().moe(w, cfg, x, prefill=True)
+            runs.append(time.perf_counter() - t0)
+        dt = float(np.median(runs))
         del keep, layer
         res[leg] = {"tokens": T, "seconds": round(dt, 3), "tokens_per_s": round(T / dt, 2),
                     "us_per_token": round(1e6 * dt / T, 1), "experts": len(experts),
                     "sample": f"{T} tokens of the {shape.name} workload through one "
                               f"k3_moe_prefill call (64-token chunks, first-seen unique "
-                              f"experts), {what}, OpenMP {threads} threads"}
+                              f"experts), {what}, OpenMP {threads} threads"
+                              + (f"; median of {reps} calls" if reps > 1 else "")}
+        if reps > 1:
+            res[leg]["runs_seconds"] = [round(r, 3) for r in runs]
+    if "streamed" in legs:
+        # 16 K2 layers x batch 8, one 8-token k3_moe_prefill call per layer with every
+        # routed expert in host RAM; bounded: the layers that fit the sample
+        times, nexp = [], []
+        for l in range(16):
+            layer = k3moe.SynthLayer(k3moe.K2, seed=seed, layer=l, device=False)
+            x = layer.tokens(8, stream_base=2950)
+            experts = O.routed_union(layer, x)
+            w, cfg, keep = O.k2_weights(layer, experts)
+            t0 = time.perf_counter()
+            O.oracle().moe(w, cfg, x, prefill=True)
+            times.append(time.perf_counter() - t0)
+            nexp.append(len(experts))
+            del keep, layer
+            if sum(times) >= seconds / 2 and len(times) >= 2:
+                break
+        per_layer = float(np.mean(times))
+        res["streamed"] = {
+            "layers_timed": len(times), "batch": 8,
+            "seconds_per_layer": round(per_layer, 4),
+            "experts_per_layer": round(float(np.mean(nexp)), 1),
+            "ms_per_step_16_layers": round(16e3 * per_layer, 1),
+            "tokens_per_s": round(8 / (16 * per_layer), 2),
+            "sample": f"the 16-layer x batch-8 streamed workload: {len(times)} of the 16 K2 "
+                      f"layers, one 8-token k3_moe_prefill call each with every routed "
+                      f"expert in host RAM, {what}, OpenMP {threads} threads; the step "
+                      f"time is 16 x the mean layer time"}
     O.set_kernels(None)
     return res
 
@@ -441,6 +509,34 @@ def prefill(a):
     ctx.profile(False)
     ctx.set_fp8(False)
     assert np.isfinite(dout.download(np.float32, T * D)).all()
+    # the engine's real prefill input: k3_decoder_layer_inc hands k3_moe_prefill the fp32
+    # hidden state (src/core/k3_ops.c:1015-1024); the same draws, not rounded to bf16, so x
+    # takes two bf16 pieces and the router's second-piece product runs
+    x32 = layer.tokens(T, stream_base=900, bf16=False)
+    dx32 = k3moe.DevBuf.from_array(x32)
+
+    def run32():
+        ctx.moe(layer.dev, dx32.ptr, T, dout.ptr, didx.ptr, dwt.ptr)
+
+    for _ in range(a.prefill_warmup):
+        run32()
+    ctx.sync()
+    idx32 = didx.download(np.int32, T * K)
+    k3moe.sync()
+    g0 = time.perf_counter()
+    for _ in range(a.prefill_steps):
+        run32()
+    k3moe.sync()
+    g1 = time.perf_counter()
+    ctx.sync()
+    ctx.profile(True)
+    for _ in range(nprof):
+        run32()
+    ctx.sync()
+    ms32_stage, n32_stage = ctx.stage_ms()
+    ctx.profile(False)
+    assert np.isfinite(dout.download(np.float32, T * D)).all()
+    del dx32
     ctx.destroy()
     del layer
     ms = (t1 - t0) * 1e3 / a.prefill_steps
@@ -454,6 +550,10 @@ def prefill(a):
     gu_us = 1e3 * ms_stage[2] / max(n_stage[2], 1)
     gu_flops = 2 * T * K * 2 * I * D
     gu_tf = gu_flops / (gu_us * 1e-6) / 1e12
+    ms32 = (g1 - g0) * 1e3 / a.prefill_steps
+    gu32_us = 1e3 * ms32_stage[2] / max(n32_stage[2], 1)
+    gu32_tf = gu_flops / (gu32_us * 1e-6) / 1e12
+    same = float(np.mean(np.sort(idx32.reshape(T, K), axis=1) == np.sort(idx.reshape(T, K), axis=1)))
     return {
         "tokens": T,
         "ms_per_step": round(ms, 4),
@@ -483,6 +583,24 @@ def prefill(a):
             "what": "routed experts on v_mfma_scale_f32_16x16x128_f8f6f4: MXFP4 weights as "
                     "stored, x and h quantised to MXFP8 (E4M3, E8M0 per 32); shared expert "
                     "bf16; rel-L2 vs the unquantised engine ~5e-2 (tests)"},
+        "fp32_x": {
+            "ms_per_step": round(ms32, 4), "tokens_per_s": round(T / (ms32 * 1e-3), 1),
+            "mfma_frac": round(flops / (ms32 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "achieved_TFLOPs": round(flops / (ms32 * 1e-3) / 1e12, 1),
+            "stage_us": {names[s]: round(1e3 * ms32_stage[s] / max(n32_stage[s], 1), 1)
+                         for s in range(len(names)) if n32_stage[s]},
+            "routing_slots_same_as_bf16_x": round(same, 4),
+            "what": "the same 4096 tokens as fp32 values (the engine's k3_decoder_layer_inc "
+                    "input, not rounded to bf16): x is two bf16 pieces, so the router adds "
+                    "the second piece's product and the routed and shared gate/up GEMMs "
+                    "multiply both pieces (8-wave workgroups); same layer, same Zipf(0.8) "
+                    "skew",
+            "roofline": {"kernel": "k_gemm routed gate/up on x's two bf16 pieces",
+                         "bound": "mfma", "achieved": round(gu32_tf, 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(gu32_tf / BF16_PEAK_TFLOPS, 4),
+                         "traffic": TRAFFIC_GATEUP_PREFILL_FP32,
+                         "flop_per_launch": gu_flops, "avg_launch_us": round(gu32_us, 1)}},
         "roofline": {"kernel": "k_gemm<0> routed gate/up (MXFP4 dequantised to bf16 in "
                                "registers, bf16 MFMA, SwiGLU epilogue)",
                      "bound": "mfma", "achieved": round(gu_tf, 1), "peak": BF16_PEAK_TFLOPS,

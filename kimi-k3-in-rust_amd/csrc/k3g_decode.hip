@@ -559,11 +559,11 @@ __device__ __forceinline__ K3ArgPtr k3d_uniform_cptr(K3ArgPtr p)
 /* The slices of the bf16 ticket classes start at multiples of 32 KB of their tiled
  * matrices, and every wave of a class streams its slice from the first 8 KB batch to the
  * last at about the same pace: left alone, the waves' reads would all fall in the same
- * 8 KB of every 32 KB at once. Batch bi of a ticket's nb is taken at position
- * (bi + rot) mod nb, rot = ticket mod nb, so waves running together start at different
- * offsets. */
+ * 8 KB of every 32 KB at once. With K3G_ROT, batch bi of a ticket's nb is taken at
+ * position (bi + rot) mod nb, rot = ticket mod nb, so waves running together start at
+ * different offsets (measured: no gain at the K2 and K3 shapes, so it is off). */
 #ifndef K3G_ROT
-#define K3G_ROT 1
+#define K3G_ROT 0
 #endif
 __device__ __forceinline__ int k3d_batch_rot(int tk, int nb) { return K3G_ROT && nb > 0 ? tk % nb : 0; }
 __device__ __forceinline__ int k3d_batch_at(int bi, int nb, int rot)
@@ -745,7 +745,10 @@ struct K3Dec {
             k3d_set_event(a.sync, G.eSEL, lane);
             return;
         }
-        if (!k3d_wait_event(a.sync, G.eR, 0, a.spin_limit, a.err, lane)) return;
+        /* every router row in: the select is the only waiter, so it reads the rows'
+         * sub-counters itself instead of waiting for the top count and the event flags
+         * (one returning atomic and a flag store less on the routed experts' path) */
+        if (!k3d_wait_sum(a.sync, G.cR + 1, NSUB, a.E, a.spin_limit, a.err, lane)) return;
         /* instrumentation: after the trace's [ticket][2] stamps, the select's own phases */
         if (a.trace && lane == 0) a.trace[3 * G.total] = wall_clock64();
         /* everything routed waits for this wave: let it issue ahead of its SIMD's others */
@@ -877,13 +880,13 @@ struct K3Dec {
         const int p = tk / per, rem = tk - p * per;
         const int gt = rem / G.KSG, ks = rem - gt * G.KSG;
         const int q0 = ks * G.nQk / G.KSG, q1 = (ks + 1) * G.nQk / G.KSG;
+        const int t = p / a.k;
         if (!k3d_wait_event(a.sync, G.eSEL, tk, a.spin_limit, a.err, lane)) return;
         /* the latent layer's routed input is z = down x */
         if (G.lat && !k3d_wait_event(a.sync, G.eZ, tk, a.spin_limit, a.err, lane)) return;
         k3d_trace_go(a.trace, G.oG + tk, lane);
         const int e = k3d_uniform(__hip_atomic_load(&a.idx[p], __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT));
-        const int t = p / a.k;
         k3v4f acc[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
         if (e >= 0 && e < a.E) {
             const uint8_t *w1 = k3d_uniform_ptr((const uint8_t *)a.eq[e].p1);

@@ -20,6 +20,14 @@
 #define K3G_SELECT_FAST 1
 #endif
 
+/* k3d_select_fast's LDS: the candidates (keys, lo, hi, score) and the selection by rank */
+struct K3RankLds {
+    unsigned long long ckey[64], rkey[64];
+    float clo[64], chi[64], csc[64];
+    float rlo[64], rhi[64], rsc[64];
+    int rsel[64];
+};
+
 struct K3SelectLds {
     float choice[K3G_MAX_E];
     float lo[K3G_MAX_E];
@@ -32,11 +40,7 @@ struct K3SelectLds {
     int ncand, nredo;
     int cert;
     double wsum;
-    /* k3d_select_fast: the candidates (keys, lo, hi, score) and the selection by rank */
-    unsigned long long ckey[64], rkey[64];
-    float clo[64], chi[64], csc[64];
-    float rlo[64], rhi[64], rsc[64];
-    int rsel[64];
+    K3RankLds rk;
 };
 
 /* {choice, lo, hi, score} of one expert from its fp64 logit sum `acc` and a bound `ab` on
@@ -330,7 +334,7 @@ __device__ __forceinline__ bool k3d_settled_float(double s, double a, int n, flo
  * nothing changed, when fewer than k lanes hold a key or the candidates are more than 64;
  * the rounds then run as before. */
 template <int NPL>
-__device__ __forceinline__ bool k3d_select_fast(K3SelectLds *s, const uint64_t (&key)[NPL],
+__device__ __forceinline__ bool k3d_select_fast(K3RankLds *s, const uint64_t (&key)[NPL],
                                                 const float4 (&v)[NPL], int k, int lane,
                                                 uint32_t &taken, bool &ok, float &minlo,
                                                 double &wsum, int &my_sel, float &my_score,
@@ -367,9 +371,16 @@ __device__ __forceinline__ bool k3d_select_fast(K3SelectLds *s, const uint64_t (
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_wave_barrier();
+    /* lane j holds candidate j; its rank from the other candidates' keys read across the
+     * wave (register reads, no LDS round trip per candidate) */
     const uint64_t mine = lane < total ? s->ckey[lane] : 0;
+    const uint32_t mhi = (uint32_t)(mine >> 32), mlo = (uint32_t)mine;
     int rank = 0;
-    for (int q = 0; q < total; ++q) rank += s->ckey[q] > mine ? 1 : 0;
+    for (int q = 0; q < total; ++q) {
+        const uint32_t oh = (uint32_t)__builtin_amdgcn_readlane((int)mhi, q);
+        const uint32_t ol = (uint32_t)__builtin_amdgcn_readlane((int)mlo, q);
+        rank += (((uint64_t)oh << 32) | ol) > mine ? 1 : 0;
+    }
     if (lane < total && rank < k) {
         s->rkey[rank] = mine;
         s->rsel[rank] = (int)~(uint32_t)mine;
@@ -464,7 +475,7 @@ k3d_select_token_n(K3SelectLds *s, int t, const float4 *rs, const float *bias,
     int my_sel = -1;          /* lane j: the j-th selected expert */
     float my_score = 0.0f, my_hi = 0.0f;
     const bool fast = K3G_SELECT_FAST &&
-                      k3d_select_fast<NPL>(s, key, v, k, lane, taken, ok, minlo, wsum, my_sel,
+                      k3d_select_fast<NPL>(&s->rk, key, v, k, lane, taken, ok, minlo, wsum, my_sel,
                                            my_score, my_hi);
     for (int j = 0; j < (fast ? 0 : k); ++j) {
         /* this lane's best untaken key: a tree over the slots */

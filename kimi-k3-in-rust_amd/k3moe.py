@@ -649,9 +649,11 @@ class SynthLayer:
         c.n_layers = 1
         return c
 
-    def tokens(self, T: int, stream_base: int = 0) -> np.ndarray:
+    def tokens(self, T: int, stream_base: int = 0, bf16=None) -> np.ndarray:
+        """T tokens of the layer's input stream; bf16 (default: the shape's x_bf16) rounds
+        the same draws to bf16 values."""
         x = host_normal(T * self.shape.hidden, self.seed, S_X + 100 * self.layer + stream_base,
-                        0.0, 1.0, bf16=self.shape.x_bf16)
+                        0.0, 1.0, bf16=self.shape.x_bf16 if bf16 is None else bf16)
         return x.reshape(T, self.shape.hidden)
 
 
