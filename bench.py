@@ -40,17 +40,18 @@ B_TOKEN = D * 2 + D * 4                    # bf16-valued input, fp32 output
 B_GATEUP_EXPERT = 2 * (I * D // 2 + I * D // 32)   # w1 + w3 of one expert
 
 # HBM bytes per launch of the fused decode kernel on this workload, from two rocprofv3
-# --pmc runs (FETCH_SIZE x 1.9994 + WRITE_SIZE x 1.0, the factors that make a 256 MiB
+# --pmc runs (FETCH_SIZE x 1.9997 + WRITE_SIZE x 1.0, the factors that make a 256 MiB
 # device-to-device copy read 256 MiB); the run and the numbers are in
 # profiles/k_decode_fused_k2_decode.md. Re-measured whenever the kernel changes.
-TRAFFIC_FUSED = 300037638
+TRAFFIC_FUSED = 302055321
 # HBM bytes per launch of the routed gate/up GEMM (k_gemm<0, 4>) of the 4096-token
 # Zipf(0.8) prefill, the same way (FETCH_SIZE x 1.9997 + WRITE_SIZE, mean of 3 launches):
 # 7.666 GB read + 0.204 GB written; profiles/k_gemm_k2_prefill4096.md.
 TRAFFIC_GATEUP_PREFILL = 7869400121
-# the same for the fp32-x sub-leg's routed gate/up (x in two bf16 pieces); None until a
-# counter run measures it
-TRAFFIC_GATEUP_PREFILL_FP32 = None
+# the same for the fp32-x sub-leg's routed gate/up (k_gemm<0, 8>: x in two bf16 pieces),
+# mean of its last 6 launches: 8.059 GB read + 0.203 GB written;
+# profiles/k_gemm_k2_prefill4096.md.
+TRAFFIC_GATEUP_PREFILL_FP32 = 8261930315
 
 
 def log(msg):
@@ -595,7 +596,8 @@ def prefill(a):
                     "the second piece's product and the routed and shared gate/up GEMMs "
                     "multiply both pieces (8-wave workgroups); same layer, same Zipf(0.8) "
                     "skew",
-            "roofline": {"kernel": "k_gemm routed gate/up on x's two bf16 pieces",
+            "roofline": {"kernel": "k_gemm<0, 8> routed gate/up on x's two bf16 pieces "
+                                   "(8-wave workgroups)",
                          "bound": "mfma", "achieved": round(gu32_tf, 1),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(gu32_tf / BF16_PEAK_TFLOPS, 4),
