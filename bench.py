@@ -656,9 +656,18 @@ def dropin(a):
         idx = np.zeros(K, np.int32)
         wt = np.zeros(K, np.float32)
 
+        # the call's pointers formed before the timed loop: the engine calls k3_moe from C,
+        # so per-call Python work (slicing, ctypes conversions) is not part of the leg
+        optr, xptr = out.ctypes.data, xs.ctypes.data
+        wrefs = [C.byref(w) for w in ws]
+        cref, iptr, wptr = C.byref(cfg), C.c_void_p(idx.ctypes.data), C.c_void_p(wt.ctypes.data)
+        ob, xb = T * D * 4, T * xs.shape[1] * 4
+        args = [(C.c_void_p(optr + i * ob), C.c_void_p(xptr + i * xb), wrefs[i % len(ws)])
+                for i in range(n)]
+
         def call(i):
-            fn(out[i * T:].ctypes.data, xs[i * T:].ctypes.data, C.byref(ws[i % len(ws)]),
-               C.byref(cfg), T, idx.ctypes.data, wt.ctypes.data, None)
+            o, xq, w = args[i]
+            fn(o, xq, w, cref, T, iptr, wptr, None)
 
         for i in range(warm):
             call(i)

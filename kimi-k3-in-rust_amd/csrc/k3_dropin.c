@@ -819,7 +819,6 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
     float *rwt = (float *)(pin + o_wt), *pout = (float *)(pin + o_out);
     float *px = (float *)(pin + io_n);
     host_copy(px, x, xbytes);
-    xfer(xd, px, xbytes, hipMemcpyHostToDevice, st);
     ctx->paths = 0;
     host_scratch(s, (size_t)T * k, E);
     int last[K3_MAX_TOPK];
@@ -834,6 +833,9 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         k3gc_wait(hc, st);
         G.experts = k3gc_layer_table(hc, w->layer, st);
         if (!G.experts) k3g_fatal("k3_moe: expert table update failed");
+        /* x goes in right before the layer, so the two launches reach the GPU back to
+         * back (host work between them would leave it idle) */
+        xfer(xd, px, xbytes, hipMemcpyHostToDevice, st);
         for (int pass = 0;; pass++) {
             if (k3g_moe(ctx, &G, xd, T, od, didx, dwt, st) != 0)
                 k3g_fatal("k3_moe: launch failed");
@@ -860,6 +862,7 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         return;
     }
 
+    xfer(xd, px, xbytes, hipMemcpyHostToDevice, st);
     if (k3g_route(ctx, &G, xd, T, didx, dwt, st) != 0) k3g_fatal("k3_moe: router launch");
     xfer(pin, io, o_out, hipMemcpyDeviceToHost, st);
     K3G_CHECK(hipStreamSynchronize(st));
