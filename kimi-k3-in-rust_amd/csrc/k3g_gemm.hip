@@ -706,16 +706,22 @@ __device__ __forceinline__ void gm_tile_mix(const K3kGemm &g, const GmTile &t,
  * on one XCD, sharing its activations in that XCD's L2. Returns false when the workgroup
  * has no tile. */
 template <int AF, int WV>
-__device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *lds, int &nb)
+__device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *lds, int &nb,
+                                         bool halves = false)
 {
-    /* dense GEMMs cut into K slices take (column tile, slice) pairs as their tiles */
+    /* dense GEMMs cut into K slices take (column tile, slice) pairs as their tiles; with
+     * halves, every column tile is two work items of up to 64 columns, dealt one after
+     * the other to the same XCD */
     const int ks_n = g.tiles ? 1 : max(1, g.ksplit);
-    const int ntl = (g.tiles ? *g.ntiles : (g.dense_rows + GM_COLS - 1) / GM_COLS) * ks_n;
+    const int ntl = (g.tiles ? *g.ntiles : (g.dense_rows + GM_COLS - 1) / GM_COLS) * ks_n *
+                    (halves ? 2 : 1);
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int rnd = slot / g.nft, f = slot - rnd * g.nft;
     const int grp = rnd / K3G_TILE_GROUP, gi = rnd - grp * K3G_TILE_GROUP;
-    const int tks = K3G_TILE_GROUP * (8 * grp + ((grp & 1) ? 7 - xcd : xcd)) + gi;
+    int tks = K3G_TILE_GROUP * (8 * grp + ((grp & 1) ? 7 - xcd : xcd)) + gi;
     if (tks >= ntl) return false;
+    const int hf = halves ? (tks & 1) : 0;
+    if (halves) tks >>= 1;
     const int tile = tks / ks_n;
     t.ks = tks - tile * ks_n;
     int e = 0;
@@ -725,6 +731,11 @@ __device__ __forceinline__ bool gm_setup(const K3kGemm &g, GmTile &t, uint8_t *l
     } else {
         t.p0 = tile * GM_COLS;
         t.np = min(GM_COLS, g.dense_rows - t.p0);
+    }
+    if (halves) {
+        if (64 * hf >= t.np) return false;               /* a tile of 64 columns or fewer */
+        t.p0 += 64 * hf;
+        t.np = min(64, t.np - 64 * hf);
     }
     nb = (t.np + 15) >> 4;                               /* 16-column blocks in use */
     t.lane = threadIdx.x & 63;
@@ -1020,39 +1031,34 @@ __global__ void __launch_bounds__(GM_WAVES * 64, 1)
 k_gemm_f8(const K3kGemm g)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * GM_F8_STAGE];
-    GmTile tt;
-    int nbt;
-    if (!gm_setup<0, GM_WAVES>(g, tt, lds, nbt)) return;
-    /* a 128-column tile runs as two halves of up to 64 columns (4 x 4 accumulators fit
-     * beside the weight pipeline; the second half finds the weights in L2) */
-    for (int half = 0; 64 * half < tt.np; ++half) {
-        GmTile t = tt;
-        t.p0 = tt.p0 + 64 * half;
-        t.np = min(64, tt.np - 64 * half);
-        const int nb = (t.np + 15) >> 4;
-        if (half) __syncthreads();                      /* the first half's stages are free */
-        /* data DMA: instruction i of wave w fills rows 8 (8 i + w) .. + 7 (only i = 0 is
-         * needed for 64 rows); lane l writes row 8 (8 i + w) + l / 8, physical unit l % 8 =
-         * logical unit (l % 8) ^ ((row / 2) % 8); logical unit 2 q holds column unit q,
-         * 2 q + 1 holds unit 4 + q */
-        uint32_t doff[2];
+    /* the tile's two 64-column halves are separate work items on one XCD, one after the
+     * other in its dispatch order (4 x 4 accumulators fit beside the weight pipeline, 4 x 8
+     * do not), so they stream the same weights at about the same time and the second
+     * finds them in the XCD's L2 */
+    GmTile t;
+    int nb;
+    if (!gm_setup<0, GM_WAVES>(g, t, lds, nb, true)) return;
+    /* data DMA: instruction i of wave w fills rows 8 (8 i + w) .. + 7 (only i = 0 is
+     * needed for 64 rows); lane l writes row 8 (8 i + w) + l / 8, physical unit l % 8 =
+     * logical unit (l % 8) ^ ((row / 2) % 8); logical unit 2 q holds column unit q,
+     * 2 q + 1 holds unit 4 + q */
+    uint32_t doff[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int r = 8 * (8 * i + t.w) + (t.lane >> 3);
-            const int ls = (t.lane & 7) ^ ((r >> 1) & 7);
-            const int u = (ls & 1) ? 4 + (ls >> 1) : (ls >> 1);
-            doff[i] = (uint32_t)gm_src_row(g, t, r) * (uint32_t)g.ldb + 16 * u;
-        }
-        const int nd = min(2, (2 * nb + 7 - t.w) / 8);
-        /* scales: wave 0 fills rows 0 .. 63, 4 bytes each */
-        const uint32_t soff = (uint32_t)gm_src_row(g, t, t.lane) * (uint32_t)(g.ldb / 32);
-        switch (nb) {
-            case 1: gm_tile_f8<1>(g, t, doff, soff, nd, 1); break;
-            case 2: gm_tile_f8<2>(g, t, doff, soff, nd, 1); break;
-            case 3: gm_tile_f8<3>(g, t, doff, soff, nd, 1); break;
-            case 4: gm_tile_f8<4>(g, t, doff, soff, nd, 1); break;
-            default: break;
-        }
+    for (int i = 0; i < 2; ++i) {
+        const int r = 8 * (8 * i + t.w) + (t.lane >> 3);
+        const int ls = (t.lane & 7) ^ ((r >> 1) & 7);
+        const int u = (ls & 1) ? 4 + (ls >> 1) : (ls >> 1);
+        doff[i] = (uint32_t)gm_src_row(g, t, r) * (uint32_t)g.ldb + 16 * u;
+    }
+    const int nd = min(2, (2 * nb + 7 - t.w) / 8);
+    /* scales: wave 0 fills rows 0 .. 63, 4 bytes each */
+    const uint32_t soff = (uint32_t)gm_src_row(g, t, t.lane) * (uint32_t)(g.ldb / 32);
+    switch (nb) {
+        case 1: gm_tile_f8<1>(g, t, doff, soff, nd, 1); break;
+        case 2: gm_tile_f8<2>(g, t, doff, soff, nd, 1); break;
+        case 3: gm_tile_f8<3>(g, t, doff, soff, nd, 1); break;
+        case 4: gm_tile_f8<4>(g, t, doff, soff, nd, 1); break;
+        default: break;
     }
 }
 
@@ -1238,7 +1244,7 @@ extern "C" int k3k_gemm_f8(const K3kGemm *g, hipStream_t st)
     if (g->tiles ? (!g->ntiles || g->max_tiles < 1) : g->dense_rows < 1) return -1;
     if ((g->scatter || (g->mode == 0 && g->tiles)) && !g->perm) return -1;
     const long long maxt = g->tiles ? g->max_tiles : (g->dense_rows + GM_COLS - 1) / GM_COLS;
-    const long long grid = 8 * (long long)K3G_TILE_ROUNDS(maxt) * g->nft;
+    const long long grid = 8 * (long long)K3G_TILE_ROUNDS(2 * maxt) * g->nft;   /* halves */
     if (grid > 0x7fffffff) return -1;
     hipLaunchKernelGGL(k_gemm_f8, dim3((unsigned)grid), dim3(GM_WAVES * 64), 0, st, *g);
     return hipGetLastError() == hipSuccess ? 0 : -1;
