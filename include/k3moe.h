@@ -191,6 +191,115 @@ int k3moe_last_kernels(void);
  * dropped first. No reference counterpart: the engine reads host weights in place. */
 void k3moe_invalidate_weights(const void *host, size_t bytes);
 
+/* ================================================= 1b. the engine's expert cache == */
+/* The engine's checkpoint index and expert geometry, field for field
+ * (src/io/k3_st.h:29-70, src/io/k3_load.h:29-43), declared only when the engine's own
+ * headers have not been included: k3_cache_init reads the K3St that the engine's
+ * k3_st_open filled in. */
+#ifndef K3_ST_H
+typedef enum { K3_DT_UNKNOWN = 0, K3_DT_U8, K3_DT_BF16, K3_DT_F16, K3_DT_F32,
+               K3_DT_I8R } K3Dtype;
+typedef struct {
+    char     *name;
+    int       shard;          /* index into K3St.fd[] */
+    K3Dtype   dtype;
+    int       ndim;
+    int64_t   shape[4];
+    int64_t   off;            /* absolute byte offset in the shard */
+    int64_t   nbytes;
+} K3Tensor;
+#define K3_ST_ALIGN 4096
+typedef struct {
+    int       *fd;            /* one descriptor per shard */
+    int       *dfd;           /* the same shards opened O_DIRECT, or -1 */
+    char     **path;
+    int        nshard;
+    K3Tensor  *t;             /* every tensor */
+    int        nt;
+    int32_t   *bucket;        /* the engine's hash index (not read here) */
+    int        nbucket;
+    char      *strpool;
+    size_t     strcap, strlen_;
+} K3St;
+#endif /* K3_ST_H */
+#ifndef K3_LOAD_H
+typedef struct {
+    int64_t p_off, p_bytes;   /* packed nibbles, offset within the run */
+    int64_t s_off, s_bytes;   /* E8M0 scales, offset within the run */
+    int     rows, pcols;
+    int     scols;
+} K3QMat;
+typedef struct {
+    int     layer, expert;
+    int     shard;
+    int64_t off;              /* file offset of the run */
+    int64_t nbytes;
+    int     contiguous;
+    K3QMat  m[3];             /* w1, w2, w3 */
+} K3ExpertRef;
+#endif /* K3_LOAD_H */
+
+/* The engine's expert cache, src/cache/k3_cache.h:47-96, field for field, so that the
+ * engine's main() (src/cli/k3_run.c:1144-1155, :1524-1534) reads nslot, slot_bytes and
+ * the counters and wires &cache->src into every K3MoeW unchanged. Here the slots are in
+ * HBM: arena is a DEVICE pointer, get() hands out device pointers (the tiled MXFP4 layout
+ * when the checkpoint's experts have one, the checkpoint layout otherwise), and k3_moe /
+ * k3_moe_prefill of this library run on them in place. A miss is read from the
+ * checkpoint (O_DIRECT where the shard has it, the misses of one getmany in parallel)
+ * into pinned staging and copied to its slot on a side stream. The fields mean what the
+ * engine's mean; slot_of, key_of, used_at, pinned and hist are the cache's live arrays,
+ * the counters are brought up to date by every call, ref[slot] is the geometry of the
+ * expert a slot holds as k3_expert_ref gives it for a run in the checkpoint order
+ * (w1p w1s w2p w2s w3p w3s; a run whose tensors are stored in another order is read as
+ * six spans into that order) and pad[] stays 0. src.ctx belongs to the cache. */
+#ifndef K3_CACHE_H
+#define K3_SLOT_EMPTY     (-1)
+#define K3_SLOT_INFLIGHT  (-2)
+typedef struct {
+    K3ExpertSrc  src;         /* first: pass &cache->src to K3MoeW */
+    const K3St  *st;
+    int          n_layers, n_experts;
+    unsigned char *arena;     /* nslot * slot_bytes of HBM */
+    int64_t      slot_bytes;
+    int          nslot;
+    int32_t     *slot_of;     /* [n_layers * n_experts] -> slot, or -1 */
+    int32_t     *key_of;      /* [nslot] -> layer * n_experts + expert, EMPTY or INFLIGHT */
+    uint64_t    *used_at;     /* [nslot] LRU stamp */
+    unsigned char *pinned;    /* [nslot] */
+    K3ExpertRef *ref;         /* [nslot] */
+    int32_t     *pad;         /* [nslot] */
+    uint64_t     clock;
+    uint64_t     hits, misses, evictions, bytes_read;
+    uint64_t     prefetch_reads;   /* misses brought in by getmany */
+    double       load_seconds;     /* host time spent reading the checkpoint */
+    uint32_t    *hist;        /* [n_layers * n_experts] requests */
+    int32_t     *trace;       /* (layer, expert) pairs in request order */
+    int64_t      ntrace, captrace;
+} K3Cache;
+#endif /* K3_CACHE_H */
+
+/* Replaces src/cache/k3_cache.h:97-100 (src/cache/k3_cache.c:262-345). Sizes a slot from
+ * the first routed expert found in the checkpoint (layers from cfg->first_dense on),
+ * takes budget_bytes of HBM on the current device, and fails with a message when that is
+ * fewer than topk + 1 slots. K3_NOPREFETCH set: no getmany, as in the engine. */
+int  k3_cache_init(K3Cache *c, const K3St *st, const K3Cfg *cfg, int64_t budget_bytes);
+/* Replaces src/cache/k3_cache.h:101 (k3_cache.c:347-353); call before the engine's
+ * k3_st_close. */
+void k3_cache_free(K3Cache *c);
+/* Replaces src/cache/k3_cache.h:103-105 (k3_cache.c:367-375): 1 when the expert was
+ * resident (and is now pinned or unpinned), 0 otherwise. */
+int  k3_cache_pin(K3Cache *c, int layer, int expert, int pin);
+/* Replaces src/cache/k3_cache.h:107-108 (k3_cache.c:377-380): 0, or -1 when it could
+ * not be brought in. */
+int  k3_cache_prefetch(K3Cache *c, int layer, int expert);
+/* Replaces src/cache/k3_cache.h:110-111 (k3_cache.c:382-394, :396-424). */
+void k3_cache_reset_stats(K3Cache *c);
+void k3_cache_report(const K3Cache *c, const char *label);
+/* Replaces src/cache/k3_cache.h:113-118 (k3_cache.c:355-365, :426-446): the engine's
+ * JSON histogram and flat int32 (layer, expert) trace. */
+int  k3_cache_dump_hist(const K3Cache *c, const char *path);
+int  k3_cache_dump_trace(const K3Cache *c, const char *path);
+
 /* ============================================================== 2. device API == */
 
 typedef struct K3gCtx K3gCtx;        /* device, streams, workspace; opaque */
@@ -459,6 +568,23 @@ int  k3gc_st_expert(const K3gcSt *st, int layer, int expert, K3gcExpertRun *run)
 /* The run's bytes in the checkpoint order into dst (run->nbytes): one read when
  * contiguous, six otherwise (src/io/k3_load.c:105-136). Returns 0, or -1 on a short read. */
 int  k3gc_st_read_run(const K3gcSt *st, const K3gcExpertRun *run, unsigned char *dst);
+/* The same into buf (cap bytes): a contiguous run with O_DIRECT straight into buf when
+ * buf is 4096-aligned and holds the run's enclosing 4096-byte window, the run then at
+ * buf + *pad (src/io/k3_st.c:457-497); ordinary reads at buf otherwise (*pad = 0). */
+int  k3gc_st_read_run_into(const K3gcSt *st, const K3gcExpertRun *run, unsigned char *buf,
+                           int64_t cap, int64_t *pad);
+/* An index over the engine's own K3St (as its k3_st_open filled it): names and spans
+ * copied, the shard descriptors borrowed, so the engine's index must outlive this one. */
+int  k3gc_st_from_engine(K3gcSt **st, const K3St *engine_index);
+/* A bank that holds nothing in host memory: every miss is read from the checkpoint into
+ * pinned staging (the misses of one getmany in parallel) and copied to its slot. The
+ * layout follows expert 0 of checkpoint layer probe_layer: the tiled MXFP4 layout (tiled
+ * on the GPU after the copy) when it is an expert of a hidden x inter layer with a tiled
+ * layout, its own run layout otherwise; every later run must match it. Cache layer l
+ * reads checkpoint layer l. st must outlive the bank. No reference counterpart as a
+ * bank: the engine's k3_cache_init reads misses from the K3St itself. */
+int  k3gc_bank_create_disk(K3gcBank **bank, const K3gcSt *st, int n_layers, int n_experts,
+                           int probe_layer);
 /* Bank layers [bank_layer0, + n_layers) from checkpoint layers [ck_layer0, + n_layers):
  * every expert's run read straight into the bank's host memory (checkpoint layout), or
  * read and tiled on the host (tiled layout). A bank with a layer shape takes only experts

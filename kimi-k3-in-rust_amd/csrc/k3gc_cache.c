@@ -20,6 +20,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 static int has_device(const K3gCache *c) { return c->device >= 0; }
 
@@ -136,6 +137,83 @@ int k3gc_bank_geometry(K3gcBank **out, int n_layers, int n_experts, int64_t expe
     return 0;
 }
 
+/* ------------------------------------------------------------ checkpoint bank ---- */
+int k3gc_bank_create_disk(K3gcBank **out, const K3gcSt *st, int n_layers, int n_experts,
+                          int probe_layer)
+{
+    *out = NULL;
+    if (!st || n_layers < 1 || n_experts < 1 || probe_layer < 0 || probe_layer >= n_layers)
+        return -1;
+    K3gcExpertRun r;
+    if (k3gc_st_expert(st, probe_layer, 0, &r) != 0) return -1;
+    const int inter = r.rows[0], hidden = 2 * r.pcols[0];
+    const int shaped = r.rows[2] == inter && r.pcols[2] == r.pcols[0] && r.rows[1] == hidden &&
+                       2 * r.pcols[1] == inter;
+    const int tiled = shaped && hidden >= 32 && inter >= 32 &&
+                      k3k_tiled_mxfp4_bytes(inter, hidden) > 0 &&
+                      k3k_tiled_mxfp4_bytes(hidden, inter) > 0;
+    K3gcBank *b = (K3gcBank *)calloc(1, sizeof *b);
+    if (!b) return -1;
+    b->n_layers = n_layers;
+    b->n_experts = n_experts;
+    b->st = st;
+    b->run_bytes = r.nbytes;
+    b->layout = tiled ? K3G_EXPERT_MXFP4_TILED : K3G_EXPERT_MXFP4;
+    if (tiled) {
+        b->hidden = hidden;
+        b->inter = inter;
+        b->expert_bytes = run_bytes(hidden, inter, K3G_EXPERT_MXFP4_TILED);
+    } else {
+        /* the run's own layout: its six matrices' offsets, which every run must share */
+        int64_t at = 0;
+        for (int i = 0; i < 3; i++) {
+            b->raw_off[2 * i] = at;
+            at += r.p_bytes[i];
+            b->raw_off[2 * i + 1] = at;
+            at += r.s_bytes[i];
+        }
+        b->raw_geometry = 1;
+        b->expert_bytes = r.nbytes;
+    }
+    b->stage_cap = ((r.nbytes + 4095) & ~(int64_t)4095) + 2 * 4096;
+    for (int i = 0; i < K3GC_NSTAGE; i++) {
+        void *p = NULL;
+        if (hipHostMalloc(&p, (size_t)b->stage_cap, hipHostMallocDefault) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            fprintf(stderr, "k3gc_bank_create_disk: cannot pin %.1f MB of staging\n",
+                    (double)b->stage_cap / 1e6);
+            k3gc_bank_free(b);
+            return -1;
+        }
+        b->stage[b->nstage++] = (unsigned char *)p;
+        if (tiled && hipMalloc((void **)&b->dstage[i], (size_t)r.nbytes) != hipSuccess) {
+            (void)hipGetLastError();
+            b->dstage[i] = NULL;
+            k3gc_bank_free(b);
+            return -1;
+        }
+    }
+    *out = b;
+    return 0;
+}
+
+/* A run of a checkpoint bank has the bank's geometry. */
+static int disk_run_fits(const K3gcBank *b, const K3gcExpertRun *r)
+{
+    if (b->layout == K3G_EXPERT_MXFP4_TILED)
+        return r->rows[0] == b->inter && 2 * r->pcols[0] == b->hidden && r->rows[2] == b->inter &&
+               2 * r->pcols[2] == b->hidden && r->rows[1] == b->hidden &&
+               2 * r->pcols[1] == b->inter && r->nbytes == b->run_bytes;
+    int64_t at = 0;
+    for (int i = 0; i < 3; i++) {
+        if (b->raw_off[2 * i] != at) return 0;
+        at += r->p_bytes[i];
+        if (b->raw_off[2 * i + 1] != at) return 0;
+        at += r->s_bytes[i];
+    }
+    return r->nbytes == b->run_bytes;
+}
+
 void k3gc_bank_free(K3gcBank *b)
 {
     if (!b) return;
@@ -146,6 +224,8 @@ void k3gc_bank_free(K3gcBank *b)
             else free(b->layer_host[l]);
         }
     for (int i = 0; i < b->nstage; i++) hipHostFree(b->stage[i]);
+    for (int i = 0; i < K3GC_NSTAGE; i++)
+        if (b->dstage[i]) hipFree(b->dstage[i]);
     free(b->layer_host);
     free(b->layer_pinned);
     free(b);
@@ -273,10 +353,93 @@ static void par_copy(unsigned char *dst, const unsigned char *src, size_t n)
  * has copied that buffer's previous run out, the host copies this run in, and the DMA
  * engine copies it to the slot at the pinned rate (the host copy of the next miss
  * overlaps this one's DMA). */
-static void copy_in(K3gCache *c, int slot, int32_t key)
+static double now_s(void)
 {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+
+/* Misses of a checkpoint bank into their slots: in groups of the staging buffers, the
+ * runs resolved and read in parallel (one thread each, O_DIRECT where the shard has it),
+ * then each copied to its slot after the last step that read the slot, and tiled there
+ * for the tiled layout. ok[i] = 1 when slots[i] now holds keys[i]. */
+static void disk_fetch(K3gCache *c, int n, const int *slots, const int32_t *keys, int *ok)
+{
+    K3gcBank *b = c->bank;
+    for (int i0 = 0; i0 < n; i0 += b->nstage) {
+        const int m = n - i0 < b->nstage ? n - i0 : b->nstage;
+        int js[K3GC_NSTAGE], good[K3GC_NSTAGE];
+        int64_t pad[K3GC_NSTAGE];
+        K3gcExpertRun r[K3GC_NSTAGE];
+        for (int k = 0; k < m; k++) {
+            const int32_t key = keys[i0 + k];
+            js[k] = (int)(c->stage_next++ % (unsigned)b->nstage);
+            if (has_device(c)) K3G_CHECK(hipEventSynchronize(c->stage_ev[js[k]]));
+            good[k] = k3gc_st_expert(b->st, key / c->n_experts, key % c->n_experts, &r[k]) == 0 &&
+                      disk_run_fits(b, &r[k]);
+            pad[k] = 0;
+        }
+        const double t0 = now_s();
+#pragma omp parallel for schedule(static, 1) num_threads(m) if (m > 1)
+        for (int k = 0; k < m; k++)
+            if (good[k])
+                good[k] = k3gc_st_read_run_into(b->st, &r[k], b->stage[js[k]], b->stage_cap,
+                                                &pad[k]) == 0;
+        c->disk_seconds += now_s() - t0;
+        for (int k = 0; k < m; k++) {
+            const int32_t key = keys[i0 + k];
+            const int slot = slots[i0 + k];
+            ok[i0 + k] = good[k];
+            if (!good[k]) {
+                c->failed_reads++;
+                fprintf(stderr, "k3gc: cannot read L%d expert %d from the checkpoint (or its "
+                                "geometry differs from the cache's)\n",
+                        key / c->n_experts, key % c->n_experts);
+                continue;
+            }
+            c->bytes_read += (uint64_t)r[k].nbytes;
+            if (!has_device(c)) continue;
+            batch_open(c);
+            const int64_t s = c->use_step[slot];
+            if (s >= 0 && c->step - s <= K3GC_STEP_RING)
+                K3G_CHECK(hipStreamWaitEvent(c->copy, c->step_ev[s % K3GC_STEP_RING], 0));
+            const unsigned char *src = b->stage[js[k]] + pad[k];
+            unsigned char *dst = c->arena + (size_t)slot * c->slot_bytes;
+            if (b->layout == K3G_EXPERT_MXFP4_TILED) {
+                /* the run in the checkpoint order (w1p w1s w2p w2s w3p w3s), then w1, w3,
+                 * w2 tiled back to back as fill_q hands them out */
+                unsigned char *d = b->dstage[js[k]];
+                K3G_CHECK(hipMemcpyAsync(d, src, (size_t)r[k].nbytes, hipMemcpyHostToDevice,
+                                         c->copy));
+                const int64_t o1 = 0, o2 = r[k].p_bytes[0] + r[k].s_bytes[0];
+                const int64_t o3 = o2 + r[k].p_bytes[1] + r[k].s_bytes[1];
+                const size_t t13 = k3k_tiled_mxfp4_bytes(b->inter, b->hidden);
+                if (k3k_tile_mxfp4(dst, d + o1, d + o1 + r[k].p_bytes[0], b->inter, b->hidden,
+                                   c->copy) != 0 ||
+                    k3k_tile_mxfp4(dst + t13, d + o3, d + o3 + r[k].p_bytes[2], b->inter,
+                                   b->hidden, c->copy) != 0 ||
+                    k3k_tile_mxfp4(dst + 2 * t13, d + o2, d + o2 + r[k].p_bytes[1], b->hidden,
+                                   b->inter, c->copy) != 0)
+                    k3g_fatal("k3gc: tiling a checkpoint run failed");
+            } else {
+                K3G_CHECK(hipMemcpyAsync(dst, src, (size_t)r[k].nbytes, hipMemcpyHostToDevice,
+                                         c->copy));
+            }
+            K3G_CHECK(hipEventRecord(c->stage_ev[js[k]], c->copy));
+        }
+    }
+}
+
+static int copy_in(K3gCache *c, int slot, int32_t key)
+{
+    if (c->bank->st) {
+        int ok = 0;
+        disk_fetch(c, 1, &slot, &key, &ok);
+        return ok ? 0 : -1;
+    }
     c->bytes_read += (uint64_t)c->bank->expert_bytes;
-    if (!has_device(c)) return;
+    if (!has_device(c)) return 0;
     batch_open(c);
     const int64_t s = c->use_step[slot];
     if (s >= 0 && c->step - s <= K3GC_STEP_RING)
@@ -296,6 +459,7 @@ static void copy_in(K3gCache *c, int slot, int32_t key)
     } else {
         K3G_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, c->copy));
     }
+    return 0;
 }
 
 /* Bring (layer, expert) resident; returns its slot or -1. src/cache/k3_cache.c:63-110 */
@@ -320,7 +484,10 @@ static int admit(K3gCache *c, int layer, int expert)
         c->slot_of[c->key_of[slot]] = -1;
         c->evictions++;
     }
-    copy_in(c, slot, key);
+    if (copy_in(c, slot, key) != 0) {
+        c->key_of[slot] = K3GC_EMPTY;        /* holds nothing: k3_cache.c:96-101 */
+        return -1;
+    }
     c->key_of[slot] = key;
     c->slot_of[key] = slot;
     key_in(c, key);
@@ -383,17 +550,30 @@ static int cache_getmany(K3ExpertSrc *self, int layer, const int *ids, int n)
         experts[nw] = e;
         nw++;
     }
-    for (int i = 0; i < nw; i++) copy_in(c, slots[i], layer * c->n_experts + experts[i]);
+    int ok[K3_MAX_TOPK];
+    int32_t keys[K3_MAX_TOPK];
+    for (int i = 0; i < nw; i++) keys[i] = layer * c->n_experts + experts[i];
+    if (c->bank->st) {
+        disk_fetch(c, nw, slots, keys, ok);
+    } else {
+        for (int i = 0; i < nw; i++) ok[i] = copy_in(c, slots[i], layer * c->n_experts + experts[i]) == 0;
+    }
     batch_close(c);
+    int pub = 0;
     for (int i = 0; i < nw; i++) {
         const int32_t key = layer * c->n_experts + experts[i];
+        if (!ok[i]) {
+            c->key_of[slots[i]] = K3GC_EMPTY;   /* a failed read publishes nothing */
+            continue;
+        }
+        pub++;
         c->key_of[slots[i]] = key;
         c->slot_of[key] = slots[i];
         key_in(c, key);
         c->used_at[slots[i]] = ++c->clock;
         c->prefetch_reads++;
     }
-    return nw;
+    return pub;
 }
 
 static int cache_resident(K3ExpertSrc *self, int layer, int expert, K3ExpertQ *out)
@@ -406,7 +586,10 @@ static int cache_resident(K3ExpertSrc *self, int layer, int expert, K3ExpertQ *o
     return 1;
 }
 
-int k3gc_is_device_src(const K3ExpertSrc *src) { return src && src->get == cache_get; }
+int k3gc_is_device_src(const K3ExpertSrc *src)
+{
+    return src && (src->get == cache_get || k3_cache_inner_of(src) != NULL);
+}
 
 int k3gc_layer_all_resident(const K3gCache *c, int layer)
 {
@@ -436,7 +619,8 @@ const K3ExpertQ *k3gc_layer_table(K3gCache *c, int layer, hipStream_t st)
 
 K3gCache *k3gc_of_src(K3ExpertSrc *src)
 {
-    return k3gc_is_device_src(src) ? (K3gCache *)src : NULL;
+    if (src && src->get == cache_get) return (K3gCache *)src;
+    return k3_cache_inner_of(src);
 }
 
 K3ExpertSrc *k3gc_src(K3gCache *c) { return c ? &c->src : NULL; }
@@ -446,7 +630,7 @@ int k3gc_init(K3gCache **out, int device, K3gcBank *bank, int topk, int64_t budg
 {
     *out = NULL;
     if (!bank || topk < 1) return -1;
-    if (device >= 0 && !bank->layer_host) {
+    if (device >= 0 && !bank->layer_host && !bank->st) {
         fprintf(stderr, "k3gc_init: the bank holds no host memory\n");
         return -1;
     }
@@ -621,7 +805,8 @@ void k3gc_reset_stats(K3gCache *c)
     if (has_device(c)) harvest_timers(c, 1);
     /* prefetch_reads covers the same window as hits (k3_cache.c:384-394) */
     c->hits = c->misses = c->evictions = c->bytes_read = c->prefetch_reads = 0;
-    c->load_seconds = 0.0;
+    c->load_seconds = c->disk_seconds = 0.0;
+    c->failed_reads = 0;
 }
 
 void k3gc_stats(K3gCache *c, K3gcStats *o)

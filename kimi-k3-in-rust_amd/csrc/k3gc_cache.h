@@ -33,6 +33,14 @@ struct K3gcBank {
      * threads), the DMA engine copies it out at the pinned rate */
     unsigned char *stage[K3GC_NSTAGE];
     int nstage;
+    /* a checkpoint bank (k3gc_bank_create_disk): no host copy of the experts; a miss is
+     * read from st into a pinned staging buffer (stage_cap bytes, room for the run's
+     * enclosing 4096-byte window) and, for the tiled layout, copied to a device staging
+     * buffer and tiled into its slot */
+    const K3gcSt *st;
+    int64_t run_bytes;            /* checkpoint bytes of one run */
+    int64_t stage_cap;
+    unsigned char *dstage[K3GC_NSTAGE];
 };
 
 struct K3gCache {
@@ -76,11 +84,16 @@ struct K3gCache {
     /* stats (src/cache/k3_cache.h:74-83) */
     uint64_t hits, misses, evictions, bytes_read, prefetch_reads;
     double load_seconds;
+    double disk_seconds;          /* checkpoint bank: host time in checkpoint reads */
+    uint64_t failed_reads;        /* checkpoint bank: runs that could not be read */
     uint32_t *hist;               /* [n_layers * n_experts] requests */
     int32_t *trace;               /* (layer, expert) pairs in request order */
     int64_t ntrace, captrace;
 };
 
+/* The HBM cache inside an engine-layout K3Cache whose src this is, or NULL
+ * (k3_cache_dropin.c). */
+K3gCache *k3_cache_inner_of(const K3ExpertSrc *src);
 /* 1 when src is an HBM expert cache, whose get() hands out device pointers. */
 int k3gc_is_device_src(const K3ExpertSrc *src);
 /* The cache behind a device source (NULL otherwise). */

@@ -50,6 +50,7 @@ struct K3gcSt {
     int *dfd;                     /* O_DIRECT descriptor of each shard, or -1 */
     StTensor *t;                  /* sorted by name */
     int nt, capt;
+    int borrowed;                 /* descriptors belong to the engine's K3St */
 };
 
 /* ------------------------------------------------------------ a JSON scanner ---- */
@@ -293,12 +294,14 @@ static int cmp_path(const void *a, const void *b)
     return strcmp(*(char *const *)a, *(char *const *)b);
 }
 
+static int sort_and_check(K3gcSt *st);
+
 void k3gc_st_close(K3gcSt *st)
 {
     if (!st) return;
     for (int i = 0; i < st->nshard; i++) {
-        if (st->fd && st->fd[i] >= 0) close(st->fd[i]);
-        if (st->dfd && st->dfd[i] >= 0) close(st->dfd[i]);
+        if (!st->borrowed && st->fd && st->fd[i] >= 0) close(st->fd[i]);
+        if (!st->borrowed && st->dfd && st->dfd[i] >= 0) close(st->dfd[i]);
         if (st->path) free(st->path[i]);
     }
     for (int i = 0; i < st->nt; i++) free(st->t[i].name);
@@ -351,18 +354,69 @@ int k3gc_st_open(K3gcSt **out, const char *dir)
         st->dfd[i] = open(st->path[i], O_RDONLY | O_DIRECT);   /* -1: not supported */
     for (int i = 0; i < st->nshard; i++)
         if (scan_shard(st, i, st->path[i]) != 0) { k3gc_st_close(st); return -1; }
-    qsort(st->t, (size_t)st->nt, sizeof *st->t, cmp_name);
-    for (int i = 1; i < st->nt; i++)
-        if (!strcmp(st->t[i].name, st->t[i - 1].name)) {
-            fprintf(stderr, "k3gc: duplicate tensor %s\n", st->t[i].name);
-            k3gc_st_close(st);
-            return -1;
-        }
+    if (sort_and_check(st) != 0) { k3gc_st_close(st); return -1; }
     *out = st;
     return 0;
 }
 
 int k3gc_st_count(const K3gcSt *st) { return st ? st->nt : 0; }
+
+static int sort_and_check(K3gcSt *st)
+{
+    qsort(st->t, (size_t)st->nt, sizeof *st->t, cmp_name);
+    for (int i = 1; i < st->nt; i++)
+        if (!strcmp(st->t[i].name, st->t[i - 1].name)) {
+            fprintf(stderr, "k3gc: duplicate tensor %s\n", st->t[i].name);
+            return -1;
+        }
+    return 0;
+}
+
+/* The engine's own index (a K3St its k3_st_open filled, src/io/k3_st.h:56-70): every
+ * tensor's name, shard and span copied into this index, the shards' descriptors borrowed
+ * (the engine's k3_st_close closes them, after the cache is freed). */
+int k3gc_st_from_engine(K3gcSt **out, const K3St *es)
+{
+    *out = NULL;
+    if (!es || es->nshard < 1 || !es->fd || es->nt < 0 || (es->nt > 0 && !es->t)) return -1;
+    K3gcSt *st = (K3gcSt *)calloc(1, sizeof *st);
+    if (!st) return -1;
+    st->borrowed = 1;
+    st->nshard = es->nshard;
+    st->fd = (int *)malloc((size_t)st->nshard * sizeof(int));
+    st->dfd = (int *)malloc((size_t)st->nshard * sizeof(int));
+    if (!st->fd || !st->dfd) { k3gc_st_close(st); return -1; }
+    for (int i = 0; i < st->nshard; i++) {
+        st->fd[i] = es->fd[i];
+        st->dfd[i] = es->dfd ? es->dfd[i] : -1;
+    }
+    for (int i = 0; i < es->nt; i++) {
+        const K3Tensor *et = &es->t[i];
+        if (!et->name || et->shard < 0 || et->shard >= es->nshard || et->off < 0 ||
+            et->nbytes < 0 || et->ndim < 0 || et->ndim > 4) {
+            fprintf(stderr, "k3gc: the engine's index holds a malformed tensor entry %d\n", i);
+            k3gc_st_close(st);
+            return -1;
+        }
+        StTensor t;
+        memset(&t, 0, sizeof t);
+        t.name = strdup(et->name);
+        t.shard = et->shard;
+        t.dtype_u8 = et->dtype == K3_DT_U8;
+        t.ndim = et->ndim;
+        for (int k = 0; k < et->ndim; k++) t.shape[k] = et->shape[k];
+        t.off = et->off;
+        t.nbytes = et->nbytes;
+        if (!t.name || push_tensor(st, &t) != 0) {
+            free(t.name);
+            k3gc_st_close(st);
+            return -1;
+        }
+    }
+    if (sort_and_check(st) != 0) { k3gc_st_close(st); return -1; }
+    *out = st;
+    return 0;
+}
 
 static const StTensor *st_find(const K3gcSt *st, const char *name)
 {
@@ -490,6 +544,38 @@ int k3gc_st_read_run(const K3gcSt *st, const K3gcExpertRun *r, unsigned char *ds
         o += r->s_bytes[i];
     }
     return 0;
+}
+
+/* The run's bytes into buf (capacity cap): a contiguous run with O_DIRECT straight into
+ * buf when buf is 4096-aligned and holds the enclosing 4096-byte window (the run then
+ * starts at buf + *pad, as the engine's k3_expert_load_direct leaves it, src/io/k3_st.c:
+ * 457-497), otherwise ordinary reads into buf (*pad = 0). Returns 0, or -1 on a short
+ * read. */
+int k3gc_st_read_run_into(const K3gcSt *st, const K3gcExpertRun *r, unsigned char *buf,
+                          int64_t cap, int64_t *pad)
+{
+    *pad = 0;
+    if (r->nbytes > cap) return -1;
+    if (r->contiguous) {
+        const int dfd = st->dfd ? st->dfd[r->shard] : -1;
+        const int64_t lo = r->off & ~(int64_t)(ST_ALIGN - 1);
+        const int64_t hi = (r->off + r->nbytes + ST_ALIGN - 1) & ~(int64_t)(ST_ALIGN - 1);
+        if (dfd >= 0 && ((uintptr_t)buf & (ST_ALIGN - 1)) == 0 && hi - lo <= cap) {
+            int64_t got = 0;
+            while (got < hi - lo) {
+                const int64_t want = hi - lo - got < ST_READ_MAX ? hi - lo - got : ST_READ_MAX;
+                const ssize_t n = pread(dfd, buf + got, (size_t)want, (off_t)(lo + got));
+                if (n <= 0) break;
+                got += n;
+            }
+            if (got >= r->off - lo + r->nbytes) {
+                *pad = r->off - lo;
+                return 0;
+            }
+        }
+        return read_full(st->fd[r->shard], buf, r->nbytes, r->off);
+    }
+    return k3gc_st_read_run(st, r, buf);
 }
 
 /* ------------------------------------------------------------- host tiling ---- */

@@ -60,6 +60,43 @@ class K3gcStats(C.Structure):
                 ("staged", C.c_int64)]
 
 
+class K3St(C.Structure):
+    """src/io/k3_st.h:56-70: the engine's checkpoint index (filled by its k3_st_open)."""
+    _fields_ = [("fd", C.c_void_p), ("dfd", C.c_void_p), ("path", C.c_void_p),
+                ("nshard", C.c_int), ("t", C.c_void_p), ("nt", C.c_int),
+                ("bucket", C.c_void_p), ("nbucket", C.c_int), ("strpool", C.c_void_p),
+                ("strcap", C.c_size_t), ("strlen_", C.c_size_t)]
+
+
+class K3QMat(C.Structure):
+    """src/io/k3_load.h:29-35."""
+    _fields_ = [("p_off", C.c_int64), ("p_bytes", C.c_int64), ("s_off", C.c_int64),
+                ("s_bytes", C.c_int64), ("rows", C.c_int), ("pcols", C.c_int),
+                ("scols", C.c_int)]
+
+
+class K3ExpertRef(C.Structure):
+    """src/io/k3_load.h:37-43."""
+    _fields_ = [("layer", C.c_int), ("expert", C.c_int), ("shard", C.c_int),
+                ("off", C.c_int64), ("nbytes", C.c_int64), ("contiguous", C.c_int),
+                ("m", K3QMat * 3)]
+
+
+class K3Cache(C.Structure):
+    """src/cache/k3_cache.h:47-96: the engine's expert cache, here on HBM slots
+    (k3_cache_init of this library)."""
+    _fields_ = [("src", K3ExpertSrc), ("st", C.c_void_p), ("n_layers", C.c_int),
+                ("n_experts", C.c_int), ("arena", C.c_void_p), ("slot_bytes", C.c_int64),
+                ("nslot", C.c_int), ("slot_of", C.POINTER(C.c_int32)),
+                ("key_of", C.POINTER(C.c_int32)), ("used_at", C.POINTER(C.c_uint64)),
+                ("pinned", C.POINTER(C.c_uint8)), ("ref", C.POINTER(K3ExpertRef)),
+                ("pad", C.POINTER(C.c_int32)), ("clock", C.c_uint64), ("hits", C.c_uint64),
+                ("misses", C.c_uint64), ("evictions", C.c_uint64), ("bytes_read", C.c_uint64),
+                ("prefetch_reads", C.c_uint64), ("load_seconds", C.c_double),
+                ("hist", C.POINTER(C.c_uint32)), ("trace", C.POINTER(C.c_int32)),
+                ("ntrace", C.c_int64), ("captrace", C.c_int64)]
+
+
 # the K3ExpertSrc entry points, called through the vtable as the engine does
 SRC_GET = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_int, C.c_void_p)
 SRC_GETMANY = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int, C.c_void_p, C.c_int)
@@ -239,6 +276,22 @@ def lib() -> C.CDLL:
         L.k3gc_dump_hist.restype = i
         L.k3gc_dump_trace.argtypes = [vp, C.c_char_p]
         L.k3gc_dump_trace.restype = i
+        L.k3_cache_init.argtypes = [C.POINTER(K3Cache), vp, C.POINTER(K3Cfg), C.c_int64]
+        L.k3_cache_init.restype = i
+        L.k3_cache_free.argtypes = [C.POINTER(K3Cache)]
+        L.k3_cache_free.restype = None
+        L.k3_cache_pin.argtypes = [C.POINTER(K3Cache), i, i, i]
+        L.k3_cache_pin.restype = i
+        L.k3_cache_prefetch.argtypes = [C.POINTER(K3Cache), i, i]
+        L.k3_cache_prefetch.restype = i
+        L.k3_cache_reset_stats.argtypes = [C.POINTER(K3Cache)]
+        L.k3_cache_reset_stats.restype = None
+        L.k3_cache_report.argtypes = [C.POINTER(K3Cache), C.c_char_p]
+        L.k3_cache_report.restype = None
+        L.k3_cache_dump_hist.argtypes = [C.POINTER(K3Cache), C.c_char_p]
+        L.k3_cache_dump_hist.restype = i
+        L.k3_cache_dump_trace.argtypes = [C.POINTER(K3Cache), C.c_char_p]
+        L.k3_cache_dump_trace.restype = i
         L.k3gc_stats.argtypes = [vp, C.POINTER(K3gcStats)]
         L.k3gc_stats.restype = None
         L.k3gc_step_begin.argtypes = [vp]
@@ -263,6 +316,13 @@ def lib() -> C.CDLL:
         L.k3gc_st_expert.restype = i
         L.k3gc_st_read_run.argtypes = [vp, C.POINTER(K3gcExpertRun), vp]
         L.k3gc_st_read_run.restype = i
+        L.k3gc_st_read_run_into.argtypes = [vp, C.POINTER(K3gcExpertRun), vp, C.c_int64,
+                                            C.POINTER(C.c_int64)]
+        L.k3gc_st_read_run_into.restype = i
+        L.k3gc_st_from_engine.argtypes = [C.POINTER(vp), vp]
+        L.k3gc_st_from_engine.restype = i
+        L.k3gc_bank_create_disk.argtypes = [C.POINTER(vp), vp, i, i, i]
+        L.k3gc_bank_create_disk.restype = i
         L.k3gc_bank_load.argtypes = [vp, vp, i, i, i]
         L.k3gc_bank_load.restype = i
         L.k3gc_tile_mxfp4_host.argtypes = [vp, vp, vp, i, i]
@@ -819,12 +879,29 @@ class Bank:
 
 
 class St:
-    """An index of the safetensors shards of a directory (k3gc_st_open)."""
+    """An index of the safetensors shards of a directory (k3gc_st_open), or of the engine's
+    own K3St (St.from_engine: k3gc_st_from_engine)."""
 
-    def __init__(self, path: str):
+    def __init__(self, path: str | None):
         self.ptr = C.c_void_p()
-        if lib().k3gc_st_open(C.byref(self.ptr), path.encode()) != 0:
+        if path is not None and lib().k3gc_st_open(C.byref(self.ptr), path.encode()) != 0:
             raise RuntimeError(f"k3gc_st_open({path}) failed")
+
+    @classmethod
+    def from_engine(cls, engine_st) -> "St":
+        """engine_st: a K3St the engine's k3_st_open filled (kept alive by the caller)."""
+        s = cls(None)
+        if lib().k3gc_st_from_engine(C.byref(s.ptr), C.byref(engine_st)) != 0:
+            raise RuntimeError("k3gc_st_from_engine failed")
+        return s
+
+    def read_run_into(self, r: K3gcExpertRun, buf: np.ndarray) -> int:
+        """The run into buf (k3gc_st_read_run_into); returns where it starts in buf."""
+        pad = C.c_int64()
+        if lib().k3gc_st_read_run_into(self.ptr, C.byref(r), buf.ctypes.data, buf.size,
+                                       C.byref(pad)) != 0:
+            raise IOError("short read")
+        return pad.value
 
     def count(self) -> int:
         return lib().k3gc_st_count(self.ptr)

@@ -412,3 +412,36 @@ def sim_pinned_lru(keys, cap, npin, hot=None, preloaded=False):
             seen[k] = 1
     return hits
 
+
+
+class EngineIO:
+    """The engine's own safetensors index and expert resolution (src/io/k3_st.c,
+    src/io/k3_load.c) from _ref/libk3ref.so: k3_st_open fills a K3St exactly as the
+    engine's main() would before it calls k3_cache_init, and k3_expert_ref /
+    k3_expert_load give the engine's geometry and bytes of an expert."""
+
+    def __init__(self, path):
+        L = C.CDLL(path)
+        vp = C.c_void_p
+        L.k3_st_open.argtypes = [vp, C.c_char_p]
+        L.k3_st_open.restype = C.c_int
+        L.k3_st_close.argtypes = [vp]
+        L.k3_st_close.restype = None
+        L.k3_expert_ref.argtypes = [vp, C.c_int, C.c_int, vp]
+        L.k3_expert_ref.restype = C.c_int
+        L.k3_expert_load.argtypes = [vp, vp, vp]
+        L.k3_expert_load.restype = C.c_int64
+        self.L = L
+
+
+_engine_io = None
+
+
+def engine_io() -> "EngineIO | None":
+    """EngineIO, or None when _ref was not built."""
+    global _engine_io
+    if _engine_io is None and os.path.exists(REF_SO):
+        lib = C.CDLL(REF_SO)
+        if hasattr(lib, "k3_st_open") and hasattr(lib, "k3_expert_load"):
+            _engine_io = EngineIO(REF_SO)
+    return _engine_io

@@ -115,9 +115,18 @@ def layouts():
                    "sh2", "wdt", "src", "layer", "cache_only"],
         "K3ExpertQ": ["p1", "s1", "p3", "s3", "p2", "s2"],
         "K3ExpertSrc": ["get", "getmany", "resident", "ctx"],
+        "K3Tensor": ["name", "shard", "dtype", "ndim", "shape", "off", "nbytes"],
+        "K3St": ["fd", "dfd", "path", "nshard", "t", "nt", "bucket", "nbucket", "strpool",
+                 "strcap", "strlen_"],
+        "K3QMat": ["p_off", "p_bytes", "s_off", "s_bytes", "rows", "pcols", "scols"],
+        "K3ExpertRef": ["layer", "expert", "shard", "off", "nbytes", "contiguous", "m"],
+        "K3Cache": ["src", "st", "n_layers", "n_experts", "arena", "slot_bytes", "nslot",
+                    "slot_of", "key_of", "used_at", "pinned", "ref", "pad", "clock", "hits",
+                    "misses", "evictions", "bytes_read", "prefetch_reads", "load_seconds",
+                    "hist", "trace", "ntrace", "captrace"],
     }
-    src = ['#include <stdio.h>', '#include <stddef.h>', '#include "k3.h"', 'int main(void){',
-           'printf("{");']
+    src = ['#include <stdio.h>', '#include <stddef.h>', '#include "k3.h"', '#include "k3_cache.h"',
+           'int main(void){', 'printf("{");']
     first = True
     for t, fs in fields.items():
         src.append(f'printf("{"" if first else ","}\\"{t}\\": {{\\"sizeof\\": %zu", sizeof({t}));')
@@ -130,13 +139,17 @@ def layouts():
         c = os.path.join(td, "probe.c")
         open(c, "w").write("\n".join(src))
         exe = os.path.join(td, "probe")
-        subprocess.check_call(["gcc", "-std=gnu99", "-I", os.path.join(REF, "include", "k3"), c,
-                               "-o", exe])
+        subprocess.check_call(["gcc", "-std=gnu99", "-I", os.path.join(REF, "include", "k3"),
+                               "-I", os.path.join(REF, "src", "io"), "-I",
+                               os.path.join(REF, "src", "cache"), c, "-o", exe])
         lay = json.loads(subprocess.check_output([exe]).decode())
     json.dump(lay, open(os.path.join(OUT, "layouts.json"), "w"), indent=1)
 
 
 if __name__ == "__main__":
+    if sys.argv[2:] == ["layouts"]:
+        layouts()
+        sys.exit(0)
     router(); moe(); situ(); mxfp4(); manifest(); trace(); cache_fixture(); layouts()
     for f in sorted(os.listdir(OUT)):
         print(f, os.path.getsize(os.path.join(OUT, f)))

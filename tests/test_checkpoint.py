@@ -213,3 +213,86 @@ def test_loader_refuses_crafted_headers(tmp_path, case):
                    hlen=(1 << 64) - 1)
     with pytest.raises(RuntimeError):
         k3moe.St(d)
+
+
+def _engine_st(path):
+    import oracle as O
+    io = O.engine_io()
+    if io is None:
+        pytest.skip("oracle/_ref was not built (the engine's k3_st.c fills the K3St)")
+    st = k3moe.K3St()
+    assert io.L.k3_st_open(C_byref(st), path.encode()) == 0
+    return io, st
+
+
+def C_byref(x):
+    import ctypes
+    return ctypes.byref(x)
+
+
+def test_index_from_the_engines_own_k3st(tmp_path):
+    """k3gc_st_from_engine over a K3St filled by the engine's k3_st_open (the index the
+    engine hands k3_cache_init): every expert of the fixture and of a synthetic two-shard
+    checkpoint (one expert out of order) resolves to the engine's k3_expert_ref geometry,
+    and k3gc_st_read_run_into gives the engine's k3_expert_load bytes, through O_DIRECT
+    into an aligned buffer (run at the returned pad) and ordinary reads otherwise."""
+    import ctypes
+    lay = k3moe.SynthLayer(k3moe.TINY, seed=5, layer=1, device=False)
+    other = k3moe.SynthLayer(k3moe.TINY, seed=5, layer=0, device=False)
+    from test_checkpoint import write_checkpoint
+    write_checkpoint(str(tmp_path), [other, lay], scramble=(1, 5))
+    checked = out_of_order = 0
+    for path, layers, ne in ((FIXTURE, [0], 24), (str(tmp_path), [0, 1], 16)):
+        io, est = _engine_st(path)
+        ours = k3moe.St.from_engine(est)
+        assert ours.count() == est.nt
+        raw = np.zeros(1 << 20, np.uint8)
+        a0 = (-raw.ctypes.data) % 4096
+        aligned = raw[a0:a0 + (1 << 19)]
+        for l in layers:
+            for e in range(ne):
+                r = k3moe.K3ExpertRef()
+                assert io.L.k3_expert_ref(ctypes.byref(est), l, e, ctypes.byref(r)) == 0
+                want = np.zeros(r.nbytes, np.uint8)
+                assert io.L.k3_expert_load(ctypes.byref(est), ctypes.byref(r),
+                                           want.ctypes.data) == r.nbytes
+                g = ours.expert(l, e)
+                # the engine calls a run contiguous when its six spans tile one window in
+                # any order; this index only when they also come in the checkpoint order
+                # (w1p w1s w2p w2s w3p w3s), reading the others as six spans in that order
+                assert (g.shard, g.nbytes) == (r.shard, r.nbytes)
+                assert g.contiguous <= r.contiguous
+                if g.contiguous:
+                    assert g.off == r.off
+                for i in range(3):
+                    assert (g.rows[i], g.pcols[i], g.p_bytes[i], g.s_bytes[i]) == \
+                        (r.m[i].rows, r.m[i].pcols, r.m[i].p_bytes, r.m[i].s_bytes)
+                canon = np.concatenate([want[o:o + n] for i in range(3) for o, n in
+                                        ((r.m[i].p_off, r.m[i].p_bytes),
+                                         (r.m[i].s_off, r.m[i].s_bytes))])
+                pad = ours.read_run_into(g, aligned)
+                assert np.array_equal(aligned[pad:pad + g.nbytes], canon), (l, e)
+                unaligned = raw[a0 + 1:a0 + 1 + (1 << 18)]
+                assert ours.read_run_into(g, unaligned) == 0
+                assert np.array_equal(unaligned[:g.nbytes], canon)
+                checked += 1
+                out_of_order += r.contiguous and not g.contiguous
+        ours.close()
+        io.L.k3_st_close(ctypes.byref(est))
+    assert checked == 24 + 32 and out_of_order == 1
+
+
+def test_index_from_a_malformed_k3st_is_refused():
+    """An engine index whose tensor points at a shard it does not have is refused."""
+    import ctypes
+    io, est = _engine_st(FIXTURE)
+    t = ctypes.cast(est.t, ctypes.POINTER(ctypes.c_byte * 72))
+    shard = ctypes.c_int.from_address(ctypes.addressof(t[3]) + 8)
+    keep = shard.value
+    shard.value = 7
+    p = ctypes.c_void_p()
+    assert k3moe.lib().k3gc_st_from_engine(ctypes.byref(p), ctypes.byref(est)) != 0
+    shard.value = keep
+    assert k3moe.lib().k3gc_st_from_engine(ctypes.byref(p), ctypes.byref(est)) == 0
+    k3moe.lib().k3gc_st_close(p)
+    io.L.k3_st_close(ctypes.byref(est))
