@@ -117,7 +117,7 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t nQd = (d + 511) / 512, nQi = (I + 511) / 512;
     const size_t o_xq8 = carve(&at, (size_t)T4 * nQd * 8448), o_hq8 = carve(&at, P4 * nQi * 8448);
     const size_t o_xq16 = carve(&at, (d / 32) * 1024), o_hq16 = carve(&at, (SI / 32 + 1) * 1024);
-    const size_t o_gpart = carve(&at, P4 * K3G_KS_G * 2 * I * 4);
+    const size_t o_gpart = carve(&at, P4 * K3G_KS_G_MAX * 2 * I * 4);
     const size_t o_sgpart = carve(&at, (size_t)K3G_KS_SG * T4 * 2 * (SI ? SI : 1) * 4);
     const size_t o_shpart = carve(&at, (size_t)K3G_KS_SD * T4 * d * 4);
     const size_t o_rpart = carve(&at, (size_t)T4 * E * K3G_KS_R * 16);

@@ -126,7 +126,10 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.nQi = (I + 511) / 512;
     g.nCsi = SI / 32;
     g.KSS = SI > 0 ? (K3G_KS_SG < g.nCd ? K3G_KS_SG : g.nCd) : 0;
-    g.KSG = K3G_KS_G < g.nQk ? K3G_KS_G : g.nQk;
+    {
+        const int ks = g.lat ? K3G_KS_G_LAT : K3G_KS_G;
+        g.KSG = ks < g.nQk ? ks : g.nQk;
+    }
     g.KSD = SI > 0 ? (K3G_KS_SD < g.nCsi ? K3G_KS_SD : g.nCsi) : 0;
     g.nRc = (d + 1023) / 1024;
     g.KSR = K3G_KS_R < g.nRc ? K3G_KS_R : g.nRc;
@@ -954,9 +957,9 @@ struct K3Dec {
             return;
         /* last slice of the tile: 32 rows of h = act(gate, up) -> FP8 pieces (one block) */
         const int r = lane & 31, row = 32 * gt + r;
-        const float gs = k3d_sum_sc1<K3G_KS_G>(rp, ((p * G.KSG * 2 + 0) * a.I + row) * 4,
+        const float gs = k3d_sum_sc1<K3G_KS_G_MAX>(rp, ((p * G.KSG * 2 + 0) * a.I + row) * 4,
                                                2 * a.I * 4, G.KSG);
-        const float us = k3d_sum_sc1<K3G_KS_G>(rp, ((p * G.KSG * 2 + 1) * a.I + row) * 4,
+        const float us = k3d_sum_sc1<K3G_KS_G_MAX>(rp, ((p * G.KSG * 2 + 1) * a.I + row) * 4,
                                                2 * a.I * 4, G.KSG);
         float h = lane < 32 ? k3d_act(gs, us, a.b1, a.b2) : 0.0f;
         const K3Rsrc rh = k3d_rsrc(a.hq8 + (size_t)p * G.nQi * K3G_BQ, (size_t)G.nQi * K3G_BQ);

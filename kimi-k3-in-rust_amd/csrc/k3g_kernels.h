@@ -65,7 +65,7 @@ typedef struct {
     double *rpart;                /* [T][E][K3G_KS_R][2] router slice sums */
     uint8_t *xq8;                 /* [T][ceil(d/512)][8448]: x's FP8 pieces, B layout */
     uint16_t *xq16;               /* [d/32][64][8]: x's bf16 pieces, column 3t + piece */
-    float *gpart;                 /* [T*k][K3G_KS_G][2][I] routed gate/up partial sums */
+    float *gpart;                 /* [T*k][K3G_KS_G_MAX][2][I] routed gate/up partial sums */
     uint8_t *hq8;                 /* [T*k][ceil(I/512)][8448]: h's FP8 pieces */
     float *sgpart;                /* [K3G_KS_SG][T][2][SI] shared gate/up partial sums */
     uint16_t *hq16;               /* [SI/32][64][8]: shared h's bf16 pieces */
@@ -169,6 +169,11 @@ int k3k_xpieces(const float *x, int T, int d, int ldb, uint16_t *xb, long long p
 #ifndef K3G_KS_G
 #define K3G_KS_G 7                /* routed gate/up: over 512-column quads of d */
 #endif
+#ifndef K3G_KS_G_LAT
+#define K3G_KS_G_LAT 2            /* the same in the latent layer (quads of L): its 16 slots
+                                   * x L/32 row tiles are many tickets already */
+#endif
+#define K3G_KS_G_MAX (K3G_KS_G > K3G_KS_G_LAT ? K3G_KS_G : K3G_KS_G_LAT)
 #ifndef K3G_KS_SG
 #define K3G_KS_SG 7               /* shared gate/up: over 32-column chunks of d */
 #endif
@@ -185,7 +190,7 @@ int k3k_xpieces(const float *x, int T, int d, int ldb, uint16_t *xb, long long p
 #define K3G_KS_LD 7               /* latent down: over 32-column chunks of d */
 #endif
 #ifndef K3G_KS_LU
-#define K3G_KS_LU 4               /* latent up: over 32-column chunks of L */
+#define K3G_KS_LU 8               /* latent up: over 32-column chunks of L */
 #endif
 #define K3G_DEC_WAVES_PER_EU 4
 
