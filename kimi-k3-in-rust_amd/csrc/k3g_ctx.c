@@ -118,11 +118,11 @@ int k3g_ctx_create(K3gCtx **out, int device, const K3gLayer *s, int max_tokens)
     const size_t o_xq8 = carve(&at, (size_t)T4 * nQd * 8448), o_hq8 = carve(&at, P4 * nQi * 8448);
     const size_t o_xq16 = carve(&at, (d / 32) * 1024), o_hq16 = carve(&at, (SI / 32 + 1) * 1024);
     const size_t o_gpart = carve(&at, P4 * K3G_KS_G_MAX * 2 * I * 4);
-    const size_t o_sgpart = carve(&at, (size_t)K3G_KS_SG * T4 * 2 * (SI ? SI : 1) * 4);
-    const size_t o_shpart = carve(&at, (size_t)K3G_KS_SD * T4 * d * 4);
-    const size_t o_rpart = carve(&at, (size_t)T4 * E * K3G_KS_R * 16);
+    const size_t o_sgpart = carve(&at, (size_t)K3G_KS_SG_MAX * T4 * 2 * (SI ? SI : 1) * 4);
+    const size_t o_shpart = carve(&at, (size_t)K3G_KS_SD_MAX * T4 * d * 4);
+    const size_t o_rpart = carve(&at, (size_t)T4 * E * K3G_KS_R_MAX * 16);
     const size_t dl = d > L ? d : L;       /* the routed down's output rows */
-    const size_t o_dcontrib = carve(&at, P4 * K3G_KS_D * dl * 4);
+    const size_t o_dcontrib = carve(&at, P4 * K3G_KS_D_MAX * dl * 4);
     /* the latent layer's: z's slices and FP8 pieces, the aggregate, its tiles' sums of
      * squares, its bf16 pieces, the latent up's slices */
     const int lat = L != d;

@@ -125,15 +125,17 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.nCL = L / 32;
     g.nQi = (I + 511) / 512;
     g.nCsi = SI / 32;
-    g.KSS = SI > 0 ? (K3G_KS_SG < g.nCd ? K3G_KS_SG : g.nCd) : 0;
+    const int kss = g.lat ? K3G_KS_SG_LAT : K3G_KS_SG, ksd = g.lat ? K3G_KS_SD_LAT : K3G_KS_SD;
+    const int ksr = g.lat ? K3G_KS_R_LAT : K3G_KS_R, ksdn = g.lat ? K3G_KS_D_LAT : K3G_KS_D;
+    g.KSS = SI > 0 ? (kss < g.nCd ? kss : g.nCd) : 0;
     {
         const int ks = g.lat ? K3G_KS_G_LAT : K3G_KS_G;
         g.KSG = ks < g.nQk ? ks : g.nQk;
     }
-    g.KSD = SI > 0 ? (K3G_KS_SD < g.nCsi ? K3G_KS_SD : g.nCsi) : 0;
+    g.KSD = SI > 0 ? (ksd < g.nCsi ? ksd : g.nCsi) : 0;
     g.nRc = (d + 1023) / 1024;
-    g.KSR = K3G_KS_R < g.nRc ? K3G_KS_R : g.nRc;
-    g.KSDN = K3G_KS_D < g.nQi ? K3G_KS_D : g.nQi;
+    g.KSR = ksr < g.nRc ? ksr : g.nRc;
+    g.KSDN = ksdn < g.nQi ? ksdn : g.nQi;
     g.KSLD = g.lat ? (K3G_KS_LD < g.nCd ? K3G_KS_LD : g.nCd) : 0;
     g.KSLU = g.lat ? (K3G_KS_LU < g.nCL ? K3G_KS_LU : g.nCL) : 0;
     g.nSGt = (SI + 16 * SG_TILES - 1) / (16 * SG_TILES);
@@ -710,9 +712,9 @@ struct K3Dec {
         /* the last slice of the row: the slices summed in slice order, then the score
          * interval (any summation order is inside the interval's bound) */
         if (lane < a.T) {
-            double2 pv[K3G_KS_R];
+            double2 pv[K3G_KS_R_MAX];
 #pragma unroll
-            for (int q = 0; q < K3G_KS_R; ++q) {
+            for (int q = 0; q < K3G_KS_R_MAX; ++q) {
                 if (wg_slices)
                     pv[q] = q < G.KSR ? make_double2(rl->part[q][lane][0], rl->part[q][lane][1])
                                      : make_double2(0.0, 0.0);
@@ -724,7 +726,7 @@ struct K3Dec {
             }
             double sv = 0.0, bv = 0.0;
 #pragma unroll
-            for (int q = 0; q < K3G_KS_R; ++q) {
+            for (int q = 0; q < K3G_KS_R_MAX; ++q) {
                 if (q < G.KSR) {
                     sv += pv[q].x;
                     bv += pv[q].y;
@@ -856,9 +858,9 @@ struct K3Dec {
         for (int tt = 0; tt < a.T; ++tt) {
             if (lane < 16 * SG_TILES && row < a.SI) {
                 const int qs = a.T * 2 * a.SI * 4;
-                const float gs = k3d_sum_sc1<K3G_KS_SG>(rp, ((tt * 2 + 0) * a.SI + row) * 4, qs,
+                const float gs = k3d_sum_sc1<K3G_KS_SG_MAX>(rp, ((tt * 2 + 0) * a.SI + row) * 4, qs,
                                                         G.KSS);
-                const float us = k3d_sum_sc1<K3G_KS_SG>(rp, ((tt * 2 + 1) * a.SI + row) * 4, qs,
+                const float us = k3d_sum_sc1<K3G_KS_SG_MAX>(rp, ((tt * 2 + 1) * a.SI + row) * 4, qs,
                                                         G.KSS);
                 float r2 = k3d_act(gs, us, a.b1, a.b2);
 #pragma unroll
@@ -1316,11 +1318,11 @@ struct K3Dec {
             }
             float c = 0.0f;
             for (int j0 = 0; j0 < a.k; j0 += 8) {
-                float y[8][K3G_KS_D];
+                float y[8][K3G_KS_D_MAX];
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
-                    for (int q = 0; q < K3G_KS_D; ++q) {
+                    for (int q = 0; q < K3G_KS_D_MAX; ++q) {
                         const int p = t * a.k + j0 + jj;
                         y[jj][q] = __uint_as_float(k3d_b32<K3_BPOL>(
                             rc, j0 + jj < a.k && q < G.KSDN
@@ -1335,7 +1337,7 @@ struct K3Dec {
                     const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), j));
                     float yy = 0.0f;
 #pragma unroll
-                    for (int q = 0; q < K3G_KS_D; ++q)
+                    for (int q = 0; q < K3G_KS_D_MAX; ++q)
                         if (q < G.KSDN) yy += y[jj][q];
                     c = __fadd_rn(c, __fmul_rn(w, yy));
                 }
@@ -1361,13 +1363,13 @@ struct K3Dec {
         const K3Rsrc ru = k3d_rsrc(a.upart, (size_t)G.KSLU * a.T * a.d * 4);
         const K3Rsrc rs = k3d_rsrc(a.shpart, (size_t)(G.KSD > 0 ? G.KSD : 1) * a.T * a.d * 4);
         for (int t = 0; t < a.T; ++t) {
-            float uv[K3G_KS_LU], sh[K3G_KS_SD];
+            float uv[K3G_KS_LU], sh[K3G_KS_SD_MAX];
 #pragma unroll
             for (int q = 0; q < K3G_KS_LU; ++q)
                 uv[q] = __uint_as_float(k3d_b32<K3_BPOL>(
                     ru, q < G.KSLU ? ((q * a.T + t) * a.d + row) * 4 : K3_OOB));
 #pragma unroll
-            for (int q = 0; q < K3G_KS_SD; ++q)
+            for (int q = 0; q < K3G_KS_SD_MAX; ++q)
                 sh[q] = __uint_as_float(k3d_b32<K3_BPOL>(
                     rs, a.SI > 0 && q < G.KSD ? ((q * a.T + t) * a.d + row) * 4 : K3_OOB));
             float c = 0.0f;
@@ -1377,7 +1379,7 @@ struct K3Dec {
             if (a.SI > 0) {
                 float s2 = 0.0f;
 #pragma unroll
-                for (int q = 0; q < K3G_KS_SD; ++q)
+                for (int q = 0; q < K3G_KS_SD_MAX; ++q)
                     if (q < G.KSD) s2 += sh[q];
                 c = __fadd_rn(c, s2);
             }
@@ -1406,18 +1408,18 @@ struct K3Dec {
                 wv = __hip_atomic_load(&a.wt[t * a.k + lane], __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
             }
-            float sh[K3G_KS_SD];
+            float sh[K3G_KS_SD_MAX];
 #pragma unroll
-            for (int q = 0; q < K3G_KS_SD; ++q)
+            for (int q = 0; q < K3G_KS_SD_MAX; ++q)
                 sh[q] = __uint_as_float(k3d_b32<K3_BPOL>(
                     rs, a.SI > 0 && q < G.KSD ? ((q * a.T + t) * a.d + row) * 4 : K3_OOB));
             float c = 0.0f;
             for (int j0 = 0; j0 < a.k; j0 += 8) {
-                float y[8][K3G_KS_D];
+                float y[8][K3G_KS_D_MAX];
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj)
 #pragma unroll
-                    for (int q = 0; q < K3G_KS_D; ++q) {
+                    for (int q = 0; q < K3G_KS_D_MAX; ++q) {
                         const int p = t * a.k + j0 + jj;
                         y[jj][q] = __uint_as_float(k3d_b32<K3_BPOL>(
                             rc, j0 + jj < a.k && q < G.KSDN ? ((p * G.KSDN + q) * a.d + row) * 4
@@ -1432,7 +1434,7 @@ struct K3Dec {
                     const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wv), j));
                     float yy = 0.0f;
 #pragma unroll
-                    for (int q = 0; q < K3G_KS_D; ++q)
+                    for (int q = 0; q < K3G_KS_D_MAX; ++q)
                         if (q < G.KSDN) yy += y[jj][q];
                     c = __fadd_rn(c, __fmul_rn(w, yy));
                 }
@@ -1440,7 +1442,7 @@ struct K3Dec {
             if (a.SI > 0) {
                 float s2 = 0.0f;
 #pragma unroll
-                for (int q = 0; q < K3G_KS_SD; ++q)
+                for (int q = 0; q < K3G_KS_SD_MAX; ++q)
                     if (q < G.KSD) s2 += sh[q];
                 c = __fadd_rn(c, s2);
             }

@@ -192,6 +192,25 @@ int k3k_xpieces(const float *x, int T, int d, int ldb, uint16_t *xb, long long p
 #ifndef K3G_KS_LU
 #define K3G_KS_LU 8               /* latent up: over 32-column chunks of L */
 #endif
+/* the shared gate/up, shared down, router and routed down slices of the latent layer
+ * (default: as the plain layer's) */
+#ifndef K3G_KS_SG_LAT
+#define K3G_KS_SG_LAT K3G_KS_SG
+#endif
+#ifndef K3G_KS_SD_LAT
+#define K3G_KS_SD_LAT K3G_KS_SD
+#endif
+#ifndef K3G_KS_R_LAT
+#define K3G_KS_R_LAT K3G_KS_R
+#endif
+#ifndef K3G_KS_D_LAT
+#define K3G_KS_D_LAT K3G_KS_D
+#endif
+#define K3G_KS_MAX2(a, b) ((a) > (b) ? (a) : (b))
+#define K3G_KS_SG_MAX K3G_KS_MAX2(K3G_KS_SG, K3G_KS_SG_LAT)
+#define K3G_KS_SD_MAX K3G_KS_MAX2(K3G_KS_SD, K3G_KS_SD_LAT)
+#define K3G_KS_R_MAX K3G_KS_MAX2(K3G_KS_R, K3G_KS_R_LAT)
+#define K3G_KS_D_MAX K3G_KS_MAX2(K3G_KS_D, K3G_KS_D_LAT)
 #define K3G_DEC_WAVES_PER_EU 4
 
 /* bytes of counters and tickets per call of the fused kernel at this shape */

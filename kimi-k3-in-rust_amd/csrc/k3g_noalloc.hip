@@ -64,15 +64,15 @@ NoallocLayout layout_for(int d, int E, int k, int I, int SI)
     NoallocLayout l;
     size_t at = 2 * (size_t)K3G_NOALLOC_BANK;
     l.rs = carve(&at, T4 * E * 16);
-    l.rpart = carve(&at, T4 * E * K3G_KS_R * 16);
+    l.rpart = carve(&at, T4 * E * K3G_KS_R_MAX * 16);
     l.xq8 = carve(&at, T4 * nQd * 8448);
     l.xq16 = carve(&at, ((size_t)d / 32) * 1024);
     l.gpart = carve(&at, P4 * K3G_KS_G_MAX * 2 * (size_t)I * 4);
     l.hq8 = carve(&at, P4 * nQi * 8448);
-    l.sgpart = carve(&at, (size_t)K3G_KS_SG * T4 * 2 * (SI ? SI : 1) * 4);
+    l.sgpart = carve(&at, (size_t)K3G_KS_SG_MAX * T4 * 2 * (SI ? SI : 1) * 4);
     l.hq16 = carve(&at, ((size_t)SI / 32 + 1) * 1024);
-    l.contrib = carve(&at, P4 * K3G_KS_D * (size_t)d * 4);
-    l.shpart = carve(&at, (size_t)K3G_KS_SD * T4 * d * 4);
+    l.contrib = carve(&at, P4 * K3G_KS_D_MAX * (size_t)d * 4);
+    l.shpart = carve(&at, (size_t)K3G_KS_SD_MAX * T4 * d * 4);
     l.idx = carve(&at, P4 * 4);
     l.wt = carve(&at, P4 * 4);
     l.err = carve(&at, 4);
