@@ -750,6 +750,10 @@ struct K3Dec {
             k3d_set_event(a.sync, G.eSEL, lane);
             return;
         }
+        /* the routed tickets also need x's pieces: the routing is published once both
+         * exist. x's pieces are done long before the router rows, so their event is
+         * checked first, off the path from the last row to the publication. */
+        if (!k3d_wait_event(a.sync, G.eX, 0, a.spin_limit, a.err, lane)) return;
         /* every router row in: the select is the only waiter, so it reads the rows'
          * sub-counters itself instead of waiting for the top count and the event flags
          * (one returning atomic and a flag store less on the routed experts' path) */
@@ -763,8 +767,6 @@ struct K3Dec {
                              a.renorm, a.routed_scale, a.idx, a.wt, a.force, a.stats, lane,
                              a.trace && t == 0 ? a.trace + 3 * G.total + 2 : nullptr);
         if (a.trace && lane == 0) a.trace[3 * G.total + 1] = wall_clock64();
-        /* the routed tickets also need x's pieces: publish the routing once both exist */
-        if (!k3d_wait_event(a.sync, G.eX, 0, a.spin_limit, a.err, lane)) return;
         k3d_set_event(a.sync, G.eSEL, lane);
         __builtin_amdgcn_s_setprio(0);
     }
