@@ -652,7 +652,10 @@ def dropin(a):
 
     def timed(ws, cfg, xs, T, warm, steps, fn):
         n = warm + steps
-        out = np.zeros((n * T, D), np.float32)
+        # every call's output kept for the check below; filled (NaN) beforehand so its
+        # pages are mapped, as the engine's reused output buffer is: a fresh page's first
+        # write is a page fault (7 per token here) that the engine never pays
+        out = np.full((n * T, D), np.nan, np.float32)
         idx = np.zeros(K, np.int32)
         wt = np.zeros(K, np.float32)
 

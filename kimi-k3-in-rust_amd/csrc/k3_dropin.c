@@ -31,6 +31,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 long k3_expert_drops = 0;
 
@@ -645,6 +646,40 @@ static void settle_tokens(unsigned char *seen, const int *ridx, int k, int E, in
     }
 }
 
+/* The engine's getmany/get calls for a layer that ran with every expert resident: all
+ * hits, in the engine's order, with the cache's counters and clock as when fetching
+ * first. */
+static void fetch_resident(Fetcher *f, DevState *s, K3gCache *hc, int *ridx, int k, int E,
+                           int T, int mode, hipStream_t st)
+{
+    f->table = s->table;
+    f->have = s->have;
+    const long d0 = k3_expert_drops;
+    k3gc_step_begin(hc);
+    fetch_tokens(f, s, ridx, k, E, 0, T, mode == 1 && T > 1, 0);
+    k3gc_step_end(hc, st);
+    if (k3_expert_drops != d0) k3g_fatal("k3_moe: a resident expert was not served");
+}
+
+/* Spin until the running layer sets a pinned flag; 0 when it has not within 0.1 s (a
+ * launch cut short by an error, or a GPU busy with other work: the caller then waits
+ * for the stream instead). */
+static int await_flag(const volatile int *flag)
+{
+    struct timespec t0, t1;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    for (unsigned i = 1;; i++) {
+        if (*flag) {
+            __atomic_thread_fence(__ATOMIC_ACQUIRE);
+            return 1;
+        }
+        if (!(i & 1023)) {
+            clock_gettime(CLOCK_MONOTONIC, &t1);
+            if ((t1.tv_sec - t0.tv_sec) * 1e9 + (t1.tv_nsec - t0.tv_nsec) > 1e8) return 0;
+        }
+    }
+}
+
 /* The end of the next token group from t0: whole units (one token, or a 64-token prefill
  * chunk, the engine's [64 m, 64 m + 64)) while the group's distinct experts fit in cap
  * slots; a unit that alone exceeds cap is split into tokens (at least one: the cache
@@ -833,24 +868,43 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         k3gc_wait(hc, st);
         G.experts = k3gc_layer_table(hc, w->layer, st);
         if (!G.experts) k3g_fatal("k3_moe: expert table update failed");
+        /* One fused decode launch writes out, the routing, a nonzero error code and two
+         * flags straight into the pinned twin (no transfer back): the engine's get calls
+         * go out as soon as the routing is there, while the layer still runs, and the
+         * call returns once the outputs are (work queued on the stream later still
+         * waits for the launch's last waves). Without the flags (a rerun, a launch cut
+         * short by an error) the stream is waited for. */
+        const int direct = k3g_fuses(ctx, &G, T);
+        volatile int *flag = (volatile int *)(pin + 128);
+        if (direct) {
+            *perr = 0;
+            flag[K3K_HFLAG_ROUTED] = 0;
+            flag[K3K_HFLAG_DONE] = 0;
+            ctx->host_idx = ridx;
+            ctx->host_wt = rwt;
+            ctx->host_err = perr;
+            ctx->host_flag = (int *)flag;
+        }
         /* x goes in right before the layer, so the two launches reach the GPU back to
          * back (host work between them would leave it idle) */
         xfer(xd, px, xbytes, hipMemcpyHostToDevice, st);
+        int reran = 0;
         for (int pass = 0;; pass++) {
-            if (k3g_moe(ctx, &G, xd, T, od, didx, dwt, st) != 0)
+            if (k3g_moe(ctx, &G, xd, T, direct ? pout : od, didx, dwt, st) != 0)
                 k3g_fatal("k3_moe: launch failed");
-            xfer(pin, io, io_n, hipMemcpyDeviceToHost, st);
+            if (!direct) xfer(pin, io, io_n, hipMemcpyDeviceToHost, st);
+            reran = pass > 0;
             if (pass > 0 || !verify_mirrors(s, st)) break;
         }
-        K3G_CHECK(hipStreamSynchronize(st));
+        ctx->host_idx = NULL;
+        ctx->host_wt = NULL;
+        ctx->host_err = NULL;
+        ctx->host_flag = NULL;
+        const int early = direct && !reran && await_flag(&flag[K3K_HFLAG_ROUTED]);
+        if (early) fetch_resident(&f, s, hc, ridx, k, E, T, mode, st);
+        if (!early || !await_flag(&flag[K3K_HFLAG_DONE])) K3G_CHECK(hipStreamSynchronize(st));
         if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error");
-        f.table = s->table;
-        f.have = s->have;
-        const long d0 = k3_expert_drops;
-        k3gc_step_begin(hc);
-        fetch_tokens(&f, s, ridx, k, E, 0, T, mode == 1 && T > 1, 0);
-        k3gc_step_end(hc, st);
-        if (k3_expert_drops != d0) k3g_fatal("k3_moe: a resident expert was not served");
+        if (!early) fetch_resident(&f, s, hc, ridx, k, E, T, mode, st);
         host_copy(out, pout, xbytes);
         g_last_paths = ctx->paths;
         const int batched = mode == 1 && T > 1;

@@ -890,11 +890,22 @@ static int run_fused(K3gCtx *c, const K3gLayer *L, const float *x, int T, float 
     a.given = given;
     a.spin_limit = 1ll << 21;
     a.trace = c->trace;
+    a.hidx = c->host_idx;
+    a.hwt = c->host_idx ? c->host_wt : NULL;
+    a.herr = c->host_err;
+    a.hflag = c->host_idx && c->host_wt && c->host_err ? c->host_flag : NULL;
     k3g_stage_begin(c, K3G_ST_FUSED, st);
     const int rc = k3k_decode_fused(&a, st);
     k3g_stage_end(c, K3G_ST_FUSED, st);
     if (rc == 0) c->epoch = (c->epoch + 1) & 0x3fffffff;   /* the next call's bank */
     return rc;
+}
+
+int k3g_fuses(const K3gCtx *c, const K3gLayer *L, int T)
+{
+    const int have = L->expert_fmt == K3G_EXPERT_F32 ? (L->w1 && L->w3 && L->w2)
+                                                     : L->experts != NULL;
+    return have && fits(c, L, T) && fusable(c, L, T);
 }
 
 int k3g_moe(K3gCtx *c, const K3gLayer *L, const float *x, int T, float *out, int32_t *idx,

@@ -85,6 +85,12 @@ struct K3gCtx {
     int gemm_fp8;                /* routed experts on the FP4 x FP8 matrix cores */
     uint8_t *xq8b, *hq8b;        /* MXFP8 x [T][d512] + scales, h [T*k][I512] + scales */
     unsigned long long *trace;   /* optional per-ticket timestamps of the fused kernel */
+    /* optional pinned host copies that the fused kernel writes directly (the routing, a
+     * nonzero error code), for callers reading the results on the host with no transfer */
+    int32_t *host_idx;
+    float *host_wt;
+    int *host_err;
+    int *host_flag;              /* with the three above: K3K_HFLAG_INTS pinned flags */
     /* optional per-stage timing: a ring of event pairs around each stage of a call,
      * harvested only when the ring wraps or the totals are read */
     int prof;
@@ -110,5 +116,8 @@ void k3g_ctx_routed_wait(K3gCtx *c, hipEvent_t ev);
  * reports it, clears it on the device and resets the fused kernel's counters, and
  * returns it (what k3g_sync does after its own read). */
 int k3g_err_settle(K3gCtx *c, int e);
+/* 1 when k3g_moe runs this layer at T tokens as one fused decode launch (the launch that
+ * writes c->host_idx/host_wt/host_err when they are set) */
+int k3g_fuses(const K3gCtx *c, const K3gLayer *L, int T);
 
 #endif /* K3G_CTX_H */

@@ -107,7 +107,7 @@ struct K3Geo {
     int nCL, KSLD, KSLU, nLDt, nLUt, nNR, nLD, nLU, oLD, oNR, oLU;
     /* counter lines */
     int lR, lSD, lD, lTSG, lTG, lRE, lDT, lLD, lLU, cX, cX16, cR, cSGF, cGF, cZ, cA, cN, eX,
-        eX16, eR, eSEL, eSGF, eGF, eZ, eA, eN, nlines;
+        eX16, eR, eSEL, eSGF, eGF, eZ, eA, eN, cOD, nlines;
 };
 
 __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int SI, int L)
@@ -189,7 +189,8 @@ __host__ __device__ inline K3Geo k3_geo(int T, int d, int E, int k, int I, int S
     g.eA = g.eZ + K3_EVLINES;
     g.eN = g.eA + K3_EVLINES;
     g.eGF = g.eN + K3_EVLINES;
-    g.nlines = g.eGF + g.P * K3_EVLINES;
+    g.cOD = g.eGF + g.P * K3_EVLINES;   /* output tiles written (host copies only) */
+    g.nlines = g.cOD + 1 + NSUB;
     return g;
 }
 
@@ -280,14 +281,19 @@ __device__ __forceinline__ void k3d_set_event(int *sync, int ev, int lane)
  * sub-counter) sets the event. Same-address atomics serialise at the memory side, so a
  * few hundred arrivals on one line would take microseconds; here at most
  * ceil(count / NSUB) + NSUB meet on one line. */
-__device__ __forceinline__ void k3d_arrive_event2(int *sync, int ctr, int count, int who,
-                                                  int ev, int lane)
+__device__ __forceinline__ bool k3d_arrive2(int *sync, int ctr, int count, int who, int lane)
 {
     const int sub = who % NSUB;
     const int members = count / NSUB + (sub < count % NSUB ? 1 : 0);
-    if (!k3d_arrive(k3d_line(sync, ctr + 1 + sub), members - 1, lane)) return;
+    if (!k3d_arrive(k3d_line(sync, ctr + 1 + sub), members - 1, lane)) return false;
     const int tops = count < NSUB ? count : NSUB;
-    if (k3d_arrive(k3d_line(sync, ctr), tops - 1, lane)) k3d_set_event(sync, ev, lane);
+    return k3d_arrive(k3d_line(sync, ctr), tops - 1, lane);
+}
+
+__device__ __forceinline__ void k3d_arrive_event2(int *sync, int ctr, int count, int who,
+                                                  int ev, int lane)
+{
+    if (k3d_arrive2(sync, ctr, count, who, lane)) k3d_set_event(sync, ev, lane);
 }
 
 /* Instrumentation: the moment a ticket's waits are over (its second trace stamp). */
@@ -748,6 +754,7 @@ struct K3Dec {
             /* the routing came with the call: publish it once x's pieces exist */
             if (!k3d_wait_event(a.sync, G.eX, 0, a.spin_limit, a.err, lane)) return;
             k3d_set_event(a.sync, G.eSEL, lane);
+            host_routing(a, lane);
             return;
         }
         /* the routed tickets also need x's pieces: the routing is published once both
@@ -769,6 +776,57 @@ struct K3Dec {
         if (a.trace && lane == 0) a.trace[3 * G.total + 1] = wall_clock64();
         k3d_set_event(a.sync, G.eSEL, lane);
         __builtin_amdgcn_s_setprio(0);
+        host_routing(a, lane);
+    }
+
+    /* the published routing to the caller's host copies (after the event, off the routed
+     * tickets' path); the event's release has made this wave's writes readable */
+    static __device__ __forceinline__ void host_routing(const K3kDecode &a, int lane)
+    {
+        if (!a.hidx) return;
+        /* system-scope stores are written through to the host's memory; the flag follows
+         * once they are complete */
+        for (int i = lane; i < a.T * a.k; i += 64) {
+            __hip_atomic_store(&a.hidx[i],
+                               __hip_atomic_load(&a.idx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(&a.hwt[i],
+                               __hip_atomic_load(&a.wt[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        if (!a.hflag) return;
+        __builtin_amdgcn_s_waitcnt(0);
+        if (lane == 0)
+            __hip_atomic_store(&a.hflag[K3K_HFLAG_ROUTED], 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+
+    /* out[i] = v: with the host flags, a store written through to the host's memory (the
+     * completion flag must not overtake it) */
+    static __device__ __forceinline__ void put_out(const K3kDecode &a, size_t i, float v)
+    {
+        if (a.hflag) __hip_atomic_store(&a.out[i], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        else a.out[i] = v;
+    }
+
+    /* With the host flags: an output tile of 32 rows counts itself out once its stores are
+     * complete (k3d_arrive waits for them); the last of the d/32 tiles passes the device
+     * error word on to the host copy and marks the outputs complete. The tiles are the
+     * last work of the launch (every other ticket feeds them), so the flag means the
+     * caller's results are all there. */
+    static __device__ __forceinline__ void out_done(const K3kDecode &a, const K3Geo &G, int tile,
+                                                    int lane)
+    {
+        if (!a.hflag || !k3d_arrive2(a.sync, G.cOD, a.d / 32, tile, lane)) return;
+        if (lane == 0) {
+            const int e = a.err ? __hip_atomic_load(a.err, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT) : 0;
+            if (e && a.herr)
+                __hip_atomic_store(a.herr, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __builtin_amdgcn_s_waitcnt(0);
+            __hip_atomic_store(&a.hflag[K3K_HFLAG_DONE], 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 
     /* ---------------------------------------------------------------- SG ---- */
@@ -1385,8 +1443,9 @@ struct K3Dec {
                     if (q < G.KSD) s2 += sh[q];
                 c = __fadd_rn(c, s2);
             }
-            if (lane < 32) a.out[(size_t)t * a.d + row] = c;
+            if (lane < 32) put_out(a, (size_t)t * a.d + row, c);
         }
+        out_done(a, G, rt, lane);
     }
 
     /* ------------------------------------------------------------ combine ---- */
@@ -1448,8 +1507,9 @@ struct K3Dec {
                     if (q < G.KSD) s2 += sh[q];
                 c = __fadd_rn(c, s2);
             }
-            if (lane < 32) a.out[(size_t)t * a.d + row] = c;
+            if (lane < 32) put_out(a, (size_t)t * a.d + row, c);
         }
+        out_done(a, G, dt, lane);
     }
 };
 
@@ -1495,6 +1555,14 @@ k_decode_fused(K3kDecode a)
         else if ((t -= G.nD) < G.nNR) K3Dec<NT>::norm(ap, t, lane);
         else K3Dec<NT>::latent_up(ap, t - G.nNR, lane);
         if (a.trace && lane == 0) a.trace[3 * tk + 2] = wall_clock64();
+    }
+    /* an error code to the caller's host copy: the error word keeps the first code raised,
+     * and every wave that raised one reads it here after its own raise (the wait orders the
+     * two), so the host copy is nonzero exactly when the word is */
+    if (a.herr && a.err && lane == 0) {
+        __builtin_amdgcn_s_waitcnt(0);
+        const int e = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (e) __hip_atomic_store(a.herr, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 

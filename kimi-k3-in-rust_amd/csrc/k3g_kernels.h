@@ -95,7 +95,24 @@ typedef struct {
     double *nss;                  /* [T][L/32] the aggregate's sums of squares per 32 rows */
     uint16_t *aq16;               /* [L/32][64][8]: the normalised aggregate's bf16 pieces */
     float *upart;                 /* [K3G_KS_LU][T][d] latent up partial sums */
+    /* Optional copies in pinned host memory, for a caller that reads the results on the
+     * host with no transfer after the launch (out may then be pinned host memory too):
+     * hidx/hwt the routing [T][k] once published, herr the error code when one was
+     * raised (the caller zeroes *herr before the launch; it stays 0 on success). */
+    int32_t *hidx;
+    float *hwt;
+    int *herr;
+    /* With hidx/hwt/herr: pinned host flags the caller zeroes before the launch and may
+     * poll while it runs: [K3K_HFLAG_ROUTED] set once hidx/hwt are complete,
+     * [K3K_HFLAG_DONE] once out (then written through to host memory) and herr are. A
+     * launch cut short by an error may never set them: the caller then waits for the
+     * stream. */
+    int *hflag;
 } K3kDecode;
+
+#define K3K_HFLAG_ROUTED 0
+#define K3K_HFLAG_DONE 16     /* a separate 64-byte line */
+#define K3K_HFLAG_INTS 32
 
 /* One grouped GEMM on the bf16 matrix cores (k3g_gemm.hip). Columns are (token, slot)
  * pairs grouped by expert (tiles) or all tokens (dense, the shared expert). */
