@@ -31,7 +31,6 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
-#include <time.h>
 
 long k3_expert_drops = 0;
 
@@ -661,25 +660,6 @@ static void fetch_resident(Fetcher *f, DevState *s, K3gCache *hc, int *ridx, int
     if (k3_expert_drops != d0) k3g_fatal("k3_moe: a resident expert was not served");
 }
 
-/* Spin until the running layer sets a pinned flag; 0 when it has not within 0.1 s (a
- * launch cut short by an error, or a GPU busy with other work: the caller then waits
- * for the stream instead). */
-static int await_flag(const volatile int *flag)
-{
-    struct timespec t0, t1;
-    clock_gettime(CLOCK_MONOTONIC, &t0);
-    for (unsigned i = 1;; i++) {
-        if (*flag) {
-            __atomic_thread_fence(__ATOMIC_ACQUIRE);
-            return 1;
-        }
-        if (!(i & 1023)) {
-            clock_gettime(CLOCK_MONOTONIC, &t1);
-            if ((t1.tv_sec - t0.tv_sec) * 1e9 + (t1.tv_nsec - t0.tv_nsec) > 1e8) return 0;
-        }
-    }
-}
-
 /* The end of the next token group from t0: whole units (one token, or a 64-token prefill
  * chunk, the engine's [64 m, 64 m + 64)) while the group's distinct experts fit in cap
  * slots; a unit that alone exceeds cap is split into tokens (at least one: the cache
@@ -900,10 +880,16 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         ctx->host_wt = NULL;
         ctx->host_err = NULL;
         ctx->host_flag = NULL;
-        const int early = direct && !reran && await_flag(&flag[K3K_HFLAG_ROUTED]);
+        const int early = direct && !reran && k3g_await_flag(&flag[K3K_HFLAG_ROUTED], 0.1);
         if (early) fetch_resident(&f, s, hc, ridx, k, E, T, mode, st);
-        if (!early || !await_flag(&flag[K3K_HFLAG_DONE])) K3G_CHECK(hipStreamSynchronize(st));
-        if (k3g_err_settle(ctx, *perr) != 0) k3g_fatal("k3_moe: device error");
+        int e = *perr;
+        if (!early || !k3g_await_flag(&flag[K3K_HFLAG_DONE], 0.1)) {
+            K3G_CHECK(hipStreamSynchronize(st));
+            /* the error word came back with the outputs' flag or the copy; else read it */
+            if (direct && !flag[K3K_HFLAG_DONE]) e = k3g_err_read(ctx);
+            else e = *perr;
+        }
+        if (k3g_err_settle(ctx, e) != 0) k3g_fatal("k3_moe: device error");
         if (!early) fetch_resident(&f, s, hc, ridx, k, E, T, mode, st);
         host_copy(out, pout, xbytes);
         g_last_paths = ctx->paths;

@@ -12,6 +12,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 void k3g_fatal_hip(const char *what, hipError_t e, const char *file, int line)
 {
@@ -893,12 +894,39 @@ static int run_fused(K3gCtx *c, const K3gLayer *L, const float *x, int T, float 
     a.hidx = c->host_idx;
     a.hwt = c->host_idx ? c->host_wt : NULL;
     a.herr = c->host_err;
-    a.hflag = c->host_idx && c->host_wt && c->host_err ? c->host_flag : NULL;
+    a.hflag = c->host_idx && c->host_wt ? c->host_flag : NULL;
     k3g_stage_begin(c, K3G_ST_FUSED, st);
     const int rc = k3k_decode_fused(&a, st);
     k3g_stage_end(c, K3G_ST_FUSED, st);
     if (rc == 0) c->epoch = (c->epoch + 1) & 0x3fffffff;   /* the next call's bank */
     return rc;
+}
+
+int k3g_await_flag(const volatile int *flag, double limit_s)
+{
+    struct timespec t0, t1;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    for (unsigned i = 1;; i++) {
+        if (*flag) {
+            __atomic_thread_fence(__ATOMIC_ACQUIRE);
+            return 1;
+        }
+        if (!(i & 1023)) {
+            clock_gettime(CLOCK_MONOTONIC, &t1);
+            if ((double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec) >
+                limit_s)
+                return 0;
+        }
+    }
+}
+
+int k3g_err_read(K3gCtx *c)
+{
+    int e = 0;
+    if (hipSetDevice(c->device) != hipSuccess ||
+        hipMemcpy(&e, c->err, sizeof e, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    return e;
 }
 
 int k3g_fuses(const K3gCtx *c, const K3gLayer *L, int T)

@@ -90,7 +90,8 @@ struct K3gCtx {
     int32_t *host_idx;
     float *host_wt;
     int *host_err;
-    int *host_flag;              /* with the three above: K3K_HFLAG_INTS pinned flags */
+    int *host_flag;              /* with host_idx/host_wt: K3K_HFLAG_INTS pinned flags
+                                  * (the outputs' flag only with host_err too) */
     /* optional per-stage timing: a ring of event pairs around each stage of a call,
      * harvested only when the ring wraps or the totals are read */
     int prof;
@@ -119,5 +120,12 @@ int k3g_err_settle(K3gCtx *c, int e);
 /* 1 when k3g_moe runs this layer at T tokens as one fused decode launch (the launch that
  * writes c->host_idx/host_wt/host_err when they are set) */
 int k3g_fuses(const K3gCtx *c, const K3gLayer *L, int T);
+/* Spin until a running launch sets a pinned host flag (host_flag above): 1 when set, 0 when
+ * not within limit_s seconds (a launch cut short by an error, a GPU busy with other work:
+ * the caller then waits for the stream instead). */
+int k3g_await_flag(const volatile int *flag, double limit_s);
+/* The device error word, read back synchronously (-1 when it cannot be read), once the
+ * caller has waited for its stream: for callers whose flags did not come */
+int k3g_err_read(K3gCtx *c);
 
 #endif /* K3G_CTX_H */

@@ -787,12 +787,10 @@ struct K3Dec {
         /* system-scope stores are written through to the host's memory; the flag follows
          * once they are complete */
         for (int i = lane; i < a.T * a.k; i += 64) {
-            __hip_atomic_store(&a.hidx[i],
-                               __hip_atomic_load(&a.idx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_store(&a.hwt[i],
-                               __hip_atomic_load(&a.wt[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            const int e = __hip_atomic_load(&a.idx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float w = __hip_atomic_load(&a.wt[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.hidx[i], e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(&a.hwt[i], w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
         if (!a.hflag) return;
         __builtin_amdgcn_s_waitcnt(0);
@@ -805,24 +803,24 @@ struct K3Dec {
      * completion flag must not overtake it) */
     static __device__ __forceinline__ void put_out(const K3kDecode &a, size_t i, float v)
     {
-        if (a.hflag) __hip_atomic_store(&a.out[i], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (a.hflag && a.herr)
+            __hip_atomic_store(&a.out[i], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         else a.out[i] = v;
     }
 
-    /* With the host flags: an output tile of 32 rows counts itself out once its stores are
-     * complete (k3d_arrive waits for them); the last of the d/32 tiles passes the device
-     * error word on to the host copy and marks the outputs complete. The tiles are the
+    /* With the host flags and herr: an output tile of 32 rows counts itself out once its
+     * stores are complete (k3d_arrive waits for them); the last of the d/32 tiles passes the
+     * device error word on to the host copy and marks the outputs complete. The tiles are the
      * last work of the launch (every other ticket feeds them), so the flag means the
      * caller's results are all there. */
     static __device__ __forceinline__ void out_done(const K3kDecode &a, const K3Geo &G, int tile,
                                                     int lane)
     {
-        if (!a.hflag || !k3d_arrive2(a.sync, G.cOD, a.d / 32, tile, lane)) return;
+        if (!a.hflag || !a.herr || !k3d_arrive2(a.sync, G.cOD, a.d / 32, tile, lane)) return;
         if (lane == 0) {
             const int e = a.err ? __hip_atomic_load(a.err, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT) : 0;
-            if (e && a.herr)
-                __hip_atomic_store(a.herr, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (e) __hip_atomic_store(a.herr, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             __builtin_amdgcn_s_waitcnt(0);
             __hip_atomic_store(&a.hflag[K3K_HFLAG_DONE], 1, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_SYSTEM);
@@ -1555,14 +1553,6 @@ k_decode_fused(K3kDecode a)
         else if ((t -= G.nD) < G.nNR) K3Dec<NT>::norm(ap, t, lane);
         else K3Dec<NT>::latent_up(ap, t - G.nNR, lane);
         if (a.trace && lane == 0) a.trace[3 * tk + 2] = wall_clock64();
-    }
-    /* an error code to the caller's host copy: the error word keeps the first code raised,
-     * and every wave that raised one reads it here after its own raise (the wait orders the
-     * two), so the host copy is nonzero exactly when the word is */
-    if (a.herr && a.err && lane == 0) {
-        __builtin_amdgcn_s_waitcnt(0);
-        const int e = __hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (e) __hip_atomic_store(a.herr, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 

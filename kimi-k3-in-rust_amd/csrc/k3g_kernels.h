@@ -97,16 +97,16 @@ typedef struct {
     float *upart;                 /* [K3G_KS_LU][T][d] latent up partial sums */
     /* Optional copies in pinned host memory, for a caller that reads the results on the
      * host with no transfer after the launch (out may then be pinned host memory too):
-     * hidx/hwt the routing [T][k] once published, herr the error code when one was
-     * raised (the caller zeroes *herr before the launch; it stays 0 on success). */
+     * hidx/hwt the routing [T][k] once published; with hflag, herr the error word as it
+     * stands when the outputs are complete (the caller zeroes *herr before the launch). */
     int32_t *hidx;
     float *hwt;
     int *herr;
-    /* With hidx/hwt/herr: pinned host flags the caller zeroes before the launch and may
-     * poll while it runs: [K3K_HFLAG_ROUTED] set once hidx/hwt are complete,
-     * [K3K_HFLAG_DONE] once out (then written through to host memory) and herr are. A
-     * launch cut short by an error may never set them: the caller then waits for the
-     * stream. */
+    /* With hidx/hwt: pinned host flags the caller zeroes before the launch and may poll
+     * while it runs: [K3K_HFLAG_ROUTED] set once hidx/hwt are complete; with herr as well,
+     * [K3K_HFLAG_DONE] once out (then written through to memory) and herr are. A launch
+     * cut short by an error may never set them: the caller then waits for the stream and
+     * reads the device error word itself. */
     int *hflag;
 } K3kDecode;
 
