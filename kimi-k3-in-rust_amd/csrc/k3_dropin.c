@@ -350,6 +350,19 @@ static void *stage(DevState *s, size_t bytes)
     return s->stage;
 }
 
+/* A decode call on the flags' path returns while its launch's last waves still retire:
+ * before the process ends it waits for every stream the drop-in used. Registered at the
+ * first such call, after the HIP runtime has set itself up, so it runs before the
+ * runtime's own exit work. Takes no lock: a fatal error exits with the lock held. */
+static void drain_at_exit(void)
+{
+    for (int d = 0; d < K3_MAX_DEV; d++)
+        if (g_dev[d].used && g_dev[d].ctx) {
+            hipSetDevice(d);
+            hipStreamSynchronize(g_dev[d].ctx->stream);
+        }
+}
+
 void k3moe_forget_weights(void)
 {
     pthread_mutex_lock(&g_lock);
@@ -856,6 +869,8 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
          * short by an error) the stream is waited for. */
         const int direct = k3g_fuses(ctx, &G, T);
         volatile int *flag = (volatile int *)(pin + 128);
+        static int drain_registered = 0;
+        if (direct && !drain_registered) drain_registered = atexit(drain_at_exit) == 0;
         if (direct) {
             *perr = 0;
             flag[K3K_HFLAG_ROUTED] = 0;
