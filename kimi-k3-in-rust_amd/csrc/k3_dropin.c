@@ -900,8 +900,9 @@ static void moe_run(float *out, const float *x, const K3MoeW *w, const K3Cfg *c,
         int e = *perr;
         if (!early || !k3g_await_flag(&flag[K3K_HFLAG_DONE], 0.1)) {
             K3G_CHECK(hipStreamSynchronize(st));
-            /* the error word came back with the outputs' flag or the copy; else read it */
-            if (direct && !flag[K3K_HFLAG_DONE]) e = k3g_err_read(ctx);
+            /* the error word came back with the copy, or with the outputs' flag of a
+             * single launch; else it is read */
+            if (direct && (reran || !flag[K3K_HFLAG_DONE])) e = k3g_err_read(ctx);
             else e = *perr;
         }
         if (k3g_err_settle(ctx, e) != 0) k3g_fatal("k3_moe: device error");
