@@ -130,7 +130,9 @@ static void xfer(void *dst, const void *src, size_t n, hipMemcpyKind kind, hipSt
     K3G_CHECK(hipMemcpyAsync(dst, src, n, kind, st));
 }
 
-/* pinned host memory of at least `bytes`, grow-only */
+/* pinned host memory of at least `bytes`, grow-only; coherent (fine-grained), since the
+ * fused decode kernel writes results and flags into it that the host reads while the
+ * launch still runs */
 static unsigned char *pinned(DevState *s, size_t bytes)
 {
     if (bytes > s->pin_bytes) {
@@ -140,7 +142,7 @@ static unsigned char *pinned(DevState *s, size_t bytes)
         }
         s->pin = NULL;
         const size_t nb = bytes + bytes / 4;
-        K3G_CHECK(hipHostMalloc((void **)&s->pin, nb, hipHostMallocDefault));
+        K3G_CHECK(hipHostMalloc((void **)&s->pin, nb, hipHostMallocCoherent));
         s->pin_bytes = nb;
     }
     return s->pin;
