@@ -367,6 +367,65 @@ def _q8_rows(rows, inn, seed, stream):
     return out
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_resident_latent_layer(gpu, T):
+    """A LatentMoE layer (bf16 latent down/up, RMSNorm of the aggregate, two shared experts
+    fused, SiTU) with every expert in a tiled HBM cache: one fused decode launch that writes
+    out, the routing and its flags straight into pinned memory (the latent up's output
+    tiles counted), the engine's get calls while it runs; against the oracle's k3_moe."""
+    d, E, k, Lw, I = 256, 32, 4, 128, 128
+    SI = 2 * I
+    say(f"case: k3_moe latent layer d={d}, E={E}, top-{k}, latent {Lw}, I={I}, shared {SI}, "
+        f"T={T}, all experts resident in a tiled HBM cache")
+    shape = k3moe.Shape("resident latent", Lw, E, k, I, n_shared=2, routed_scale=1.0,
+                        x_bf16=False)
+    layer = k3moe.SynthLayer(shape, seed=63, layout="tiled")
+    bank = k3moe.Bank(1, E, Lw, I, k3moe.K3G_EXPERT_MXFP4_TILED)
+    bank.fill_from_layer(layer, 0)
+    slot = (bank.expert_bytes + 65535) // 65536 * 65536
+    cache = k3moe.Cache(bank, topk=k, budget_bytes=(E + 1) * slot)
+    for e in range(E):
+        assert cache.prefetch(0, e) == 0
+    cache.reset_stats()
+    gate = np.ascontiguousarray(k3moe.host_normal(E * d, 63, 801, 0.0, 0.05))
+    bias = k3moe.host_normal(E, 63, 802, 0.0, 0.01)
+    lnorm = k3moe.host_normal(Lw, 63, 803, 1.0, 0.1)
+    bf = lambda n, s_: k3moe.bf16_bits(k3moe.host_normal(n, 63, s_, 0.0, 0.05, bf16=True))  # noqa: E731
+    down, up = bf(Lw * d, 804), bf(d * Lw, 805)
+    sh1, sh3, sh2 = bf(SI * d, 806), bf(SI * d, 807), bf(d * SI, 808)
+    x = np.ascontiguousarray(k3moe.host_normal(T * d, 63, 809, 0.0, 1.0).reshape(T, d))
+
+    def weights(src_ptr):
+        w = k3moe.K3MoeW()
+        w.gate, w.bias, w.latent_norm = gate.ctypes.data, bias.ctypes.data, lnorm.ctypes.data
+        w.down, w.up = down.ctypes.data, up.ctypes.data
+        w.sh1, w.sh3, w.sh2 = sh1.ctypes.data, sh3.ctypes.data, sh2.ctypes.data
+        w.wdt = k3moe.K3_WBF16
+        w.src, w.layer = src_ptr, 0
+        return w
+
+    cfg = k3moe.K3Cfg()
+    cfg.hidden, cfg.latent, cfg.moe_inter = d, Lw, I
+    cfg.n_experts, cfg.topk, cfg.n_shared = E, k, 2
+    cfg.routed_scale, cfg.moe_renorm, cfg.latent_norm = 1.0, 1, 1
+    cfg.rms_eps, cfg.situ_b1, cfg.situ_b2, cfg.n_layers = 1e-6, 4.0, 25.0, 1
+    d0 = drops()
+    out, idx, wt, paths = dropin(weights(cache.src_ptr), cfg, x)
+    st = cache.stats()
+    k3moe.lib().k3moe_forget_weights()
+    src = O.MemSrc({(0, e): layer.expert_host(e) for e in range(E)}, 1, E, layer.geo)
+    oo, oi, ow = O.oracle().moe(weights(src.ptr), cfg, x)
+    r = rel_l2(out, oo)
+    say(f"  kernels {paths}, rel-L2 {r:.3e}, requests {st.requests}, hits {st.hits}")
+    assert paths == FUSED and drops() == d0
+    assert np.isfinite(out).all() and r <= REL
+    assert st.misses == 0 and st.requests > 0 and st.hits == st.requests
+    assert np.array_equal(idx, oi)
+    np.testing.assert_allclose(wt, ow, rtol=1e-6)
+    cache.free()
+    bank.free()
+
+
 @pytest.mark.parametrize("latent,prefill,T", [(True, False, 1), (True, True, 6),
                                               (False, False, 3), (False, True, 9)])
 def test_int8_draft_weights(gpu, latent, prefill, T):
