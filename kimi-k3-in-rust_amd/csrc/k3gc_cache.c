@@ -462,6 +462,15 @@ static int copy_in(K3gCache *c, int slot, int32_t key)
     return 0;
 }
 
+/* A slot handed out: its LRU stamp, and, inside a step, the step whose end event any later
+ * copy into the slot must wait for (a slot used in the open step is never evicted before
+ * the step ends, so no copy waits on that event before it is recorded) */
+static void touch(K3gCache *c, int slot)
+{
+    c->used_at[slot] = ++c->clock;
+    if (c->step_open) c->use_step[slot] = c->step;
+}
+
 /* Bring (layer, expert) resident; returns its slot or -1. src/cache/k3_cache.c:63-110 */
 static int admit(K3gCache *c, int layer, int expert)
 {
@@ -469,7 +478,7 @@ static int admit(K3gCache *c, int layer, int expert)
     int slot = c->slot_of[key];
     if (slot >= 0) {
         c->hits++;
-        c->used_at[slot] = ++c->clock;
+        touch(c, slot);
         return slot;
     }
     c->misses++;
@@ -491,7 +500,7 @@ static int admit(K3gCache *c, int layer, int expert)
     c->key_of[slot] = key;
     c->slot_of[key] = slot;
     key_in(c, key);
-    c->used_at[slot] = ++c->clock;
+    touch(c, slot);
     return slot;
 }
 
@@ -545,6 +554,8 @@ static int cache_getmany(K3ExpertSrc *self, int layer, const int *ids, int n)
             c->evictions++;
         }
         c->key_of[slot] = K3GC_INFLIGHT;
+        /* the LRU stamp only: the copy below waits on the step of the slot's last user,
+         * and the step of this use is marked when the slot is published */
         c->used_at[slot] = ++c->clock;
         slots[nw] = slot;
         experts[nw] = e;
@@ -570,7 +581,7 @@ static int cache_getmany(K3ExpertSrc *self, int layer, const int *ids, int n)
         c->key_of[slots[i]] = key;
         c->slot_of[key] = slots[i];
         key_in(c, key);
-        c->used_at[slots[i]] = ++c->clock;
+        touch(c, slots[i]);
         c->prefetch_reads++;
     }
     return pub;
@@ -764,10 +775,6 @@ void k3gc_step_end(K3gCache *c, void *stream)
         if (c->step >= K3GC_STEP_RING) K3G_CHECK(hipEventSynchronize(ev));
         K3G_CHECK(hipEventRecord(ev, (hipStream_t)stream));
     }
-    if (c->step_open)
-        for (int i = 0; i < c->nslot; i++)
-            if (c->key_of[i] != K3GC_EMPTY && c->used_at[i] >= c->step_clock)
-                c->use_step[i] = c->step;
     c->step++;
     c->step_open = 0;
 }

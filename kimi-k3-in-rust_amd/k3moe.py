@@ -1031,12 +1031,21 @@ class Cache:
               T: int, rms_eps: float = 1e-5) -> None:
         """k3gc_chain: h (device [T][hidden]) through the MoE half of len(layers) layers;
         post_norms: device pointers of the RMSNorm weights (None entries: no norm)."""
+        self.chain_call(ctx, layers, post_norms, first_layer, h_ptr, T, rms_eps)()
+
+    def chain_call(self, ctx: "Ctx", layers: list, post_norms: list, first_layer: int,
+                   h_ptr: int, T: int, rms_eps: float = 1e-5):
+        """The same call with its argument arrays formed once, as a C caller holds them:
+        returns a function that runs k3gc_chain (and raises on failure)."""
         arr = (K3gLayer * len(layers))(*layers)
         pn = (C.c_void_p * len(layers))(*[p if p else None for p in post_norms])
-        rc = lib().k3gc_chain(ctx.ptr, self.ptr, arr, pn, first_layer, len(layers),
-                              C.c_void_p(h_ptr), T, rms_eps, None)
-        if rc != 0:
-            raise RuntimeError("k3gc_chain failed")
+        fn, n = lib().k3gc_chain, len(layers)
+        cp, sp, hp = ctx.ptr, self.ptr, C.c_void_p(h_ptr)
+
+        def run() -> None:
+            if fn(cp, sp, arr, pn, first_layer, n, hp, T, rms_eps, None) != 0:
+                raise RuntimeError("k3gc_chain failed")
+        return run
 
     def free(self) -> None:
         if self.ptr:
